@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""RotateK decode benchmark on one MI355X (BASELINE.json metric).
+
+Workload: one decode step at batch 32, 32 heads (MHA),
+head_dim 128, fp16; visual span 14,000 tokens stored rotated and truncated to
+32 of 128 channels, plus 2,000 full-width text tokens; synthetic seeded
+inputs (no checkpoints offline).  A "step" is one call of
+``rotatek_decode`` (a single fused HIP launch) with every input resident in
+HBM.
+
+Printed JSON line (rank 0): ``value`` = microseconds per decode step (eager,
+wall clock over exactly ``--steps`` steps between device synchronisations);
+``roofline`` = algorithmic bytes per launch / average launch duration (HIP
+events around each launch on the launching stream) against the 8 TB/s HBM
+peak; ``cpu_baseline`` = the CPU oracle (numpy fp32) on a bounded sample of
+the same workload, scaled to a full step.  Also reported: hipGraph-replayed
+step time and the full-channel HIP baseline on the same seeded data.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "µs per decode step + achieved HBM GB/s (% of peak), B=32, 16k ctx, keep 25%"
+HBM_PEAK_GBPS = 8000.0
+
+
+def _log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _time_wall(fn, steps):
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e6
+
+
+def _time_launches(fn, steps):
+    """Average per-launch duration (us) from event pairs on the current stream."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for s, e in evs:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in evs) / steps * 1e3
+
+
+def _time_graph(fn, steps, warmup):
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(1, warmup)):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    for _ in range(5):
+        g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(steps):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / steps * 1e3
+
+
+def _cpu_baseline(inp, cfg, budget_s=12.0):
+    """CPU oracle (numpy fp32) over whole batch elements of the same inputs,
+    cycling over the batch until ~budget_s of CPU work; returns us per full
+    step (median per-element time x B)."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from oracle import decode as od
+
+    def host(t, b):
+        return None if t is None else t[b:b + 1].float().cpu().numpy()
+
+    names = ("q_full", "R_partial", "delta_mu", "k_full", "v_full", "mask_full", "k_sparse", "v_sparse")
+    nb = min(cfg.B, 4)
+    elems = []
+    for b in range(nb):
+        a = {k: host(inp[k], b) for k in names}
+        elems.append({k: (v.astype(np.float32) if v is not None else v) for k, v in a.items()})
+    times, t_total, i = [], 0.0, 0
+    while t_total < budget_s or len(times) < 3:
+        a = elems[i % nb]
+        t0 = time.perf_counter()
+        od.rotatek_decode(a["q_full"], a["R_partial"], a["delta_mu"], a["k_full"], a["v_full"],
+                          a["mask_full"], a["k_sparse"], a["v_sparse"], inp["num_kv_groups"],
+                          compute_dtype=np.float32)
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        t_total += dt
+        i += 1
+    per_b = sorted(times)[len(times) // 2]
+    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    return {
+        "value": per_b * cfg.B * 1e6,
+        "unit": "us/step",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"numpy fp32 oracle (oracle/decode.py) on batch elements 0..{nb - 1} of the same inputs "
+                  f"(all {cfg.H_q} heads, full {cfg.S_v}+{cfg.S_f} context each), {len(times)} runs, "
+                  f"median per-element time x B={cfg.B}; {t_total:.1f} s of CPU work",
+    }
+
+
+def _traffic(cfg_name):
+    path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="cfg2")
+    ap.add_argument("--family", default="paper", choices=["paper", "gqa"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-dense", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the RotateK decode "
+              "shards by (batch, KV head) with no exchange, so N GPUs run N independent copies.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from rotatek_amd import synth
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    from rotatek_amd.kernels.full_channel_flash_decoding import full_channel_decode
+    from rotatek_amd.kernels.gqa_decode import full_channel_decode_gqa, rotatek_decode_gqa
+
+    cfg = synth.CONFIGS[args.config]
+    torch.cuda.set_device(0)
+    _log(f"[bench] {torch.cuda.get_device_name(0)}; generating {cfg}")
+    inp = synth.make_decode_inputs(cfg, "cuda", seed=0, with_dense=not args.no_dense)
+    dargs = synth.decode_args(inp)
+    rot = rotatek_decode_gqa if args.family == "gqa" else rotatek_decode_fused
+    dense = full_channel_decode_gqa if args.family == "gqa" else full_channel_decode
+
+    def step():
+        return rot(**dargs)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    _log("[bench] warmup done")
+    us = _time_wall(step, args.steps)
+    us_launch = _time_launches(step, args.steps)
+    us_graph = _time_graph(step, args.steps, args.warmup)
+    nbytes = synth.decode_bytes(cfg)
+    gbps = nbytes / (us_launch * 1e-6) / 1e9
+    _log(f"[bench] rotatek eager {us:.1f} us/step, per-launch {us_launch:.1f} us, graph {us_graph:.1f} us, "
+         f"{gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS * 100:.1f}% of peak)")
+
+    extra = {}
+    if not args.no_dense:
+        kd, vd = inp["k_dense"], inp["v_dense"]
+
+        def dstep():
+            return dense(inp["q_full"], kd, vd, num_kv_groups=cfg.G)
+
+        for _ in range(args.warmup):
+            dstep()
+        d_us = _time_wall(dstep, args.steps)
+        d_launch = _time_launches(dstep, args.steps)
+        d_graph = _time_graph(dstep, args.steps, args.warmup)
+        dbytes = synth.decode_bytes(cfg, dense=True)
+        extra = {
+            "dense_us_per_step": round(d_us, 2),
+            "dense_graph_us_per_step": round(d_graph, 2),
+            "dense_achieved_gbps": round(dbytes / (d_launch * 1e-6) / 1e9, 1),
+            "speedup_vs_dense": round(d_us / us, 3),
+            "speedup_vs_dense_graph": round(d_graph / us_graph, 3),
+        }
+        _log(f"[bench] dense eager {d_us:.1f} us/step, graph {d_graph:.1f} us -> speedup "
+             f"{d_us / us:.2f}x eager, {d_graph / us_graph:.2f}x graph")
+
+    cpu = None
+    if not args.no_cpu:
+        _log("[bench] timing the CPU oracle on a bounded sample")
+        cpu = _cpu_baseline(inp, cfg)
+        _log(f"[bench] cpu baseline {cpu['value']:.0f} us/step on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(us, 2),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us / 1e3, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16" if cfg.dtype == torch.float16 else "bf16",
+        "data": "synthetic: seeded N(0,1) q/K/V, x8 outlier Key channels, orthogonal R_k per head, "
+                "top-32 channels by mean |K R_k|",
+        "config": {
+            "workload": f"{cfg.name}: RotateK decode step, B={cfg.B}, H_q={cfg.H_q}, H_kv={cfg.H_kv}, D=128, "
+                        f"S_v={cfg.S_v} (keep {cfg.keep}), S_f={cfg.S_f}, family={args.family}",
+            "batch": cfg.B, "heads_q": cfg.H_q, "heads_kv": cfg.H_kv, "visual_tokens": cfg.S_v,
+            "full_tokens": cfg.S_f, "kept_channels": cfg.keep, "family": args.family,
+        },
+        "achieved_gbps": round(gbps, 1),
+        "pct_of_peak_hbm": round(gbps / HBM_PEAK_GBPS * 100, 2),
+        "graph_us_per_step": round(us_graph, 2),
+        "launch_us": round(us_launch, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": _traffic(cfg.name),
+        },
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,178 @@
+/*
+ * rotatek_hip.h -- C ABI of librotatek_hip.so, the MI355X (gfx950) library
+ * behind the RotateK decode hot path and its prefill producer.
+ *
+ * Every entry point is plain C: device pointers, element strides, sizes, a
+ * dtype code, a caller-owned workspace and a hipStream_t passed as void*.
+ * Nothing here allocates device memory, throws, exits or synchronises the
+ * host; every function returns an rk_status (0 = success, negative = error)
+ * that rk_strerror() turns into text.  Shapes and strides are validated on
+ * the host before any HIP call, so the *_check() variants and the error
+ * paths of every entry point run without a GPU.
+ *
+ * Tensors are described by rk_tensor: a device pointer, a dtype, the rank
+ * and per-dimension sizes and strides (in elements, any sign-free layout;
+ * views such as V[:, :, s_p:s_p+s_v] are accepted as they are).
+ *
+ * Reference interfaces replaced (beomseokg/rotatek, file:line):
+ *   rk_rotatek_decode      rotatek/kernels/fused_decode.py:303-420
+ *                          (rotatek_decode_fused_triton, ROTATEK_KERNEL=paper)
+ *                          and rotatek/kernels/gqa_decode.py:280-321
+ *                          (rotatek_decode_gqa, ROTATEK_KERNEL=gqa)
+ *   rk_full_channel_decode rotatek/kernels/full_channel_flash_decoding.py:162-229
+ *                          (full_channel_decode_triton) and
+ *                          rotatek/kernels/gqa_decode.py:254-277
+ *                          (full_channel_decode_gqa)
+ *   rk_key_covariance      integrations/lmms_eval/models/model_utils/
+ *                          kv_pruning_utils.py:112-115 (mean, centering,
+ *                          covariance einsum, symmetrisation)
+ *   rk_rotate_keys         kv_pruning_utils.py:152 (K_vis @ R_partial, the
+ *                          truncated visual-Key write)
+ *   rk_channel_scores      channel scoring of the head-wise top-k selection
+ *                          (mean |K_vis R|), no reference counterpart beyond
+ *                          the keep mask of kv_pruning_utils.py:158-159
+ *   rk_topk_channels       head-wise channel top-k -> ascending indices + mask
+ *                          (kv_pruning_utils.py:158-159 keep_mask)
+ *   rk_gather_rotation     R_partial = R_full[..., idx] and
+ *                          delta_mu = mu - (mu R) R^T (kv_pruning_utils.py:150-156)
+ */
+#ifndef ROTATEK_HIP_H
+#define ROTATEK_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RK_ABI_VERSION 1
+
+/* Element types. */
+typedef enum rk_dtype {
+  RK_F16 = 0,
+  RK_BF16 = 1,
+  RK_F32 = 2,
+  RK_F64 = 3,
+  RK_U8 = 4,    /* also used for bool masks */
+  RK_I32 = 5,
+  RK_I64 = 6
+} rk_dtype;
+
+/* Status codes (0 = success). */
+typedef enum rk_status {
+  RK_OK = 0,
+  RK_ERR_NULL = -1,          /* required pointer or descriptor is NULL      */
+  RK_ERR_RANK = -2,          /* tensor has the wrong number of dimensions   */
+  RK_ERR_DTYPE = -3,         /* unsupported or mismatched element type      */
+  RK_ERR_SHAPE = -4,         /* sizes disagree between tensors              */
+  RK_ERR_HEADS = -5,         /* H_q / num_kv_groups != H_kv                 */
+  RK_ERR_HEAD_DIM = -6,      /* head_dim other than 128                     */
+  RK_ERR_KEEP_DIM = -7,      /* kept channels outside 1..head_dim           */
+  RK_ERR_STRIDE = -8,        /* negative or overflowing stride              */
+  RK_ERR_WORKSPACE = -9,     /* workspace NULL, misaligned or too small     */
+  RK_ERR_ARG = -10,          /* other invalid scalar argument               */
+  RK_ERR_HIP = -11,          /* a HIP runtime call failed                   */
+  RK_ERR_NO_DEVICE = -12     /* no HIP device visible                       */
+} rk_status;
+
+/* Decode launch policy (ROTATEK_KERNEL). */
+typedef enum rk_policy {
+  RK_POLICY_PAPER = 0,  /* one work unit per query head: K/V re-read per head */
+  RK_POLICY_GQA = 1     /* the query heads of a KV group share each K/V tile  */
+} rk_policy;
+
+#define RK_MAX_DIMS 4
+
+typedef struct rk_tensor {
+  void* data;                  /* device pointer                               */
+  int32_t dtype;               /* rk_dtype                                     */
+  int32_t ndim;                /* 1..4                                         */
+  int64_t shape[RK_MAX_DIMS];  /* sizes; entries >= ndim ignored               */
+  int64_t stride[RK_MAX_DIMS]; /* element strides                              */
+} rk_tensor;
+
+/* ------------------------------------------------------------------ misc */
+const char* rk_strerror(int status);
+int rk_abi_version(void);
+/* Compute units of HIP device `device` (0 on error, sets *status). */
+int rk_device_cu_count(int device, int* status);
+
+/* ------------------------------------------------------------------ decode
+ * One RotateK decode step (fused_decode.py:303-420 / gqa_decode.py:280-321):
+ *   out[b,h,:] = softmax over {visual, prompt+text} tokens of
+ *     visual:      (k_sparse . (q R_partial) + q . delta_mu) / sqrt(D)
+ *     prompt+text: (k_full . q) / sqrt(D), tokens with mask_full == 0 skipped
+ *   applied to v_sparse / v_full, written as acc / (l + 1e-6).
+ * Shapes: q_full [B,H_q,D]; R_partial [B,H_kv,D,Dk]; delta_mu [B,H_kv,D] or
+ * NULL; k_full, v_full [B,H_kv,S_f,D]; mask_full [B,S_f] u8 or NULL (= all
+ * ones); k_sparse [B,H_kv,S_v,Dk]; v_sparse [B,H_kv,S_v,D]; out [B,H_q,D]
+ * (dtype of q_full).  D must be 128.  q, K, V and out share one dtype
+ * (F16 or BF16); R_partial and delta_mu may be F16, BF16 or F32.
+ * The workspace (rk_rotatek_decode_check) holds split partials and one
+ * ticket counter per work unit; it must be zero-filled once when first
+ * allocated and is left zeroed by every completed call, so the call is
+ * hipGraph-capturable.  Calls that overlap on one workspace race.
+ */
+int rk_rotatek_decode_check(const rk_tensor* q_full, const rk_tensor* R_partial,
+                            const rk_tensor* delta_mu, const rk_tensor* k_full,
+                            const rk_tensor* v_full, const rk_tensor* mask_full,
+                            const rk_tensor* k_sparse, const rk_tensor* v_sparse,
+                            int64_t num_kv_groups, const rk_tensor* out,
+                            int32_t policy, int32_t num_cus,
+                            size_t* workspace_bytes);
+
+int rk_rotatek_decode(const rk_tensor* q_full, const rk_tensor* R_partial,
+                      const rk_tensor* delta_mu, const rk_tensor* k_full,
+                      const rk_tensor* v_full, const rk_tensor* mask_full,
+                      const rk_tensor* k_sparse, const rk_tensor* v_sparse,
+                      int64_t num_kv_groups, const rk_tensor* out,
+                      int32_t policy, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* Dense (full-channel) decode, the baseline the RotateK speed-up is measured
+ * against (full_channel_flash_decoding.py:162-229, gqa_decode.py:254-277):
+ * q [B,H_q,D], k/v [B,H_kv,S,D], out [B,H_q,D]. */
+int rk_full_channel_decode_check(const rk_tensor* q, const rk_tensor* k,
+                                 const rk_tensor* v, int64_t num_kv_groups,
+                                 const rk_tensor* out, int32_t policy,
+                                 int32_t num_cus, size_t* workspace_bytes);
+
+int rk_full_channel_decode(const rk_tensor* q, const rk_tensor* k,
+                           const rk_tensor* v, int64_t num_kv_groups,
+                           const rk_tensor* out, int32_t policy,
+                           void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Split plan the decode entry points use for a shape (host only), exposed
+ * for tests and benchmarks.  Fields are filled on RK_OK. */
+typedef struct rk_decode_plan {
+  int64_t units;          /* work units (B*H_kv for GQA, B*H_q for paper)    */
+  int32_t heads_per_unit; /* query heads handled per unit (<= 16)            */
+  int32_t head_blocks;    /* ceil(G / 16) under GQA, else 1                  */
+  int32_t wg_vis;         /* workgroups per unit over the visual span        */
+  int32_t wg_full;        /* workgroups per unit over the prompt+text span   */
+  int64_t chunk_vis;      /* visual tokens per workgroup                     */
+  int64_t chunk_full;     /* prompt+text tokens per workgroup                */
+  int64_t grid;           /* total workgroups launched                       */
+  size_t workspace_bytes;
+} rk_decode_plan;
+
+int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
+                   int64_t S_v, int64_t S_f, int32_t elem_bytes,
+                   int32_t policy, int32_t num_cus, rk_decode_plan* plan);
+
+/* Tuning knobs of the split planner (bytes of K/V streamed per workgroup
+ * are clamped to [min_bytes, max_bytes] and the planner aims for
+ * wgs_per_cu workgroups per compute unit).  Pass 0 to keep a value. */
+void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu);
+
+/* Select the two-launch variant (split kernel + separate merge kernel)
+ * instead of the single launch whose last workgroup merges (default 0). */
+void rk_set_decode_two_pass(int32_t enable);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ROTATEK_HIP_H */

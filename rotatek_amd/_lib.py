@@ -1,0 +1,179 @@
+"""ctypes binding of ``librotatek_hip.so`` (declared in include/rotatek_hip.h).
+
+The library is the only compute path: if it is missing, every entry point
+raises ``RuntimeError`` telling the caller to build it; there is no CPU or
+PyTorch fallback.  Torch is used here only to pass device pointers, strides
+and the current HIP stream, and to allocate the cached, zero-initialised
+decode workspace.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librotatek_hip.so")
+
+RK_F16, RK_BF16, RK_F32, RK_F64, RK_U8, RK_I32, RK_I64 = range(7)
+RK_POLICY_PAPER, RK_POLICY_GQA = 0, 1
+
+_DTYPES = {
+    torch.float16: RK_F16,
+    torch.bfloat16: RK_BF16,
+    torch.float32: RK_F32,
+    torch.float64: RK_F64,
+    torch.uint8: RK_U8,
+    torch.bool: RK_U8,
+    torch.int32: RK_I32,
+    torch.int64: RK_I64,
+}
+
+# status codes whose Python counterpart is ValueError (bad arguments)
+_VALUE_ERRORS = {-2, -3, -4, -5, -6, -7, -8, -10}
+
+
+class RkTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * 4),
+        ("stride", ctypes.c_int64 * 4),
+    ]
+
+
+class RkDecodePlan(ctypes.Structure):
+    _fields_ = [
+        ("units", ctypes.c_int64),
+        ("heads_per_unit", ctypes.c_int32),
+        ("head_blocks", ctypes.c_int32),
+        ("wg_vis", ctypes.c_int32),
+        ("wg_full", ctypes.c_int32),
+        ("chunk_vis", ctypes.c_int64),
+        ("chunk_full", ctypes.c_int64),
+        ("grid", ctypes.c_int64),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+_P = ctypes.POINTER(RkTensor)
+_SIGNATURES = {
+    "rk_strerror": (ctypes.c_char_p, [ctypes.c_int]),
+    "rk_abi_version": (ctypes.c_int, []),
+    "rk_device_cu_count": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),
+    "rk_rotatek_decode_check": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int64, _P,
+                                               ctypes.c_int32, ctypes.c_int32,
+                                               ctypes.POINTER(ctypes.c_size_t)]),
+    "rk_rotatek_decode": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int64, _P,
+                                         ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t,
+                                         ctypes.c_void_p]),
+    "rk_full_channel_decode_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P, ctypes.c_int32,
+                                                    ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
+    "rk_full_channel_decode": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P, ctypes.c_int32,
+                                              ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "rk_plan_decode": (ctypes.c_int, [ctypes.c_int64] * 6 + [ctypes.c_int32] * 3
+                       + [ctypes.POINTER(RkDecodePlan)]),
+    "rk_set_decode_tuning": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
+    "rk_set_decode_two_pass": (None, [ctypes.c_int32]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+class HipLibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load (once) and return the HIP library with typed signatures."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise HipLibraryMissing(
+                    f"{path} is not built; run `python -m rotatek_amd.build` "
+                    "(there is no CPU fallback for the RotateK kernels)")
+            lib = ctypes.CDLL(path)
+            for name, (res, args) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def strerror(status: int) -> str:
+    return load().rk_strerror(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status == 0:
+        return
+    msg = f"{what}: {strerror(status)} (status {status})"
+    if status in _VALUE_ERRORS:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def desc(t: torch.Tensor | None):
+    """rk_tensor descriptor of a torch tensor (None -> NULL pointer)."""
+    if t is None:
+        return None
+    if t.dim() > 4:
+        raise ValueError("tensors of rank > 4 are not supported")
+    if t.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {t.dtype}")
+    d = RkTensor()
+    d.data = t.data_ptr() if t.numel() > 0 else 0
+    d.dtype = _DTYPES[t.dtype]
+    d.ndim = t.dim()
+    for i in range(t.dim()):
+        d.shape[i] = t.shape[i]
+        d.stride[i] = t.stride(i)
+    return d
+
+
+def ref(d):
+    return None if d is None else ctypes.byref(d)
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+# ---------------------------------------------------------------- workspace
+_WORKSPACE: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-initialised decode workspace, cached per device and grown on
+    demand.  Completed decode calls leave its ticket counters at zero, so it
+    is reused as-is (and stays valid inside captured HIP graphs once it has
+    been allocated before capture).  Concurrent decodes on different streams
+    of one device would share it and must not overlap."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _WORKSPACE.get(idx)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        _WORKSPACE[idx] = buf
+    return buf
+
+
+def plan_decode(B, H_q, H_kv, Dk, S_v, S_f, elem_bytes=2, policy=RK_POLICY_GQA, num_cus=256):
+    p = RkDecodePlan()
+    check(load().rk_plan_decode(B, H_q, H_kv, Dk, S_v, S_f, elem_bytes, policy, num_cus,
+                                ctypes.byref(p)), "rk_plan_decode")
+    return {f: getattr(p, f) for f, _ in RkDecodePlan._fields_}
+
+
+def set_decode_tuning(min_bytes=0, max_bytes=0, wgs_per_cu=0, two_pass=None):
+    lib = load()
+    lib.rk_set_decode_tuning(int(min_bytes), int(max_bytes), int(wgs_per_cu))
+    if two_pass is not None:
+        lib.rk_set_decode_two_pass(1 if two_pass else 0)

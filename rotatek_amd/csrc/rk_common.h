@@ -1,0 +1,116 @@
+// rk_common.h -- device helpers shared by the RotateK HIP kernels (gfx950).
+//
+// Wave64 conventions used throughout: lane = threadIdx.x & 63, the wave is
+// four 16-lane rows, g = lane >> 4 is the row and n = lane & 15 the column.
+// The MFMA helpers wrap v_mfma_f32_16x16x32_{f16,bf16}: for D = A x B + C
+// (A 16x32, B 32x16) lane (g, n) supplies A[n][8g..8g+7] and B[8g..8g+7][n]
+// and receives D[4g+i][n], i = 0..3.  Only the pairing of A's and B's k
+// index matters to the kernels, so they never depend on how the hardware
+// orders k inside a lane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rk {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegInit = -1e30f;  // running-max start (fused_decode.py:151)
+constexpr float kDenomEps = 1e-6f;  // output guard (fused_decode.py:293)
+
+// ------------------------------------------------------------ dtype traits
+struct F16 {
+  using elem = _Float16;
+  using vec8 = f16x8;
+  static __device__ __forceinline__ float to_f32(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  static __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // lo 16 bits of the result hold x rounded; hi/lo split helper
+  static __device__ __forceinline__ void split(float x, uint16_t& hi, uint16_t& lo) {
+    _Float16 h = (_Float16)x;
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, (_Float16)(x - (float)h));
+  }
+};
+
+struct BF16 {
+  using elem = __bf16;
+  using vec8 = bf16x8;
+  static __device__ __forceinline__ float to_f32(uint16_t b) {
+    return __builtin_bit_cast(float, (uint32_t)b << 16);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float x) {
+    // round to nearest even; NaN kept quiet
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+  }
+  static __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ void split(float x, uint16_t& hi, uint16_t& lo) {
+    hi = from_f32(x);
+    lo = from_f32(x - to_f32(hi));
+  }
+};
+
+// Scalar load of one element of a runtime dtype (0 f16, 1 bf16, 2 f32).
+__device__ __forceinline__ float load_any(const void* p, int64_t idx, int dtype) {
+  if (dtype == 2) return ((const float*)p)[idx];
+  uint16_t b = ((const uint16_t*)p)[idx];
+  return dtype == 0 ? F16::to_f32(b) : BF16::to_f32(b);
+}
+
+// ------------------------------------------------------------ memory
+// Eight 16-bit elements starting at `p` with element stride `sd`; `nvalid`
+// of them (from the front) are read, the rest are zero.  VEC: one 16-byte
+// load (caller guarantees sd == 1, 16-byte alignment, nvalid in {0, 8}).
+template <bool VEC>
+__device__ __forceinline__ uint4 load8(const uint16_t* p, int64_t sd, int nvalid) {
+  if constexpr (VEC) {
+    if (nvalid <= 0) return make_uint4(0, 0, 0, 0);
+    return *(const uint4*)p;
+  } else {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t v = (e < nvalid) ? (uint32_t)p[e * sd] : 0u;
+      w[e >> 1] |= v << ((e & 1) * 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Pack (lo16 of a, lo16 of b) or (hi16 of a, hi16 of b) into one dword.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+// ------------------------------------------------------------ cross-lane
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+  return __builtin_bit_cast(float, __shfl_xor(__builtin_bit_cast(int, v), mask, 64));
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace rk

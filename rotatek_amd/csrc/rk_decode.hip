@@ -1,0 +1,918 @@
+// rk_decode.hip -- fused split-K RotateK decode for MI355X (gfx950).
+//
+// One launch computes a whole decode step (fused_decode.py:303-420,
+// gqa_decode.py:280-321, and the dense baseline of
+// full_channel_flash_decoding.py:162-229 when the visual span is empty):
+//
+//   grid.y  = work units: (b, kv head, block of <= 16 query heads) under the
+//             GQA policy, (b, query head) under the paper policy;
+//   grid.x  = the unit's workgroups: wg_vis chunks of the rotated visual span
+//             followed by wg_full chunks of the full-width prompt+text span.
+//
+// A workgroup is 4 independent waves that walk interleaved 32-token blocks
+// of its chunk.  Each wave keeps a ring of NBUF blocks of K/V in registers:
+// the loads of block i + NBUF are issued before block i is computed, so a
+// wave always has NBUF-1..NBUF blocks (10-16 KB) in flight.  Loads are
+// unconditional 16-byte loads at 32-bit offsets from wave-uniform head
+// bases, with rows clamped into the chunk (clamped rows get probability 0).
+// Per block a wave
+//   * scores 16 query heads x 32 tokens with v_mfma_f32_16x16x32 (the visual
+//     path feeds q R as an fp16/bf16 hi+lo pair so the score keeps ~fp32
+//     precision; the full path feeds q exactly),
+//   * runs the online softmax in the log2 domain (q . delta_mu bias and
+//     1/sqrt(D) folded into one fused multiply-add per score; the
+//     accumulator is rescaled only when some head's running max moved),
+//   * accumulates O^T += V^T P^T on the MFMA with P split hi+lo, V^T built
+//     by an in-register 8x8 transpose of eight 16-byte row loads.
+// Prompt/text validity (chunk range and mask_full) is staged once per
+// workgroup as bytes in LDS.  The four wave states are merged through LDS
+// into one partial (m, l, acc) per workgroup; a per-unit ticket counter lets
+// the last workgroup to finish merge the unit's partials and write
+// acc / (l + 1e-6) in the output dtype, then re-arm the counter, so a step
+// is one graph-capturable launch.
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "rk_common.h"
+#include "rotatek_hip.h"
+
+namespace rk {
+
+struct DecodeArgs {
+  const uint16_t* q;
+  const void* R;
+  const void* dm;
+  const uint16_t* kf;
+  const uint16_t* vf;
+  const uint8_t* mask;
+  const uint16_t* ks;
+  const uint16_t* vs;
+  uint16_t* out;
+  float* part_m;
+  float* part_l;
+  float* part_acc;
+  int* counters;
+  int64_t q_sb, q_sh, q_sd;
+  int64_t R_sb, R_sh, R_sd, R_sk;
+  int64_t dm_sb, dm_sh, dm_sd;
+  int64_t kf_sb, kf_sh;
+  int64_t vf_sb, vf_sh;
+  int64_t mf_sb, mf_ss;
+  int64_t ks_sb, ks_sh;
+  int64_t vs_sb, vs_sh;
+  int64_t o_sb, o_sh, o_sd;
+  int64_t S_v, S_f, chunk_vis, chunk_full;
+  // within-head strides (elements); a head's span is < 2^31 elements
+  uint32_t kf_ss, kf_sd, vf_ss, vf_sd, ks_ss, ks_sd, vs_ss, vs_sd;
+  int32_t G, Dk, hpu, spk, units_per_b, wg_vis, np;
+  int32_t r_dtype, dm_dtype, has_bias, has_mask, two_pass;
+  float scale_log2;
+};
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+constexpr int kBlk = 32;
+constexpr int kMaskChunk = 4096;  // max prompt+text tokens per workgroup
+
+// Eight 16-bit elements of one row: channels chan..chan+7 (element index,
+// not yet scaled by the channel stride) at element offset `row_off` from a
+// wave-uniform head base.  VEC: one 16-byte load at a 32-bit byte offset
+// (unit channel stride, 16-byte aligned rows).  Otherwise element loads of
+// the first `nvalid` channels only, zeros for the rest.
+template <bool VEC>
+__device__ __forceinline__ uint4 load_row8(const uint16_t* base, uint32_t row_off, uint32_t chan,
+                                           uint32_t sd, int nvalid) {
+  if constexpr (VEC) {
+    const uint32_t boff = (row_off + chan) * 2u;
+    return *(const uint4*)((const char*)base + boff);
+  } else {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (e < nvalid) w[e >> 1] |= (uint32_t)base[row_off + (chan + e) * sd] << ((e & 1) * 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+__device__ __forceinline__ uint4 zero_if(bool keep, uint4 v) {
+  return keep ? v : make_uint4(0, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint4 pack8(const uint16_t (&h)[8]) {
+  return make_uint4(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16),
+                    h[4] | ((uint32_t)h[5] << 16), h[6] | ((uint32_t)h[7] << 16));
+}
+
+// Online-softmax update of one 32-token block for the lane's head n.
+// s[r] = log2-domain score of token 8g + r (-inf when invalid); vr[r] = the
+// lane's 16-byte slice (channels 8n..8n+7) of V row 8g + r.
+template <class TT>
+__device__ __forceinline__ void softmax_pv(const float (&s)[8], const uint4 (&vr)[8], float& m,
+                                           float& l, f32x4 (&acc)[8]) {
+  float mx = s[0];
+#pragma unroll
+  for (int r = 1; r < 8; ++r) mx = fmaxf(mx, s[r]);
+  mx = fmaxf(mx, shfl_xor(mx, 16));
+  mx = fmaxf(mx, shfl_xor(mx, 32));
+  const float m_new = fmaxf(m, mx);
+  const float alpha = fast_exp2(m - m_new);
+  if (__any(m_new != m)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] *= alpha;
+  }
+  m = m_new;
+  float p[8], ps = 0.f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    p[r] = fast_exp2(s[r] - m_new);
+    ps += p[r];
+  }
+  l = l * alpha + ps;
+  // P^T operand: tokens 8g..8g+7 of head n, hi + lo parts
+  uint16_t hi[8], lo[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) TT::split(p[r], hi[r], lo[r]);
+  const uint4 ph = pack8(hi), pl = pack8(lo);
+  // V^T operand for channel slot j: element r = V[8g + r][8n + j]
+  uint4 av[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int wi = j >> 1;
+    if (j & 1) {
+      av[j].x = pack_hi(word(vr[0], wi), word(vr[1], wi));
+      av[j].y = pack_hi(word(vr[2], wi), word(vr[3], wi));
+      av[j].z = pack_hi(word(vr[4], wi), word(vr[5], wi));
+      av[j].w = pack_hi(word(vr[6], wi), word(vr[7], wi));
+    } else {
+      av[j].x = pack_lo(word(vr[0], wi), word(vr[1], wi));
+      av[j].y = pack_lo(word(vr[2], wi), word(vr[3], wi));
+      av[j].z = pack_lo(word(vr[4], wi), word(vr[5], wi));
+      av[j].w = pack_lo(word(vr[6], wi), word(vr[7], wi));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = TT::mfma(av[j], ph, acc[j]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = TT::mfma(av[j], pl, acc[j]);
+}
+
+// Register ring over this wave's blocks wave, wave+4, ... < nblk: block
+// j + NBUF is loaded right after block j is consumed, so NBUF-1..NBUF
+// blocks are always in flight.  Loads past the wave's last block repeat
+// that block (cache hits) so the steady-state loop has no exits other than
+// its trip count; the last nw % NBUF blocks are consumed after it.
+template <int NBUF, class Buf, class Load, class Compute>
+__device__ __forceinline__ void run_ring(int64_t nblk, int wave, const Load& load,
+                                         const Compute& compute) {
+  if (wave >= nblk) return;
+  const int64_t nw = (nblk - 1 - wave) / kWaves + 1;  // blocks of this wave
+  auto blk_of = [&](int64_t j) { return (int64_t)wave + (int64_t)kWaves * min(j, nw - 1); };
+  Buf buf[NBUF];
+#pragma unroll
+  for (int i = 0; i < NBUF; ++i) load(buf[i], blk_of(i));
+  int64_t j = 0;
+  for (; j + NBUF <= nw; j += NBUF) {
+#pragma unroll
+    for (int i = 0; i < NBUF; ++i) {
+      compute(buf[i], blk_of(j + i));
+      load(buf[i], blk_of(j + i + NBUF));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NBUF - 1; ++i)
+    if (j + i < nw) compute(buf[i], blk_of(j + i));
+}
+
+template <int DKB>
+struct VisBuf {
+  uint4 k[2][DKB];
+  uint4 v[8];
+};
+
+struct FullBuf {
+  uint4 k[2][4];
+  uint4 v[8];
+};
+
+// Final merge of one unit's np partials: out = sum_p acc_p 2^(m_p - M) /
+// (sum_p l_p 2^(m_p - M) + 1e-6), M = max_p m_p (fused_decode.py:275-296).
+// Thread t handles head t / 16, channels 8 (t % 16) .. +7.
+template <class TT>
+__device__ __forceinline__ void merge_unit(const DecodeArgs& a, int u, int b, int h0, int nh) {
+  const int tid = threadIdx.x;
+  const int h = tid >> 4, c8 = tid & 15;
+  if (h >= nh) return;
+  const int64_t unit_base = (int64_t)u * a.np;
+  float M = -INFINITY;
+  for (int p = 0; p < a.np; ++p) M = fmaxf(M, a.part_m[(unit_base + p) * a.hpu + h]);
+  float L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < a.np; ++p) {
+    const int64_t pi = (unit_base + p) * a.hpu + h;
+    const float wt = fast_exp2(a.part_m[pi] - M);
+    L += a.part_l[pi] * wt;
+    const float4* src = (const float4*)(a.part_acc + pi * 128 + 8 * c8);
+    const float4 v0 = src[0], v1 = src[1];
+    A[0] += v0.x * wt; A[1] += v0.y * wt; A[2] += v0.z * wt; A[3] += v0.w * wt;
+    A[4] += v1.x * wt; A[5] += v1.y * wt; A[6] += v1.z * wt; A[7] += v1.w * wt;
+  }
+  const float den = L + kDenomEps;
+  uint16_t o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = TT::from_f32(A[e] / den);
+  uint16_t* dst = a.out + b * a.o_sb + (int64_t)(h0 + h) * a.o_sh + 8 * c8 * a.o_sd;
+  if (a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
+    *(uint4*)dst = pack8(o);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dst[e * a.o_sd] = o[e];
+  }
+}
+
+template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+decode_kernel(const DecodeArgs a) {
+  constexpr int DKP = DKB * 32;
+  constexpr int NBUF_V = DKB == 1 ? 3 : 2;
+  constexpr int NBUF_F = 2;
+  __shared__ float s_q[HMAX][128];
+  __shared__ float s_qt[HMAX][DKP];
+  __shared__ float s_bias[HMAX];
+  __shared__ float s_m[kWaves][HMAX];
+  __shared__ float s_l[kWaves][HMAX];
+  __shared__ float s_acc[kWaves][HMAX][128];
+  __shared__ __attribute__((aligned(16))) uint8_t s_valid[kMaskChunk];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+  const int nq = n < HMAX ? n : 0;  // LDS row for this lane's head column
+  const int u = blockIdx.y;
+  const int x = blockIdx.x;
+  const int b = u / a.units_per_b;
+  const int r_in_b = u - b * a.units_per_b;
+  const int kv = r_in_b / a.spk;
+  const int jblk = r_in_b - kv * a.spk;
+  const int h0 = kv * a.G + jblk * a.hpu;
+  const int nh = min(a.hpu, a.G - jblk * a.hpu);
+  const bool is_vis = HAS_VIS && x < a.wg_vis;
+  const int xf = HAS_VIS ? x - a.wg_vis : x;
+
+  // ---- prologue: q rows, then q R and q . delta_mu (visual) or the
+  //      prompt/text validity bytes (full)
+  for (int i = tid; i < HMAX * 128; i += kThreads) {
+    const int h = i >> 7, d = i & 127;
+    s_q[h][d] = (h < nh) ? TT::to_f32(a.q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + d * a.q_sd]) : 0.f;
+  }
+  if (!is_vis) {
+    const int64_t t_begin = (int64_t)xf * a.chunk_full;
+    const int64_t t_end = min(a.S_f, t_begin + a.chunk_full);
+    const uint8_t* mb = a.mask ? a.mask + b * a.mf_sb : nullptr;
+    for (int i = tid; i < a.chunk_full; i += kThreads) {
+      const int64_t t = t_begin + i;
+      s_valid[i] = (t < t_end) && (!mb || mb[t * a.mf_ss] != 0);
+    }
+  }
+  __syncthreads();
+  if (is_vis) {
+    const int64_t rb = b * a.R_sb + kv * a.R_sh;
+    constexpr int kHG = (kThreads / DKP) > 0 ? (kThreads / DKP) : 1;
+    constexpr int kPer = (HMAX + kHG - 1) / kHG;
+    for (int i = tid; i < DKP * kHG; i += kThreads) {
+      const int c = i % DKP, hg = i / DKP;
+      float accq[kPer];
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) accq[k] = 0.f;
+      if (c < a.Dk) {
+        for (int d = 0; d < 128; ++d) {
+          const float rv = load_any(a.R, rb + d * a.R_sd + c * a.R_sk, a.r_dtype);
+#pragma unroll
+          for (int k = 0; k < kPer; ++k) {
+            const int h = hg + k * kHG;
+            if (h < HMAX) accq[k] += s_q[h][d] * rv;
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int h = hg + k * kHG;
+        if (h < HMAX) s_qt[h][c] = accq[k];
+      }
+    }
+    if (tid < HMAX) {
+      float bsum = 0.f;
+      if (a.has_bias && tid < nh) {
+        const int64_t db = b * a.dm_sb + kv * a.dm_sh;
+        for (int d = 0; d < 128; ++d) bsum += s_q[tid][d] * load_any(a.dm, db + d * a.dm_sd, a.dm_dtype);
+      }
+      s_bias[tid] = bsum;
+    }
+    __syncthreads();
+  }
+
+  float m = kNegInit, l = 0.f;
+  f32x4 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // A-operand token row of this lane inside a block, per score sub-block
+  const uint32_t krow0 = 8 * (n >> 2) + (n & 3), krow1 = krow0 + 4;
+
+  if (is_vis) {
+    // ---- visual span: rotated, truncated Keys (Dk channels)
+    uint4 qh[DKB], ql[DKB];
+#pragma unroll
+    for (int kb = 0; kb < DKB; ++kb) {
+      uint16_t hv[8], lv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = (n < HMAX) ? s_qt[nq][kb * 32 + 8 * g + e] : 0.f;
+        TT::split(v, hv[e], lv[e]);
+      }
+      qh[kb] = pack8(hv);
+      ql[kb] = pack8(lv);
+    }
+    const float bias2 = (n < HMAX ? s_bias[nq] : 0.f) * a.scale_log2;
+    const int64_t t_begin = (int64_t)x * a.chunk_vis;
+    const int64_t t_end = min(a.S_v, t_begin + a.chunk_vis);
+    const uint32_t t_last = (uint32_t)(t_end - 1);
+    const uint16_t* ksb = a.ks + b * a.ks_sb + kv * a.ks_sh;
+    const uint16_t* vsb = a.vs + b * a.vs_sb + kv * a.vs_sh;
+    bool kval[DKB];
+    uint32_t kch[DKB];
+    int knv[DKB];
+#pragma unroll
+    for (int kb = 0; kb < DKB; ++kb) {
+      const int c0 = kb * 32 + 8 * g;
+      kval[kb] = c0 < a.Dk;
+      kch[kb] = kval[kb] ? (uint32_t)c0 : 0u;
+      knv[kb] = kval[kb] ? min(a.Dk - c0, 8) : 0;
+    }
+    const uint32_t vch = 8u * n;
+    const int64_t nblk = (t_end - t_begin + kBlk - 1) / kBlk;
+    auto load = [&](VisBuf<DKB>& B, int64_t blk) {
+      const uint32_t t0 = (uint32_t)(t_begin + blk * kBlk);
+      const uint32_t r0 = min(t0 + krow0, t_last) * a.ks_ss, r1 = min(t0 + krow1, t_last) * a.ks_ss;
+#pragma unroll
+      for (int kb = 0; kb < DKB; ++kb) {
+        B.k[0][kb] = load_row8<VEC>(ksb, r0, kch[kb], a.ks_sd, knv[kb]);
+        B.k[1][kb] = load_row8<VEC>(ksb, r1, kch[kb], a.ks_sd, knv[kb]);
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        B.v[r] = load_row8<VEC>(vsb, min(t0 + 8u * g + r, t_last) * a.vs_ss, vch, a.vs_sd, 8);
+    };
+    auto compute = [&](VisBuf<DKB>& B, int64_t blk) {
+      const int64_t t0 = t_begin + blk * kBlk;
+      float s[8];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < DKB; ++kb) c = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), qh[kb], c);
+#pragma unroll
+        for (int kb = 0; kb < DKB; ++kb) c = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), ql[kb], c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t t = t0 + 8 * g + 4 * sb + i;
+          s[4 * sb + i] = (t < t_end) ? fmaf(c[i], a.scale_log2, bias2) : -INFINITY;
+        }
+      }
+      softmax_pv<TT>(s, B.v, m, l, acc);
+    };
+    run_ring<NBUF_V, VisBuf<DKB>>(nblk, wave, load, compute);
+  } else {
+    // ---- prompt + text span: full-width Keys
+    uint4 qf[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      uint16_t hv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hv[e] = TT::from_f32((n < HMAX) ? s_q[nq][kb * 32 + 8 * g + e] : 0.f);
+      qf[kb] = pack8(hv);
+    }
+    const int64_t t_begin = (int64_t)xf * a.chunk_full;
+    const int64_t t_end = min(a.S_f, t_begin + a.chunk_full);
+    const uint32_t t_last = (uint32_t)max((int64_t)0, t_end - 1);
+    const uint16_t* kfb = a.kf + b * a.kf_sb + kv * a.kf_sh;
+    const uint16_t* vfb = a.vf + b * a.vf_sb + kv * a.vf_sh;
+    const uint32_t vch = 8u * n;
+    const int64_t nblk = (t_end - t_begin + kBlk - 1) / kBlk;
+    auto load = [&](FullBuf& B, int64_t blk) {
+      const uint32_t t0 = (uint32_t)(t_begin + blk * kBlk);
+      const uint32_t r0 = min(t0 + krow0, t_last) * a.kf_ss, r1 = min(t0 + krow1, t_last) * a.kf_ss;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        B.k[0][kb] = load_row8<VEC>(kfb, r0, (uint32_t)(kb * 32 + 8 * g), a.kf_sd, 8);
+        B.k[1][kb] = load_row8<VEC>(kfb, r1, (uint32_t)(kb * 32 + 8 * g), a.kf_sd, 8);
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        B.v[r] = load_row8<VEC>(vfb, min(t0 + 8u * g + r, t_last) * a.vf_ss, vch, a.vf_sd, 8);
+    };
+    auto compute = [&](FullBuf& B, int64_t blk) {
+      const uint2 vb = *(const uint2*)&s_valid[blk * kBlk + 8 * g];
+      float s[8];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb) {
+        f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) c = TT::mfma(B.k[sb][kb], qf[kb], c);
+        const uint32_t w = sb ? vb.y : vb.x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          s[4 * sb + i] = ((w >> (8 * i)) & 0xffu) ? c[i] * a.scale_log2 : -INFINITY;
+      }
+      softmax_pv<TT>(s, B.v, m, l, acc);
+    };
+    run_ring<NBUF_F, FullBuf>(nblk, wave, load, compute);
+  }
+
+  // ---- merge the four wave states into this workgroup's partial
+  float lt = l + shfl_xor(l, 16);
+  lt += shfl_xor(lt, 32);
+  if (n < HMAX) {
+    if (g == 0) {
+      s_m[wave][nq] = m;
+      s_l[wave][nq] = lt;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_acc[wave][nq][32 * g + 8 * i + j] = acc[j][i];
+  }
+  __syncthreads();
+  {
+    const int h = tid >> 4, c8 = tid & 15;
+    if (h < nh) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
+      float L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float wt = fast_exp2(s_m[w][h] - M);
+        L += s_l[w][h] * wt;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) A[e] += s_acc[w][h][8 * c8 + e] * wt;
+      }
+      const int64_t pi = ((int64_t)u * a.np + x) * a.hpu + h;
+      if (c8 == 0) {
+        a.part_m[pi] = M;
+        a.part_l[pi] = L;
+      }
+      float4* dst = (float4*)(a.part_acc + pi * 128 + 8 * c8);
+      dst[0] = make_float4(A[0], A[1], A[2], A[3]);
+      dst[1] = make_float4(A[4], A[5], A[6], A[7]);
+    }
+  }
+
+  // ---- ticket: the last workgroup of the unit merges all partials
+  if (a.two_pass) return;
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = atomicAdd(&a.counters[u], 1);
+    s_last = (prev == a.np - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  merge_unit<TT>(a, u, b, h0, nh);
+  if (tid == 0) a.counters[u] = 0;
+}
+
+// Second launch of the two-pass variant: one workgroup per unit merges the
+// unit's partials (the same arithmetic the ticket winner runs).
+template <class TT>
+__global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
+  const int u = blockIdx.x;
+  const int b = u / a.units_per_b;
+  const int r_in_b = u - b * a.units_per_b;
+  const int kv = r_in_b / a.spk;
+  const int jblk = r_in_b - kv * a.spk;
+  merge_unit<TT>(a, u, b, kv * a.G + jblk * a.hpu, min(a.hpu, a.G - jblk * a.hpu));
+}
+
+}  // namespace rk
+
+// =====================================================================
+// host side
+// =====================================================================
+#include "rk_host.h"
+
+namespace {
+
+int64_t g_min_wg_bytes = INT64_C(256) << 10;
+int64_t g_max_wg_bytes = INT64_C(2) << 20;
+int32_t g_wgs_per_cu = 4;
+int32_t g_two_pass = 0;
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
+
+struct WsLayout {
+  size_t counters, part_m, part_l, part_acc, total;
+};
+
+WsLayout ws_layout(const rk_decode_plan& p) {
+  const int64_t np = p.wg_vis + p.wg_full;
+  const size_t parts = (size_t)p.units * np * p.heads_per_unit;
+  WsLayout w;
+  w.counters = 0;
+  w.part_m = align256((size_t)p.units * sizeof(int));
+  w.part_l = w.part_m + align256(parts * sizeof(float));
+  w.part_acc = w.part_l + align256(parts * sizeof(float));
+  w.total = w.part_acc + align256(parts * 128 * sizeof(float));
+  return w;
+}
+
+}  // namespace
+
+extern "C" void rk_set_decode_two_pass(int32_t enable) { g_two_pass = enable ? 1 : 0; }
+
+extern "C" void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu) {
+  if (min_bytes > 0) g_min_wg_bytes = min_bytes;
+  if (max_bytes > 0) g_max_wg_bytes = max_bytes;
+  if (wgs_per_cu > 0) g_wgs_per_cu = wgs_per_cu;
+  if (g_max_wg_bytes < g_min_wg_bytes) g_max_wg_bytes = g_min_wg_bytes;
+}
+
+extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, int64_t S_v,
+                              int64_t S_f, int32_t elem_bytes, int32_t policy, int32_t num_cus,
+                              rk_decode_plan* plan) {
+  if (!plan) return RK_ERR_NULL;
+  if (B < 0 || H_q <= 0 || H_kv <= 0 || S_v < 0 || S_f < 0 || elem_bytes <= 0 || num_cus <= 0)
+    return RK_ERR_ARG;
+  if (H_q % H_kv != 0) return RK_ERR_HEADS;
+  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
+  const int64_t G = H_q / H_kv;
+  rk_decode_plan p;
+  memset(&p, 0, sizeof(p));
+  if (policy == RK_POLICY_GQA) {
+    p.heads_per_unit = (int32_t)(G < 16 ? G : 16);
+    p.head_blocks = (int32_t)cdiv(G, 16);
+    p.units = B * H_kv * p.head_blocks;
+  } else {
+    p.heads_per_unit = 1;
+    p.head_blocks = 1;
+    p.units = B * H_q;
+  }
+  const int64_t unit_vis = S_v * (Dk + 128) * elem_bytes;
+  const int64_t unit_full = S_f * 256 * elem_bytes;
+  const int64_t total = p.units * (unit_vis + unit_full);
+  int64_t per_wg = total / ((int64_t)num_cus * g_wgs_per_cu);
+  if (per_wg < g_min_wg_bytes) per_wg = g_min_wg_bytes;
+  if (per_wg > g_max_wg_bytes) per_wg = g_max_wg_bytes;
+  if (S_v > 0) {
+    const int64_t w = cdiv(unit_vis, per_wg);
+    p.chunk_vis = round_up(cdiv(S_v, w), kWgTokens);
+    p.wg_vis = (int32_t)cdiv(S_v, p.chunk_vis);
+  }
+  if (S_f > 0) {
+    const int64_t w = cdiv(unit_full, per_wg);
+    p.chunk_full = round_up(cdiv(S_f, w), kWgTokens);
+    if (p.chunk_full > rk::kMaskChunk) p.chunk_full = rk::kMaskChunk;
+    p.wg_full = (int32_t)cdiv(S_f, p.chunk_full);
+  }
+  if (p.wg_vis + p.wg_full == 0) {  // nothing to attend: one empty chunk writes zeros
+    p.wg_full = 1;
+    p.chunk_full = kWgTokens;
+  }
+  p.grid = p.units * (p.wg_vis + p.wg_full);
+  if (p.units > 65535 * 1024 || p.wg_vis + p.wg_full > (1 << 30)) return RK_ERR_SHAPE;
+  p.workspace_bytes = ws_layout(p).total;
+  *plan = p;
+  return RK_OK;
+}
+
+namespace {
+
+struct Checked {
+  int64_t B, H_q, H_kv, G, Dk, S_v, S_f;
+  int dtype;
+};
+
+int check_out(const rk_tensor* out, const Checked& c) {
+  int st = rk::check_desc(out, 3);
+  if (st) return st;
+  if (out->dtype != c.dtype) return RK_ERR_DTYPE;
+  if (out->shape[0] != c.B || out->shape[1] != c.H_q || out->shape[2] != 128) return RK_ERR_SHAPE;
+  return RK_OK;
+}
+
+int check_kv4(const rk_tensor* t, const Checked& c, int64_t S, int64_t last, bool dtype_must_match) {
+  int st = rk::check_desc(t, 4);
+  if (st) return st;
+  if (dtype_must_match && t->dtype != c.dtype) return RK_ERR_DTYPE;
+  if (t->shape[0] != c.B || t->shape[1] != c.H_kv || t->shape[2] != S || t->shape[3] != last)
+    return RK_ERR_SHAPE;
+  return RK_OK;
+}
+
+// Validation mirroring fused_decode.py:323-338 (plus the shape agreement
+// the Triton kernels assume but do not check).
+int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
+                  const rk_tensor* kf, const rk_tensor* vf, const rk_tensor* mask,
+                  const rk_tensor* ks, const rk_tensor* vs, int64_t G, Checked* c) {
+  if (!q || !R || !kf || !vf || !ks || !vs) return RK_ERR_NULL;
+  if (q->ndim != 3) return RK_ERR_RANK;
+  if (R->ndim != 4) return RK_ERR_RANK;
+  if (mask && mask->dtype != RK_U8) return RK_ERR_DTYPE;
+  int st = rk::check_desc(q, 3);
+  if (st) return st;
+  st = rk::check_desc(R, 4);
+  if (st) return st;
+  if (G <= 0) return RK_ERR_ARG;
+  c->B = q->shape[0];
+  c->H_q = q->shape[1];
+  c->H_kv = R->shape[1];
+  c->G = G;
+  c->Dk = R->shape[3];
+  c->dtype = q->dtype;
+  if (c->H_q / G != c->H_kv || c->H_q % G != 0) return RK_ERR_HEADS;
+  if (!rk::is_half(q->dtype)) return RK_ERR_DTYPE;
+  if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
+  if (!rk::is_float_param(R->dtype)) return RK_ERR_DTYPE;
+  if (R->shape[0] != c->B || R->shape[2] != 128) return RK_ERR_SHAPE;
+  if (c->Dk < 1 || c->Dk > 128) return RK_ERR_KEEP_DIM;
+  if (dm) {
+    st = rk::check_desc(dm, 3);
+    if (st) return st;
+    if (!rk::is_float_param(dm->dtype)) return RK_ERR_DTYPE;
+    if (dm->shape[0] != c->B || dm->shape[1] != c->H_kv || dm->shape[2] != 128) return RK_ERR_SHAPE;
+  }
+  st = rk::check_desc(kf, 4);
+  if (st) return st;
+  c->S_f = kf->shape[2];
+  st = rk::check_desc(ks, 4);
+  if (st) return st;
+  c->S_v = ks->shape[2];
+  if ((st = check_kv4(kf, *c, c->S_f, 128, true))) return st;
+  if ((st = check_kv4(vf, *c, c->S_f, 128, true))) return st;
+  if ((st = check_kv4(ks, *c, c->S_v, c->Dk, true))) return st;
+  if ((st = check_kv4(vs, *c, c->S_v, 128, true))) return st;
+  if (mask) {
+    st = rk::check_desc(mask, 2);
+    if (st) return st;
+    if (mask->shape[0] != c->B || mask->shape[1] != c->S_f) return RK_ERR_SHAPE;
+  }
+  return RK_OK;
+}
+
+int resolve_cus(int32_t num_cus, int* st) {
+  *st = RK_OK;
+  if (num_cus > 0) return num_cus;
+  int dev = 0;
+  const int cus = rk::current_device_cus(&dev);
+  if (cus <= 0) *st = RK_ERR_NO_DEVICE;
+  return cus;
+}
+
+template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
+hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS>), grid, dim3(rk::kThreads), 0, s,
+                     a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !a.two_pass) return e;
+  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3(grid.y), dim3(rk::kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+template <class TT, int DKB, bool VEC, int HMAX>
+hipError_t launch_vis(bool has_vis, const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
+  return has_vis ? launch_one<TT, DKB, VEC, HMAX, true>(a, grid, s)
+                 : launch_one<TT, 1, VEC, HMAX, false>(a, grid, s);
+}
+
+template <class TT, int DKB, bool VEC>
+hipError_t launch_h(int hmax, bool has_vis, const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
+  return hmax > 1 ? launch_vis<TT, DKB, VEC, 16>(has_vis, a, grid, s)
+                  : launch_vis<TT, DKB, VEC, 1>(has_vis, a, grid, s);
+}
+
+template <class TT, int DKB>
+hipError_t launch_v(bool vec, int hmax, bool has_vis, const rk::DecodeArgs& a, dim3 grid,
+                    hipStream_t s) {
+  return vec ? launch_h<TT, DKB, true>(hmax, has_vis, a, grid, s)
+             : launch_h<TT, DKB, false>(hmax, has_vis, a, grid, s);
+}
+
+template <class TT>
+hipError_t launch_dk(int dkb, bool vec, int hmax, bool has_vis, const rk::DecodeArgs& a, dim3 grid,
+                     hipStream_t s) {
+  switch (dkb) {
+    case 1: return launch_v<TT, 1>(vec, hmax, has_vis, a, grid, s);
+    case 2: return launch_v<TT, 2>(vec, hmax, has_vis, a, grid, s);
+    default: return launch_v<TT, 4>(vec, hmax, has_vis, a, grid, s);
+  }
+}
+
+void set4(const rk_tensor* t, int64_t& s0, int64_t& s1, int64_t& s2, int64_t& s3) {
+  s0 = t->stride[0];
+  s1 = t->stride[1];
+  s2 = t->stride[2];
+  s3 = t->stride[3];
+}
+
+// Head strides (b, h) as int64; token/channel strides as uint32 with the
+// whole within-head span below 2^31 elements (kernel offsets are 32-bit).
+bool set_head(const rk_tensor* t, int64_t& sb, int64_t& sh, uint32_t& ss, uint32_t& sd) {
+  sb = t->stride[0];
+  sh = t->stride[1];
+  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1) * t->stride[2] : 0) +
+                       (t->shape[3] > 0 ? (t->shape[3] - 1) * t->stride[3] : 0) + 8;
+  if (span >= (INT64_C(1) << 31) || t->stride[2] >= (INT64_C(1) << 31) ||
+      t->stride[3] >= (INT64_C(1) << 31))
+    return false;
+  ss = (uint32_t)t->stride[2];
+  sd = (uint32_t)t->stride[3];
+  return true;
+}
+
+int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
+               const rk_tensor* kf, const rk_tensor* vf, const rk_tensor* mask,
+               const rk_tensor* ks, const rk_tensor* vs, const rk_tensor* out, int32_t policy,
+               void* ws, size_t ws_bytes, void* stream, bool has_vis) {
+  int st = RK_OK;
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  rk_decode_plan p;
+  st = rk_plan_decode(c.B, c.H_q, c.H_kv, has_vis ? c.Dk : 0, has_vis ? c.S_v : 0, c.S_f, 2,
+                      policy, cus, &p);
+  if (st) return st;
+  if (!ws || (((uintptr_t)ws) & 255) != 0 || ws_bytes < p.workspace_bytes) return RK_ERR_WORKSPACE;
+  if (c.B == 0) return RK_OK;
+  const bool vis_work = has_vis && c.S_v > 0;
+  if (!q->data || !out->data || (vis_work && (!R->data || !ks->data || !vs->data)) ||
+      (c.S_f > 0 && (!kf->data || !vf->data)))
+    return RK_ERR_NULL;
+  const WsLayout w = ws_layout(p);
+  rk::DecodeArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = (const uint16_t*)q->data;
+  a.out = (uint16_t*)out->data;
+  a.kf = (const uint16_t*)kf->data;
+  a.vf = (const uint16_t*)vf->data;
+  a.counters = (int*)((char*)ws + w.counters);
+  a.part_m = (float*)((char*)ws + w.part_m);
+  a.part_l = (float*)((char*)ws + w.part_l);
+  a.part_acc = (float*)((char*)ws + w.part_acc);
+  a.q_sb = q->stride[0];
+  a.q_sh = q->stride[1];
+  a.q_sd = q->stride[2];
+  a.o_sb = out->stride[0];
+  a.o_sh = out->stride[1];
+  a.o_sd = out->stride[2];
+  if (!set_head(kf, a.kf_sb, a.kf_sh, a.kf_ss, a.kf_sd) ||
+      !set_head(vf, a.vf_sb, a.vf_sh, a.vf_ss, a.vf_sd))
+    return RK_ERR_STRIDE;
+  if (mask && mask->data) {
+    a.mask = (const uint8_t*)mask->data;
+    a.mf_sb = mask->stride[0];
+    a.mf_ss = mask->stride[1];
+    a.has_mask = 1;
+  }
+  bool vec = rk::vec_ok(kf) && rk::vec_ok(vf);
+  int dkb = 1;
+  if (has_vis) {
+    a.R = R->data;
+    a.r_dtype = R->dtype;
+    set4(R, a.R_sb, a.R_sh, a.R_sd, a.R_sk);
+    if (dm && dm->data) {
+      a.dm = dm->data;
+      a.dm_dtype = dm->dtype;
+      a.dm_sb = dm->stride[0];
+      a.dm_sh = dm->stride[1];
+      a.dm_sd = dm->stride[2];
+      a.has_bias = 1;
+    }
+    a.ks = (const uint16_t*)ks->data;
+    a.vs = (const uint16_t*)vs->data;
+    if (!set_head(ks, a.ks_sb, a.ks_sh, a.ks_ss, a.ks_sd) ||
+        !set_head(vs, a.vs_sb, a.vs_sh, a.vs_ss, a.vs_sd))
+      return RK_ERR_STRIDE;
+    a.S_v = c.S_v;
+    a.Dk = (int32_t)c.Dk;
+    vec = vec && rk::vec_ok(ks) && rk::vec_ok(vs) && (c.Dk % 8 == 0);
+    dkb = c.Dk <= 32 ? 1 : c.Dk <= 64 ? 2 : 4;
+  }
+  a.S_f = c.S_f;
+  a.chunk_vis = p.chunk_vis;
+  a.chunk_full = p.chunk_full;
+  a.G = (int32_t)c.G;
+  a.hpu = p.heads_per_unit;
+  a.spk = policy == RK_POLICY_GQA ? p.head_blocks : (int32_t)c.G;
+  a.units_per_b = (int32_t)(p.units / c.B);
+  a.wg_vis = p.wg_vis;
+  a.np = p.wg_vis + p.wg_full;
+  a.scale_log2 = (float)(rk::kLog2e / sqrt(128.0));
+  a.two_pass = g_two_pass;
+  const dim3 grid((unsigned)a.np, (unsigned)p.units);
+  const int hmax = p.heads_per_unit > 1 ? 16 : 1;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = c.dtype == RK_F16 ? launch_dk<rk::F16>(dkb, vec, hmax, has_vis, a, grid, s)
+                                   : launch_dk<rk::BF16>(dkb, vec, hmax, has_vis, a, grid, s);
+  return e == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int rk_rotatek_decode_check(const rk_tensor* q_full, const rk_tensor* R_partial,
+                                       const rk_tensor* delta_mu, const rk_tensor* k_full,
+                                       const rk_tensor* v_full, const rk_tensor* mask_full,
+                                       const rk_tensor* k_sparse, const rk_tensor* v_sparse,
+                                       int64_t num_kv_groups, const rk_tensor* out,
+                                       int32_t policy, int32_t num_cus, size_t* workspace_bytes) {
+  Checked c;
+  int st = check_rotatek(q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse,
+                         num_kv_groups, &c);
+  if (st) return st;
+  if (out && (st = check_out(out, c))) return st;
+  const int cus = resolve_cus(num_cus, &st);
+  if (st) return st;
+  rk_decode_plan p;
+  st = rk_plan_decode(c.B, c.H_q, c.H_kv, c.Dk, c.S_v, c.S_f, 2, policy, cus, &p);
+  if (st) return st;
+  if (workspace_bytes) *workspace_bytes = p.workspace_bytes;
+  return RK_OK;
+}
+
+extern "C" int rk_rotatek_decode(const rk_tensor* q_full, const rk_tensor* R_partial,
+                                 const rk_tensor* delta_mu, const rk_tensor* k_full,
+                                 const rk_tensor* v_full, const rk_tensor* mask_full,
+                                 const rk_tensor* k_sparse, const rk_tensor* v_sparse,
+                                 int64_t num_kv_groups, const rk_tensor* out, int32_t policy,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  Checked c;
+  int st = check_rotatek(q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse,
+                         num_kv_groups, &c);
+  if (st) return st;
+  if (!out) return RK_ERR_NULL;
+  if ((st = check_out(out, c))) return st;
+  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
+  return run_decode(c, q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse,
+                    out, policy, workspace, workspace_bytes, stream, true);
+}
+
+namespace {
+
+// Validation mirroring full_channel_flash_decoding.py:173-178.
+int check_dense(const rk_tensor* q, const rk_tensor* k, const rk_tensor* v, int64_t G, Checked* c) {
+  if (!q || !k || !v) return RK_ERR_NULL;
+  if (q->ndim != 3) return RK_ERR_RANK;
+  int st = rk::check_desc(q, 3);
+  if (st) return st;
+  if ((st = rk::check_desc(k, 4))) return st;
+  if (G <= 0) return RK_ERR_ARG;
+  c->B = q->shape[0];
+  c->H_q = q->shape[1];
+  c->H_kv = k->shape[1];
+  c->G = G;
+  c->Dk = 0;
+  c->S_v = 0;
+  c->S_f = k->shape[2];
+  c->dtype = q->dtype;
+  if (k->shape[3] != q->shape[2] || v->ndim < 1 || v->shape[v->ndim - 1] != q->shape[2])
+    return RK_ERR_SHAPE;
+  if (c->H_kv <= 0 || c->H_q / G != c->H_kv || c->H_q % G != 0) return RK_ERR_HEADS;
+  if (!rk::is_half(q->dtype)) return RK_ERR_DTYPE;
+  if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
+  if ((st = check_kv4(k, *c, c->S_f, 128, true))) return st;
+  if ((st = check_kv4(v, *c, c->S_f, 128, true))) return st;
+  return RK_OK;
+}
+
+}  // namespace
+
+extern "C" int rk_full_channel_decode_check(const rk_tensor* q, const rk_tensor* k,
+                                            const rk_tensor* v, int64_t num_kv_groups,
+                                            const rk_tensor* out, int32_t policy, int32_t num_cus,
+                                            size_t* workspace_bytes) {
+  Checked c;
+  int st = check_dense(q, k, v, num_kv_groups, &c);
+  if (st) return st;
+  if (out && (st = check_out(out, c))) return st;
+  const int cus = resolve_cus(num_cus, &st);
+  if (st) return st;
+  rk_decode_plan p;
+  st = rk_plan_decode(c.B, c.H_q, c.H_kv, 0, 0, c.S_f, 2, policy, cus, &p);
+  if (st) return st;
+  if (workspace_bytes) *workspace_bytes = p.workspace_bytes;
+  return RK_OK;
+}
+
+extern "C" int rk_full_channel_decode(const rk_tensor* q, const rk_tensor* k, const rk_tensor* v,
+                                      int64_t num_kv_groups, const rk_tensor* out, int32_t policy,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+  Checked c;
+  int st = check_dense(q, k, v, num_kv_groups, &c);
+  if (st) return st;
+  if (!out) return RK_ERR_NULL;
+  if ((st = check_out(out, c))) return st;
+  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
+  return run_decode(c, q, nullptr, nullptr, k, v, nullptr, nullptr, nullptr, out, policy, workspace,
+                    workspace_bytes, stream, false);
+}

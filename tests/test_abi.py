@@ -1,0 +1,167 @@
+"""CPU checks of the C ABI boundary (no GPU needed).
+
+* the library loads and exports every function include/rotatek_hip.h
+  declares;
+* the host-side validators return the status codes that mirror the
+  reference's ``ValueError`` guards (fused_decode.py:323-338,
+  full_channel_flash_decoding.py:173-178) for descriptors without device
+  memory;
+* the split planner covers every token exactly once.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from rotatek_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rotatek_hip.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = _declared_functions()
+    assert len(names) >= 10
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_abi_version_and_strerror():
+    lib = _lib.load()
+    assert lib.rk_abi_version() == 1
+    assert _lib.strerror(0) == "success"
+    assert "H_kv" in _lib.strerror(-5)
+    assert _lib.strerror(-999) == "unknown status"
+
+
+def _t(shape, dtype=_lib.RK_F16, strides=None):
+    d = _lib.RkTensor()
+    d.data = 0
+    d.dtype = dtype
+    d.ndim = len(shape)
+    if strides is None:
+        strides, acc = [], 1
+        for s in reversed(shape):
+            strides.insert(0, acc)
+            acc *= s
+    for i, (s, st) in enumerate(zip(shape, strides)):
+        d.shape[i] = s
+        d.stride[i] = st
+    return d
+
+
+def _rot_check(B=2, Hq=8, Hkv=4, D=128, Dk=32, S_v=100, S_f=20, G=None, mask_dtype=_lib.RK_U8,
+               q_shape=None, R_shape=None, dtype=_lib.RK_F16, out=True, policy=1):
+    G = Hq // Hkv if G is None else G
+    q = _t(q_shape or (B, Hq, D), dtype)
+    R = _t(R_shape or (B, Hkv, D, Dk), dtype)
+    dm = _t((B, Hkv, D), dtype)
+    kf = _t((B, Hkv, S_f, D), dtype)
+    vf = _t((B, Hkv, S_f, D), dtype)
+    mask = _t((B, S_f), mask_dtype)
+    ks = _t((B, Hkv, S_v, Dk), dtype)
+    vs = _t((B, Hkv, S_v, D), dtype)
+    o = _t((B, Hq, D), dtype) if out else None
+    need = ctypes.c_size_t(0)
+    args = [ctypes.byref(x) for x in (q, R, dm, kf, vf, mask, ks, vs)]
+    st = _lib.load().rk_rotatek_decode_check(*args, G, ctypes.byref(o) if o else None, policy, 256,
+                                             ctypes.byref(need))
+    return st, need.value
+
+
+def test_rotatek_check_ok_and_workspace():
+    st, need = _rot_check()
+    assert st == 0 and need > 0
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(q_shape=(2, 8)), -2),                 # q rank != 3
+    (dict(R_shape=(2, 4, 128)), -2),            # R rank != 4
+    (dict(mask_dtype=_lib.RK_F16), -3),         # mask not uint8
+    (dict(G=3), -5),                            # H_q / G != H_kv
+    (dict(D=64), -6),                           # head_dim != 128
+    (dict(dtype=_lib.RK_F32), -3),              # fp32 K/V not supported
+    (dict(Dk=0), -7),
+    (dict(policy=7), -10),
+])
+def test_rotatek_check_errors(kw, code):
+    st, _ = _rot_check(**kw)
+    assert st == code, (st, _lib.strerror(st))
+
+
+def test_rotatek_check_shape_mismatch():
+    lib = _lib.load()
+    B, Hq, Hkv, D = 2, 8, 4, 128
+    q, R = _t((B, Hq, D)), _t((B, Hkv, D, 32))
+    kf, vf = _t((B, Hkv, 10, D)), _t((B, Hkv, 11, D))        # S_f disagree
+    mask = _t((B, 10), _lib.RK_U8)
+    ks, vs = _t((B, Hkv, 50, 32)), _t((B, Hkv, 50, D))
+    st = lib.rk_rotatek_decode_check(*[ctypes.byref(x) for x in (q, R, R, kf, vf, mask, ks, vs)], 2,
+                                     None, 1, 256, None)
+    assert st == -4 or st == -2  # delta_mu passed with the wrong rank, or S_f mismatch
+    dm = _t((B, Hkv, D))
+    st = lib.rk_rotatek_decode_check(*[ctypes.byref(x) for x in (q, R, dm, kf, vf, mask, ks, vs)], 2,
+                                     None, 1, 256, None)
+    assert st == -4
+
+
+def test_rotatek_check_null_descriptor():
+    lib = _lib.load()
+    st = lib.rk_rotatek_decode_check(None, None, None, None, None, None, None, None, 1, None, 1, 256,
+                                     None)
+    assert st == -1
+
+
+def test_dense_check():
+    lib = _lib.load()
+    q, k, v, o = _t((2, 8, 128)), _t((2, 4, 64, 128)), _t((2, 4, 64, 128)), _t((2, 8, 128))
+    need = ctypes.c_size_t(0)
+    args = [ctypes.byref(x) for x in (q, k, v)]
+    assert lib.rk_full_channel_decode_check(*args, 2, ctypes.byref(o), 0, 256, ctypes.byref(need)) == 0
+    assert need.value > 0
+    assert lib.rk_full_channel_decode_check(*args, 3, None, 0, 256, None) == -5
+    kbad = _t((2, 4, 64, 96))
+    assert lib.rk_full_channel_decode_check(ctypes.byref(q), ctypes.byref(kbad), ctypes.byref(v), 2,
+                                            None, 0, 256, None) == -4
+    q2 = _t((2, 8))
+    assert lib.rk_full_channel_decode_check(ctypes.byref(q2), ctypes.byref(k), ctypes.byref(v), 2,
+                                            None, 0, 256, None) == -2
+
+
+def test_launch_without_workspace_fails_cleanly():
+    """The launch entry validates the workspace before any HIP call."""
+    lib = _lib.load()
+    q, k, v, o = _t((2, 8, 128)), _t((2, 4, 64, 128)), _t((2, 4, 64, 128)), _t((2, 8, 128))
+    st = lib.rk_full_channel_decode(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), 2,
+                                    ctypes.byref(o), 0, None, 0, None)
+    # no device here -> NO_DEVICE; with a device -> WORKSPACE
+    assert st in (-9, -12)
+
+
+@pytest.mark.parametrize("shape", [
+    (32, 32, 32, 32, 14000, 2000), (1, 32, 32, 32, 15360, 640), (16, 28, 4, 32, 30720, 2048),
+    (8, 28, 4, 16, 12001, 61), (1, 4, 4, 64, 1, 1), (3, 8, 2, 128, 0, 77), (2, 8, 8, 8, 300, 0),
+    (1, 64, 2, 32, 500, 40), (2, 4, 4, 32, 0, 0),
+])
+@pytest.mark.parametrize("policy", [0, 1])
+def test_plan_covers_every_token(shape, policy):
+    B, Hq, Hkv, Dk, S_v, S_f = shape
+    p = _lib.plan_decode(B, Hq, Hkv, Dk, S_v, S_f, policy=policy)
+    G = Hq // Hkv
+    if policy == 1:
+        assert p["heads_per_unit"] == min(G, 16) and p["units"] == B * Hkv * -(-G // 16)
+    else:
+        assert p["heads_per_unit"] == 1 and p["units"] == B * Hq
+    for S, wg, ch in ((S_v, p["wg_vis"], p["chunk_vis"]), (S_f, p["wg_full"], p["chunk_full"])):
+        if S > 0:
+            assert ch % 128 == 0 and wg * ch >= S and (wg - 1) * ch < S
+    assert p["wg_vis"] + p["wg_full"] >= 1
+    assert p["grid"] == p["units"] * (p["wg_vis"] + p["wg_full"])

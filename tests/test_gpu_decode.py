@@ -1,0 +1,272 @@
+"""GPU parity of the HIP decode kernels against the CPU oracle.
+
+Tolerances (north star): max-abs 2e-3 for fp16 and 1e-2 for bf16 outputs
+against the float64 oracle evaluated on the very same (already rounded)
+inputs.  Every case prints its name before touching the GPU.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as od
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}
+
+
+def _np(t):
+    return None if t is None else t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _rand_inputs(B, Hq, Hkv, Dk, S_v, S_f, dtype, seed=0, mask_p=0.0, bias=True, view_v=True):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = "cuda"
+
+    def rn(*s, scale=1.0):
+        return (torch.randn(*s, generator=g, device=dev) * scale).to(dtype)
+
+    D = 128
+    q = rn(B, Hq, D)
+    R = torch.linalg.qr(torch.randn(B, Hkv, D, D, generator=g, device=dev))[0][..., :Dk].contiguous().to(dtype)
+    dm = rn(B, Hkv, D, scale=0.5) if bias else None
+    if view_v:
+        V = rn(B, Hkv, S_v + S_f, D)
+        vs, vf = V[:, :, :S_v], V[:, :, S_v:]
+    else:
+        vs, vf = rn(B, Hkv, S_v, D), rn(B, Hkv, S_f, D)
+    kf = rn(B, Hkv, S_f, D)
+    ks = rn(B, Hkv, S_v, Dk, scale=2.0)
+    mask = (torch.rand(B, S_f, generator=g, device=dev) >= mask_p).to(torch.uint8)
+    return dict(q_full=q, R_partial=R, delta_mu=dm, k_full=kf, v_full=vf, mask_full=mask,
+                k_sparse=ks, v_sparse=vs, num_kv_groups=Hq // Hkv)
+
+
+def _oracle(inp, heads=None):
+    a = {k: (_np(v) if torch.is_tensor(v) else v) for k, v in inp.items()}
+    return od.rotatek_decode(a["q_full"], a["R_partial"], a["delta_mu"], a["k_full"], a["v_full"],
+                             a["mask_full"], a["k_sparse"], a["v_sparse"], a["num_kv_groups"])
+
+
+def _decode(inp, family):
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
+    fn = rotatek_decode_gqa if family == "gqa" else rotatek_decode_fused
+    out, a, b = fn(**inp)
+    assert a is None and b is None
+    torch.cuda.synchronize()
+    return out
+
+
+CASES = [
+    # B, Hq, Hkv, Dk, S_v, S_f
+    (1, 4, 4, 32, 300, 50),
+    (2, 8, 8, 32, 1000, 129),
+    (2, 8, 4, 32, 517, 64),
+    (1, 28, 4, 32, 2049, 100),      # G = 7
+    (1, 16, 1, 32, 700, 33),        # G = 16
+    (1, 40, 2, 32, 300, 20),        # G = 20 -> two head blocks
+    (2, 4, 4, 16, 333, 31),
+    (2, 4, 4, 64, 1025, 0),         # no prompt/text
+    (2, 4, 2, 128, 640, 7),
+    (1, 4, 4, 40, 250, 17),         # Dk not a power of two
+    (1, 4, 4, 8, 129, 1),
+    (2, 4, 4, 32, 0, 300),          # no visual span
+    (1, 2, 2, 32, 1, 1),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("family", ["paper", "gqa"])
+@pytest.mark.parametrize("case", CASES)
+def test_rotatek_decode_matches_oracle(case, family, dtype):
+    B, Hq, Hkv, Dk, S_v, S_f = case
+    _say(f"rotatek {family} {dtype} B={B} Hq={Hq} Hkv={Hkv} Dk={Dk} S_v={S_v} S_f={S_f}")
+    inp = _rand_inputs(B, Hq, Hkv, Dk, S_v, S_f, dtype, seed=hash(case) % 1000, mask_p=0.2)
+    out = _decode(inp, family)
+    assert out.shape == (B, 1, Hq, 128) and out.dtype == dtype
+    want = _oracle(inp)
+    err = np.abs(_np(out) - want).max()
+    assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_no_bias_contiguous_values_and_all_masked(dtype):
+    _say(f"rotatek no-bias/all-masked {dtype}")
+    inp = _rand_inputs(2, 8, 4, 32, 400, 60, dtype, seed=3, bias=False, view_v=False)
+    inp["mask_full"][0] = 0
+    out = _decode(inp, "gqa")
+    assert np.abs(_np(out) - _oracle(inp)).max() <= TOL[dtype]
+
+
+def test_empty_spans_give_zeros():
+    _say("rotatek empty spans")
+    inp = _rand_inputs(2, 4, 4, 32, 0, 0, torch.float16)
+    out = _decode(inp, "paper")
+    assert torch.count_nonzero(out) == 0
+    inp = _rand_inputs(2, 4, 4, 32, 0, 20, torch.float16)
+    inp["mask_full"].zero_()
+    assert torch.count_nonzero(_decode(inp, "gqa")) == 0
+
+
+def test_strided_inputs_take_the_scalar_path():
+    """Non-unit channel strides (a transposed view) select the element-wise
+    load variant; results must not change."""
+    _say("rotatek strided inputs")
+    inp = _rand_inputs(1, 4, 2, 32, 300, 40, torch.float16, seed=9)
+    ref = _decode(inp, "gqa")
+    ks = inp["k_sparse"]
+    inp2 = dict(inp)
+    inp2["k_sparse"] = ks.transpose(-1, -2).contiguous().transpose(-1, -2)   # stride_d = S_v
+    assert inp2["k_sparse"].stride(-1) != 1
+    out = _decode(inp2, "gqa")
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_dense_decode_matches_oracle(dtype):
+    from rotatek_amd.kernels.full_channel_flash_decoding import full_channel_decode
+    from rotatek_amd.kernels.gqa_decode import full_channel_decode_gqa
+    for (B, Hq, Hkv, S) in [(2, 8, 8, 1000), (1, 28, 4, 3001), (2, 8, 2, 64), (1, 4, 4, 1)]:
+        _say(f"dense {dtype} B={B} Hq={Hq} Hkv={Hkv} S={S}")
+        g = torch.Generator(device="cuda").manual_seed(S)
+        q = torch.randn(B, Hq, 128, generator=g, device="cuda").to(dtype)
+        k = torch.randn(B, Hkv, S, 128, generator=g, device="cuda").to(dtype)
+        v = torch.randn(B, Hkv, S, 128, generator=g, device="cuda").to(dtype)
+        want = od.full_channel_decode(_np(q), _np(k), _np(v), Hq // Hkv)
+        for fn in (full_channel_decode, full_channel_decode_gqa):
+            out = fn(q, k, v, num_kv_groups=Hq // Hkv)
+            torch.cuda.synchronize()
+            assert out.shape == (B, 1, Hq, 128)
+            assert np.abs(_np(out) - want).max() <= TOL[dtype]
+
+
+def test_rotatek_with_identity_rotation_equals_dense():
+    """Dk = D, R = I, delta_mu = 0: RotateK over (visual, full) equals the
+    dense kernel over the concatenated Keys (HIP vs HIP, same dtype)."""
+    from rotatek_amd.kernels.gqa_decode import full_channel_decode_gqa, rotatek_decode_gqa
+    _say("rotatek identity == dense")
+    B, Hq, Hkv, S_v, S_f = 2, 8, 4, 900, 100
+    g = torch.Generator(device="cuda").manual_seed(5)
+    dt = torch.float16
+    q = torch.randn(B, Hq, 128, generator=g, device="cuda").to(dt)
+    K = torch.randn(B, Hkv, S_v + S_f, 128, generator=g, device="cuda").to(dt)
+    V = torch.randn(B, Hkv, S_v + S_f, 128, generator=g, device="cuda").to(dt)
+    R = torch.eye(128, device="cuda", dtype=dt).expand(B, Hkv, 128, 128).contiguous()
+    out, _, _ = rotatek_decode_gqa(q, R, torch.zeros(B, Hkv, 128, device="cuda", dtype=dt),
+                                   K[:, :, S_v:], V[:, :, S_v:], torch.ones(B, S_f, device="cuda", dtype=torch.uint8),
+                                   K[:, :, :S_v], V[:, :, :S_v], Hq // Hkv)
+    dense = full_channel_decode_gqa(q, K, V, Hq // Hkv)
+    torch.cuda.synchronize()
+    assert (out.float() - dense.float()).abs().max().item() <= 2e-3
+
+
+def test_two_pass_equals_single_launch_and_counters_rearm():
+    from rotatek_amd import _lib
+    _say("two-pass vs ticket merge")
+    inp = _rand_inputs(2, 8, 4, 32, 3000, 300, torch.float16, seed=11)
+    a = _decode(inp, "gqa")
+    try:
+        _lib.set_decode_tuning(two_pass=True)
+        b = _decode(inp, "gqa")
+    finally:
+        _lib.set_decode_tuning(two_pass=False)
+    assert torch.equal(a, b)
+    for _ in range(3):
+        assert torch.equal(_decode(inp, "gqa"), a)
+    ws = _lib._WORKSPACE[torch.cuda.current_device()]
+    p = _lib.plan_decode(2, 8, 4, 32, 3000, 300, policy=1,
+                         num_cus=torch.cuda.get_device_properties(0).multi_processor_count)
+    assert torch.count_nonzero(ws[: p["units"] * 4]) == 0
+
+
+def test_split_granularity_does_not_change_results_beyond_rounding():
+    from rotatek_amd import _lib
+    _say("split granularity sweep")
+    inp = _rand_inputs(1, 8, 8, 32, 5000, 700, torch.float16, seed=12)
+    want = _oracle(inp)
+    try:
+        for lo, hi in [(64 << 10, 64 << 10), (1 << 20, 1 << 20), (16 << 20, 16 << 20)]:
+            _lib.set_decode_tuning(lo, hi, 4)
+            out = _decode(inp, "paper")
+            assert np.abs(_np(out) - want).max() <= 2e-3
+    finally:
+        _lib.set_decode_tuning(256 << 10, 2 << 20, 4)
+
+
+def test_graph_capture_replays_match_eager():
+    from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
+    _say("hipGraph capture")
+    inp = _rand_inputs(2, 8, 4, 32, 2000, 200, torch.float16, seed=13)
+    eager = rotatek_decode_gqa(**inp)[0].clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            rotatek_decode_gqa(**inp)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = rotatek_decode_gqa(**inp)[0]
+    for i in range(5):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        junk = torch.randn(1000, device="cuda") * 2     # eager work between replays
+        torch.cuda.synchronize()
+        del junk
+    # the inputs can change between replays
+    inp["q_full"].mul_(-1.0)
+    eager2 = rotatek_decode_gqa(**inp)[0].clone()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager2)
+
+
+def _sample_oracle(inp, pairs):
+    """Oracle on selected (b, kv) groups only (host memory stays small)."""
+    G = inp["num_kv_groups"]
+    res = {}
+    for (b, kv) in pairs:
+        sub = {}
+        for k in ("R_partial", "delta_mu", "k_full", "v_full", "k_sparse", "v_sparse"):
+            sub[k] = _np(inp[k][b:b + 1, kv:kv + 1])
+        sub["q_full"] = _np(inp["q_full"][b:b + 1, kv * G:(kv + 1) * G])
+        sub["mask_full"] = _np(inp["mask_full"][b:b + 1])
+        res[(b, kv)] = od.rotatek_decode(sub["q_full"], sub["R_partial"], sub["delta_mu"], sub["k_full"],
+                                         sub["v_full"], sub["mask_full"], sub["k_sparse"], sub["v_sparse"],
+                                         G)[0, 0]
+    return res
+
+
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+def test_benchmark_configs_full_size(cfg):
+    """Full BASELINE shapes: sampled (b, kv) groups against the oracle, the
+    rest through properties (paper == gqa family for MHA, finite outputs)."""
+    from rotatek_amd import synth
+    c = synth.CONFIGS[cfg]
+    _say(f"full-size {cfg}")
+    inp = synth.make_decode_inputs(c, "cuda", seed=1)
+    args = synth.decode_args(inp)
+    out = _decode(args, "gqa")
+    assert torch.isfinite(out.float()).all()
+    rng = np.random.default_rng(0)
+    pairs = {(int(rng.integers(c.B)), int(rng.integers(c.H_kv))) for _ in range(6)}
+    pairs |= {(0, 0), (c.B - 1, c.H_kv - 1)}
+    want = _sample_oracle(args, sorted(pairs))
+    G = c.G
+    for (b, kv), w in want.items():
+        got = _np(out[b, 0, kv * G:(kv + 1) * G])
+        assert np.abs(got - w).max() <= TOL[c.dtype], (b, kv)
+    if c.G == 1:
+        out_p = _decode(args, "paper")
+        assert torch.equal(out_p, out)
