@@ -109,10 +109,10 @@ int rk_device_cu_count(int device, int* status);
  * ones); k_sparse [B,H_kv,S_v,Dk]; v_sparse [B,H_kv,S_v,D]; out [B,H_q,D]
  * (dtype of q_full).  D must be 128.  q, K, V and out share one dtype
  * (F16 or BF16); R_partial and delta_mu may be F16, BF16 or F32.
- * The workspace (rk_rotatek_decode_check) holds split partials and one
- * ticket counter per work unit; it must be zero-filled once when first
- * allocated and is left zeroed by every completed call, so the call is
- * hipGraph-capturable.  Calls that overlap on one workspace race.
+ * The workspace (size from rk_rotatek_decode_check, 256-byte aligned, no
+ * initialisation needed) holds the split partials; a step is two launches
+ * on `stream` (split kernel, merge kernel) and is hipGraph-capturable.
+ * Calls that overlap on one workspace race.
  */
 int rk_rotatek_decode_check(const rk_tensor* q_full, const rk_tensor* R_partial,
                             const rk_tensor* delta_mu, const rk_tensor* k_full,
@@ -166,10 +166,6 @@ int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
  * are clamped to [min_bytes, max_bytes] and the planner aims for
  * wgs_per_cu workgroups per compute unit).  Pass 0 to keep a value. */
 void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu);
-
-/* Select the two-launch variant (split kernel + separate merge kernel)
- * instead of the single launch whose last workgroup merges (default 0). */
-void rk_set_decode_two_pass(int32_t enable);
 
 #ifdef __cplusplus
 }

@@ -3,8 +3,7 @@
 The library is the only compute path: if it is missing, every entry point
 raises ``RuntimeError`` telling the caller to build it; there is no CPU or
 PyTorch fallback.  Torch is used here only to pass device pointers, strides
-and the current HIP stream, and to allocate the cached, zero-initialised
-decode workspace.
+and the current HIP stream, and to allocate the cached decode workspace.
 """
 from __future__ import annotations
 
@@ -77,7 +76,6 @@ _SIGNATURES = {
     "rk_plan_decode": (ctypes.c_int, [ctypes.c_int64] * 6 + [ctypes.c_int32] * 3
                        + [ctypes.POINTER(RkDecodePlan)]),
     "rk_set_decode_tuning": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
-    "rk_set_decode_two_pass": (None, [ctypes.c_int32]),
 }
 
 _lib = None
@@ -152,15 +150,15 @@ _WORKSPACE: dict = {}
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised decode workspace, cached per device and grown on
-    demand.  Completed decode calls leave its ticket counters at zero, so it
-    is reused as-is (and stays valid inside captured HIP graphs once it has
-    been allocated before capture).  Concurrent decodes on different streams
-    of one device would share it and must not overlap."""
+    """Decode workspace (split partials), cached per device and grown on
+    demand, so steady-state calls allocate nothing (it stays valid inside
+    captured HIP graphs once it has been allocated before capture).
+    Concurrent decodes on different streams of one device would share it
+    and must not overlap."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     buf = _WORKSPACE.get(idx)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
         _WORKSPACE[idx] = buf
     return buf
 
@@ -172,8 +170,5 @@ def plan_decode(B, H_q, H_kv, Dk, S_v, S_f, elem_bytes=2, policy=RK_POLICY_GQA, 
     return {f: getattr(p, f) for f, _ in RkDecodePlan._fields_}
 
 
-def set_decode_tuning(min_bytes=0, max_bytes=0, wgs_per_cu=0, two_pass=None):
-    lib = load()
-    lib.rk_set_decode_tuning(int(min_bytes), int(max_bytes), int(wgs_per_cu))
-    if two_pass is not None:
-        lib.rk_set_decode_two_pass(1 if two_pass else 0)
+def set_decode_tuning(min_bytes=0, max_bytes=0, wgs_per_cu=0):
+    load().rk_set_decode_tuning(int(min_bytes), int(max_bytes), int(wgs_per_cu))

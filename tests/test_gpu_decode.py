@@ -169,23 +169,16 @@ def test_rotatek_with_identity_rotation_equals_dense():
     assert (out.float() - dense.float()).abs().max().item() <= 2e-3
 
 
-def test_two_pass_equals_single_launch_and_counters_rearm():
-    from rotatek_amd import _lib
-    _say("two-pass vs ticket merge")
+def test_repeated_calls_are_bitwise_stable():
+    """The workspace is reused uninitialised across calls and shapes: every
+    call must fully overwrite what it reads back."""
+    _say("repeated calls / workspace reuse")
     inp = _rand_inputs(2, 8, 4, 32, 3000, 300, torch.float16, seed=11)
     a = _decode(inp, "gqa")
-    try:
-        _lib.set_decode_tuning(two_pass=True)
-        b = _decode(inp, "gqa")
-    finally:
-        _lib.set_decode_tuning(two_pass=False)
-    assert torch.equal(a, b)
+    other = _rand_inputs(1, 4, 4, 64, 5000, 17, torch.float16, seed=12)
+    _decode(other, "paper")
     for _ in range(3):
         assert torch.equal(_decode(inp, "gqa"), a)
-    ws = _lib._WORKSPACE[torch.cuda.current_device()]
-    p = _lib.plan_decode(2, 8, 4, 32, 3000, 300, policy=1,
-                         num_cus=torch.cuda.get_device_properties(0).multi_processor_count)
-    assert torch.count_nonzero(ws[: p["units"] * 4]) == 0
 
 
 def test_split_granularity_does_not_change_results_beyond_rounding():
@@ -199,7 +192,7 @@ def test_split_granularity_does_not_change_results_beyond_rounding():
             out = _decode(inp, "paper")
             assert np.abs(_np(out) - want).max() <= 2e-3
     finally:
-        _lib.set_decode_tuning(256 << 10, 2 << 20, 4)
+        _lib.set_decode_tuning(64 << 10, 512 << 10, 16)
 
 
 def test_graph_capture_replays_match_eager():
