@@ -50,12 +50,9 @@ struct BF16 {
   static __device__ __forceinline__ float to_f32(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
   }
+  // round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
   static __device__ __forceinline__ uint16_t from_f32(float x) {
-    // round to nearest even; NaN kept quiet
-    uint32_t u = __builtin_bit_cast(uint32_t, x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
   }
   static __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),

@@ -159,40 +159,52 @@ __device__ __forceinline__ void softmax_pv(const float (&s)[8], const uint4 (&vr
   for (int j = 0; j < 8; ++j) acc[j] = TT::mfma(av[j], pl, acc[j]);
 }
 
-// Register ring over this wave's blocks wave, wave+4, ... < nblk (visited
-// in a rotated order): block j + NBUF is loaded right after block j is
-// consumed, so NBUF-1..NBUF blocks are always in flight.  Loads past the wave's last block repeat
-// that block (cache hits) so the steady-state loop has no exits other than
-// its trip count; the last nw % NBUF blocks are consumed after it.
-template <int NBUF, class Buf, class Load, class Compute>
-__device__ __forceinline__ void run_ring(int64_t nblk, int wave, uint32_t rot_seed, const Load& load,
-                                         const Compute& compute) {
-  if (wave >= nblk) return;
-  const int64_t nw = (nblk - 1 - wave) / kWaves + 1;  // blocks of this wave
-  // Workgroups start at different points of their chunks, so the thousands
-  // of chunks that begin at the same offset inside equally strided heads do
-  // not all hit the same memory channels at once.
-  const int64_t rot = (int64_t)(rot_seed % (uint32_t)nw);
-  auto blk_of = [&](int64_t j) {
+// Register ring over this wave's blocks wave, wave+4, ... < nblk, visited
+// in a rotated order (workgroups start at different points of their chunks,
+// so the many chunks that begin at the same offset inside equally strided
+// heads do not all hit the same memory channels at once).  prime() issues
+// the first NBUF blocks; run() consumes block j and then loads block
+// j + NBUF into the freed slot, so NBUF-1..NBUF blocks are always in
+// flight.  Loads past the wave's last block repeat that block (cache hits),
+// which keeps the steady-state loop free of exits other than its trip
+// count; the last nw % NBUF blocks are consumed after it.
+template <int NBUF, class Buf>
+struct Ring {
+  Buf buf[NBUF];
+  int64_t nw, rot;
+  int wave;
+
+  __device__ __forceinline__ Ring(int64_t nblk, int wave_, uint32_t seed) : wave(wave_) {
+    nw = wave_ < nblk ? (nblk - 1 - wave_) / kWaves + 1 : 0;
+    rot = nw > 0 ? (int64_t)(seed % (uint32_t)nw) : 0;
+  }
+  __device__ __forceinline__ int64_t blk_of(int64_t j) const {
     int64_t r = min(j, nw - 1) + rot;
     r = r >= nw ? r - nw : r;
     return (int64_t)wave + (int64_t)kWaves * r;
-  };
-  Buf buf[NBUF];
-#pragma unroll
-  for (int i = 0; i < NBUF; ++i) load(buf[i], blk_of(i));
-  int64_t j = 0;
-  for (; j + NBUF <= nw; j += NBUF) {
-#pragma unroll
-    for (int i = 0; i < NBUF; ++i) {
-      compute(buf[i], blk_of(j + i));
-      load(buf[i], blk_of(j + i + NBUF));
-    }
   }
+  template <class Load>
+  __device__ __forceinline__ void prime(const Load& load) {
+    if (nw == 0) return;
 #pragma unroll
-  for (int i = 0; i < NBUF - 1; ++i)
-    if (j + i < nw) compute(buf[i], blk_of(j + i));
-}
+    for (int i = 0; i < NBUF; ++i) load(buf[i], blk_of(i));
+  }
+  template <class Load, class Compute>
+  __device__ __forceinline__ void run(const Load& load, const Compute& compute) {
+    if (nw == 0) return;
+    int64_t j = 0;
+    for (; j + NBUF <= nw; j += NBUF) {
+#pragma unroll
+      for (int i = 0; i < NBUF; ++i) {
+        compute(buf[i], blk_of(j + i));
+        load(buf[i], blk_of(j + i + NBUF));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i)
+      if (j + i < nw) compute(buf[i], blk_of(j + i));
+  }
+};
 
 template <int DKB>
 struct VisBuf {
@@ -205,32 +217,58 @@ struct FullBuf {
   uint4 v[8];
 };
 
-// Final merge of one unit's np partials: out = sum_p acc_p 2^(m_p - M) /
-// (sum_p l_p 2^(m_p - M) + 1e-6), M = max_p m_p (fused_decode.py:275-296).
-// Thread t handles head t / 16, channels 8 (t % 16) .. +7.
+// Final merge of the np partials of one (unit, head) row:
+//   out = sum_p acc_p 2^(m_p - M) / (sum_p l_p 2^(m_p - M) + 1e-6),
+//   M = max_p m_p                                  (fused_decode.py:275-296)
+// computed as an online merge, four partials per step with all their loads
+// issued together.  The calling thread owns channels 8*c8 .. 8*c8+7.
 template <class TT>
-__device__ __forceinline__ void merge_unit(const DecodeArgs& a, int u, int b, int h0, int nh) {
-  const int tid = threadIdx.x;
-  const int h = tid >> 4, c8 = tid & 15;
-  if (h >= nh) return;
-  const int64_t unit_base = (int64_t)u * a.np;
-  float M = -INFINITY;
-  for (int p = 0; p < a.np; ++p) M = fmaxf(M, a.part_m[(unit_base + p) * a.hpu + h]);
-  float L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int p = 0; p < a.np; ++p) {
-    const int64_t pi = (unit_base + p) * a.hpu + h;
-    const float wt = fast_exp2(a.part_m[pi] - M);
-    L += a.part_l[pi] * wt;
+__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int hq, int h,
+                                          int c8) {
+  const int64_t base = u * a.np;
+  float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  auto fold = [&](const float* mm, const float* ll, const float4* v0, const float4* v1, int k) {
+    float mx = M;
+    for (int i = 0; i < k; ++i) mx = fmaxf(mx, mm[i]);
+    const float sc = fast_exp2(M - mx);
+    L *= sc;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) A[e] *= sc;
+    for (int i = 0; i < k; ++i) {
+      const float w = fast_exp2(mm[i] - mx);
+      L += ll[i] * w;
+      A[0] += v0[i].x * w; A[1] += v0[i].y * w; A[2] += v0[i].z * w; A[3] += v0[i].w * w;
+      A[4] += v1[i].x * w; A[5] += v1[i].y * w; A[6] += v1[i].z * w; A[7] += v1[i].w * w;
+    }
+    M = mx;
+  };
+  int p = 0;
+  for (; p + 4 <= a.np; p += 4) {
+    float mm[4], ll[4];
+    float4 v0[4], v1[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t pi = (base + p + i) * a.hpu + h;
+      mm[i] = a.part_m[pi];
+      ll[i] = a.part_l[pi];
+      const float4* src = (const float4*)(a.part_acc + pi * 128 + 8 * c8);
+      v0[i] = src[0];
+      v1[i] = src[1];
+    }
+    fold(mm, ll, v0, v1, 4);
+  }
+  for (; p < a.np; ++p) {
+    const int64_t pi = (base + p) * a.hpu + h;
+    const float mm = a.part_m[pi], ll = a.part_l[pi];
     const float4* src = (const float4*)(a.part_acc + pi * 128 + 8 * c8);
     const float4 v0 = src[0], v1 = src[1];
-    A[0] += v0.x * wt; A[1] += v0.y * wt; A[2] += v0.z * wt; A[3] += v0.w * wt;
-    A[4] += v1.x * wt; A[5] += v1.y * wt; A[6] += v1.z * wt; A[7] += v1.w * wt;
+    fold(&mm, &ll, &v0, &v1, 1);
   }
   const float den = L + kDenomEps;
   uint16_t o[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = TT::from_f32(A[e] / den);
-  uint16_t* dst = a.out + b * a.o_sb + (int64_t)(h0 + h) * a.o_sh + 8 * c8 * a.o_sd;
+  uint16_t* dst = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 8 * c8 * a.o_sd;
   if (a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
     *(uint4*)dst = pack8(o);
   } else {
@@ -268,79 +306,6 @@ decode_kernel(const DecodeArgs a) {
   const bool is_vis = HAS_VIS && x < a.wg_vis;
   const int xf = HAS_VIS ? x - a.wg_vis : x;
 
-  // ---- prologue: q rows, then q R and q . delta_mu (visual) or the
-  //      prompt/text validity bytes (full).  Every global load of the
-  //      prologue is issued before any is consumed.
-  for (int i = tid; i < HMAX * 128; i += kThreads) {
-    const int h = i >> 7, d = i & 127;
-    s_q[h][d] = (h < nh) ? TT::to_f32(a.q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + d * a.q_sd]) : 0.f;
-  }
-  if (!is_vis) {
-    const int64_t t_begin = (int64_t)xf * a.chunk_full;
-    const int64_t t_end = min(a.S_f, t_begin + a.chunk_full);
-    const uint8_t* mb = a.mask ? a.mask + b * a.mf_sb : nullptr;
-    uint8_t mv[kMaskChunk / kThreads];
-#pragma unroll
-    for (int k = 0; k < kMaskChunk / kThreads; ++k) {
-      const int64_t t = min(t_begin + tid + k * kThreads, max(t_end - 1, (int64_t)0));
-      mv[k] = (mb && t_end > t_begin) ? mb[t * a.mf_ss] : (uint8_t)1;
-    }
-#pragma unroll
-    for (int k = 0; k < kMaskChunk / kThreads; ++k) {
-      const int i = tid + k * kThreads;
-      s_valid[i] = (t_begin + i < t_end) && mv[k] != 0;
-    }
-  } else {
-    // q R: thread (c, part) loads R[part*L .. part*L+L-1][c] at once, forms
-    // partial dot products for every head, and the parts are summed in LDS.
-    constexpr int kParts = kThreads / DKP, kL = 128 / kParts;
-    const int c = tid % DKP, part = tid / DKP;
-    const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)c * a.R_sk;
-    float rv[kL];
-    if (c < a.Dk) {
-      if (a.r_dtype == 2) {
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = ((const float*)a.R)[rb + (int64_t)(part * kL + i) * a.R_sd];
-      } else {
-        uint16_t rr[kL];
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rr[i] = ((const uint16_t*)a.R)[rb + (int64_t)(part * kL + i) * a.R_sd];
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = a.r_dtype == 0 ? F16::to_f32(rr[i]) : BF16::to_f32(rr[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kL; ++i) rv[i] = 0.f;
-    }
-    if (tid < 128) {
-      const int64_t di = b * a.dm_sb + kv * a.dm_sh + (int64_t)tid * a.dm_sd;
-      s_dm[tid] = a.has_bias ? load_any(a.dm, di, a.dm_dtype) : 0.f;
-    }
-    __syncthreads();
-    float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
-#pragma unroll
-    for (int h = 0; h < HMAX; ++h) {
-      float acc_h = 0.f;
-#pragma unroll
-      for (int i = 0; i < kL; ++i) acc_h += s_q[h][part * kL + i] * rv[i];
-      s_part[(part * HMAX + h) * DKP + c] = acc_h;
-    }
-    __syncthreads();
-    for (int i = tid; i < HMAX * DKP; i += kThreads) {
-      const int h = i / DKP, cc = i % DKP;
-      float sum = 0.f;
-#pragma unroll
-      for (int pp = 0; pp < kParts; ++pp) sum += s_part[(pp * HMAX + h) * DKP + cc];
-      s_qt[h][cc] = sum;
-    }
-    if (tid < HMAX) {
-      float bsum = 0.f;
-      for (int d = 0; d < 128; ++d) bsum += s_q[tid][d] * s_dm[d];
-      s_bias[tid] = bsum;
-    }
-  }
-  __syncthreads();
-
   float m = kNegInit, l = 0.f;
   f32x4 acc[8];
 #pragma unroll
@@ -349,21 +314,31 @@ decode_kernel(const DecodeArgs a) {
   const uint32_t krow0 = 8 * (n >> 2) + (n & 3), krow1 = krow0 + 4;
   const uint32_t rot_seed = ((uint32_t)u * 0x9E3779B1u) ^ ((uint32_t)x * 0x85EBCA77u);
 
+  // Prologue order: issue the prologue's own loads (q rows, and R / delta_mu
+  // or the mask bytes), then the first NBUF K/V blocks, and only then wait
+  // for the prologue data, so its latency hides under the first blocks.
+  constexpr int kQPer = (HMAX * 128 + kThreads - 1) / kThreads;
+  float qv[kQPer];
+  auto load_q = [&]() {
+#pragma unroll
+    for (int k = 0; k < kQPer; ++k) {
+      const int i = tid + k * kThreads;
+      const int h = i >> 7, d = i & 127;
+      qv[k] = (i < HMAX * 128 && h < nh)
+                  ? TT::to_f32(a.q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + d * a.q_sd])
+                  : 0.f;
+    }
+  };
+  auto store_q = [&]() {
+#pragma unroll
+    for (int k = 0; k < kQPer; ++k) {
+      const int i = tid + k * kThreads;
+      if (i < HMAX * 128) s_q[i >> 7][i & 127] = qv[k];
+    }
+  };
+
   if (is_vis) {
     // ---- visual span: rotated, truncated Keys (Dk channels)
-    uint4 qh[DKB], ql[DKB];
-#pragma unroll
-    for (int kb = 0; kb < DKB; ++kb) {
-      uint16_t hv[8], lv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = (n < HMAX) ? s_qt[nq][kb * 32 + 8 * g + e] : 0.f;
-        TT::split(v, hv[e], lv[e]);
-      }
-      qh[kb] = pack8(hv);
-      ql[kb] = pack8(lv);
-    }
-    const float bias2 = (n < HMAX ? s_bias[nq] : 0.f) * a.scale_log2;
     const int64_t t_begin = (int64_t)x * a.chunk_vis;
     const int64_t t_end = min(a.S_v, t_begin + a.chunk_vis);
     const uint32_t t_last = (uint32_t)(t_end - 1);
@@ -393,35 +368,96 @@ decode_kernel(const DecodeArgs a) {
       for (int r = 0; r < 8; ++r)
         B.v[r] = load_row8<VEC>(vsb, min(t0 + 8u * g + r, t_last) * a.vs_ss, vch, a.vs_sd, 8);
     };
+
+    // q R: thread (c, part) loads R[part*L .. part*L+L-1][c], forms partial
+    // dot products for every head, and the parts are summed in LDS.
+    constexpr int kParts = kThreads / DKP, kL = 128 / kParts;
+    const int c = tid % DKP, part = tid / DKP;
+    load_q();
+    const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)c * a.R_sk;
+    float rv[kL];
+    if (c < a.Dk) {
+      if (a.r_dtype == 2) {
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rv[i] = ((const float*)a.R)[rb + (int64_t)(part * kL + i) * a.R_sd];
+      } else {
+        uint16_t rr[kL];
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rr[i] = ((const uint16_t*)a.R)[rb + (int64_t)(part * kL + i) * a.R_sd];
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rv[i] = a.r_dtype == 0 ? F16::to_f32(rr[i]) : BF16::to_f32(rr[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kL; ++i) rv[i] = 0.f;
+    }
+    float dmv = 0.f;
+    if (tid < 128 && a.has_bias)
+      dmv = load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)tid * a.dm_sd, a.dm_dtype);
+
+    Ring<NBUF_V, VisBuf<DKB>> ring(nblk, wave, rot_seed);
+    ring.prime(load);
+
+    store_q();
+    if (tid < 128) s_dm[tid] = dmv;
+    __syncthreads();
+    float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
+#pragma unroll
+    for (int h = 0; h < HMAX; ++h) {
+      float acc_h = 0.f;
+#pragma unroll
+      for (int i = 0; i < kL; ++i) acc_h += s_q[h][part * kL + i] * rv[i];
+      s_part[(part * HMAX + h) * DKP + c] = acc_h;
+    }
+    __syncthreads();
+    for (int i = tid; i < HMAX * DKP; i += kThreads) {
+      const int h = i / DKP, cc = i % DKP;
+      float sum = 0.f;
+#pragma unroll
+      for (int pp = 0; pp < kParts; ++pp) sum += s_part[(pp * HMAX + h) * DKP + cc];
+      s_qt[h][cc] = sum;
+    }
+    if (tid < HMAX) {
+      float bsum = 0.f;
+      for (int d = 0; d < 128; ++d) bsum += s_q[tid][d] * s_dm[d];
+      s_bias[tid] = bsum;
+    }
+    __syncthreads();
+
+    uint4 qh[DKB], ql[DKB];
+#pragma unroll
+    for (int kb = 0; kb < DKB; ++kb) {
+      uint16_t hv[8], lv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = (n < HMAX) ? s_qt[nq][kb * 32 + 8 * g + e] : 0.f;
+        TT::split(v, hv[e], lv[e]);
+      }
+      qh[kb] = pack8(hv);
+      ql[kb] = pack8(lv);
+    }
+    const float bias2 = (n < HMAX ? s_bias[nq] : 0.f) * a.scale_log2;
     auto compute = [&](VisBuf<DKB>& B, int64_t blk) {
       const int64_t t0 = t_begin + blk * kBlk;
       float s[8];
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 cc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < DKB; ++kb) c = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), qh[kb], c);
+        for (int kb = 0; kb < DKB; ++kb) cc = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), qh[kb], cc);
 #pragma unroll
-        for (int kb = 0; kb < DKB; ++kb) c = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), ql[kb], c);
+        for (int kb = 0; kb < DKB; ++kb) cc = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), ql[kb], cc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int64_t t = t0 + 8 * g + 4 * sb + i;
-          s[4 * sb + i] = (t < t_end) ? fmaf(c[i], a.scale_log2, bias2) : -INFINITY;
+          s[4 * sb + i] = (t < t_end) ? fmaf(cc[i], a.scale_log2, bias2) : -INFINITY;
         }
       }
       softmax_pv<TT>(s, B.v, m, l, acc);
     };
-    run_ring<NBUF_V, VisBuf<DKB>>(nblk, wave, rot_seed, load, compute);
+    ring.run(load, compute);
   } else {
     // ---- prompt + text span: full-width Keys
-    uint4 qf[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      uint16_t hv[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) hv[e] = TT::from_f32((n < HMAX) ? s_q[nq][kb * 32 + 8 * g + e] : 0.f);
-      qf[kb] = pack8(hv);
-    }
     const int64_t t_begin = (int64_t)xf * a.chunk_full;
     const int64_t t_end = min(a.S_f, t_begin + a.chunk_full);
     const uint32_t t_last = (uint32_t)max((int64_t)0, t_end - 1);
@@ -441,22 +477,51 @@ decode_kernel(const DecodeArgs a) {
       for (int r = 0; r < 8; ++r)
         B.v[r] = load_row8<VEC>(vfb, min(t0 + 8u * g + r, t_last) * a.vf_ss, vch, a.vf_sd, 8);
     };
+
+    load_q();
+    const uint8_t* mb = a.mask ? a.mask + b * a.mf_sb : nullptr;
+    uint8_t mv[kMaskChunk / kThreads];
+#pragma unroll
+    for (int k = 0; k < kMaskChunk / kThreads; ++k) {
+      const int64_t t = min(t_begin + tid + k * kThreads, max(t_end - 1, (int64_t)0));
+      mv[k] = (mb && t_end > t_begin) ? mb[t * a.mf_ss] : (uint8_t)1;
+    }
+
+    Ring<NBUF_F, FullBuf> ring(nblk, wave, rot_seed);
+    ring.prime(load);
+
+    store_q();
+#pragma unroll
+    for (int k = 0; k < kMaskChunk / kThreads; ++k) {
+      const int i = tid + k * kThreads;
+      s_valid[i] = (t_begin + i < t_end) && mv[k] != 0;
+    }
+    __syncthreads();
+
+    uint4 qf[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      uint16_t hv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hv[e] = TT::from_f32((n < HMAX) ? s_q[nq][kb * 32 + 8 * g + e] : 0.f);
+      qf[kb] = pack8(hv);
+    }
     auto compute = [&](FullBuf& B, int64_t blk) {
       const uint2 vb = *(const uint2*)&s_valid[blk * kBlk + 8 * g];
       float s[8];
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
-        f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 cc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) c = TT::mfma(B.k[sb][kb], qf[kb], c);
+        for (int kb = 0; kb < 4; ++kb) cc = TT::mfma(B.k[sb][kb], qf[kb], cc);
         const uint32_t w = sb ? vb.y : vb.x;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          s[4 * sb + i] = ((w >> (8 * i)) & 0xffu) ? c[i] * a.scale_log2 : -INFINITY;
+          s[4 * sb + i] = ((w >> (8 * i)) & 0xffu) ? cc[i] * a.scale_log2 : -INFINITY;
       }
       softmax_pv<TT>(s, B.v, m, l, acc);
     };
-    run_ring<NBUF_F, FullBuf>(nblk, wave, rot_seed, load, compute);
+    ring.run(load, compute);
   }
 
   // ---- merge the four wave states into this workgroup's partial
@@ -500,15 +565,20 @@ decode_kernel(const DecodeArgs a) {
 
 }
 
-// Second launch: one workgroup per unit merges the unit's partials.
+// Second launch: 16 threads per (unit, head) row, 16 rows per workgroup.
 template <class TT>
-__global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
-  const int u = blockIdx.x;
-  const int b = u / a.units_per_b;
-  const int r_in_b = u - b * a.units_per_b;
+__global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a, int64_t rows) {
+  const int tid = threadIdx.x;
+  const int64_t row = (int64_t)blockIdx.x * 16 + (tid >> 4);
+  if (row >= rows) return;
+  const int64_t u = row / a.hpu;
+  const int h = (int)(row - u * a.hpu);
+  const int b = (int)(u / a.units_per_b);
+  const int r_in_b = (int)(u - (int64_t)b * a.units_per_b);
   const int kv = r_in_b / a.spk;
   const int jblk = r_in_b - kv * a.spk;
-  merge_unit<TT>(a, u, b, kv * a.G + jblk * a.hpu, min(a.hpu, a.G - jblk * a.hpu));
+  if (h >= min(a.hpu, a.G - jblk * a.hpu)) return;
+  merge_row<TT>(a, u, b, kv * a.G + jblk * a.hpu + h, h, tid & 15);
 }
 
 }  // namespace rk
@@ -520,9 +590,13 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
 
 namespace {
 
+// Bytes of K/V a workgroup streams: total / (2 * CUs), clamped to
+// [64 KB, 512 KB].  Measured on MI355X: 512 KB chunks are within 2-5% of the
+// best split at B=32/16k (MHA), B=16/32k (GQA) and B=1/16k; small problems
+// get at least ~2 workgroups per CU.
 int64_t g_min_wg_bytes = INT64_C(64) << 10;
 int64_t g_max_wg_bytes = INT64_C(512) << 10;
-int32_t g_wgs_per_cu = 16;
+int32_t g_wgs_per_cu = 2;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
@@ -691,7 +765,9 @@ hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
                      a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3(grid.y), dim3(rk::kThreads), 0, s, a);
+  const int64_t rows = (int64_t)grid.y * a.hpu;
+  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)((rows + 15) / 16)), dim3(rk::kThreads), 0, s,
+                     a, rows);
   return hipGetLastError();
 }
 
