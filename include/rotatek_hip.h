@@ -167,6 +167,56 @@ int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
  * wgs_per_cu workgroups per compute unit).  Pass 0 to keep a value. */
 void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu);
 
+/* ------------------------------------------------------------------ prefill
+ * Keys are the visual span of the layer's Keys, [B, H_kv, S_v, 128] in F16
+ * or BF16, any strides (a head must span < 2^31 elements).
+ *
+ * Key covariance (kv_pruning_utils.py:112-115):
+ *   mean_out[b,h,:] = fp32 mean of K over S_v                (F32, optional)
+ *   cov_out[b,h]    = 0.5 (C + C^T), C = dtype(Kc^T Kc) in fp32,
+ *                     Kc = dtype(K - dtype(mean))            (F32 [B,H,128,128])
+ * Three launches (mean partials, MFMA covariance partials, finalise); the
+ * workspace size comes from rk_key_covariance_check. */
+int rk_key_covariance_check(const rk_tensor* keys, const rk_tensor* mean_out,
+                            const rk_tensor* cov_out, int32_t num_cus,
+                            size_t* workspace_bytes);
+int rk_key_covariance(const rk_tensor* keys, const rk_tensor* mean_out,
+                      const rk_tensor* cov_out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Truncated visual-Key write (kv_pruning_utils.py:152):
+ * out[b,h,s,:] = dtype(K[b,h,s,:] @ R_partial[b,h]), R_partial
+ * [B,H,128,Dk] (F16/BF16/F32), out [B,H,S_v,Dk] in the key dtype. */
+int rk_rotate_keys(const rk_tensor* keys, const rk_tensor* R_partial,
+                   const rk_tensor* out, void* stream);
+
+/* Channel scores of the head-wise selection: scores_out[b,h,c] =
+ * mean_s |K R_full|[s,c] with fp64 final reduction; R_full [B,H,128,Dc]
+ * (Dc <= 128), scores_out [B,H,Dc] F64. */
+int rk_channel_scores_check(const rk_tensor* keys, const rk_tensor* R_full,
+                            const rk_tensor* scores_out, int32_t num_cus,
+                            size_t* workspace_bytes);
+int rk_channel_scores(const rk_tensor* keys, const rk_tensor* R_full,
+                      const rk_tensor* scores_out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Head-wise channel top-k (keep mask of kv_pruning_utils.py:158-159):
+ * scores [B,H,D] F64 (D <= 128) -> idx_out [B,H,k] I64, the k channels with
+ * the largest scores (ties to the lower index) in ascending order, and
+ * mask_out [B,H,D] U8 (optional). */
+int rk_topk_channels(const rk_tensor* scores, int64_t k, const rk_tensor* idx_out,
+                     const rk_tensor* mask_out, void* stream);
+
+/* R_partial / delta_mu (kv_pruning_utils.py:150-156):
+ * R_out[b,h,:,j] = dtype(R_full[b,h,:,idx[b,h,j]]) and
+ * delta_mu_out[b,h] = dtype(mean - (mean R_out) R_out^T) computed in fp32
+ * from the rounded R_out.  R_full [B,H,128,*] F16/BF16/F32, idx [B,H,k] I64,
+ * mean [B,H,128] F32, R_out [B,H,128,k] and delta_mu_out [B,H,128] in
+ * F16/BF16. */
+int rk_gather_rotation(const rk_tensor* R_full, const rk_tensor* idx,
+                       const rk_tensor* mean, const rk_tensor* R_out,
+                       const rk_tensor* delta_mu_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

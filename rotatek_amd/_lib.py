@@ -76,6 +76,13 @@ _SIGNATURES = {
     "rk_plan_decode": (ctypes.c_int, [ctypes.c_int64] * 6 + [ctypes.c_int32] * 3
                        + [ctypes.POINTER(RkDecodePlan)]),
     "rk_set_decode_tuning": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
+    "rk_key_covariance_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
+    "rk_key_covariance": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "rk_rotate_keys": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p]),
+    "rk_channel_scores_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
+    "rk_channel_scores": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "rk_topk_channels": (ctypes.c_int, [_P, ctypes.c_int64, _P, _P, ctypes.c_void_p]),
+    "rk_gather_rotation": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_void_p]),
 }
 
 _lib = None

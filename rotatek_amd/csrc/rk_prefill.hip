@@ -1,0 +1,788 @@
+// rk_prefill.hip -- RotateK prefill producer kernels for MI355X (gfx950).
+//
+// Per (batch, KV head) of the visual Keys K [S, 128] (any strides):
+//
+//   covariance   (kv_pruning_utils.py:112-115)
+//     mean_kernel   split-S fp32 partial sums of K               (pass 1)
+//     cov_kernel    mu = sum / S (fp32), c = dtype(mu); Kc = dtype(K - c);
+//                   split-S partial Kc^T Kc on v_mfma_f32_16x16x32 with
+//                   fp32 accumulation, upper 36 of 64 16x16 tiles (pass 2)
+//     covfin_kernel sum of partials -> dtype -> fp32 -> 0.5 (C + C^T)
+//   rotate / score (kv_pruning_utils.py:152; BASELINE config 0 selection)
+//     rot_kernel    C^T = R^T K^T on the MFMA, 64 tokens per step; STORE
+//                   writes dtype(K R) (the truncated visual-Key write),
+//                   SCORE accumulates |K R| per rotated channel
+//     scorefin_kernel  fp64 sum of the per-workgroup partial sums / S
+//   selection
+//     topk_kernel   head-wise top-k by (score desc, index asc) -> ascending
+//                   indices + keep mask (kv_pruning_utils.py:158-159)
+//     gather_kernel R_partial = dtype(R_full[:, idx]),
+//                   delta_mu = dtype(mu - (mu R_partial) R_partial^T)
+//                   (kv_pruning_utils.py:150-156)
+//
+// Operand layout (see rk_common.h): for the covariance a lane (g, n) loads
+// rows 8g..8g+7 (tokens) x channels 8n..8n+7 of a 32-token block and
+// transposes them in registers; slot i of that transpose is the MFMA
+// operand for the channel set {8m + i : m = 0..15}, so tile (i, j) of the
+// accumulator holds C[8m + i][8m' + j].
+#include <math.h>
+#include <string.h>
+
+#include "rk_common.h"
+#include "rk_host.h"
+#include "rotatek_hip.h"
+
+namespace rk {
+namespace prefill {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = 4;
+
+struct KeyView {
+  const uint16_t* data;
+  int64_t sb, sh;      // batch / head strides (elements)
+  uint32_t ss, sd;     // token / channel strides; a head spans < 2^31 elements
+  int64_t S;           // tokens
+  int32_t H;
+};
+
+__device__ __forceinline__ const uint16_t* head_base(const KeyView& k, int bh) {
+  const int b = bh / k.H, h = bh - b * k.H;
+  return k.data + b * k.sb + (int64_t)h * k.sh;
+}
+
+// Eight channels c0..c0+7 of row `t` (clamped by the caller).
+template <bool VEC>
+__device__ __forceinline__ uint4 ldrow(const uint16_t* base, const KeyView& k, uint32_t t, uint32_t c0) {
+  if constexpr (VEC) {
+    return *(const uint4*)((const char*)base + (t * k.ss + c0) * 2u);
+  } else {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e >> 1] |= (uint32_t)base[t * k.ss + (c0 + e) * k.sd] << ((e & 1) * 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <class TT>
+__device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = TT::to_f32((uint16_t)(word(v, e >> 1) >> ((e & 1) * 16)));
+}
+
+// ------------------------------------------------------------------ pass 1
+// grid (splits, B*H): workgroup x sums tokens [x*chunk, (x+1)*chunk) of one
+// head into part[bh][x][128] (fp32).  Thread (row group rg = t/16, channel
+// chunk c8 = t%16) walks rows rg, rg+16, ... four at a time.
+template <class TT, bool VEC>
+__global__ void __launch_bounds__(kThreads) mean_kernel(KeyView k, int64_t chunk, int splits,
+                                                        float* part) {
+  __shared__ float s_sum[16][128];
+  const int tid = threadIdx.x, rg = tid >> 4, c8 = tid & 15;
+  const int x = blockIdx.x, bh = blockIdx.y;
+  const uint16_t* base = head_base(k, bh);
+  const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
+  for (int64_t t = t0 + rg; t < t1; t += 64) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = ldrow<VEC>(base, k, min((uint32_t)(t + 16 * i), last), 8u * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (t + 16 * i < t1) {
+        float f[8];
+        unpack8<TT>(v[i], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += f[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_sum[rg][8 * c8 + e] = acc[e];
+  __syncthreads();
+  if (tid < 128) {
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += s_sum[r][tid];
+    part[((int64_t)bh * splits + x) * 128 + tid] = s;
+  }
+}
+
+// mean of one head from the pass-1 partials (fixed summation order, so every
+// kernel that needs mu gets the same bits).
+__device__ __forceinline__ float head_mean(const float* part, int bh, int splits, int c, int64_t S) {
+  float s = 0.f;
+  for (int x = 0; x < splits; ++x) s += part[((int64_t)bh * splits + x) * 128 + c];
+  return S > 0 ? s / (float)S : 0.f;
+}
+
+// ------------------------------------------------------------------ pass 2
+constexpr int kTiles = 36;  // upper-triangle 16x16 tiles (i <= j) of the 8x8 grid
+
+// Tiles (i, j), i <= j, enumerated row-major: t = 8i - i(i-1)/2 + (j - i).
+__host__ __device__ constexpr int tile_index(int i, int j) { return 8 * i - i * (i - 1) / 2 + (j - i); }
+__host__ __device__ constexpr int tile_row(int t) {
+  return t < 8 ? 0 : t < 15 ? 1 : t < 21 ? 2 : t < 26 ? 3 : t < 30 ? 4 : t < 33 ? 5 : t < 35 ? 6 : 7;
+}
+__host__ __device__ constexpr int tile_col(int t) { return tile_row(t) + t - tile_index(tile_row(t), tile_row(t)); }
+
+// grid (splits, B*H): each wave accumulates Kc^T Kc over its interleaved
+// 32-token blocks for all 36 upper tiles; the four waves are summed in LDS
+// and the workgroup writes one [36][256] partial.
+template <class TT, bool VEC>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mean_splits, float* part) {
+  __shared__ float s_c[128];
+  __shared__ float s_red[kTiles * 256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+  const int x = blockIdx.x, bh = blockIdx.y;
+  const uint16_t* base = head_base(k, bh);
+  if (tid < 128) {
+    // centre = mean rounded to the key dtype (kv_pruning_utils.py:113)
+    s_c[tid] = TT::to_f32(TT::from_f32(head_mean(mean_part, bh, mean_splits, tid, k.S)));
+  }
+  __syncthreads();
+  float cen[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) cen[e] = s_c[8 * n + e];
+
+  f32x4 acc[kTiles];
+#pragma unroll
+  for (int t = 0; t < kTiles; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
+  const int64_t nblk = (t1 - t0 + 31) / 32;
+  const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
+  for (int64_t blk = wave; blk < nblk; blk += kWaves) {
+    const int64_t tb = t0 + blk * 32 + 8 * g;
+    uint4 rows[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) rows[r] = ldrow<VEC>(base, k, min((uint32_t)(tb + r), last), 8u * n);
+    // centre in fp32, round to the key dtype; rows past the end are zero
+    uint16_t cb[8][8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      float f[8];
+      unpack8<TT>(rows[r], f);
+      const bool ok = tb + r < t1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cb[r][e] = ok ? TT::from_f32(f[e] - cen[e]) : (uint16_t)0;
+    }
+    // transpose: op[i] element r = Kc[token 8g + r][channel 8n + i]
+    uint4 op[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      op[i] = make_uint4(cb[0][i] | ((uint32_t)cb[1][i] << 16), cb[2][i] | ((uint32_t)cb[3][i] << 16),
+                         cb[4][i] | ((uint32_t)cb[5][i] << 16), cb[6][i] | ((uint32_t)cb[7][i] << 16));
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = TT::mfma(op[tile_row(t)], op[tile_col(t)], acc[t]);
+  }
+  // reduce the four waves: lane (g, n) of tile t holds C[8(4g+r)+i][8n+j]
+  for (int w = 0; w < kWaves; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float& dst = s_red[t * 256 + (4 * g + r) * 16 + n];
+          dst = (w == 0) ? acc[t][r] : dst + acc[t][r];
+        }
+    }
+    __syncthreads();
+  }
+  float* out = part + ((int64_t)bh * splits + x) * (kTiles * 256);
+  for (int i = tid; i < kTiles * 256; i += kThreads) out[i] = s_red[i];
+}
+
+// Sum over the pass-2 partials of entry (m, n) of tile t, rounded to the key
+// dtype (the einsum output dtype, kv_pruning_utils.py:114) and back to fp32.
+template <class TT>
+__device__ __forceinline__ float tile_sum(const float* part, int bh, int splits, int t, int m, int n) {
+  const int e = t * 256 + m * 16 + n;
+  float s = 0.f;
+  for (int x = 0; x < splits; ++x) s += part[((int64_t)bh * splits + x) * (kTiles * 256) + e];
+  return TT::to_f32(TT::from_f32(s));
+}
+
+// grid (B*H): cov[r][c] = 0.5 (C[r][c] + C[c][r]) in fp32 (kv_pruning_utils.py:115)
+// where C[8m+i][8n+j] lives in tile (i, j) if i <= j, else mirrored in
+// tile (j, i); also writes mu [128].
+template <class TT>
+__global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int splits,
+                                                          const float* mean_part, int mean_splits,
+                                                          int64_t S, float* cov, int64_t cs_b, int64_t cs_h,
+                                                          int64_t cs_r, int64_t cs_c, float* mu, int64_t ms_b,
+                                                          int64_t ms_h, int64_t ms_c, int H) {
+  const int tid = threadIdx.x, bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  float* cb = cov + b * cs_b + (int64_t)h * cs_h;
+  for (int e = tid; e < 128 * 128; e += kThreads) {
+    const int r = e >> 7, c = e & 127;
+    const int i = r & 7, m = r >> 3, j = c & 7, n = c >> 3;
+    const float rc = i <= j ? tile_sum<TT>(part, bh, splits, tile_index(i, j), m, n)
+                            : tile_sum<TT>(part, bh, splits, tile_index(j, i), n, m);
+    const float cr = i == j ? tile_sum<TT>(part, bh, splits, tile_index(i, i), n, m) : rc;
+    cb[r * cs_r + c * cs_c] = 0.5f * (rc + cr);
+  }
+  if (tid < 128 && mu)
+    mu[b * ms_b + (int64_t)h * ms_h + tid * ms_c] = head_mean(mean_part, bh, mean_splits, tid, S);
+}
+
+// ------------------------------------------------------------------ rotate / score
+// grid (splits, B*H).  C^T[kept][token] = sum_c R[c][kept] K[token][c]:
+// A = R^T tile (from LDS, transposed once per workgroup), B = K^T (lane
+// (g, n) loads 16 bytes of token row n at channel 32 ks + 8 g).  A wave
+// takes 64 tokens (four 16-token column blocks) per step and reuses each A
+// fragment across them.
+//   STORE: out[token][16 t + 4 g + r] = dtype(C^T), the truncated write.
+//   SCORE: per-lane sums of |C^T| per rotated channel, reduced over the
+//          workgroup into spart[bh][x][kept] (fp32).
+struct RotArgs {
+  KeyView k;
+  const void* R;
+  int32_t r_dtype;
+  int64_t R_sb, R_sh, R_sd, R_sk;
+  int32_t Dk;
+  uint16_t* out;
+  int64_t o_sb, o_sh, o_ss, o_sd;
+  float* spart;
+  int64_t chunk;
+  int32_t splits;
+};
+
+template <class TT, int NT, bool VEC, bool SCORE>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+rot_kernel(const RotArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t s_rt[NT * 16][128 + 8];  // R^T, padded rows
+  __shared__ float s_sc[kWaves][NT * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+  const int x = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / a.k.H, h = bh - b * a.k.H;
+  const uint16_t* base = head_base(a.k, bh);
+  // stage R^T (kept rows >= Dk are zero) in the key dtype
+  const int64_t rb = b * a.R_sb + (int64_t)h * a.R_sh;
+  for (int e = tid; e < NT * 16 * 128; e += kThreads) {
+    const int kk = e >> 7, c = e & 127;
+    const float v = kk < a.Dk ? load_any(a.R, rb + c * a.R_sd + kk * a.R_sk, a.r_dtype) : 0.f;
+    s_rt[kk][c] = TT::from_f32(v);
+  }
+  __syncthreads();
+
+  float sc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[t][r] = 0.f;
+  const int64_t t0 = (int64_t)x * a.chunk, t1 = min(a.k.S, t0 + a.chunk);
+  const int64_t nstep = (t1 - t0 + 63) / 64;
+  const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
+  for (int64_t st = wave; st < nstep; st += kWaves) {
+    const int64_t ts = t0 + st * 64;
+    uint4 bk[4][4];  // [token block][k-step]
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      const int64_t tok = ts + 16 * tb + n;
+      const uint32_t tr = min((uint32_t)tok, last);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        uint4 v = ldrow<VEC>(base, a.k, tr, (uint32_t)(32 * ks + 8 * g));
+        if (SCORE && tok >= t1) v = make_uint4(0, 0, 0, 0);
+        bk[tb][ks] = v;
+      }
+    }
+#pragma unroll(NT <= 2 ? NT : 1)
+    for (int t = 0; t < NT; ++t) {
+      f32x4 c[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const uint4 av = *(const uint4*)&s_rt[16 * t + n][32 * ks + 8 * g];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) c[tb] = TT::mfma(av, bk[tb][ks], c[tb]);
+      }
+      if constexpr (SCORE) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[t][r] += fabsf(c[tb][r]);
+      } else {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const int64_t tok = ts + 16 * tb + n;
+          if (tok < t1) {
+            uint16_t* o = a.out + b * a.o_sb + (int64_t)h * a.o_sh + tok * a.o_ss;
+            const int k0 = 16 * t + 4 * g;
+            if (k0 + 3 < a.Dk && a.o_sd == 1 && (((uintptr_t)(o + k0)) & 7) == 0) {
+              uint2 w;
+              w.x = TT::from_f32(c[tb][0]) | ((uint32_t)TT::from_f32(c[tb][1]) << 16);
+              w.y = TT::from_f32(c[tb][2]) | ((uint32_t)TT::from_f32(c[tb][3]) << 16);
+              *(uint2*)(o + k0) = w;
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                if (k0 + r < a.Dk) o[(k0 + r) * a.o_sd] = TT::from_f32(c[tb][r]);
+            }
+          }
+        }
+      }
+    }
+  }
+  if constexpr (SCORE) {
+    // lanes of one row (fixed g) hold different tokens of the same channels
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = sc[t][r];
+        v += shfl_xor(v, 1);
+        v += shfl_xor(v, 2);
+        v += shfl_xor(v, 4);
+        v += shfl_xor(v, 8);
+        if (n == 0) s_sc[wave][16 * t + 4 * g + r] = v;
+      }
+    __syncthreads();
+    for (int kk = tid; kk < NT * 16; kk += kThreads) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) v += s_sc[w][kk];
+      a.spart[((int64_t)bh * a.splits + x) * (NT * 16) + kk] = v;
+    }
+  }
+}
+
+// grid (B*H): scores[c] = (sum of partials in fp64) / S for c < nk;
+// partial rows are `pstride` floats apart.
+__global__ void __launch_bounds__(128) scorefin_kernel(const float* spart, int splits, int pstride, int nk,
+                                                       int64_t S, double* scores, int64_t s_b, int64_t s_h,
+                                                       int64_t s_c, int H) {
+  const int c = threadIdx.x, bh = blockIdx.x;
+  if (c >= nk) return;
+  const int b = bh / H, h = bh - b * H;
+  double s = 0.0;
+  for (int x = 0; x < splits; ++x) s += (double)spart[((int64_t)bh * splits + x) * pstride + c];
+  scores[b * s_b + (int64_t)h * s_h + c * s_c] = S > 0 ? s / (double)S : 0.0;
+}
+
+// ------------------------------------------------------------------ selection
+// grid (B*H), 128 threads: rank of channel c = #{j : s_j > s_c or
+// (s_j == s_c and j < c)}; kept iff rank < k; the output indices are the
+// kept channels in ascending order.
+__global__ void __launch_bounds__(128) topk_kernel(const double* scores, int64_t s_b, int64_t s_h,
+                                                   int64_t s_c, int D, int k, int H, int64_t* idx,
+                                                   int64_t i_b, int64_t i_h, int64_t i_k, uint8_t* mask,
+                                                   int64_t m_b, int64_t m_h, int64_t m_c) {
+  __shared__ double s_v[128];
+  __shared__ int s_keep[128];
+  const int c = threadIdx.x, bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  if (c < D) s_v[c] = scores[b * s_b + (int64_t)h * s_h + c * s_c];
+  __syncthreads();
+  int keep = 0;
+  if (c < D) {
+    const double v = s_v[c];
+    int rank = 0;
+    for (int j = 0; j < D; ++j) {
+      const double w = s_v[j];
+      rank += (w > v) || (w == v && j < c);
+    }
+    keep = rank < k;
+    if (mask) mask[b * m_b + (int64_t)h * m_h + c * m_c] = (uint8_t)keep;
+  }
+  s_keep[c] = keep;
+  __syncthreads();
+  if (c < D && keep) {
+    int pos = 0;
+    for (int j = 0; j < c; ++j) pos += s_keep[j];
+    idx[b * i_b + (int64_t)h * i_h + pos * i_k] = c;
+  }
+}
+
+// grid (B*H), 128 threads: R_partial[:, kk] = dtype(R_full[:, idx[kk]]);
+// delta_mu = dtype(mu - (mu Rp) Rp^T) with Rp already in the key dtype.
+template <class TT>
+__global__ void __launch_bounds__(128) gather_kernel(const void* R, int r_dtype, int64_t R_sb, int64_t R_sh,
+                                                     int64_t R_sd, int64_t R_sk, const int64_t* idx,
+                                                     int64_t i_b, int64_t i_h, int64_t i_k, int k,
+                                                     const float* mu, int64_t u_b, int64_t u_h, int64_t u_c,
+                                                     uint16_t* Rp, int64_t p_b, int64_t p_h, int64_t p_d,
+                                                     int64_t p_k, uint16_t* dm, int64_t d_b, int64_t d_h,
+                                                     int64_t d_c, int H) {
+  __shared__ float s_mu[128];
+  __shared__ float s_proj[128];
+  __shared__ int64_t s_col[128];
+  const int d = threadIdx.x, bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  s_mu[d] = mu[b * u_b + (int64_t)h * u_h + d * u_c];
+  if (d < k) s_col[d] = idx[b * i_b + (int64_t)h * i_h + d * i_k];
+  __syncthreads();
+  const int64_t rb = b * R_sb + (int64_t)h * R_sh;
+  auto rp = [&](int row, int kk) {
+    return TT::from_f32(load_any(R, rb + row * R_sd + s_col[kk] * R_sk, r_dtype));
+  };
+  for (int kk = 0; kk < k; ++kk) Rp[b * p_b + (int64_t)h * p_h + d * p_d + kk * p_k] = rp(d, kk);
+  if (d < k) {
+    float s = 0.f;
+    for (int e = 0; e < 128; ++e) s += s_mu[e] * TT::to_f32(rp(e, d));
+    s_proj[d] = s;
+  }
+  __syncthreads();
+  float p = 0.f;
+  for (int kk = 0; kk < k; ++kk) p += s_proj[kk] * TT::to_f32(rp(d, kk));
+  dm[b * d_b + (int64_t)h * d_h + d * d_c] = TT::from_f32(s_mu[d] - p);
+}
+
+}  // namespace prefill
+}  // namespace rk
+
+// =====================================================================
+// host side
+// =====================================================================
+namespace {
+
+using namespace rk::prefill;
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// Keys descriptor [B, H, S, 128] (16-bit float).  Sets the view and the
+// fast-path flag.
+int key_view(const rk_tensor* t, KeyView* k, bool* vec) {
+  int st = rk::check_desc(t, 4);
+  if (st) return st;
+  if (!rk::is_half(t->dtype)) return RK_ERR_DTYPE;
+  if (t->shape[3] != 128) return RK_ERR_HEAD_DIM;
+  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1) * t->stride[2] : 0) + 127 * t->stride[3] + 8;
+  if (span >= (INT64_C(1) << 31) || t->stride[2] >= (INT64_C(1) << 31)) return RK_ERR_STRIDE;
+  if (t->shape[0] * t->shape[1] > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
+  k->data = (const uint16_t*)t->data;
+  k->sb = t->stride[0];
+  k->sh = t->stride[1];
+  k->ss = (uint32_t)t->stride[2];
+  k->sd = (uint32_t)t->stride[3];
+  k->S = t->shape[2];
+  k->H = (int32_t)t->shape[1];
+  *vec = rk::vec_ok(t);
+  return RK_OK;
+}
+
+// Token split of a per-head pass: about 2 workgroups per CU in total, at
+// least 256 tokens per workgroup.
+int splits_for(int64_t bh, int64_t S, int cus, int64_t min_tokens) {
+  if (S <= 0 || bh <= 0) return 1;
+  int64_t want = cdiv(2 * (int64_t)cus, bh);
+  const int64_t cap = cdiv(S, min_tokens);
+  if (want > cap) want = cap;
+  if (want < 1) want = 1;
+  if (want > 4096) want = 4096;
+  return (int)want;
+}
+
+struct CovPlan {
+  int mean_splits, cov_splits;
+  int64_t mean_chunk, cov_chunk;
+  size_t off_mean, off_cov, total;
+};
+
+CovPlan cov_plan(int64_t B, int64_t H, int64_t S, int cus) {
+  CovPlan p;
+  const int64_t bh = B * H;
+  p.mean_splits = splits_for(bh, S, cus, 256);
+  p.mean_chunk = cdiv(S > 0 ? S : 1, p.mean_splits);
+  p.cov_splits = splits_for(bh, S, cus, 512);
+  p.cov_chunk = cdiv(S > 0 ? S : 1, p.cov_splits);
+  p.off_mean = 0;
+  p.off_cov = align256((size_t)bh * p.mean_splits * 128 * sizeof(float));
+  p.total = p.off_cov + align256((size_t)bh * p.cov_splits * kTiles * 256 * sizeof(float));
+  return p;
+}
+
+int resolve_cus(int32_t num_cus, int* st) {
+  *st = RK_OK;
+  if (num_cus > 0) return num_cus;
+  int dev = 0;
+  const int cus = rk::current_device_cus(&dev);
+  if (cus <= 0) *st = RK_ERR_NO_DEVICE;
+  return cus;
+}
+
+int check_f32_out(const rk_tensor* t, int ndim, int64_t B, int64_t H, int64_t last, int dtype) {
+  int st = rk::check_desc(t, ndim);
+  if (st) return st;
+  if (t->dtype != dtype) return RK_ERR_DTYPE;
+  if (t->shape[0] != B || t->shape[1] != H || t->shape[ndim - 1] != last) return RK_ERR_SHAPE;
+  if (ndim == 4 && t->shape[2] != last) return RK_ERR_SHAPE;
+  return RK_OK;
+}
+
+template <class TT>
+hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, float* ws, float* cov,
+                      const rk_tensor* cov_t, float* mu, const rk_tensor* mu_t, hipStream_t s) {
+  const int64_t bh = B * k.H;
+  float* mpart = (float*)((char*)ws + p.off_mean);
+  float* cpart = (float*)((char*)ws + p.off_cov);
+  const dim3 gm((unsigned)p.mean_splits, (unsigned)bh), gc((unsigned)p.cov_splits, (unsigned)bh);
+  if (vec) {
+    hipLaunchKernelGGL((mean_kernel<TT, true>), gm, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits, mpart);
+    hipLaunchKernelGGL((cov_kernel<TT, true>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
+                       p.mean_splits, cpart);
+  } else {
+    hipLaunchKernelGGL((mean_kernel<TT, false>), gm, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits, mpart);
+    hipLaunchKernelGGL((cov_kernel<TT, false>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
+                       p.mean_splits, cpart);
+  }
+  hipLaunchKernelGGL((covfin_kernel<TT>), dim3((unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits, mpart,
+                     p.mean_splits, k.S, cov, cov_t->stride[0], cov_t->stride[1], cov_t->stride[2],
+                     cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0, mu_t ? mu_t->stride[1] : 0,
+                     mu_t ? mu_t->stride[2] : 0, k.H);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int rk_key_covariance_check(const rk_tensor* keys, const rk_tensor* mean_out,
+                                       const rk_tensor* cov_out, int32_t num_cus,
+                                       size_t* workspace_bytes) {
+  KeyView k;
+  bool vec;
+  int st = key_view(keys, &k, &vec);
+  if (st) return st;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  if (!cov_out) return RK_ERR_NULL;
+  if ((st = check_f32_out(cov_out, 4, B, H, 128, RK_F32))) return st;
+  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, 128, RK_F32))) return st;
+  const int cus = resolve_cus(num_cus, &st);
+  if (st) return st;
+  if (workspace_bytes) *workspace_bytes = cov_plan(B, H, k.S, cus).total;
+  return RK_OK;
+}
+
+extern "C" int rk_key_covariance(const rk_tensor* keys, const rk_tensor* mean_out, const rk_tensor* cov_out,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  KeyView k;
+  bool vec;
+  int st = key_view(keys, &k, &vec);
+  if (st) return st;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  if (!cov_out) return RK_ERR_NULL;
+  if ((st = check_f32_out(cov_out, 4, B, H, 128, RK_F32))) return st;
+  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, 128, RK_F32))) return st;
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  const CovPlan p = cov_plan(B, H, k.S, cus);
+  if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < p.total) return RK_ERR_WORKSPACE;
+  if (B * H == 0) return RK_OK;
+  if ((k.S > 0 && !k.data) || !cov_out->data) return RK_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  const hipError_t e =
+      keys->dtype == RK_F16
+          ? launch_cov<rk::F16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
+                                mean_out ? (float*)mean_out->data : nullptr, mean_out, s)
+          : launch_cov<rk::BF16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
+                                 mean_out ? (float*)mean_out->data : nullptr, mean_out, s);
+  return e == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+namespace {
+
+int check_rotation(const rk_tensor* R, int64_t B, int64_t H, int64_t* Dk) {
+  int st = rk::check_desc(R, 4);
+  if (st) return st;
+  if (!rk::is_float_param(R->dtype)) return RK_ERR_DTYPE;
+  if (R->shape[0] != B || R->shape[1] != H || R->shape[2] != 128) return RK_ERR_SHAPE;
+  *Dk = R->shape[3];
+  if (*Dk < 1 || *Dk > 128) return RK_ERR_KEEP_DIM;
+  return RK_OK;
+}
+
+template <class TT, int NT, bool SCORE>
+hipError_t launch_rot(const RotArgs& a, bool vec, dim3 grid, hipStream_t s) {
+  if (vec)
+    hipLaunchKernelGGL((rot_kernel<TT, NT, true, SCORE>), grid, dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((rot_kernel<TT, NT, false, SCORE>), grid, dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+template <class TT>
+hipError_t launch_rot_nt(int nt, bool score, const RotArgs& a, bool vec, dim3 grid, hipStream_t s) {
+  if (score) return launch_rot<TT, 8, true>(a, vec, grid, s);
+  switch (nt) {
+    case 1: return launch_rot<TT, 1, false>(a, vec, grid, s);
+    case 2: return launch_rot<TT, 2, false>(a, vec, grid, s);
+    case 3:
+    case 4: return launch_rot<TT, 4, false>(a, vec, grid, s);
+    default: return launch_rot<TT, 8, false>(a, vec, grid, s);
+  }
+}
+
+void fill_rot(RotArgs& a, const KeyView& k, const rk_tensor* R, int64_t Dk) {
+  a.k = k;
+  a.R = R->data;
+  a.r_dtype = R->dtype;
+  a.R_sb = R->stride[0];
+  a.R_sh = R->stride[1];
+  a.R_sd = R->stride[2];
+  a.R_sk = R->stride[3];
+  a.Dk = (int32_t)Dk;
+}
+
+int rot_splits(int64_t bh, int64_t S, int cus) { return splits_for(bh, S, cus, 512); }
+
+}  // namespace
+
+extern "C" int rk_rotate_keys(const rk_tensor* keys, const rk_tensor* R_partial, const rk_tensor* out,
+                              void* stream) {
+  KeyView k;
+  bool vec;
+  int st = key_view(keys, &k, &vec);
+  if (st) return st;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  int64_t Dk = 0;
+  if ((st = check_rotation(R_partial, B, H, &Dk))) return st;
+  if ((st = rk::check_desc(out, 4))) return st;
+  if (out->dtype != keys->dtype) return RK_ERR_DTYPE;
+  if (out->shape[0] != B || out->shape[1] != H || out->shape[2] != k.S || out->shape[3] != Dk)
+    return RK_ERR_SHAPE;
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  if (B * H == 0 || k.S == 0) return RK_OK;
+  if (!k.data || !R_partial->data || !out->data) return RK_ERR_NULL;
+  RotArgs a;
+  memset(&a, 0, sizeof(a));
+  fill_rot(a, k, R_partial, Dk);
+  a.out = (uint16_t*)out->data;
+  a.o_sb = out->stride[0];
+  a.o_sh = out->stride[1];
+  a.o_ss = out->stride[2];
+  a.o_sd = out->stride[3];
+  a.splits = rot_splits(B * H, k.S, cus);
+  a.chunk = cdiv(k.S, a.splits);
+  const dim3 grid((unsigned)a.splits, (unsigned)(B * H));
+  const int nt = (int)cdiv(Dk, 16);
+  hipStream_t s = (hipStream_t)stream;
+  const hipError_t e = keys->dtype == RK_F16 ? launch_rot_nt<rk::F16>(nt, false, a, vec, grid, s)
+                                             : launch_rot_nt<rk::BF16>(nt, false, a, vec, grid, s);
+  return e == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+extern "C" int rk_channel_scores_check(const rk_tensor* keys, const rk_tensor* R_full,
+                                       const rk_tensor* scores_out, int32_t num_cus,
+                                       size_t* workspace_bytes) {
+  KeyView k;
+  bool vec;
+  int st = key_view(keys, &k, &vec);
+  if (st) return st;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  int64_t Dk = 0;
+  if ((st = check_rotation(R_full, B, H, &Dk))) return st;
+  if (scores_out && (st = check_f32_out(scores_out, 3, B, H, Dk, RK_F64))) return st;
+  const int cus = resolve_cus(num_cus, &st);
+  if (st) return st;
+  if (workspace_bytes)
+    *workspace_bytes = align256((size_t)B * H * rot_splits(B * H, k.S, cus) * 128 * sizeof(float));
+  return RK_OK;
+}
+
+extern "C" int rk_channel_scores(const rk_tensor* keys, const rk_tensor* R_full, const rk_tensor* scores_out,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  KeyView k;
+  bool vec;
+  int st = key_view(keys, &k, &vec);
+  if (st) return st;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  int64_t Dk = 0;
+  if ((st = check_rotation(R_full, B, H, &Dk))) return st;
+  if (!scores_out) return RK_ERR_NULL;
+  if ((st = check_f32_out(scores_out, 3, B, H, Dk, RK_F64))) return st;
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  RotArgs a;
+  memset(&a, 0, sizeof(a));
+  fill_rot(a, k, R_full, Dk);
+  a.splits = rot_splits(B * H, k.S, cus);
+  a.chunk = cdiv(k.S > 0 ? k.S : 1, a.splits);
+  const size_t need = align256((size_t)B * H * a.splits * 128 * sizeof(float));
+  if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < need) return RK_ERR_WORKSPACE;
+  if (B * H == 0) return RK_OK;
+  if ((k.S > 0 && !k.data) || !R_full->data || !scores_out->data) return RK_ERR_NULL;
+  a.spart = (float*)workspace;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)a.splits, (unsigned)(B * H));
+  hipError_t e = keys->dtype == RK_F16 ? launch_rot_nt<rk::F16>(8, true, a, vec, grid, s)
+                                       : launch_rot_nt<rk::BF16>(8, true, a, vec, grid, s);
+  if (e != hipSuccess) return RK_ERR_HIP;
+  hipLaunchKernelGGL(scorefin_kernel, dim3((unsigned)(B * H)), dim3(128), 0, s, a.spart, a.splits, 128,
+                     (int)Dk, k.S, (double*)scores_out->data, scores_out->stride[0], scores_out->stride[1],
+                     scores_out->stride[2], k.H);
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+extern "C" int rk_topk_channels(const rk_tensor* scores, int64_t k, const rk_tensor* idx_out,
+                                const rk_tensor* mask_out, void* stream) {
+  int st = rk::check_desc(scores, 3);
+  if (st) return st;
+  if (scores->dtype != RK_F64) return RK_ERR_DTYPE;
+  const int64_t B = scores->shape[0], H = scores->shape[1], D = scores->shape[2];
+  if (D < 1 || D > 128) return RK_ERR_SHAPE;
+  if (k < 0 || k > D) return RK_ERR_KEEP_DIM;
+  if (!idx_out) return RK_ERR_NULL;
+  if ((st = rk::check_desc(idx_out, 3))) return st;
+  if (idx_out->dtype != RK_I64) return RK_ERR_DTYPE;
+  if (idx_out->shape[0] != B || idx_out->shape[1] != H || idx_out->shape[2] != k) return RK_ERR_SHAPE;
+  if (mask_out) {
+    if ((st = rk::check_desc(mask_out, 3))) return st;
+    if (mask_out->dtype != RK_U8) return RK_ERR_DTYPE;
+    if (mask_out->shape[0] != B || mask_out->shape[1] != H || mask_out->shape[2] != D) return RK_ERR_SHAPE;
+  }
+  if (B * H == 0) return RK_OK;
+  if (!scores->data || (k > 0 && !idx_out->data) || (mask_out && !mask_out->data)) return RK_ERR_NULL;
+  if (B * H > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
+  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)(B * H)), dim3(128), 0, (hipStream_t)stream,
+                     (const double*)scores->data, scores->stride[0], scores->stride[1], scores->stride[2],
+                     (int)D, (int)k, (int)H, (int64_t*)idx_out->data, idx_out->stride[0], idx_out->stride[1],
+                     idx_out->stride[2], mask_out ? (uint8_t*)mask_out->data : nullptr,
+                     mask_out ? mask_out->stride[0] : 0, mask_out ? mask_out->stride[1] : 0,
+                     mask_out ? mask_out->stride[2] : 0);
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+extern "C" int rk_gather_rotation(const rk_tensor* R_full, const rk_tensor* idx, const rk_tensor* mean,
+                                  const rk_tensor* R_out, const rk_tensor* delta_mu_out, void* stream) {
+  int st = rk::check_desc(R_full, 4);
+  if (st) return st;
+  if (!rk::is_float_param(R_full->dtype)) return RK_ERR_DTYPE;
+  const int64_t B = R_full->shape[0], H = R_full->shape[1];
+  if (R_full->shape[2] != 128) return RK_ERR_HEAD_DIM;
+  if (!idx || !mean || !R_out || !delta_mu_out) return RK_ERR_NULL;
+  if ((st = rk::check_desc(idx, 3))) return st;
+  if (idx->dtype != RK_I64) return RK_ERR_DTYPE;
+  const int64_t k = idx->shape[2];
+  if (idx->shape[0] != B || idx->shape[1] != H) return RK_ERR_SHAPE;
+  if (k < 1 || k > 128) return RK_ERR_KEEP_DIM;
+  if ((st = check_f32_out(mean, 3, B, H, 128, RK_F32))) return st;
+  if ((st = rk::check_desc(R_out, 4))) return st;
+  if (!rk::is_half(R_out->dtype)) return RK_ERR_DTYPE;
+  if (R_out->shape[0] != B || R_out->shape[1] != H || R_out->shape[2] != 128 || R_out->shape[3] != k)
+    return RK_ERR_SHAPE;
+  if ((st = check_f32_out(delta_mu_out, 3, B, H, 128, R_out->dtype))) return st;
+  if (B * H == 0) return RK_OK;
+  if (!R_full->data || !idx->data || !mean->data || !R_out->data || !delta_mu_out->data) return RK_ERR_NULL;
+  if (B * H > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
+  hipStream_t s = (hipStream_t)stream;
+  auto go = [&](auto tt) {
+    using TT = decltype(tt);
+    hipLaunchKernelGGL((gather_kernel<TT>), dim3((unsigned)(B * H)), dim3(128), 0, s, R_full->data,
+                       (int)R_full->dtype, R_full->stride[0], R_full->stride[1], R_full->stride[2],
+                       R_full->stride[3], (const int64_t*)idx->data, idx->stride[0], idx->stride[1],
+                       idx->stride[2], (int)k, (const float*)mean->data, mean->stride[0], mean->stride[1],
+                       mean->stride[2], (uint16_t*)R_out->data, R_out->stride[0], R_out->stride[1],
+                       R_out->stride[2], R_out->stride[3], (uint16_t*)delta_mu_out->data,
+                       delta_mu_out->stride[0], delta_mu_out->stride[1], delta_mu_out->stride[2], (int)H);
+  };
+  if (R_out->dtype == RK_F16)
+    go(rk::F16{});
+  else
+    go(rk::BF16{});
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+}

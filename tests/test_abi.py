@@ -165,3 +165,50 @@ def test_plan_covers_every_token(shape, policy):
             assert ch % 128 == 0 and wg * ch >= S and (wg - 1) * ch < S
     assert p["wg_vis"] + p["wg_full"] >= 1
     assert p["grid"] == p["units"] * (p["wg_vis"] + p["wg_full"])
+
+
+# ----------------------------------------------------------------- prefill ABI
+def _cov_check(shape=(2, 4, 300, 128), dtype=_lib.RK_BF16, cov_shape=None, mean_shape=None):
+    lib = _lib.load()
+    k = _t(shape, dtype)
+    B, H = shape[:2]
+    c = _t(cov_shape or (B, H, 128, 128), _lib.RK_F32)
+    m = _t(mean_shape or (B, H, 128), _lib.RK_F32)
+    need = ctypes.c_size_t(0)
+    st = lib.rk_key_covariance_check(ctypes.byref(k), ctypes.byref(m), ctypes.byref(c), 256, ctypes.byref(need))
+    return st, need.value
+
+
+def test_covariance_check():
+    st, need = _cov_check()
+    assert st == 0 and need > 0
+    assert _cov_check(shape=(2, 4, 300, 64))[0] == -6
+    assert _cov_check(dtype=_lib.RK_F32)[0] == -3
+    assert _cov_check(cov_shape=(2, 4, 128, 64))[0] == -4
+    assert _cov_check(mean_shape=(2, 3, 128))[0] == -4
+
+
+def test_rotate_and_select_validation():
+    lib = _lib.load()
+    k = _t((1, 2, 50, 128), _lib.RK_F16)
+    R = _t((1, 2, 128, 32), _lib.RK_F16)
+    out_bad = _t((1, 2, 50, 16), _lib.RK_F16)
+    assert lib.rk_rotate_keys(ctypes.byref(k), ctypes.byref(R), ctypes.byref(out_bad), None) == -4
+    out_dt = _t((1, 2, 50, 32), _lib.RK_BF16)
+    assert lib.rk_rotate_keys(ctypes.byref(k), ctypes.byref(R), ctypes.byref(out_dt), None) == -3
+    sc = _t((1, 2, 128), _lib.RK_F32)
+    idx = _t((1, 2, 32), _lib.RK_I64)
+    assert lib.rk_topk_channels(ctypes.byref(sc), 32, ctypes.byref(idx), None, None) == -3
+    sc = _t((1, 2, 128), _lib.RK_F64)
+    assert lib.rk_topk_channels(ctypes.byref(sc), 129, ctypes.byref(idx), None, None) == -7
+    Rf = _t((1, 2, 128, 128), _lib.RK_F32)
+    mean = _t((1, 2, 128), _lib.RK_F32)
+    Ro = _t((1, 2, 128, 32), _lib.RK_F32)      # output must be 16-bit
+    dm = _t((1, 2, 128), _lib.RK_F32)
+    assert lib.rk_gather_rotation(ctypes.byref(Rf), ctypes.byref(idx), ctypes.byref(mean), ctypes.byref(Ro),
+                                  ctypes.byref(dm), None) == -3
+    need = ctypes.c_size_t(0)
+    scores = _t((1, 2, 128), _lib.RK_F64)
+    assert lib.rk_channel_scores_check(ctypes.byref(k), ctypes.byref(Rf), ctypes.byref(scores), 256,
+                                       ctypes.byref(need)) == 0
+    assert need.value > 0
