@@ -130,6 +130,34 @@ int rk_rotatek_decode(const rk_tensor* q_full, const rk_tensor* R_partial,
                       int32_t policy, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* Variable-length variant for a preallocated span cache (no reference
+ * counterpart: the reference re-concatenates the spans every decode step,
+ * cache_utils.py:52-53, llama_visionzip.py:207-208).
+ *   k_full    [B,H_kv,C,128]   prompt then text Keys, capacity C rows.
+ *   v_buf     [B,H_kv,C+v_gap,128]  Values; logical prompt/text row t lives
+ *             at row t + (t >= v_gap_at ? v_gap : 0), so the cache's
+ *             [prompt | visual | text] Value buffer is passed whole with
+ *             v_gap_at = S_prompt and v_gap = S_visual (v_gap 0: plain).
+ *   mask_full [B,C] or NULL;  v_sparse usually a view of v_buf's visual rows.
+ *   len_full  device int32 [B]: only rows t < len_full[b] are attended.
+ * Shapes fixed by capacity, so one captured HIP graph replays across
+ * growing decode steps. */
+int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor* R_partial,
+                             const rk_tensor* delta_mu, const rk_tensor* k_full,
+                             const rk_tensor* v_buf, int64_t v_gap_at, int64_t v_gap,
+                             const rk_tensor* mask_full, const rk_tensor* k_sparse,
+                             const rk_tensor* v_sparse, int64_t num_kv_groups,
+                             const int32_t* len_full, const rk_tensor* out, int32_t policy,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* In-place decode append for the span cache (replaces the per-step
+ * torch.cat of cache_utils.py:52-53): k_new/v_new [B,H,1,128] are written
+ * to slot len_full[b] of k_buf/v_buf [B,H,capacity,128] and len_full[b] is
+ * incremented on the device (a full buffer is left unchanged).  v_new and
+ * v_buf may both be NULL. */
+int rk_append_kv(const rk_tensor* k_new, const rk_tensor* v_new, const rk_tensor* k_buf,
+                 const rk_tensor* v_buf, int32_t* len_full, void* stream);
+
 /* Dense (full-channel) decode, the baseline the RotateK speed-up is measured
  * against (full_channel_flash_decoding.py:162-229, gqa_decode.py:254-277):
  * q [B,H_q,D], k/v [B,H_kv,S,D], out [B,H_q,D]. */

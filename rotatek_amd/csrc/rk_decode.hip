@@ -49,6 +49,10 @@ struct DecodeArgs {
   const uint16_t* kf;
   const uint16_t* vf;
   const uint8_t* mask;
+  const int32_t* len_full;  // optional per-batch valid prompt/text length (device)
+  // Prompt/text V rows at or past vf_gap_at live vf_gap rows further on (the
+  // visual span sits between them in the span cache); UINT32_MAX = no gap.
+  uint32_t vf_gap_at, vf_gap;
   const uint16_t* ks;
   const uint16_t* vs;
   uint16_t* out;
@@ -459,8 +463,9 @@ decode_kernel(const DecodeArgs a) {
   } else {
     // ---- prompt + text span: full-width Keys
     const int64_t t_begin = (int64_t)xf * a.chunk_full;
-    const int64_t t_end = min(a.S_f, t_begin + a.chunk_full);
-    const uint32_t t_last = (uint32_t)max((int64_t)0, t_end - 1);
+    const int64_t s_f = a.len_full ? min(a.S_f, (int64_t)max(a.len_full[b], 0)) : a.S_f;
+    const int64_t t_end = max(t_begin, min(s_f, t_begin + a.chunk_full));
+    const uint32_t t_last = (uint32_t)max(t_begin, t_end - 1);
     const uint16_t* kfb = a.kf + b * a.kf_sb + kv * a.kf_sh;
     const uint16_t* vfb = a.vf + b * a.vf_sb + kv * a.vf_sh;
     const uint32_t vch = 8u * n;
@@ -474,8 +479,11 @@ decode_kernel(const DecodeArgs a) {
         B.k[1][kb] = load_row8<VEC>(kfb, r1, (uint32_t)(kb * 32 + 8 * g), a.kf_sd, 8);
       }
 #pragma unroll
-      for (int r = 0; r < 8; ++r)
-        B.v[r] = load_row8<VEC>(vfb, min(t0 + 8u * g + r, t_last) * a.vf_ss, vch, a.vf_sd, 8);
+      for (int r = 0; r < 8; ++r) {
+        uint32_t row = min(t0 + 8u * g + r, t_last);
+        row += row >= a.vf_gap_at ? a.vf_gap : 0u;
+        B.v[r] = load_row8<VEC>(vfb, row * a.vf_ss, vch, a.vf_sd, 8);
+      }
     };
 
     load_q();
@@ -825,7 +833,8 @@ bool set_head(const rk_tensor* t, int64_t& sb, int64_t& sh, uint32_t& ss, uint32
 int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
                const rk_tensor* kf, const rk_tensor* vf, const rk_tensor* mask,
                const rk_tensor* ks, const rk_tensor* vs, const rk_tensor* out, int32_t policy,
-               void* ws, size_t ws_bytes, void* stream, bool has_vis) {
+               void* ws, size_t ws_bytes, void* stream, bool has_vis,
+               const int32_t* len_full = nullptr, int64_t v_gap_at = -1, int64_t v_gap = 0) {
   int st = RK_OK;
   const int cus = resolve_cus(0, &st);
   if (st) return st;
@@ -889,6 +898,9 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     dkb = c.Dk <= 32 ? 1 : c.Dk <= 64 ? 2 : 4;
   }
   a.S_f = c.S_f;
+  a.len_full = len_full;
+  a.vf_gap_at = v_gap_at < 0 ? UINT32_MAX : (uint32_t)v_gap_at;
+  a.vf_gap = (uint32_t)v_gap;
   a.chunk_vis = p.chunk_vis;
   a.chunk_full = p.chunk_full;
   a.G = (int32_t)c.G;
@@ -943,6 +955,94 @@ extern "C" int rk_rotatek_decode(const rk_tensor* q_full, const rk_tensor* R_par
   if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
   return run_decode(c, q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse,
                     out, policy, workspace, workspace_bytes, stream, true);
+}
+
+extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor* R_partial,
+                                        const rk_tensor* delta_mu, const rk_tensor* k_full,
+                                        const rk_tensor* v_buf, int64_t v_gap_at, int64_t v_gap,
+                                        const rk_tensor* mask_full, const rk_tensor* k_sparse,
+                                        const rk_tensor* v_sparse, int64_t num_kv_groups,
+                                        const int32_t* len_full, const rk_tensor* out,
+                                        int32_t policy, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  if (!k_full || !v_buf) return RK_ERR_NULL;
+  int st = rk::check_desc(v_buf, 4);
+  if (st) return st;
+  if ((st = rk::check_desc(k_full, 4))) return st;
+  const int64_t S_f = k_full->shape[2];
+  if (v_gap < 0 || v_gap_at < 0 || v_gap_at > S_f || v_gap >= (INT64_C(1) << 31)) return RK_ERR_ARG;
+  if (v_buf->shape[2] != S_f + v_gap) return RK_ERR_SHAPE;
+  rk_tensor v_logical = *v_buf;  // prompt/text rows only, for the shape checks
+  v_logical.shape[2] = S_f;
+  Checked c;
+  st = check_rotatek(q_full, R_partial, delta_mu, k_full, &v_logical, mask_full, k_sparse, v_sparse,
+                     num_kv_groups, &c);
+  if (st) return st;
+  if (!out || !len_full) return RK_ERR_NULL;
+  if ((st = check_out(out, c))) return st;
+  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
+  return run_decode(c, q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse,
+                    out, policy, workspace, workspace_bytes, stream, true, len_full,
+                    v_gap > 0 ? v_gap_at : -1, v_gap);
+}
+
+namespace {
+
+// One workgroup per batch row: copy the new token's K (and V) of every head
+// into slot len[b] of the span buffers, then advance len[b].  A full buffer
+// (len[b] >= capacity) is left untouched.
+__global__ void __launch_bounds__(256) append_kernel(const uint16_t* kn, int64_t kn_b, int64_t kn_h,
+                                                     int64_t kn_d, const uint16_t* vn, int64_t vn_b,
+                                                     int64_t vn_h, int64_t vn_d, uint16_t* kb,
+                                                     int64_t kb_b, int64_t kb_h, int64_t kb_s,
+                                                     int64_t kb_d, uint16_t* vb, int64_t vb_b,
+                                                     int64_t vb_h, int64_t vb_s, int64_t vb_d,
+                                                     int32_t* len, int H, int64_t cap) {
+  const int b = blockIdx.x;
+  const int32_t pos = len[b];
+  __syncthreads();
+  if (pos >= 0 && pos < cap) {
+    for (int i = threadIdx.x; i < H * 128; i += blockDim.x) {
+      const int h = i >> 7, d = i & 127;
+      kb[b * kb_b + h * kb_h + pos * kb_s + d * kb_d] = kn[b * kn_b + h * kn_h + d * kn_d];
+      if (vn) vb[b * vb_b + h * vb_h + pos * vb_s + d * vb_d] = vn[b * vn_b + h * vn_h + d * vn_d];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) len[b] = pos + 1;
+  }
+}
+
+}  // namespace
+
+extern "C" int rk_append_kv(const rk_tensor* k_new, const rk_tensor* v_new, const rk_tensor* k_buf,
+                            const rk_tensor* v_buf, int32_t* len_full, void* stream) {
+  if (!k_new || !k_buf || !len_full) return RK_ERR_NULL;
+  int st = rk::check_desc(k_new, 4);
+  if (st) return st;
+  if ((st = rk::check_desc(k_buf, 4))) return st;
+  if (!rk::is_half(k_new->dtype) || k_buf->dtype != k_new->dtype) return RK_ERR_DTYPE;
+  const int64_t B = k_new->shape[0], H = k_new->shape[1];
+  if (k_new->shape[2] != 1 || k_new->shape[3] != 128) return RK_ERR_SHAPE;
+  if (k_buf->shape[0] != B || k_buf->shape[1] != H || k_buf->shape[3] != 128) return RK_ERR_SHAPE;
+  if ((v_new == nullptr) != (v_buf == nullptr)) return RK_ERR_NULL;
+  if (v_new) {
+    if ((st = rk::check_desc(v_new, 4)) || (st = rk::check_desc(v_buf, 4))) return st;
+    if (v_new->dtype != k_new->dtype || v_buf->dtype != k_new->dtype) return RK_ERR_DTYPE;
+    for (int i = 0; i < 4; ++i)
+      if (v_new->shape[i] != k_new->shape[i] || v_buf->shape[i] != k_buf->shape[i]) return RK_ERR_SHAPE;
+  }
+  if (B == 0 || H == 0) return RK_OK;
+  if (!k_new->data || !k_buf->data || (v_new && (!v_new->data || !v_buf->data))) return RK_ERR_NULL;
+  if (B > (INT64_C(1) << 30) || H * 128 > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
+  hipLaunchKernelGGL(append_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)k_new->data, k_new->stride[0], k_new->stride[1], k_new->stride[3],
+                     v_new ? (const uint16_t*)v_new->data : nullptr, v_new ? v_new->stride[0] : 0,
+                     v_new ? v_new->stride[1] : 0, v_new ? v_new->stride[3] : 0, (uint16_t*)k_buf->data,
+                     k_buf->stride[0], k_buf->stride[1], k_buf->stride[2], k_buf->stride[3],
+                     v_buf ? (uint16_t*)v_buf->data : nullptr, v_buf ? v_buf->stride[0] : 0,
+                     v_buf ? v_buf->stride[1] : 0, v_buf ? v_buf->stride[2] : 0, v_buf ? v_buf->stride[3] : 0,
+                     len_full, (int)H, k_buf->shape[2]);
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 
 namespace {

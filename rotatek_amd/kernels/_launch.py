@@ -58,3 +58,54 @@ def full_channel_decode(q, k, v, num_kv_groups: int, policy: int) -> torch.Tenso
                                           ws.numel(), _lib.stream_handle(q.device)),
                "full_channel_decode")
     return out
+
+
+def rotatek_decode_varlen(q_full, R_partial, delta_mu, k_full, v_buf, v_gap_at: int, v_gap: int,
+                          mask_full, k_sparse, v_sparse, num_kv_groups: int, len_full: torch.Tensor,
+                          policy: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """RotateK decode over capacity-sized span buffers (rk_rotatek_decode_varlen).
+
+    ``k_full [B,H_kv,C,D]`` holds prompt then text Keys; ``v_buf`` holds the
+    Values with the visual span between prompt and text (logical row ``t``
+    at ``t + v_gap`` once ``t >= v_gap_at``); only rows ``t < len_full[b]``
+    (device int32) are attended.  Shapes stay fixed as the cache grows, so
+    the launch can be captured once and replayed every decode step.
+    """
+    _require_gpu(q_full, "q_full")
+    if len_full.dtype != torch.int32 or not len_full.is_cuda or len_full.dim() != 1 \
+            or len_full.shape[0] != q_full.shape[0] or not len_full.is_contiguous():
+        raise ValueError("len_full must be a contiguous device int32 tensor [B]")
+    lib = _lib.load()
+    S_f = k_full.shape[2]
+    d = [_lib.desc(t) for t in (q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse)]
+    if out is None:
+        out = torch.empty(q_full.shape, dtype=q_full.dtype, device=q_full.device)
+    do = _lib.desc(out)
+    # workspace size: the plan depends only on the capacity-sized shapes
+    dv = _lib.desc(v_buf.narrow(2, 0, min(S_f, v_buf.shape[2])))
+    need = ctypes.c_size_t(0)
+    _lib.check(lib.rk_rotatek_decode_check(*[_lib.ref(x) for x in d[:4]], ctypes.byref(dv),
+                                           *[_lib.ref(x) for x in d[5:]], int(num_kv_groups),
+                                           ctypes.byref(do), policy, 0, ctypes.byref(need)),
+               "rotatek_decode_varlen")
+    ws = _lib.workspace(q_full.device, need.value)
+    _lib.check(lib.rk_rotatek_decode_varlen(*[_lib.ref(x) for x in d[:5]], int(v_gap_at), int(v_gap),
+                                            *[_lib.ref(x) for x in d[5:]], int(num_kv_groups),
+                                            len_full.data_ptr(), ctypes.byref(do), policy, ws.data_ptr(),
+                                            ws.numel(), _lib.stream_handle(q_full.device)),
+               "rotatek_decode_varlen")
+    return out
+
+
+def append_kv(k_new, v_new, k_buf, v_buf, len_full: torch.Tensor) -> None:
+    """Write one token's K/V [B,H,1,D] at row ``len_full[b]`` of the span
+    buffers and advance ``len_full`` on the device (rk_append_kv)."""
+    _require_gpu(k_buf, "k_buf")
+    if len_full.dtype != torch.int32 or not len_full.is_cuda or not len_full.is_contiguous():
+        raise ValueError("len_full must be a contiguous device int32 tensor [B]")
+    if len_full.numel() != k_buf.shape[0]:
+        raise ValueError("len_full must hold one length per batch row")
+    d = [_lib.desc(t) for t in (k_new, v_new, k_buf, v_buf)]
+    _lib.check(_lib.load().rk_append_kv(*[_lib.ref(x) for x in d], len_full.data_ptr(),
+                                        _lib.stream_handle(k_buf.device)),
+               "append_kv")

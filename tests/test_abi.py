@@ -212,3 +212,42 @@ def test_rotate_and_select_validation():
     assert lib.rk_channel_scores_check(ctypes.byref(k), ctypes.byref(Rf), ctypes.byref(scores), 256,
                                        ctypes.byref(need)) == 0
     assert need.value > 0
+
+
+# ------------------------------------------------------------- span cache ABI
+def _varlen(S_cap=40, gap_at=10, gap=100, v_rows=None, lens=1, B=2, Hq=8, Hkv=4):
+    lib = _lib.load()
+    q, R, dm = _t((B, Hq, 128)), _t((B, Hkv, 128, 32)), _t((B, Hkv, 128))
+    kf = _t((B, Hkv, S_cap, 128))
+    vb = _t((B, Hkv, S_cap + gap if v_rows is None else v_rows, 128))
+    ks, vs, o = _t((B, Hkv, gap, 32)), _t((B, Hkv, gap, 128)), _t((B, Hq, 128))
+    return lib.rk_rotatek_decode_varlen(ctypes.byref(q), ctypes.byref(R), ctypes.byref(dm), ctypes.byref(kf),
+                                        ctypes.byref(vb), gap_at, gap, None, ctypes.byref(ks),
+                                        ctypes.byref(vs), Hq // Hkv, lens, ctypes.byref(o), 1, None, 0, None)
+
+
+def test_varlen_decode_validation():
+    # argument errors come back before any device query
+    assert _varlen(v_rows=139) == -4               # V rows != capacity + gap
+    assert _varlen(gap_at=41) == -10               # gap start past the capacity
+    assert _varlen(gap=-1, v_rows=39) == -10
+    assert _varlen(lens=None) == -1                # device lengths required
+    # well-formed, no device / no workspace
+    assert _varlen() in (-9, -12)
+
+
+def test_append_kv_validation():
+    lib = _lib.load()
+    kn, vn = _t((2, 4, 1, 128)), _t((2, 4, 1, 128))
+    kb, vb = _t((2, 4, 64, 128)), _t((2, 4, 64, 128))
+    r = ctypes.byref
+    assert lib.rk_append_kv(r(kn), r(vn), r(kb), r(vb), None, None) == -1
+    two = _t((2, 4, 2, 128))
+    assert lib.rk_append_kv(r(two), r(vn), r(kb), r(vb), 1, None) == -4       # more than one token
+    vb_short = _t((2, 4, 63, 128))
+    assert lib.rk_append_kv(r(kn), r(vn), r(kb), r(vb_short), 1, None) == -4
+    kb_bf = _t((2, 4, 64, 128), _lib.RK_BF16)
+    assert lib.rk_append_kv(r(kn), r(vn), r(kb_bf), r(vb), 1, None) == -3
+    assert lib.rk_append_kv(r(kn), None, r(kb), r(vb), 1, None) == -1          # V given for one side only
+    empty_k, empty_b = _t((0, 4, 1, 128)), _t((0, 4, 64, 128))
+    assert lib.rk_append_kv(r(empty_k), None, r(empty_b), None, 1, None) == 0   # nothing to do
