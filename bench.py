@@ -5,8 +5,8 @@ Workload: one decode step at batch 32, 32 heads (MHA),
 head_dim 128, fp16; visual span 14,000 tokens stored rotated and truncated to
 32 of 128 channels, plus 2,000 full-width text tokens; synthetic seeded
 inputs (no checkpoints offline).  A "step" is one call of
-``rotatek_decode`` (a single fused HIP launch) with every input resident in
-HBM.
+``rotatek_decode`` (two HIP launches on the current stream: the split-K
+decode kernel, then the merge kernel) with every input resident in HBM.
 
 Printed JSON line (rank 0): ``value`` = microseconds per decode step (eager,
 wall clock over exactly ``--steps`` steps between device synchronisations);
@@ -15,6 +15,12 @@ events around each launch on the launching stream) against the 8 TB/s HBM
 peak; ``cpu_baseline`` = the CPU oracle (numpy fp32) on a bounded sample of
 the same workload, scaled to a full step.  Also reported: hipGraph-replayed
 step time and the full-channel HIP baseline on the same seeded data.
+
+``--copy-calibration BYTES`` adds a plain device-to-device copy of BYTES
+bytes per step (after the timed region), so that a ``rocprofv3 --pmc
+FETCH_SIZE`` / ``WRITE_SIZE`` pass over this script sees a kernel of known
+traffic next to the decode kernel; ``roofline.traffic`` is read from the
+committed summary of those passes (profiles/traffic_<config>.json).
 """
 from __future__ import annotations
 
@@ -133,6 +139,52 @@ def _traffic(cfg_name):
         return json.load(f).get("hbm_bytes_per_launch")
 
 
+def _pmc_rows(path):
+    import csv
+    with open(path) as f:
+        rows = list(csv.DictReader(f))
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    return rows
+
+
+def pmc_summary(fetch_csv, write_csv, calib_bytes, calib_copies, cfg_name):
+    """Turn two ``rocprofv3 --pmc`` passes over ``bench.py --copy-calibration``
+    (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch) into HBM bytes per
+    launch of the decode and merge kernels.  Each counter is scaled by what
+    it reads for the calibration copies (the last ``calib_copies``
+    dispatches of the run, ``calib_bytes`` read and written each)."""
+    from rotatek_amd import synth
+    out = {"config": cfg_name, "calibration_bytes": calib_bytes}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        rows = [r for r in _pmc_rows(path) if r["Counter_Name"] == counter]
+        calib = rows[-calib_copies:]
+        kib = sum(float(r["Counter_Value"]) for r in calib) / len(calib)
+        factor = kib * 1024.0 / calib_bytes
+        out[counter] = {"calibration_kernel": calib[0]["Kernel_Name"][:60],
+                        "calibration_kib": round(kib, 1), "factor": round(factor, 4), "kernels": {}}
+        for tag in ("rk::decode_kernel", "rk::merge_kernel"):
+            sel = [float(r["Counter_Value"]) for r in rows if tag in r["Kernel_Name"]]
+            if sel:
+                avg = sum(sel) / len(sel)
+                out[counter]["kernels"][tag] = {"dispatches": len(sel), "kib": round(avg, 1),
+                                                "bytes": round(avg * 1024.0 / factor)}
+    dk = "rk::decode_kernel"
+    rd = out["FETCH_SIZE"]["kernels"][dk]["bytes"]
+    wr = out["WRITE_SIZE"]["kernels"][dk]["bytes"]
+    cfg = synth.CONFIGS[cfg_name]
+    alg = synth.decode_bytes(cfg)
+    out["hbm_bytes_per_launch"] = rd + wr
+    out["decode_kernel_read_bytes"] = rd
+    out["decode_kernel_write_bytes"] = wr
+    out["algorithmic_bytes_per_step"] = alg
+    out["traffic_over_algorithmic"] = round((rd + wr) / alg, 4)
+    path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+        f.write("\n")
+    print(json.dumps(out, indent=1))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,7 +194,14 @@ def main():
     ap.add_argument("--family", default="paper", choices=["paper", "gqa"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc passes (no GPU needed)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.copy_calibration, args.steps, args.config)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the RotateK decode "
               "shards by (batch, KV head) with no exchange, so N GPUs run N independent copies.",
@@ -173,10 +232,10 @@ def main():
     _log("[bench] warmup done")
     us = _time_wall(step, args.steps)
     us_launch = _time_launches(step, args.steps)
-    us_graph = _time_graph(step, args.steps, args.warmup)
+    us_graph = _time_graph(step, args.steps, args.warmup) if not args.no_graph else None
     nbytes = synth.decode_bytes(cfg)
     gbps = nbytes / (us_launch * 1e-6) / 1e9
-    _log(f"[bench] rotatek eager {us:.1f} us/step, per-launch {us_launch:.1f} us, graph {us_graph:.1f} us, "
+    _log(f"[bench] rotatek eager {us:.1f} us/step, per-launch {us_launch:.1f} us, graph {us_graph} us, "
          f"{gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS * 100:.1f}% of peak)")
 
     extra = {}
@@ -190,17 +249,26 @@ def main():
             dstep()
         d_us = _time_wall(dstep, args.steps)
         d_launch = _time_launches(dstep, args.steps)
-        d_graph = _time_graph(dstep, args.steps, args.warmup)
+        d_graph = _time_graph(dstep, args.steps, args.warmup) if not args.no_graph else None
         dbytes = synth.decode_bytes(cfg, dense=True)
         extra = {
             "dense_us_per_step": round(d_us, 2),
             "dense_graph_us_per_step": round(d_graph, 2),
             "dense_achieved_gbps": round(dbytes / (d_launch * 1e-6) / 1e9, 1),
             "speedup_vs_dense": round(d_us / us, 3),
-            "speedup_vs_dense_graph": round(d_graph / us_graph, 3),
+            "speedup_vs_dense_graph": round(d_graph / us_graph, 3) if d_graph else None,
         }
-        _log(f"[bench] dense eager {d_us:.1f} us/step, graph {d_graph:.1f} us -> speedup "
-             f"{d_us / us:.2f}x eager, {d_graph / us_graph:.2f}x graph")
+        _log(f"[bench] dense eager {d_us:.1f} us/step, graph {d_graph} us -> speedup {d_us / us:.2f}x eager")
+
+    if args.copy_calibration > 0:
+        n = args.copy_calibration
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(max(args.steps, 1)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        _log(f"[bench] copy calibration: {args.steps} copies of {n} bytes")
+        del src, dst
 
     cpu = None
     if not args.no_cpu:
@@ -230,7 +298,7 @@ def main():
         },
         "achieved_gbps": round(gbps, 1),
         "pct_of_peak_hbm": round(gbps / HBM_PEAK_GBPS * 100, 2),
-        "graph_us_per_step": round(us_graph, 2),
+        "graph_us_per_step": round(us_graph, 2) if us_graph else None,
         "launch_us": round(us_launch, 2),
         "roofline": {
             "bound": "hbm",
