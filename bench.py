@@ -185,6 +185,93 @@ def pmc_summary(fetch_csv, write_csv, calib_bytes, calib_copies, cfg_name):
     print(json.dumps(out, indent=1))
 
 
+def run_flow(args):
+    """Config 4: per (visual length, keep) point, prefill a 28-layer stack
+    (HIP covariance -> eigh -> head-wise channel top-k -> truncated Key
+    write into the span cache), then time ``--steps`` decode steps, each one
+    replay of a HIP graph that appends a token and runs the RotateK decode
+    for every layer."""
+    import torch
+
+    from rotatek_amd import synth
+    from rotatek_amd.cache import DynamicCache
+    from rotatek_amd.pruning import ChannelPruner
+
+    from rotatek_amd._lib import RK_POLICY_GQA, RK_POLICY_PAPER
+
+    c = synth.FLOW
+    steps = args.steps if args.steps_given else c.steps
+    # a GQA stack (G = 7): the gqa family shares each K/V tile across the
+    # query heads of its group; ``--family paper`` re-reads it per query head
+    family = args.family if args.family_given else "gqa"
+    policy = RK_POLICY_GQA if family == "gqa" else RK_POLICY_PAPER
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    sweep = []
+    for S_v in c.visual:
+        for keep in c.keep:
+            pruner = ChannelPruner(synth.KEEP_TO_RATIO[keep], c.prompt, c.text, solver="eigh", select="score",
+                                   query_aware=True)
+            cache = DynamicCache(reserve_tokens=steps + 1)
+            pre_ms = []
+            for layer in range(c.layers):
+                st = synth.make_flow_layer(c, S_v, seed=1000 * S_v + layer, device=dev)
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                kept, kp, kt, mask, v = pruner.update_rotatek(st["K"], st["Q"], st["V"], None, c.G)
+                cache.store_pruned(kept, kp, kt, mask, v, layer)
+                cache.rotatek_rotations.append(pruner.current_rotatek_R_partial)
+                cache.rotatek_means.append(pruner.current_rotatek_delta_mu)
+                torch.cuda.synchronize()
+                pre_ms.append((time.perf_counter() - t0) * 1e3)
+                del st, kept, kp, kt, v
+            g = torch.Generator(device=dev).manual_seed(S_v + keep)
+            q = torch.randn(c.layers, c.B, c.H_q, c.D, generator=g, device=dev).to(c.dtype)
+            kn = torch.randn(c.layers, c.B, c.H_kv, 1, c.D, generator=g, device=dev).to(c.dtype)
+            vn = torch.randn(c.layers, c.B, c.H_kv, 1, c.D, generator=g, device=dev).to(c.dtype)
+            out = torch.empty(c.layers, c.B, c.H_q, c.D, device=dev, dtype=c.dtype)
+            lens0 = [cache.lengths(i).clone() for i in range(c.layers)]
+            graph = cache.capture_decode(q, kn, vn, out, c.G, policy=policy)
+            graph.replay()                      # warm-up replay, then rewind the lengths
+            torch.cuda.synchronize()
+            for i in range(c.layers):
+                cache.lengths(i).copy_(lens0[i])
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(steps):
+                graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / steps
+            cache.sync_lengths()
+            want = c.prompt + S_v + c.text + steps
+            if cache.get_seq_length(0) != want or cache.get_seq_length(c.layers - 1) != want:
+                raise RuntimeError(f"cache length {cache.get_seq_length(0)} after {steps} steps, expected {want}")
+            nbytes = sum(synth.flow_step_bytes(c, S_v, keep, c.prompt + c.text + i + 1) for i in range(steps))
+            gbps = nbytes / steps / (us * 1e-6) / 1e9
+            pre = sorted(pre_ms)[len(pre_ms) // 2]
+            _log(f"[flow] S_v={S_v} keep={keep}: prefill {pre:.2f} ms/layer (median), decode {us:.1f} us/step "
+                 f"({c.layers} layers, graph), {gbps:.0f} GB/s")
+            sweep.append({"visual_tokens": S_v, "keep": keep, "prefill_ms_per_layer": round(pre, 3),
+                          "decode_us_per_step": round(us, 2), "decode_gbps": round(gbps, 1),
+                          "decode_pct_of_peak_hbm": round(gbps / HBM_PEAK_GBPS * 100, 2)})
+            del cache, graph, q, kn, vn, out
+            torch.cuda.empty_cache()
+    head = next(r for r in sweep if r["visual_tokens"] == max(c.visual) and r["keep"] == 32)
+    line = {
+        "metric": "config 4 flow: decode us per step over 28 layers (hipGraph replay) + prefill ms per layer",
+        "value": head["decode_us_per_step"], "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": 1,
+        "ms_per_step": round(head["decode_us_per_step"] / 1e3, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: visual Keys 4 Z U^T + 0.5 E (rank 16), N(0,1) elsewhere",
+        "config": {"workload": f"cfg4: {c.layers} layers, B={c.B}, H_q={c.H_q}, H_kv={c.H_kv}, prompt {c.prompt} + "
+                               f"text {c.text} growing, eigh + head-wise top-k, family={family}; value at "
+                               f"S_v={head['visual_tokens']}, keep 32", "family": family, "sweep": sweep},
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +286,14 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc passes (no GPU needed)")
     args = ap.parse_args()
+    args.steps_given = any(a == "--steps" or a.startswith("--steps=") for a in sys.argv[1:])
+    args.family_given = any(a == "--family" or a.startswith("--family=") for a in sys.argv[1:])
+    if args.config == "cfg4":
+        if args.gpus != 1:
+            print("bench.py measures one GPU only", file=sys.stderr)
+            sys.exit(2)
+        run_flow(args)
+        return
     if args.pmc_summary:
         pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.copy_calibration, args.steps, args.config)
         return

@@ -140,15 +140,21 @@ int rk_rotatek_decode(const rk_tensor* q_full, const rk_tensor* R_partial,
  *             v_gap_at = S_prompt and v_gap = S_visual (v_gap 0: plain).
  *   mask_full [B,C] or NULL;  v_sparse usually a view of v_buf's visual rows.
  *   len_full  device int32 [B]: only rows t < len_full[b] are attended.
- * Shapes fixed by capacity, so one captured HIP graph replays across
+ *   k_new, v_new  [B,H_kv,1,128] or both NULL.  If given, the step appends
+ *             them first: the new token is attended, written to row
+ *             len_full[b] of k_full / v_buf, and len_full[b] is incremented
+ *             (all in the same two launches; a row whose buffer is full,
+ *             len_full[b] >= C, neither attends nor stores it).
+ * Shapes are fixed by capacity, so one captured HIP graph replays across
  * growing decode steps. */
 int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor* R_partial,
                              const rk_tensor* delta_mu, const rk_tensor* k_full,
                              const rk_tensor* v_buf, int64_t v_gap_at, int64_t v_gap,
                              const rk_tensor* mask_full, const rk_tensor* k_sparse,
                              const rk_tensor* v_sparse, int64_t num_kv_groups,
-                             const int32_t* len_full, const rk_tensor* out, int32_t policy,
-                             void* workspace, size_t workspace_bytes, void* stream);
+                             const rk_tensor* k_new, const rk_tensor* v_new, int32_t* len_full,
+                             const rk_tensor* out, int32_t policy, void* workspace,
+                             size_t workspace_bytes, void* stream);
 
 /* In-place decode append for the span cache (replaces the per-step
  * torch.cat of cache_utils.py:52-53): k_new/v_new [B,H,1,128] are written

@@ -71,6 +71,18 @@ __device__ __forceinline__ float load_any(const void* p, int64_t idx, int dtype)
   return dtype == 0 ? F16::to_f32(b) : BF16::to_f32(b);
 }
 
+// Split form of load_any for prologues: load_raw issues the load (32 bits
+// for F32, 16 bits otherwise, chosen by a dtype that is uniform across the
+// launch), raw_to_f32 converts later, so the wait for the data can be placed
+// after other loads have been issued.
+__device__ __forceinline__ uint32_t load_raw(const void* p, int64_t idx, int dtype) {
+  return dtype == 2 ? ((const uint32_t*)p)[idx] : (uint32_t)((const uint16_t*)p)[idx];
+}
+__device__ __forceinline__ float raw_to_f32(uint32_t v, int dtype) {
+  return dtype == 2 ? __builtin_bit_cast(float, v)
+                    : (dtype == 0 ? F16::to_f32((uint16_t)v) : BF16::to_f32((uint16_t)v));
+}
+
 // ------------------------------------------------------------ memory
 // Eight 16-bit elements starting at `p` with element stride `sd`; `nvalid`
 // of them (from the front) are read, the rest are zero.  VEC: one 16-byte

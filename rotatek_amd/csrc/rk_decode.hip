@@ -49,10 +49,19 @@ struct DecodeArgs {
   const uint16_t* kf;
   const uint16_t* vf;
   const uint8_t* mask;
-  const int32_t* len_full;  // optional per-batch valid prompt/text length (device)
+  int32_t* len_full;  // optional per-batch valid prompt/text length (device)
   // Prompt/text V rows at or past vf_gap_at live vf_gap rows further on (the
   // visual span sits between them in the span cache); UINT32_MAX = no gap.
   uint32_t vf_gap_at, vf_gap;
+  // Fused append (span cache): the token k_new / v_new [B, H_kv, 128] joins
+  // at row pos[b] = len_full[b] (captured by the split pass into ws_pos),
+  // the merge folds it in, writes it to kf_w / vf_w and advances len_full.
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  uint16_t* kf_w;
+  uint16_t* vf_w;
+  int32_t* ws_pos;
+  int64_t kn_sb, kn_sh, kn_sd, vn_sb, vn_sh, vn_sd;
   const uint16_t* ks;
   const uint16_t* vs;
   uint16_t* out;
@@ -73,6 +82,10 @@ struct DecodeArgs {
   uint32_t kf_ss, kf_sd, vf_ss, vf_sd, ks_ss, ks_sd, vs_ss, vs_sd;
   int32_t G, Dk, hpu, spk, units_per_b, wg_vis, np;
   int32_t r_dtype, dm_dtype, has_bias, has_mask;
+  // prologue layouts: q rows contiguous and 16-byte aligned (one 16-byte load
+  // per thread); R a contiguous, 16-byte aligned [128][Dk] 16-bit block
+  // with Dk <= 64 (staged through LDS with 16-byte loads)
+  int32_t q_vec, r_vec;
   float scale_log2;
 };
 
@@ -224,11 +237,16 @@ struct FullBuf {
 // Final merge of the np partials of one (unit, head) row:
 //   out = sum_p acc_p 2^(m_p - M) / (sum_p l_p 2^(m_p - M) + 1e-6),
 //   M = max_p m_p                                  (fused_decode.py:275-296)
-// computed as an online merge, four partials per step with all their loads
-// issued together.  The calling thread owns channels 8*c8 .. 8*c8+7.
+// One wave per row.  Lane (sl, c8) = (lane >> 4, lane & 15) owns channels
+// 8 c8 .. 8 c8 + 7 and folds partials p = sl, sl + 4, ... (eight partials'
+// loads in flight at a time); the four slices are then combined across
+// lanes.  With a fused append the new token (score q . k_new, value v_new)
+// is folded in last, written to the span buffers once per (b, KV head), and
+// len_full[b] advances.
 template <class TT>
-__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int hq, int h,
-                                          int c8) {
+__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int kv, int hq, int h,
+                                          int lane) {
+  const int sl = lane >> 4, c8 = lane & 15;
   const int64_t base = u * a.np;
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   auto fold = [&](const float* mm, const float* ll, const float4* v0, const float4* v1, int k) {
@@ -246,28 +264,79 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
     }
     M = mx;
   };
-  int p = 0;
-  for (; p + 4 <= a.np; p += 4) {
-    float mm[4], ll[4];
-    float4 v0[4], v1[4];
+  // eight of this slice's partials per batch, loads issued together; entries
+  // past np are clamped in-bounds loads with weight zero (the batch's first
+  // entry is always valid, so its max is finite)
+  for (int p = sl; p < a.np; p += 32) {
+    float mm[8], ll[8];
+    float4 v0[8], v1[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t pi = (base + p + i) * a.hpu + h;
-      mm[i] = a.part_m[pi];
-      ll[i] = a.part_l[pi];
+    for (int i = 0; i < 8; ++i) {
+      const int q = p + 4 * i;
+      const bool ok = q < a.np;
+      const int64_t pi = (base + (ok ? q : a.np - 1)) * a.hpu + h;
       const float4* src = (const float4*)(a.part_acc + pi * 128 + 8 * c8);
-      v0[i] = src[0];
-      v1[i] = src[1];
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f), s0 = src[0], s1 = src[1];
+      mm[i] = ok ? a.part_m[pi] : -INFINITY;
+      ll[i] = ok ? a.part_l[pi] : 0.f;
+      v0[i] = ok ? s0 : z;
+      v1[i] = ok ? s1 : z;
     }
-    fold(mm, ll, v0, v1, 4);
+    fold(mm, ll, v0, v1, 8);
   }
-  for (; p < a.np; ++p) {
-    const int64_t pi = (base + p) * a.hpu + h;
-    const float mm = a.part_m[pi], ll = a.part_l[pi];
-    const float4* src = (const float4*)(a.part_acc + pi * 128 + 8 * c8);
-    const float4 v0 = src[0], v1 = src[1];
-    fold(&mm, &ll, &v0, &v1, 1);
+  // combine the four slices (a slice without partials has M = -inf)
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    const float Mo = shfl_xor(M, off), Lo = shfl_xor(L, off);
+    const float Mx = fmaxf(M, Mo);
+    const float ws = M == -INFINITY ? 0.f : fast_exp2(M - Mx);
+    const float wo = Mo == -INFINITY ? 0.f : fast_exp2(Mo - Mx);
+    L = L * ws + Lo * wo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) A[e] = A[e] * ws + shfl_xor(A[e], off) * wo;
+    M = Mx;
   }
+  if (a.k_new) {
+    const int32_t pos = a.ws_pos[b];
+    if (pos < a.S_f) {
+      const uint16_t* qr = a.q + b * a.q_sb + (int64_t)hq * a.q_sh;
+      const uint16_t* kr = a.k_new + b * a.kn_sb + (int64_t)kv * a.kn_sh;
+      const uint16_t* vr = a.v_new + b * a.vn_sb + (int64_t)kv * a.vn_sh;
+      uint16_t kn[8], vn[8];
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int ch = 8 * c8 + e;
+        kn[e] = kr[ch * a.kn_sd];
+        vn[e] = vr[ch * a.vn_sd];
+        d = fmaf(TT::to_f32(qr[ch * a.q_sd]), TT::to_f32(kn[e]), d);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) d += shfl_xor(d, off);
+      const float sn = d * a.scale_log2;
+      const float Mx = fmaxf(M, sn);
+      const float ws = fast_exp2(M - Mx), wn = fast_exp2(sn - Mx);
+      L = L * ws + wn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) A[e] = A[e] * ws + TT::to_f32(vn[e]) * wn;
+      M = Mx;
+      if (hq == kv * a.G) {  // first query head of the group writes the token once
+        if (sl == 1) {
+          uint16_t* dst = a.kf_w + b * a.kf_sb + (int64_t)kv * a.kf_sh + (int64_t)pos * a.kf_ss;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dst[(int64_t)(8 * c8 + e) * a.kf_sd] = kn[e];
+        } else if (sl == 2) {
+          const uint32_t row = (uint32_t)pos + ((uint32_t)pos >= a.vf_gap_at ? a.vf_gap : 0u);
+          uint16_t* dst = a.vf_w + b * a.vf_sb + (int64_t)kv * a.vf_sh + (int64_t)row * a.vf_ss;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dst[(int64_t)(8 * c8 + e) * a.vf_sd] = vn[e];
+        } else if (sl == 3 && c8 == 0 && hq == 0) {
+          a.len_full[b] = pos + 1;
+        }
+      }
+    }
+  }
+  if (sl != 0) return;
   const float den = L + kDenomEps;
   uint16_t o[8];
 #pragma unroll
@@ -295,6 +364,10 @@ decode_kernel(const DecodeArgs a) {
   __shared__ float s_l[kWaves][HMAX];
   __shared__ float s_acc[kWaves][HMAX][128];
   __shared__ __attribute__((aligned(16))) uint8_t s_valid[kMaskChunk];
+  // raw R [128][Dk] (Dk <= 64, 16 KB): the upper half of s_acc when that is
+  // large enough (its lower half holds the q R partial sums), else its own
+  constexpr int kRawChunks = 1024;
+  __shared__ uint4 s_rsep[HMAX >= 16 ? 1 : kRawChunks];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
@@ -310,6 +383,9 @@ decode_kernel(const DecodeArgs a) {
   const bool is_vis = HAS_VIS && x < a.wg_vis;
   const int xf = HAS_VIS ? x - a.wg_vis : x;
 
+  if (a.k_new && r_in_b == 0 && x == 0 && tid == 0)
+    a.ws_pos[b] = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
+
   float m = kNegInit, l = 0.f;
   f32x4 acc[8];
 #pragma unroll
@@ -323,21 +399,47 @@ decode_kernel(const DecodeArgs a) {
   // for the prologue data, so its latency hides under the first blocks.
   constexpr int kQPer = (HMAX * 128 + kThreads - 1) / kThreads;
   float qv[kQPer];
+  // q rows: unconditional loads from clamped (in-bounds) rows, masked after,
+  // so every load of the prologue is in flight at once
+  // Fast layout: thread t loads channels 8 (t & 15) .. + 7 of head t >> 4
+  // (clamped to a valid head) with one 16-byte load.
+  uint16_t qraw[kQPer];
+  uint4 q16 = make_uint4(0u, 0u, 0u, 0u);
+  // load_q issues the fast-layout load before the first K/V blocks; the
+  // element-wise fallback loads inside store_q, after them.
   auto load_q = [&]() {
-#pragma unroll
-    for (int k = 0; k < kQPer; ++k) {
-      const int i = tid + k * kThreads;
-      const int h = i >> 7, d = i & 127;
-      qv[k] = (i < HMAX * 128 && h < nh)
-                  ? TT::to_f32(a.q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + d * a.q_sd])
-                  : 0.f;
+    if (a.q_vec) {
+      const int h = min(tid >> 4, nh - 1);
+      q16 = *(const uint4*)(a.q + b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + 8 * (tid & 15));
     }
   };
   auto store_q = [&]() {
+    if (!a.q_vec) {
 #pragma unroll
-    for (int k = 0; k < kQPer; ++k) {
-      const int i = tid + k * kThreads;
-      if (i < HMAX * 128) s_q[i >> 7][i & 127] = qv[k];
+      for (int k = 0; k < kQPer; ++k) {
+        const int i = tid + k * kThreads;
+        const int h = min(i >> 7, nh - 1), d = i & 127;
+        qraw[k] = a.q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + d * a.q_sd];
+      }
+    }
+    if (a.q_vec) {
+      const int h = tid >> 4;
+      if (h < HMAX) {
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          f[e] = h < nh ? TT::to_f32((uint16_t)(word(q16, e >> 1) >> ((e & 1) * 16))) : 0.f;
+        float4* dst = (float4*)&s_q[h][8 * (tid & 15)];
+        dst[0] = make_float4(f[0], f[1], f[2], f[3]);
+        dst[1] = make_float4(f[4], f[5], f[6], f[7]);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < kQPer; ++k) {
+        const int i = tid + k * kThreads;
+        qv[k] = (i < HMAX * 128 && (i >> 7) < nh) ? TT::to_f32(qraw[k]) : 0.f;
+        if (i < HMAX * 128) s_q[i >> 7][i & 127] = qv[k];
+      }
     }
   };
 
@@ -377,34 +479,50 @@ decode_kernel(const DecodeArgs a) {
     // dot products for every head, and the parts are summed in LDS.
     constexpr int kParts = kThreads / DKP, kL = 128 / kParts;
     const int c = tid % DKP, part = tid / DKP;
-    load_q();
-    const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)c * a.R_sk;
-    float rv[kL];
-    if (c < a.Dk) {
-      if (a.r_dtype == 2) {
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = ((const float*)a.R)[rb + (int64_t)(part * kL + i) * a.R_sd];
-      } else {
-        uint16_t rr[kL];
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rr[i] = ((const uint16_t*)a.R)[rb + (int64_t)(part * kL + i) * a.R_sd];
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = a.r_dtype == 0 ? F16::to_f32(rr[i]) : BF16::to_f32(rr[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < kL; ++i) rv[i] = 0.f;
-    }
-    float dmv = 0.f;
-    if (tid < 128 && a.has_bias)
-      dmv = load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)tid * a.dm_sd, a.dm_dtype);
-
+    // The first K/V blocks, then the prologue's own loads (q; R straight
+    // into LDS in the fast layout; delta_mu) are issued back to back, so one
+    // memory latency covers them all.
+    uint4* s_r = HMAX >= 16 ? (uint4*)&s_acc[0][0][0] + kRawChunks : s_rsep;
+    constexpr int kRPer = kRawChunks / kThreads;
+    const int nchunks = 16 * a.Dk;  // [128][Dk] 16-bit elements in 16-byte chunks
     Ring<NBUF_V, VisBuf<DKB>> ring(nblk, wave, rot_seed);
     ring.prime(load);
+    load_q();
+    if (a.r_vec) {
+      // LDS DMA (global_load_lds_dwordx4): wave w copies 1 KB blocks
+      // r * 4 + w of R straight into s_r, holding no registers across the
+      // K/V prime; lanes past the end re-read the last chunk into unused slots
+      const uint4* rsrc = (const uint4*)((const uint16_t*)a.R + b * a.R_sb + kv * a.R_sh);
+#pragma unroll
+      for (int r = 0; r < kRPer; ++r) {
+        const int j0 = (r * kWaves + wave) * 64;
+        if (j0 < nchunks)
+          __builtin_amdgcn_global_load_lds(
+              (__attribute__((address_space(1))) void*)(rsrc + min(j0 + lane, nchunks - 1)),
+              (__attribute__((address_space(3))) void*)(s_r + j0), 16, 0, 0);
+      }
+    }
+    uint32_t dmraw = 0u;
+    if (a.has_bias) {
+      const int64_t di = b * a.dm_sb + kv * a.dm_sh + (int64_t)(tid & 127) * a.dm_sd;
+      dmraw = a.dm_dtype == 2 ? ((const uint32_t*)a.dm)[di] : (uint32_t)((const uint16_t*)a.dm)[di];
+    }
 
+    const float dmv = (tid < 128 && a.has_bias) ? raw_to_f32(dmraw, a.dm_dtype) : 0.f;
     store_q();
     if (tid < 128) s_dm[tid] = dmv;
     __syncthreads();
+    float rv[kL];
+    if (a.r_vec) {
+      const uint16_t* rl = (const uint16_t*)s_r;
+#pragma unroll
+      for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? raw_to_f32(rl[(part * kL + i) * a.Dk + c], a.r_dtype) : 0.f;
+    } else {  // element-wise fallback (column c, clamped in-bounds)
+      const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)min(c, a.Dk - 1) * a.R_sk;
+#pragma unroll
+      for (int i = 0; i < kL; ++i)
+        rv[i] = c < a.Dk ? load_any(a.R, rb + (int64_t)(part * kL + i) * a.R_sd, a.r_dtype) : 0.f;
+    }
     float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
 #pragma unroll
     for (int h = 0; h < HMAX; ++h) {
@@ -421,10 +539,14 @@ decode_kernel(const DecodeArgs a) {
       for (int pp = 0; pp < kParts; ++pp) sum += s_part[(pp * HMAX + h) * DKP + cc];
       s_qt[h][cc] = sum;
     }
-    if (tid < HMAX) {
+    {  // q . delta_mu: 16 lanes per head, eight channels each
+      const int hb = tid >> 4, j = tid & 15, hs = min(hb, HMAX - 1);
       float bsum = 0.f;
-      for (int d = 0; d < 128; ++d) bsum += s_q[tid][d] * s_dm[d];
-      s_bias[tid] = bsum;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bsum = fmaf(s_q[hs][8 * j + e], s_dm[8 * j + e], bsum);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) bsum += shfl_xor(bsum, off);
+      if (hb < HMAX && j == 0) s_bias[hb] = bsum;
     }
     __syncthreads();
 
@@ -486,17 +608,24 @@ decode_kernel(const DecodeArgs a) {
       }
     };
 
-    load_q();
-    const uint8_t* mb = a.mask ? a.mask + b * a.mf_sb : nullptr;
-    uint8_t mv[kMaskChunk / kThreads];
-#pragma unroll
-    for (int k = 0; k < kMaskChunk / kThreads; ++k) {
-      const int64_t t = min(t_begin + tid + k * kThreads, max(t_end - 1, (int64_t)0));
-      mv[k] = (mb && t_end > t_begin) ? mb[t * a.mf_ss] : (uint8_t)1;
-    }
-
+    // first K/V blocks, then q and the mask bytes (see the visual path)
     Ring<NBUF_F, FullBuf> ring(nblk, wave, rot_seed);
     ring.prime(load);
+    load_q();
+    const uint8_t* mb = a.mask ? a.mask + b * a.mf_sb : nullptr;
+    uint32_t mv[kMaskChunk / kThreads];  // one register each: no byte packing between loads
+    if (mb && t_end > t_begin) {  // uniform: all mask loads issued together
+#pragma unroll
+      for (int k = 0; k < kMaskChunk / kThreads; ++k)
+        mv[k] = mb[min(t_begin + tid + k * kThreads, t_end - 1) * a.mf_ss];
+    } else {
+#pragma unroll
+      for (int k = 0; k < kMaskChunk / kThreads; ++k) mv[k] = 1;
+    }
+    // keep the compares on the mask below this point (the compiler would
+    // otherwise test each byte as it arrives, one memory latency per byte)
+#pragma unroll
+    for (int k = 0; k < kMaskChunk / kThreads; ++k) asm volatile("" : "+v"(mv[k]));
 
     store_q();
 #pragma unroll
@@ -573,11 +702,11 @@ decode_kernel(const DecodeArgs a) {
 
 }
 
-// Second launch: 16 threads per (unit, head) row, 16 rows per workgroup.
+// Second launch: one wave per (unit, head) row, four rows per workgroup.
 template <class TT>
 __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a, int64_t rows) {
   const int tid = threadIdx.x;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (tid >> 4);
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (tid >> 6);
   if (row >= rows) return;
   const int64_t u = row / a.hpu;
   const int h = (int)(row - u * a.hpu);
@@ -586,7 +715,7 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a, int
   const int kv = r_in_b / a.spk;
   const int jblk = r_in_b - kv * a.spk;
   if (h >= min(a.hpu, a.G - jblk * a.hpu)) return;
-  merge_row<TT>(a, u, b, kv * a.G + jblk * a.hpu + h, h, tid & 15);
+  merge_row<TT>(a, u, b, kv, kv * a.G + jblk * a.hpu + h, h, tid & 63);
 }
 
 }  // namespace rk
@@ -613,17 +742,20 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
 
 struct WsLayout {
-  size_t part_m, part_l, part_acc, total;
+  size_t part_m, part_l, part_acc, pos, total;
 };
 
-WsLayout ws_layout(const rk_decode_plan& p) {
+// partials (m, l, acc) per (unit, workgroup, head), then one int32 append
+// position per batch row (units / units_per_b = B)
+WsLayout ws_layout(const rk_decode_plan& p, int64_t B) {
   const int64_t np = p.wg_vis + p.wg_full;
   const size_t parts = (size_t)p.units * np * p.heads_per_unit;
   WsLayout w;
   w.part_m = 0;
   w.part_l = w.part_m + align256(parts * sizeof(float));
   w.part_acc = w.part_l + align256(parts * sizeof(float));
-  w.total = w.part_acc + align256(parts * 128 * sizeof(float));
+  w.pos = w.part_acc + align256(parts * 128 * sizeof(float));
+  w.total = w.pos + align256((size_t)B * sizeof(int32_t));
   return w;
 }
 
@@ -656,20 +788,38 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
     p.head_blocks = 1;
     p.units = B * H_q;
   }
+  // Workgroups run in rounds of `slots` resident workgroups (two per CU at
+  // the kernel's register budget).  A partial last round costs as much as a
+  // full one, so the grid is sized to whole rounds: the fewest rounds that
+  // keep a workgroup at <= g_max_wg_bytes, then as many workgroups per unit
+  // as those rounds hold (but none below g_min_wg_bytes), split between the
+  // visual and prompt/text spans in proportion to their bytes.
   const int64_t unit_vis = S_v * (Dk + 128) * elem_bytes;
   const int64_t unit_full = S_f * 256 * elem_bytes;
-  const int64_t total = p.units * (unit_vis + unit_full);
-  int64_t per_wg = total / ((int64_t)num_cus * g_wgs_per_cu);
-  if (per_wg < g_min_wg_bytes) per_wg = g_min_wg_bytes;
-  if (per_wg > g_max_wg_bytes) per_wg = g_max_wg_bytes;
+  const int64_t unit_bytes = unit_vis + unit_full;
+  const int64_t total = p.units * unit_bytes;
+  const int64_t slots = (int64_t)num_cus * g_wgs_per_cu;
+  int64_t rounds = cdiv(total, slots * g_max_wg_bytes);
+  if (rounds < 1) rounds = 1;
+  int64_t budget = p.units > 0 ? rounds * slots / p.units : 1;
+  const int64_t by_min = unit_bytes / g_min_wg_bytes;
+  if (budget > by_min) budget = by_min;
+  if (budget < 1) budget = 1;
+  int64_t w_full = 0, w_vis = 0;
+  if (S_f > 0) {
+    w_full = (budget * unit_full + unit_bytes / 2) / unit_bytes;
+    if (w_full < 1) w_full = 1;
+  }
   if (S_v > 0) {
-    const int64_t w = cdiv(unit_vis, per_wg);
-    p.chunk_vis = round_up(cdiv(S_v, w), kWgTokens);
+    w_vis = budget - w_full;
+    if (w_vis < 1) w_vis = 1;
+  }
+  if (S_v > 0) {
+    p.chunk_vis = round_up(cdiv(S_v, w_vis), kWgTokens);
     p.wg_vis = (int32_t)cdiv(S_v, p.chunk_vis);
   }
   if (S_f > 0) {
-    const int64_t w = cdiv(unit_full, per_wg);
-    p.chunk_full = round_up(cdiv(S_f, w), kWgTokens);
+    p.chunk_full = round_up(cdiv(S_f, w_full), kWgTokens);
     if (p.chunk_full > rk::kMaskChunk) p.chunk_full = rk::kMaskChunk;
     p.wg_full = (int32_t)cdiv(S_f, p.chunk_full);
   }
@@ -679,7 +829,7 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   }
   p.grid = p.units * (p.wg_vis + p.wg_full);
   if (p.units > 65535 * 1024 || p.wg_vis + p.wg_full > (1 << 30)) return RK_ERR_SHAPE;
-  p.workspace_bytes = ws_layout(p).total;
+  p.workspace_bytes = ws_layout(p, B).total;
   *plan = p;
   return RK_OK;
 }
@@ -774,8 +924,8 @@ hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)grid.y * a.hpu;
-  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)((rows + 15) / 16)), dim3(rk::kThreads), 0, s,
-                     a, rows);
+  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)((rows + rk::kWaves - 1) / rk::kWaves)),
+                     dim3(rk::kThreads), 0, s, a, rows);
   return hipGetLastError();
 }
 
@@ -834,7 +984,8 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
                const rk_tensor* kf, const rk_tensor* vf, const rk_tensor* mask,
                const rk_tensor* ks, const rk_tensor* vs, const rk_tensor* out, int32_t policy,
                void* ws, size_t ws_bytes, void* stream, bool has_vis,
-               const int32_t* len_full = nullptr, int64_t v_gap_at = -1, int64_t v_gap = 0) {
+               int32_t* len_full = nullptr, int64_t v_gap_at = -1, int64_t v_gap = 0,
+               const rk_tensor* k_new = nullptr, const rk_tensor* v_new = nullptr) {
   int st = RK_OK;
   const int cus = resolve_cus(0, &st);
   if (st) return st;
@@ -848,7 +999,7 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   if (!q->data || !out->data || (vis_work && (!R->data || !ks->data || !vs->data)) ||
       (c.S_f > 0 && (!kf->data || !vf->data)))
     return RK_ERR_NULL;
-  const WsLayout w = ws_layout(p);
+  const WsLayout w = ws_layout(p, c.B);
   rk::DecodeArgs a;
   memset(&a, 0, sizeof(a));
   a.q = (const uint16_t*)q->data;
@@ -874,6 +1025,8 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     a.has_mask = 1;
   }
   bool vec = rk::vec_ok(kf) && rk::vec_ok(vf);
+  a.q_vec = q->stride[2] == 1 && q->stride[1] % 8 == 0 && q->stride[0] % 8 == 0 &&
+            (((uintptr_t)q->data) & 15) == 0;
   int dkb = 1;
   if (has_vis) {
     a.R = R->data;
@@ -887,6 +1040,8 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
       a.dm_sd = dm->stride[2];
       a.has_bias = 1;
     }
+    a.r_vec = rk::is_half(R->dtype) && c.Dk <= 64 && R->stride[3] == 1 && R->stride[2] == c.Dk &&
+              R->stride[1] % 8 == 0 && R->stride[0] % 8 == 0 && (((uintptr_t)R->data) & 15) == 0;
     a.ks = (const uint16_t*)ks->data;
     a.vs = (const uint16_t*)vs->data;
     if (!set_head(ks, a.ks_sb, a.ks_sh, a.ks_ss, a.ks_sd) ||
@@ -899,6 +1054,19 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   }
   a.S_f = c.S_f;
   a.len_full = len_full;
+  if (k_new) {
+    a.k_new = (const uint16_t*)k_new->data;
+    a.v_new = (const uint16_t*)v_new->data;
+    a.kf_w = (uint16_t*)kf->data;
+    a.vf_w = (uint16_t*)vf->data;
+    a.ws_pos = (int32_t*)((char*)ws + w.pos);
+    a.kn_sb = k_new->stride[0];
+    a.kn_sh = k_new->stride[1];
+    a.kn_sd = k_new->stride[3];
+    a.vn_sb = v_new->stride[0];
+    a.vn_sh = v_new->stride[1];
+    a.vn_sd = v_new->stride[3];
+  }
   a.vf_gap_at = v_gap_at < 0 ? UINT32_MAX : (uint32_t)v_gap_at;
   a.vf_gap = (uint32_t)v_gap;
   a.chunk_vis = p.chunk_vis;
@@ -962,9 +1130,9 @@ extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor
                                         const rk_tensor* v_buf, int64_t v_gap_at, int64_t v_gap,
                                         const rk_tensor* mask_full, const rk_tensor* k_sparse,
                                         const rk_tensor* v_sparse, int64_t num_kv_groups,
-                                        const int32_t* len_full, const rk_tensor* out,
-                                        int32_t policy, void* workspace, size_t workspace_bytes,
-                                        void* stream) {
+                                        const rk_tensor* k_new, const rk_tensor* v_new,
+                                        int32_t* len_full, const rk_tensor* out, int32_t policy,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
   if (!k_full || !v_buf) return RK_ERR_NULL;
   int st = rk::check_desc(v_buf, 4);
   if (st) return st;
@@ -981,9 +1149,19 @@ extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor
   if (!out || !len_full) return RK_ERR_NULL;
   if ((st = check_out(out, c))) return st;
   if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
+  if ((k_new == nullptr) != (v_new == nullptr)) return RK_ERR_NULL;
+  if (k_new) {
+    for (const rk_tensor* t : {k_new, v_new}) {
+      if ((st = rk::check_desc(t, 4))) return st;
+      if (t->dtype != c.dtype) return RK_ERR_DTYPE;
+      if (t->shape[0] != c.B || t->shape[1] != c.H_kv || t->shape[2] != 1 || t->shape[3] != 128)
+        return RK_ERR_SHAPE;
+      if (c.B > 0 && !t->data) return RK_ERR_NULL;
+    }
+  }
   return run_decode(c, q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse,
                     out, policy, workspace, workspace_bytes, stream, true, len_full,
-                    v_gap > 0 ? v_gap_at : -1, v_gap);
+                    v_gap > 0 ? v_gap_at : -1, v_gap, k_new, v_new);
 }
 
 namespace {

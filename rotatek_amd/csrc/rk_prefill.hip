@@ -194,37 +194,44 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
   for (int i = tid; i < kTiles * 256; i += kThreads) out[i] = s_red[i];
 }
 
-// Sum over the pass-2 partials of entry (m, n) of tile t, rounded to the key
-// dtype (the einsum output dtype, kv_pruning_utils.py:114) and back to fp32.
-template <class TT>
-__device__ __forceinline__ float tile_sum(const float* part, int bh, int splits, int t, int m, int n) {
-  const int e = t * 256 + m * 16 + n;
-  float s = 0.f;
-  for (int x = 0; x < splits; ++x) s += part[((int64_t)bh * splits + x) * (kTiles * 256) + e];
-  return TT::to_f32(TT::from_f32(s));
-}
-
-// grid (B*H): cov[r][c] = 0.5 (C[r][c] + C[c][r]) in fp32 (kv_pruning_utils.py:115)
-// where C[8m+i][8n+j] lives in tile (i, j) if i <= j, else mirrored in
-// tile (j, i); also writes mu [128].
+// grid (kTiles, B*H): one workgroup per upper tile (i, j) of one head.
+// Thread (m, n) sums entry (m, n) of the tile over the pass-2 partials
+// (consecutive threads read consecutive floats), rounds the sum to the key
+// dtype (the einsum output dtype, kv_pruning_utils.py:114) and back to fp32,
+// and the tile writes cov[r][c] = 0.5 (C[r][c] + C[c][r])
+// (kv_pruning_utils.py:115) for r = 8m + i, c = 8n + j and the mirrored
+// entry.  C[c][r] of an off-diagonal tile is the same stored sum (the
+// accumulator holds the upper tiles only); a diagonal tile pairs (m, n)
+// with (n, m).  Tile 0 also writes mu [128].
 template <class TT>
 __global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int splits,
                                                           const float* mean_part, int mean_splits,
                                                           int64_t S, float* cov, int64_t cs_b, int64_t cs_h,
                                                           int64_t cs_r, int64_t cs_c, float* mu, int64_t ms_b,
                                                           int64_t ms_h, int64_t ms_c, int H) {
-  const int tid = threadIdx.x, bh = blockIdx.x;
+  __shared__ float s_t[256];
+  const int tid = threadIdx.x, t = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
-  float* cb = cov + b * cs_b + (int64_t)h * cs_h;
-  for (int e = tid; e < 128 * 128; e += kThreads) {
-    const int r = e >> 7, c = e & 127;
-    const int i = r & 7, m = r >> 3, j = c & 7, n = c >> 3;
-    const float rc = i <= j ? tile_sum<TT>(part, bh, splits, tile_index(i, j), m, n)
-                            : tile_sum<TT>(part, bh, splits, tile_index(j, i), n, m);
-    const float cr = i == j ? tile_sum<TT>(part, bh, splits, tile_index(i, i), n, m) : rc;
-    cb[r * cs_r + c * cs_c] = 0.5f * (rc + cr);
+  const float* src = part + (int64_t)bh * splits * (kTiles * 256) + t * 256 + tid;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  int x = 0;
+  for (; x + 4 <= splits; x += 4) {
+    a0 += src[(int64_t)(x + 0) * (kTiles * 256)];
+    a1 += src[(int64_t)(x + 1) * (kTiles * 256)];
+    a2 += src[(int64_t)(x + 2) * (kTiles * 256)];
+    a3 += src[(int64_t)(x + 3) * (kTiles * 256)];
   }
-  if (tid < 128 && mu)
+  for (; x < splits; ++x) a0 += src[(int64_t)x * (kTiles * 256)];
+  s_t[tid] = TT::to_f32(TT::from_f32((a0 + a1) + (a2 + a3)));
+  __syncthreads();
+  const int i = tile_row(t), j = tile_col(t), m = tid >> 4, n = tid & 15;
+  float* cb = cov + b * cs_b + (int64_t)h * cs_h;
+  const int r = 8 * m + i, c = 8 * n + j;
+  const float rc = s_t[tid];
+  const float cr = i == j ? s_t[n * 16 + m] : rc;
+  cb[r * cs_r + c * cs_c] = 0.5f * (rc + cr);
+  if (i != j) cb[c * cs_r + r * cs_c] = 0.5f * (cr + rc);
+  if (t == 0 && tid < 128 && mu)
     mu[b * ms_b + (int64_t)h * ms_h + tid * ms_c] = head_mean(mean_part, bh, mean_splits, tid, S);
 }
 
@@ -531,7 +538,8 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
     hipLaunchKernelGGL((cov_kernel<TT, false>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
                        p.mean_splits, cpart);
   }
-  hipLaunchKernelGGL((covfin_kernel<TT>), dim3((unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits, mpart,
+  hipLaunchKernelGGL((covfin_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits,
+                     mpart,
                      p.mean_splits, k.S, cov, cov_t->stride[0], cov_t->stride[1], cov_t->stride[2],
                      cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0, mu_t ? mu_t->stride[1] : 0,
                      mu_t ? mu_t->stride[2] : 0, k.H);

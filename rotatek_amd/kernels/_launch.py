@@ -62,7 +62,8 @@ def full_channel_decode(q, k, v, num_kv_groups: int, policy: int) -> torch.Tenso
 
 def rotatek_decode_varlen(q_full, R_partial, delta_mu, k_full, v_buf, v_gap_at: int, v_gap: int,
                           mask_full, k_sparse, v_sparse, num_kv_groups: int, len_full: torch.Tensor,
-                          policy: int, out: torch.Tensor | None = None) -> torch.Tensor:
+                          policy: int, out: torch.Tensor | None = None, k_new=None,
+                          v_new=None) -> torch.Tensor:
     """RotateK decode over capacity-sized span buffers (rk_rotatek_decode_varlen).
 
     ``k_full [B,H_kv,C,D]`` holds prompt then text Keys; ``v_buf`` holds the
@@ -70,31 +71,43 @@ def rotatek_decode_varlen(q_full, R_partial, delta_mu, k_full, v_buf, v_gap_at: 
     at ``t + v_gap`` once ``t >= v_gap_at``); only rows ``t < len_full[b]``
     (device int32) are attended.  Shapes stay fixed as the cache grows, so
     the launch can be captured once and replayed every decode step.
+    With ``k_new`` / ``v_new`` ([B,H_kv,1,D]) the step first appends that
+    token (attended, stored at row ``len_full[b]``, length advanced).
     """
     _require_gpu(q_full, "q_full")
     if len_full.dtype != torch.int32 or not len_full.is_cuda or len_full.dim() != 1 \
             or len_full.shape[0] != q_full.shape[0] or not len_full.is_contiguous():
         raise ValueError("len_full must be a contiguous device int32 tensor [B]")
     lib = _lib.load()
-    S_f = k_full.shape[2]
     d = [_lib.desc(t) for t in (q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse)]
     if out is None:
         out = torch.empty(q_full.shape, dtype=q_full.dtype, device=q_full.device)
     do = _lib.desc(out)
-    # workspace size: the plan depends only on the capacity-sized shapes
-    dv = _lib.desc(v_buf.narrow(2, 0, min(S_f, v_buf.shape[2])))
-    need = ctypes.c_size_t(0)
-    _lib.check(lib.rk_rotatek_decode_check(*[_lib.ref(x) for x in d[:4]], ctypes.byref(dv),
-                                           *[_lib.ref(x) for x in d[5:]], int(num_kv_groups),
-                                           ctypes.byref(do), policy, 0, ctypes.byref(need)),
-               "rotatek_decode_varlen")
-    ws = _lib.workspace(q_full.device, need.value)
+    need = varlen_workspace_bytes(q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse,
+                                  num_kv_groups, policy)
+    ws = _lib.workspace(q_full.device, need)
+    dkn, dvn = _lib.desc(k_new), _lib.desc(v_new)
     _lib.check(lib.rk_rotatek_decode_varlen(*[_lib.ref(x) for x in d[:5]], int(v_gap_at), int(v_gap),
                                             *[_lib.ref(x) for x in d[5:]], int(num_kv_groups),
-                                            len_full.data_ptr(), ctypes.byref(do), policy, ws.data_ptr(),
+                                            _lib.ref(dkn), _lib.ref(dvn), len_full.data_ptr(),
+                                            ctypes.byref(do), policy, ws.data_ptr(),
                                             ws.numel(), _lib.stream_handle(q_full.device)),
                "rotatek_decode_varlen")
     return out
+
+
+def varlen_workspace_bytes(q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse,
+                           num_kv_groups: int, policy: int) -> int:
+    """Workspace bytes ``rotatek_decode_varlen`` needs (host-only; the plan
+    depends only on the capacity-sized shapes)."""
+    S_f = k_full.shape[2]
+    d = [_lib.desc(t) for t in (q_full, R_partial, delta_mu, k_full, None, mask_full, k_sparse, v_sparse)]
+    d[4] = _lib.desc(v_buf.narrow(2, 0, min(S_f, v_buf.shape[2])))
+    need = ctypes.c_size_t(0)
+    _lib.check(_lib.load().rk_rotatek_decode_check(*[_lib.ref(x) for x in d], int(num_kv_groups), None, policy,
+                                                   0, ctypes.byref(need)),
+               "rotatek_decode_varlen")
+    return need.value
 
 
 def append_kv(k_new, v_new, k_buf, v_buf, len_full: torch.Tensor) -> None:

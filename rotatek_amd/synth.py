@@ -161,3 +161,66 @@ DECODE_KEYS = ("q_full", "R_partial", "delta_mu", "k_full", "v_full", "mask_full
 def decode_args(inp: dict) -> dict:
     """The keyword arguments ``rotatek_decode`` takes, picked from ``inp``."""
     return {k: inp[k] for k in DECODE_KEYS}
+
+
+# ------------------------------------------------------------ config 4 flow
+@dataclasses.dataclass(frozen=True)
+class FlowConfig:
+    """Prefill rotation + decode sweep of a Qwen2.5-VL-7B-shaped stack:
+    prompt and text spans of 30 tokens, the text span growing by one token
+    per decode step (model_end_to_end_qwen.py:51-52)."""
+    layers: int = 28
+    B: int = 8
+    H_q: int = 28
+    H_kv: int = 4
+    prompt: int = 30
+    text: int = 30
+    steps: int = 128
+    visual: tuple = (4097, 12001)
+    keep: tuple = (64, 32, 16)
+    rank: int = 16
+    dtype: torch.dtype = torch.bfloat16
+    D: int = 128
+
+    @property
+    def G(self) -> int:
+        return self.H_q // self.H_kv
+
+
+FLOW = FlowConfig()
+KEEP_TO_RATIO = {64: 0.5, 32: 0.75, 16: 0.875}   # keep = 128 - int(128 * ratio)
+
+
+def make_flow_layer(c: FlowConfig, S_v: int, seed: int, device="cuda") -> dict:
+    """One layer's prefill states ``K, V [B, H_kv, S, D]`` and ``Q [B, H_q, S, D]``
+    with S = prompt + S_v + text.  Visual Keys are ``4 Z U^T + 0.5 E``: a
+    rank-``c.rank`` signal (Z ~ N(0,1) [S_v, rank], U orthonormal [D, rank]
+    per KV head) plus N(0,1) noise E; everything else is N(0,1)."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    B, Hq, Hkv, D = c.B, c.H_q, c.H_kv, c.D
+    S = c.prompt + S_v + c.text
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)
+
+    U = torch.linalg.qr(randn(B, Hkv, D, c.rank))[0]
+    K = randn(B, Hkv, S, D)
+    vis = K[:, :, c.prompt:c.prompt + S_v]
+    vis.mul_(0.5).add_(4.0 * torch.matmul(randn(B, Hkv, S_v, c.rank), U.transpose(-1, -2)))
+    K = K.to(c.dtype)
+    V = randn(B, Hkv, S, D).to(c.dtype)
+    Q = torch.empty(B, Hq, S, D, device=dev, dtype=c.dtype)
+    for h in range(Hq):
+        Q[:, h] = randn(B, S, D).to(c.dtype)
+    return {"K": K, "V": V, "Q": Q}
+
+
+def flow_step_bytes(c: FlowConfig, S_v: int, keep: int, S_f: int) -> int:
+    """Algorithmic HBM bytes of one decode step over all layers with S_f
+    prompt + text tokens attended: per layer, the RotateK decode bytes plus
+    the append (new K and V rows read and written)."""
+    layer = DecodeConfig("flow", c.B, c.H_q, c.H_kv, S_v, S_f, keep, c.dtype)
+    append = 2 * 2 * c.B * c.H_kv * c.D * torch.tensor([], dtype=c.dtype).element_size()
+    # the span-cache decode takes no mask
+    return c.layers * (decode_bytes(layer) - c.B * S_f + append)

@@ -215,15 +215,19 @@ def test_rotate_and_select_validation():
 
 
 # ------------------------------------------------------------- span cache ABI
-def _varlen(S_cap=40, gap_at=10, gap=100, v_rows=None, lens=1, B=2, Hq=8, Hkv=4):
+def _varlen(S_cap=40, gap_at=10, gap=100, v_rows=None, lens=1, B=2, Hq=8, Hkv=4, new=None):
     lib = _lib.load()
+    kn = vn = None
+    if new is not None:
+        kn, vn = (ctypes.byref(_t(s)) if s else None for s in new)
     q, R, dm = _t((B, Hq, 128)), _t((B, Hkv, 128, 32)), _t((B, Hkv, 128))
     kf = _t((B, Hkv, S_cap, 128))
     vb = _t((B, Hkv, S_cap + gap if v_rows is None else v_rows, 128))
     ks, vs, o = _t((B, Hkv, gap, 32)), _t((B, Hkv, gap, 128)), _t((B, Hq, 128))
     return lib.rk_rotatek_decode_varlen(ctypes.byref(q), ctypes.byref(R), ctypes.byref(dm), ctypes.byref(kf),
                                         ctypes.byref(vb), gap_at, gap, None, ctypes.byref(ks),
-                                        ctypes.byref(vs), Hq // Hkv, lens, ctypes.byref(o), 1, None, 0, None)
+                                        ctypes.byref(vs), Hq // Hkv, kn, vn, lens, ctypes.byref(o), 1, None, 0,
+                                        None)
 
 
 def test_varlen_decode_validation():
@@ -232,6 +236,9 @@ def test_varlen_decode_validation():
     assert _varlen(gap_at=41) == -10               # gap start past the capacity
     assert _varlen(gap=-1, v_rows=39) == -10
     assert _varlen(lens=None) == -1                # device lengths required
+    assert _varlen(new=((2, 4, 1, 128), None)) == -1                  # k_new without v_new
+    assert _varlen(new=((2, 4, 2, 128), (2, 4, 2, 128))) == -4        # more than one token
+    assert _varlen(new=((2, 4, 1, 128), (2, 4, 1, 128))) == -1        # well-formed, but no device memory
     # well-formed, no device / no workspace
     assert _varlen() in (-9, -12)
 

@@ -215,3 +215,108 @@ def test_graph_of_append_and_decode_replays_across_steps(policy):
     cache.sync_lengths()
     assert torch.equal(cache.key_cache_text[0], ref.k_text) and torch.equal(cache.value_cache[0], ref.v)
     assert cache.get_seq_length(0) == s_p + s_v + s_t + steps
+
+
+def test_capture_decode_over_layers_matches_eager():
+    from rotatek_amd.cache import DynamicCache
+    L, B, Hq, Hkv, Dk, s_p, s_v, s_t, steps = 3, 2, 8, 2, 16, 7, 333, 5, 4
+    dtype = torch.bfloat16
+    _say(f"capture_decode over {L} layers, {steps} replays")
+    cache = DynamicCache(reserve_tokens=steps)
+    refs, ps = [], []
+    for layer in range(L):
+        p = _prefill(B, Hkv, Dk, s_p, s_v, s_t, dtype, seed=40 + layer)
+        cache.store_pruned(p["k_pruned"], p["k_prompt"], p["k_text"], None, p["v"], layer)
+        cache.rotatek_rotations.append(p["R"])
+        cache.rotatek_means.append(p["dm"])
+        refs.append(_CatCache(p))
+        ps.append(p)
+    q = torch.zeros(L, B, Hq, D, dtype=dtype, device="cuda")
+    kn = torch.zeros(L, B, Hkv, 1, D, dtype=dtype, device="cuda")
+    vn = torch.zeros_like(kn)
+    out = torch.empty(L, B, Hq, D, dtype=dtype, device="cuda")
+    graph = cache.capture_decode(q, kn, vn, out, Hq // Hkv)
+    torch.cuda.synchronize()
+    for step in range(steps):
+        for layer in range(L):
+            rn = ps[layer]["rn"]
+            q[layer].copy_(rn(B, Hq, D))
+            kn[layer].copy_(rn(B, Hkv, 1, D))
+            vn[layer].copy_(rn(B, Hkv, 1, D))
+            refs[layer].update(kn[layer].clone(), vn[layer].clone())
+        graph.replay()
+        torch.cuda.synchronize()
+        for layer in range(L):
+            want = _oracle(refs[layer].rotatek_args(q[layer], ps[layer]["R"], ps[layer]["dm"], Hq // Hkv))
+            assert np.abs(_np(out[layer])[:, None] - want).max() <= TOL[dtype], (step, layer)
+    cache.sync_lengths()
+    for layer in range(L):
+        assert torch.equal(cache.key_cache_text[layer], refs[layer].k_text)
+        assert torch.equal(cache.value_cache[layer], refs[layer].v)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("policy", [0, 1])
+def test_fused_append_decode_step_matches_reference(dtype, policy):
+    """decode_step = append then decode, in the decode's own two launches."""
+    from rotatek_amd.cache import DynamicCache
+    B, Hq, Hkv, Dk, s_p, s_v, s_t = 2, 28, 4, 32, 30, 700, 30
+    _say(f"fused append+decode {dtype} policy={policy}")
+    p = _prefill(B, Hkv, Dk, s_p, s_v, s_t, dtype, seed=17)
+    cache = DynamicCache(reserve_tokens=5)
+    cache.store_pruned(p["k_pruned"], p["k_prompt"], p["k_text"], None, p["v"], 0)
+    cache.rotatek_rotations.append(p["R"])
+    cache.rotatek_means.append(p["dm"])
+    ref = _CatCache(p)
+    for step in range(5):
+        k, v, q = p["rn"](B, Hkv, 1, D), p["rn"](B, Hkv, 1, D), p["rn"](B, Hq, D)
+        out, _, _ = cache.decode_step(q, k, v, 0, Hq // Hkv, policy=policy)
+        torch.cuda.synchronize()
+        ref.update(k, v)
+        want = _oracle(ref.rotatek_args(q, p["R"], p["dm"], Hq // Hkv))
+        assert np.abs(_np(out) - want).max() <= TOL[dtype], step
+        assert torch.equal(cache.lengths(0).cpu(), torch.full((B,), s_p + s_t + step + 1, dtype=torch.int32))
+    cache.sync_lengths()
+    assert torch.equal(cache.key_cache_text[0], ref.k_text) and torch.equal(cache.value_cache[0], ref.v)
+    # the buffers are now full: a further step neither stores nor attends the token
+    sp = cache._spans[0]
+    k_before, v_before = sp.k.clone(), sp.v.clone()
+    k, v, q = p["rn"](B, Hkv, 1, D), p["rn"](B, Hkv, 1, D), p["rn"](B, Hq, D)
+    out, _, _ = cache.decode_step(q, k, v, 0, Hq // Hkv, policy=policy)
+    torch.cuda.synchronize()
+    assert torch.equal(sp.k, k_before) and torch.equal(sp.v, v_before)
+    want = _oracle(ref.rotatek_args(q, p["R"], p["dm"], Hq // Hkv))
+    assert np.abs(_np(out) - want).max() <= TOL[dtype]
+
+
+def test_fused_append_with_ragged_lengths():
+    from rotatek_amd._lib import RK_POLICY_GQA
+    from rotatek_amd.kernels import _launch
+    dtype, B, Hq, Hkv, Dk, s_p, s_v, cap = torch.float16, 3, 8, 2, 32, 9, 200, 40
+    _say("fused append, ragged per-row lengths")
+    p = _prefill(B, Hkv, Dk, s_p, s_v, cap, dtype, seed=23)
+    kf = torch.cat([p["k_prompt"], p["k_text"]], dim=-2).contiguous()
+    vbuf = p["v"].clone()
+    lens = torch.tensor([0, 20, s_p + cap], dtype=torch.int32, device="cuda")   # last row is full
+    kn, vn, q = p["rn"](B, Hkv, 1, D), p["rn"](B, Hkv, 1, D), p["rn"](B, Hq, D)
+    kf0, vb0, lens0 = kf.clone(), vbuf.clone(), lens.clone()
+    out = _launch.rotatek_decode_varlen(q, p["R"], p["dm"], kf, vbuf, s_p, s_v, None, p["k_pruned"],
+                                        vbuf[:, :, s_p:s_p + s_v], Hq // Hkv, lens, RK_POLICY_GQA,
+                                        k_new=kn, v_new=vn)
+    torch.cuda.synchronize()
+    # expected buffers: token written at row lens0[b] of rows that had room
+    kf_want, vb_want = kf0.clone(), vb0.clone()
+    for b in range(B):
+        pos = int(lens0[b])
+        if pos < s_p + cap:
+            kf_want[b, :, pos] = kn[b, :, 0]
+            row = pos + (s_v if pos >= s_p else 0)
+            vb_want[b, :, row] = vn[b, :, 0]
+    assert torch.equal(kf, kf_want) and torch.equal(vbuf, vb_want)
+    assert lens.tolist() == [1, 21, s_p + cap]
+    vf = torch.cat([vb_want[:, :, :s_p], vb_want[:, :, s_p + s_v:]], dim=-2)
+    mask = (torch.arange(s_p + cap, device="cuda")[None, :] < lens[:, None].long()).to(torch.uint8)
+    want = _oracle(dict(q_full=q, R_partial=p["R"], delta_mu=p["dm"], k_full=kf_want, v_full=vf,
+                        mask_full=mask, k_sparse=p["k_pruned"], v_sparse=vb_want[:, :, s_p:s_p + s_v],
+                        num_kv_groups=Hq // Hkv))
+    assert np.abs(_np(out)[:, None] - want).max() <= TOL[dtype]
