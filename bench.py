@@ -272,6 +272,68 @@ def run_flow(args):
     print(json.dumps(line), flush=True)
 
 
+def run_prefill(args):
+    """Config 4 prefill, one layer per visual length, each stage timed on
+    the device (HIP events over ``--steps`` repetitions): key covariance
+    (mean pass + MFMA covariance pass + finalize), query weighting (torch),
+    eigh (torch, on the host as the reference), channel scores, top-k,
+    R_partial / delta_mu gather and the truncated Key write."""
+    import torch
+
+    from rotatek_amd import prefill, synth
+
+    c = synth.FLOW
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    reps = args.steps if args.steps_given else 20
+    keep = 32
+    rows = []
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for _ in range(reps):
+            out = fn()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / reps * 1e6
+        return out, e0.elapsed_time(e1) * 1e3 / reps, wall
+
+    for S_v in c.visual:
+        st = synth.make_flow_layer(c, S_v, seed=S_v, device=dev)
+        kv = st["K"][:, :, c.prompt:c.prompt + S_v]
+        (mean, cov), t_cov, _ = timed(lambda: prefill.key_covariance(kv))
+        covw, t_qw, _ = timed(lambda: prefill.query_weight(cov, st["Q"], c.G))
+        R_full, _, w_eigh = timed(lambda: prefill.eigen_rotation(covw))
+        scores, t_sc, _ = timed(lambda: prefill.channel_scores(kv, R_full))
+        (idx, mask), t_tk, _ = timed(lambda: prefill.topk_channels(scores, keep))
+        (Rp, dmu), t_ga, _ = timed(lambda: prefill.gather_rotation(R_full, idx, mean, kv.dtype))
+        _, t_rot, _ = timed(lambda: prefill.rotate_keys(kv, Rp))
+        heads = c.B * c.H_kv
+        kbytes = heads * S_v * c.D * 2
+        cov_flops = heads * 36 * 256 * 2 * S_v   # the 36 upper 16x16 tiles computed on the MFMA
+        row = {"visual_tokens": S_v, "keep": keep,
+               "covariance_us": round(t_cov, 2),
+               "covariance_gbps_two_passes": round(2 * kbytes / t_cov / 1e3, 1),
+               "covariance_mfma_tflops": round(cov_flops / t_cov / 1e6, 2),
+               "query_weight_us": round(t_qw, 2), "eigh_host_us": round(w_eigh, 1),
+               "channel_scores_us": round(t_sc, 2), "topk_us": round(t_tk, 2),
+               "gather_us": round(t_ga, 2), "rotate_write_us": round(t_rot, 2),
+               "rotate_write_gbps": round((kbytes + heads * S_v * keep * 2) / t_rot / 1e3, 1)}
+        _log(f"[prefill] S_v={S_v}: " + ", ".join(f"{k}={v}" for k, v in row.items() if k != "visual_tokens"))
+        rows.append(row)
+        del st, kv
+    line = {"metric": "config 4 prefill stages per layer (us, HIP events)", "value": rows[-1]["covariance_us"],
+            "unit": "us", "n_gpus": 1, "steps": reps, "warmup": 1, "higher_is_better": False, "dtype": "bf16",
+            "data": "synthetic: visual Keys 4 Z U^T + 0.5 E (rank 16)",
+            "config": {"workload": f"cfg4 prefill, B={c.B}, H_kv={c.H_kv}, keep {keep}, eigh + head-wise top-k; "
+                                   f"value = key covariance at S_v={c.visual[-1]}", "stages": rows}}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -282,6 +344,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true", help="config 4: time the prefill stages")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc passes (no GPU needed)")
@@ -292,7 +355,7 @@ def main():
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)
             sys.exit(2)
-        run_flow(args)
+        run_prefill(args) if args.prefill_only else run_flow(args)
         return
     if args.pmc_summary:
         pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.copy_calibration, args.steps, args.config)

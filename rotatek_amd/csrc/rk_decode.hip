@@ -249,6 +249,23 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
   const int sl = lane >> 4, c8 = lane & 15;
   const int64_t base = u * a.np;
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  // fused append: the new token's q, k, v and position are loaded up front,
+  // together with the partials
+  uint16_t qn[8], kn[8], vn[8];
+  int32_t pos = 0;
+  if (a.k_new) {
+    const uint16_t* qr = a.q + b * a.q_sb + (int64_t)hq * a.q_sh;
+    const uint16_t* kr = a.k_new + b * a.kn_sb + (int64_t)kv * a.kn_sh;
+    const uint16_t* vr = a.v_new + b * a.vn_sb + (int64_t)kv * a.vn_sh;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int ch = 8 * c8 + e;
+      qn[e] = qr[ch * a.q_sd];
+      kn[e] = kr[ch * a.kn_sd];
+      vn[e] = vr[ch * a.vn_sd];
+    }
+    pos = a.ws_pos[b];
+  }
   auto fold = [&](const float* mm, const float* ll, const float4* v0, const float4* v1, int k) {
     float mx = M;
     for (int i = 0; i < k; ++i) mx = fmaxf(mx, mm[i]);
@@ -297,20 +314,10 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
     M = Mx;
   }
   if (a.k_new) {
-    const int32_t pos = a.ws_pos[b];
     if (pos < a.S_f) {
-      const uint16_t* qr = a.q + b * a.q_sb + (int64_t)hq * a.q_sh;
-      const uint16_t* kr = a.k_new + b * a.kn_sb + (int64_t)kv * a.kn_sh;
-      const uint16_t* vr = a.v_new + b * a.vn_sb + (int64_t)kv * a.vn_sh;
-      uint16_t kn[8], vn[8];
       float d = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int ch = 8 * c8 + e;
-        kn[e] = kr[ch * a.kn_sd];
-        vn[e] = vr[ch * a.vn_sd];
-        d = fmaf(TT::to_f32(qr[ch * a.q_sd]), TT::to_f32(kn[e]), d);
-      }
+      for (int e = 0; e < 8; ++e) d = fmaf(TT::to_f32(qn[e]), TT::to_f32(kn[e]), d);
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) d += shfl_xor(d, off);
       const float sn = d * a.scale_log2;
@@ -526,17 +533,21 @@ decode_kernel(const DecodeArgs a) {
     float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
 #pragma unroll
     for (int h = 0; h < HMAX; ++h) {
-      float acc_h = 0.f;
+      if (h < nh) {  // uniform; rows of absent heads are never read
+        float acc_h = 0.f;
 #pragma unroll
-      for (int i = 0; i < kL; ++i) acc_h += s_q[h][part * kL + i] * rv[i];
-      s_part[(part * HMAX + h) * DKP + c] = acc_h;
+        for (int i = 0; i < kL; ++i) acc_h += s_q[h][part * kL + i] * rv[i];
+        s_part[(part * HMAX + h) * DKP + c] = acc_h;
+      }
     }
     __syncthreads();
     for (int i = tid; i < HMAX * DKP; i += kThreads) {
       const int h = i / DKP, cc = i % DKP;
       float sum = 0.f;
+      if (h < nh) {
 #pragma unroll
-      for (int pp = 0; pp < kParts; ++pp) sum += s_part[(pp * HMAX + h) * DKP + cc];
+        for (int pp = 0; pp < kParts; ++pp) sum += s_part[(pp * HMAX + h) * DKP + cc];
+      }
       s_qt[h][cc] = sum;
     }
     {  // q . delta_mu: 16 lanes per head, eight channels each
@@ -799,7 +810,12 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   const int64_t unit_bytes = unit_vis + unit_full;
   const int64_t total = p.units * unit_bytes;
   const int64_t slots = (int64_t)num_cus * g_wgs_per_cu;
-  int64_t rounds = cdiv(total, slots * g_max_wg_bytes);
+  // A unit with several query heads pays more per workgroup (q R for every
+  // head, one merge row each), so it takes larger chunks: measured on MI355X,
+  // a GQA group of 7 runs best in a single round of up to 4 MB workgroups,
+  // one query head per unit at 512 KB.
+  const int64_t max_wg = p.heads_per_unit > 1 ? 8 * g_max_wg_bytes : g_max_wg_bytes;
+  int64_t rounds = cdiv(total, slots * max_wg);
   if (rounds < 1) rounds = 1;
   int64_t budget = p.units > 0 ? rounds * slots / p.units : 1;
   const int64_t by_min = unit_bytes / g_min_wg_bytes;
