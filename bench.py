@@ -15,6 +15,8 @@ events around each launch on the launching stream) against the 8 TB/s HBM
 peak; ``cpu_baseline`` = the CPU oracle (numpy fp32) on a bounded sample of
 the same workload, scaled to a full step.  Also reported: hipGraph-replayed
 step time and the full-channel HIP baseline on the same seeded data.
+Working sets under 1 GB (configs 1 and 3) are cycled through up to eight
+copies of the inputs so that repeated steps read HBM, not the 256 MB MALL.
 
 ``--copy-calibration BYTES`` adds a plain device-to-device copy of BYTES
 bytes per step (after the timed region), so that a ``rocprofv3 --pmc
@@ -64,7 +66,9 @@ def _time_launches(fn, steps):
     return sum(s.elapsed_time(e) for s, e in evs) / steps * 1e3
 
 
-def _time_graph(fn, steps, warmup):
+def _time_graph(fn, steps, warmup, per_graph=1):
+    """hipGraph replay time per call of ``fn``; the graph holds ``per_graph``
+    consecutive calls (one per input copy when inputs are rotated)."""
     import torch
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -75,18 +79,20 @@ def _time_graph(fn, steps, warmup):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        fn()
+        for _ in range(per_graph):
+            fn()
     torch.cuda.synchronize()
     for _ in range(5):
         g.replay()
     torch.cuda.synchronize()
+    reps = max(1, -(-steps // per_graph))
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(steps):
+    for _ in range(reps):
         g.replay()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / steps * 1e3
+    return s.elapsed_time(e) / (reps * per_graph) * 1e3
 
 
 def _cpu_baseline(inp, cfg, budget_s=12.0):
@@ -276,11 +282,13 @@ def run_prefill(args):
     """Config 4 prefill, one layer per visual length, each stage timed on
     the device (HIP events over ``--steps`` repetitions): key covariance
     (mean pass + MFMA covariance pass + finalize), query weighting (torch),
-    eigh (torch, on the host as the reference), channel scores, top-k,
-    R_partial / delta_mu gather and the truncated Key write."""
+    eigh (torch, on the host as the reference), the HIP subspace iteration
+    (the reference's default solver), channel scores, top-k, R_partial /
+    delta_mu gather and the truncated Key write."""
     import torch
 
     from rotatek_amd import prefill, synth
+    from rotatek_amd.rotation import power_iteration_gpu
 
     c = synth.FLOW
     torch.cuda.set_device(0)
@@ -308,6 +316,7 @@ def run_prefill(args):
         (mean, cov), t_cov, _ = timed(lambda: prefill.key_covariance(kv))
         covw, t_qw, _ = timed(lambda: prefill.query_weight(cov, st["Q"], c.G))
         R_full, _, w_eigh = timed(lambda: prefill.eigen_rotation(covw))
+        _, t_pi, _ = timed(lambda: power_iteration_gpu(covw, keep, num_iters=5, seed=0))
         scores, t_sc, _ = timed(lambda: prefill.channel_scores(kv, R_full))
         (idx, mask), t_tk, _ = timed(lambda: prefill.topk_channels(scores, keep))
         (Rp, dmu), t_ga, _ = timed(lambda: prefill.gather_rotation(R_full, idx, mean, kv.dtype))
@@ -320,6 +329,7 @@ def run_prefill(args):
                "covariance_gbps_two_passes": round(2 * kbytes / t_cov / 1e3, 1),
                "covariance_mfma_tflops": round(cov_flops / t_cov / 1e6, 2),
                "query_weight_us": round(t_qw, 2), "eigh_host_us": round(w_eigh, 1),
+               "power_iteration_us": round(t_pi, 2),
                "channel_scores_us": round(t_sc, 2), "topk_us": round(t_tk, 2),
                "gather_us": round(t_ga, 2), "rotate_write_us": round(t_rot, 2),
                "rotate_write_gbps": round((kbytes + heads * S_v * keep * 2) / t_rot / 1e3, 1)}
@@ -377,12 +387,19 @@ def main():
     torch.cuda.set_device(0)
     _log(f"[bench] {torch.cuda.get_device_name(0)}; generating {cfg}")
     inp = synth.make_decode_inputs(cfg, "cuda", seed=0, with_dense=not args.no_dense)
-    dargs = synth.decode_args(inp)
+    nbytes = synth.decode_bytes(cfg)
+    # working sets under 1 GB would be served partly from the 256 MB MALL when
+    # the same inputs are read back to back: cycle through copies instead
+    copies = 1 if nbytes >= (1 << 30) else min(8, -(-(1 << 30) // nbytes))
+    sets = [inp] + [synth.clone_inputs(inp) for _ in range(copies - 1)]
+    dsets = [synth.decode_args(x) for x in sets]
     rot = rotatek_decode_gqa if args.family == "gqa" else rotatek_decode_fused
     dense = full_channel_decode_gqa if args.family == "gqa" else full_channel_decode
+    turn = [0, 0]
 
     def step():
-        return rot(**dargs)
+        turn[0] += 1
+        return rot(**dsets[turn[0] % copies])
 
     for _ in range(args.warmup):
         step()
@@ -390,28 +407,27 @@ def main():
     _log("[bench] warmup done")
     us = _time_wall(step, args.steps)
     us_launch = _time_launches(step, args.steps)
-    us_graph = _time_graph(step, args.steps, args.warmup) if not args.no_graph else None
-    nbytes = synth.decode_bytes(cfg)
+    us_graph = _time_graph(step, args.steps, args.warmup, copies) if not args.no_graph else None
     gbps = nbytes / (us_launch * 1e-6) / 1e9
     _log(f"[bench] rotatek eager {us:.1f} us/step, per-launch {us_launch:.1f} us, graph {us_graph} us, "
          f"{gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS * 100:.1f}% of peak)")
 
     extra = {}
     if not args.no_dense:
-        kd, vd = inp["k_dense"], inp["v_dense"]
-
         def dstep():
-            return dense(inp["q_full"], kd, vd, num_kv_groups=cfg.G)
+            turn[1] += 1
+            x = sets[turn[1] % copies]
+            return dense(x["q_full"], x["k_dense"], x["v_dense"], num_kv_groups=cfg.G)
 
         for _ in range(args.warmup):
             dstep()
         d_us = _time_wall(dstep, args.steps)
         d_launch = _time_launches(dstep, args.steps)
-        d_graph = _time_graph(dstep, args.steps, args.warmup) if not args.no_graph else None
+        d_graph = _time_graph(dstep, args.steps, args.warmup, copies) if not args.no_graph else None
         dbytes = synth.decode_bytes(cfg, dense=True)
         extra = {
             "dense_us_per_step": round(d_us, 2),
-            "dense_graph_us_per_step": round(d_graph, 2),
+            "dense_graph_us_per_step": round(d_graph, 2) if d_graph else None,
             "dense_achieved_gbps": round(dbytes / (d_launch * 1e-6) / 1e9, 1),
             "speedup_vs_dense": round(d_us / us, 3),
             "speedup_vs_dense_graph": round(d_graph / us_graph, 3) if d_graph else None,
@@ -457,6 +473,7 @@ def main():
         "achieved_gbps": round(gbps, 1),
         "pct_of_peak_hbm": round(gbps / HBM_PEAK_GBPS * 100, 2),
         "graph_us_per_step": round(us_graph, 2) if us_graph else None,
+        "input_copies": copies,
         "launch_us": round(us_launch, 2),
         "roofline": {
             "bound": "hbm",

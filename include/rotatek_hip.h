@@ -156,6 +156,15 @@ int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor* R_partial
                              const rk_tensor* out, int32_t policy, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* Top-k eigenbasis of each 128 x 128 covariance by subspace iteration with
+ * Cholesky-QR orthonormalisation, replacing rotation.py:21-91
+ * (_power_iter_loop; power_iteration_gpu draws v0 with torch.randn from a
+ * seeded device generator and calls this).  cov [B,H,128,128], v0 / out
+ * [B,H,128,k] F32, 1 <= k <= 64; per iteration V = C V, G = V^T V +
+ * eps * mean(diag G) * I, V = V chol(G)^-T.  out may alias v0. */
+int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, const rk_tensor* out, int32_t num_iters,
+                       float eps, void* stream);
+
 /* In-place decode append for the span cache (replaces the per-step
  * torch.cat of cache_utils.py:52-53): k_new/v_new [B,H,1,128] are written
  * to slot len_full[b] of k_buf/v_buf [B,H,capacity,128] and len_full[b] is

@@ -154,6 +154,22 @@ def make_decode_inputs(c: DecodeConfig, device="cuda", seed: int = 0, with_raw: 
     return out
 
 
+def clone_inputs(inp: dict) -> dict:
+    """Same values at new addresses (V cloned once, its span views re-derived),
+    so that a benchmark can cycle through copies and read from HBM rather than
+    from the 256 MB MALL."""
+    out = dict(inp)
+    S_v = inp["v_sparse"].shape[2]
+    V = inp["V"].clone()
+    out["V"], out["v_sparse"], out["v_full"] = V, V[:, :, :S_v], V[:, :, S_v:]
+    for k in ("q_full", "R_partial", "delta_mu", "k_full", "mask_full", "k_sparse", "k_dense"):
+        if inp.get(k) is not None:
+            out[k] = inp[k].clone()
+    if "v_dense" in inp:
+        out["v_dense"] = V
+    return out
+
+
 DECODE_KEYS = ("q_full", "R_partial", "delta_mu", "k_full", "v_full", "mask_full", "k_sparse",
                "v_sparse", "num_kv_groups")
 

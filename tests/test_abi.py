@@ -258,3 +258,19 @@ def test_append_kv_validation():
     assert lib.rk_append_kv(r(kn), None, r(kb), r(vb), 1, None) == -1          # V given for one side only
     empty_k, empty_b = _t((0, 4, 1, 128)), _t((0, 4, 64, 128))
     assert lib.rk_append_kv(r(empty_k), None, r(empty_b), None, 1, None) == 0   # nothing to do
+
+
+def test_power_iteration_validation():
+    lib = _lib.load()
+    r = ctypes.byref
+    cov, v0, out = _t((2, 4, 128, 128), _lib.RK_F32), _t((2, 4, 128, 16), _lib.RK_F32), _t((2, 4, 128, 16), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(cov), r(v0), r(out), 5, 1e-4, None) == -1        # no device memory
+    bad = _t((2, 4, 128, 16), _lib.RK_F16)
+    assert lib.rk_power_iteration(r(cov), r(bad), r(out), 5, 1e-4, None) == -3
+    wide = _t((2, 4, 128, 65), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(cov), r(wide), r(wide), 5, 1e-4, None) == -7     # k > 64
+    c64 = _t((2, 4, 64, 64), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(c64), r(v0), r(out), 5, 1e-4, None) == -6
+    o2 = _t((2, 4, 128, 8), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(cov), r(v0), r(o2), 5, 1e-4, None) == -4
+    assert lib.rk_power_iteration(r(cov), r(v0), r(out), -1, 1e-4, None) == -10

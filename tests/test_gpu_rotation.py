@@ -1,0 +1,85 @@
+"""GPU parity of the HIP subspace iteration (rk_power_iteration) with the
+float64 oracle of rotation.py:21-53 started from the same block V0, with
+the reference's torch loop on the device, and with eigh's subspace."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import prefill as op
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _cov(B, H, seed, gap=True):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    Q = torch.linalg.qr(torch.randn(B, H, 128, 128, generator=g, device="cuda", dtype=torch.float64))[0]
+    lam = torch.linspace(1.0, 0.01, 128, device="cuda", dtype=torch.float64)
+    if gap:
+        lam[:16] *= 20.0   # separated top block
+    lam = lam * (1 + 0.1 * torch.rand(B, H, 128, generator=g, device="cuda", dtype=torch.float64))
+    C = (Q * lam[..., None, :]) @ Q.transpose(-1, -2)
+    C = 0.5 * (C + C.transpose(-1, -2))
+    return C.float().contiguous()
+
+
+@pytest.mark.parametrize("k", [1, 16, 32, 40, 64])
+@pytest.mark.parametrize("eps", [1e-4, 1e-6])
+def test_power_iteration_matches_oracle_from_same_start(k, eps):
+    from rotatek_amd.rotation import power_iteration_hip
+    _say(f"power iteration k={k} eps={eps}")
+    cov = _cov(2, 3, seed=k)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    V0 = torch.randn(2, 3, 128, k, generator=g, device="cuda")
+    got = power_iteration_hip(cov, V0, 5, eps)
+    torch.cuda.synchronize()
+    want = op.power_iteration(cov.double().cpu().numpy(), V0.double().cpu().numpy(), 5, eps)
+    g_np = got.double().cpu().numpy()
+    assert np.abs(g_np - want).max() < 2e-3 * max(1.0, np.abs(want).max())
+    # V^T V is the identity only up to the ridge (the reference's Cholesky
+    # guard, rotation.py:36-50): it must deviate exactly as the oracle's does
+    VtV = np.swapaxes(g_np, -1, -2) @ g_np
+    VtV_want = np.swapaxes(want, -1, -2) @ want
+    assert np.abs(VtV - VtV_want).max() < 2e-3
+    if eps == 1e-6:
+        assert np.abs(VtV - np.eye(k)).max() < 1e-2
+
+
+def test_power_iteration_agrees_with_torch_loop_and_eigh():
+    from rotatek_amd import rotation
+    _say("power iteration vs torch loop / eigh")
+    cov = _cov(4, 4, seed=99)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    V0 = torch.randn(4, 4, 128, 16, generator=g, device="cuda")
+    hip = rotation.power_iteration_hip(cov, V0, 5, 1e-4)
+    ref = rotation._power_iter_loop(cov, V0.clone(), 5, 1e-4)
+    torch.cuda.synchronize()
+    assert (hip - ref).abs().max().item() < 2e-3
+    # the gapped top-16 block: projector equals eigh's
+    w, U = torch.linalg.eigh(cov.double().cpu())
+    Ut = U[..., -16:]
+    P_e = Ut @ Ut.transpose(-1, -2)
+    H = hip.double().cpu()
+    P_h = H @ H.transpose(-1, -2)
+    assert (P_e - P_h).abs().max().item() < 2e-2
+
+
+def test_power_iteration_gpu_uses_hip_and_zero_iterations():
+    from rotatek_amd import rotation
+    _say("power_iteration_gpu dispatch / iters=0")
+    cov = _cov(1, 2, seed=3)
+    out = rotation.power_iteration_gpu(cov, k=32, num_iters=5, seed=0)
+    g = torch.Generator(device="cuda").manual_seed(0)
+    V0 = torch.randn(1, 2, 128, 32, device="cuda", generator=g)
+    same = rotation.power_iteration_hip(cov, V0, 5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, same)
+    zero = rotation.power_iteration_hip(cov, V0, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(zero, V0)
