@@ -266,12 +266,21 @@ rot_kernel(const RotArgs a) {
   const int x = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.k.H, h = bh - b * a.k.H;
   const uint16_t* base = head_base(a.k, bh);
-  // stage R^T (kept rows >= Dk are zero) in the key dtype
+  // stage R^T (kept rows >= Dk are zero) in the key dtype.  Element e of
+  // this thread's batch is (c, kk) = (e % 128, e / 128): consecutive threads
+  // take consecutive c; all loads are issued before any is converted.
   const int64_t rb = b * a.R_sb + (int64_t)h * a.R_sh;
-  for (int e = tid; e < NT * 16 * 128; e += kThreads) {
-    const int kk = e >> 7, c = e & 127;
-    const float v = kk < a.Dk ? load_any(a.R, rb + c * a.R_sd + kk * a.R_sk, a.r_dtype) : 0.f;
-    s_rt[kk][c] = TT::from_f32(v);
+  constexpr int kPer = NT * 16 * 128 / kThreads;
+  uint32_t raw[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid + i * kThreads, kk = e >> 7, c = e & 127;
+    raw[i] = load_raw(a.R, rb + c * a.R_sd + min(kk, a.Dk - 1) * a.R_sk, a.r_dtype);
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid + i * kThreads, kk = e >> 7, c = e & 127;
+    s_rt[kk][c] = TT::from_f32(kk < a.Dk ? raw_to_f32(raw[i], a.r_dtype) : 0.f);
   }
   __syncthreads();
 
@@ -281,41 +290,53 @@ rot_kernel(const RotArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) sc[t][r] = 0.f;
   const int64_t t0 = (int64_t)x * a.chunk, t1 = min(a.k.S, t0 + a.chunk);
-  const int64_t nstep = (t1 - t0 + 63) / 64;
+  // steps of TB 16-token column blocks, double-buffered: the next step's
+  // loads are in flight while this one is on the MFMA (steps past the end
+  // reload the last token, in bounds, and are not computed).  The score
+  // variant takes 64-token steps (each R^T fragment feeds four MFMAs); the
+  // store variant 32-token steps, so its output path fits in registers.
+  constexpr int TB = SCORE ? 4 : 2;
+  constexpr int kStep = 16 * TB;
+  const int64_t nstep = (t1 - t0 + kStep - 1) / kStep;
   const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
-  for (int64_t st = wave; st < nstep; st += kWaves) {
-    const int64_t ts = t0 + st * 64;
-    uint4 bk[4][4];  // [token block][k-step]
+  auto load = [&](uint4 (&bk)[TB][4], int64_t st) {
+    const int64_t ts = t0 + st * kStep;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tb = 0; tb < TB; ++tb) {
       const int64_t tok = ts + 16 * tb + n;
-      const uint32_t tr = min((uint32_t)tok, last);
+      const uint32_t tr = min((uint32_t)min(tok, (int64_t)last), last);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        uint4 v = ldrow<VEC>(base, a.k, tr, (uint32_t)(32 * ks + 8 * g));
-        if (SCORE && tok >= t1) v = make_uint4(0, 0, 0, 0);
-        bk[tb][ks] = v;
-      }
+      for (int ks = 0; ks < 4; ++ks) bk[tb][ks] = ldrow<VEC>(base, a.k, tr, (uint32_t)(32 * ks + 8 * g));
+    }
+  };
+  auto compute = [&](uint4 (&bk)[TB][4], int64_t st) {
+    const int64_t ts = t0 + st * kStep;
+    if constexpr (SCORE) {
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb)
+        if (ts + 16 * tb + n >= t1)
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) bk[tb][ks] = make_uint4(0, 0, 0, 0);
     }
 #pragma unroll(NT <= 2 ? NT : 1)
     for (int t = 0; t < NT; ++t) {
-      f32x4 c[4];
+      f32x4 c[TB];
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int tb = 0; tb < TB; ++tb) c[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const uint4 av = *(const uint4*)&s_rt[16 * t + n][32 * ks + 8 * g];
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) c[tb] = TT::mfma(av, bk[tb][ks], c[tb]);
+        for (int tb = 0; tb < TB; ++tb) c[tb] = TT::mfma(av, bk[tb][ks], c[tb]);
       }
       if constexpr (SCORE) {
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
+        for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) sc[t][r] += fabsf(c[tb][r]);
       } else {
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+        for (int tb = 0; tb < TB; ++tb) {
           const int64_t tok = ts + 16 * tb + n;
           if (tok < t1) {
             uint16_t* o = a.out + b * a.o_sb + (int64_t)h * a.o_sh + tok * a.o_ss;
@@ -334,6 +355,15 @@ rot_kernel(const RotArgs a) {
         }
       }
     }
+  };
+  uint4 bA[TB][4], bB[TB][4];
+  if (wave < nstep) load(bA, wave);
+  for (int64_t st = wave; st < nstep; st += 2 * kWaves) {
+    load(bB, st + kWaves);
+    compute(bA, st);
+    if (st + kWaves >= nstep) break;
+    load(bA, st + 2 * kWaves);
+    compute(bB, st + kWaves);
   }
   if constexpr (SCORE) {
     // lanes of one row (fixed g) hold different tokens of the same channels
