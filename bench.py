@@ -280,7 +280,8 @@ def run_flow(args):
 
 def run_prefill(args):
     """Config 4 prefill, one layer per visual length, each stage timed on
-    the device (HIP events over ``--steps`` repetitions): key covariance
+    the device (HIP events over ``--steps`` repetitions, replayed from a HIP
+    graph where the stage is device-only): key covariance
     (mean pass + MFMA covariance pass + finalize), query weighting (torch),
     eigh (torch, on the host as the reference), the HIP subspace iteration
     (the reference's default solver), channel scores, top-k, R_partial /
@@ -297,14 +298,32 @@ def run_prefill(args):
     keep = 32
     rows = []
 
-    def timed(fn):
-        fn()
+    def timed(fn, graph=True):
+        """(result, device us per call, wall us per call).  Device-only stages
+        are replayed from a HIP graph, so small kernels are not timed at the
+        speed of the Python call that launches them."""
+        out = fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if graph:
+            g = torch.cuda.CUDAGraph()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(g, stream=side):
+                    for _ in range(reps):
+                        fn()
+            torch.cuda.current_stream().wait_stream(side)
+            g.replay()
+            torch.cuda.synchronize()
+            run = g.replay
+        else:
+            def run():
+                for _ in range(reps):
+                    fn()
         t0 = time.perf_counter()
         e0.record()
-        for _ in range(reps):
-            out = fn()
+        run()
         e1.record()
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) / reps * 1e6
@@ -315,8 +334,8 @@ def run_prefill(args):
         kv = st["K"][:, :, c.prompt:c.prompt + S_v]
         (mean, cov), t_cov, _ = timed(lambda: prefill.key_covariance(kv))
         covw, t_qw, _ = timed(lambda: prefill.query_weight(cov, st["Q"], c.G))
-        R_full, _, w_eigh = timed(lambda: prefill.eigen_rotation(covw))
-        _, t_pi, _ = timed(lambda: power_iteration_gpu(covw, keep, num_iters=5, seed=0))
+        R_full, _, w_eigh = timed(lambda: prefill.eigen_rotation(covw), graph=False)
+        _, t_pi, _ = timed(lambda: power_iteration_gpu(covw, keep, num_iters=5, seed=0), graph=False)
         scores, t_sc, _ = timed(lambda: prefill.channel_scores(kv, R_full))
         (idx, mask), t_tk, _ = timed(lambda: prefill.topk_channels(scores, keep))
         (Rp, dmu), t_ga, _ = timed(lambda: prefill.gather_rotation(R_full, idx, mean, kv.dtype))

@@ -448,24 +448,42 @@ __global__ void __launch_bounds__(128) gather_kernel(const void* R, int r_dtype,
   __shared__ float s_mu[128];
   __shared__ float s_proj[128];
   __shared__ int64_t s_col[128];
+  __shared__ uint16_t s_rp[128][130];  // R_partial in the key dtype, row d
   const int d = threadIdx.x, bh = blockIdx.x;
   const int b = bh / H, h = bh - b * H;
   s_mu[d] = mu[b * u_b + (int64_t)h * u_h + d * u_c];
   if (d < k) s_col[d] = idx[b * i_b + (int64_t)h * i_h + d * i_k];
   __syncthreads();
-  const int64_t rb = b * R_sb + (int64_t)h * R_sh;
-  auto rp = [&](int row, int kk) {
-    return TT::from_f32(load_any(R, rb + row * R_sd + s_col[kk] * R_sk, r_dtype));
-  };
-  for (int kk = 0; kk < k; ++kk) Rp[b * p_b + (int64_t)h * p_h + d * p_d + kk * p_k] = rp(d, kk);
+  // row d of R_partial, 32 columns per pass: all loads of a pass are issued
+  // before any store (the stores could alias them otherwise)
+  const int64_t rb = b * R_sb + (int64_t)h * R_sh + d * R_sd;
+  for (int k0 = 0; k0 < k; k0 += 32) {
+    uint32_t raw[32];
+    if (r_dtype == 2) {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) raw[j] = ((const uint32_t*)R)[rb + s_col[min(k0 + j, k - 1)] * R_sk];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) raw[j] = ((const uint16_t*)R)[rb + s_col[min(k0 + j, k - 1)] * R_sk];
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      if (k0 + j < k) {
+        const uint16_t v = TT::from_f32(raw_to_f32(raw[j], r_dtype));
+        s_rp[d][k0 + j] = v;
+        Rp[b * p_b + (int64_t)h * p_h + d * p_d + (k0 + j) * p_k] = v;
+      }
+    }
+  }
+  __syncthreads();
   if (d < k) {
     float s = 0.f;
-    for (int e = 0; e < 128; ++e) s += s_mu[e] * TT::to_f32(rp(e, d));
+    for (int e = 0; e < 128; ++e) s += s_mu[e] * TT::to_f32(s_rp[e][d]);
     s_proj[d] = s;
   }
   __syncthreads();
   float p = 0.f;
-  for (int kk = 0; kk < k; ++kk) p += s_proj[kk] * TT::to_f32(rp(d, kk));
+  for (int kk = 0; kk < k; ++kk) p += s_proj[kk] * TT::to_f32(s_rp[d][kk]);
   dm[b * d_b + (int64_t)h * d_h + d * d_c] = TT::from_f32(s_mu[d] - p);
 }
 
