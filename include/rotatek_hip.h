@@ -156,6 +156,13 @@ int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor* R_partial
                              const rk_tensor* out, int32_t policy, void* workspace,
                              size_t workspace_bytes, void* stream);
 
+/* Query-aware weighting of the Key covariance, replacing
+ * kv_pruning_utils.py:116-140: cov [B,H_kv,128,128] F32, queries
+ * [B,H_kv*G,S,128] F16/BF16 (the last min(window, S) rows are used,
+ * window <= 32), out like cov (may alias it). */
+int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, int64_t num_kv_groups, int32_t window,
+                    const rk_tensor* out, void* stream);
+
 /* Top-k eigenbasis of each 128 x 128 covariance by subspace iteration with
  * Cholesky-QR orthonormalisation, replacing rotation.py:21-91
  * (_power_iter_loop; power_iteration_gpu draws v0 with torch.randn from a

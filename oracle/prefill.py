@@ -81,9 +81,20 @@ def query_weight(cov, queries, num_kv_groups: int, window: int = QUERY_WINDOW,
     w = min(window, Q.shape[2])
     Qr = Q[..., -w:, :]
     if Qr.shape[1] != Hkv:
-        Qr = Qr.reshape(B, Hkv, num_kv_groups, w, D).mean(axis=2)
-        if dtype is not None:
-            Qr = round_to(Qr, dtype)
+        # torch's mean of a bf16/fp16 tensor accumulates in fp32 and scales by
+        # the fp32 factor 1/G before rounding to the tensor's dtype
+        # (ATen mean_kernel_impl / MeanOps::project: acc * factor); with a
+        # non-power-of-two G that differs from an exact division
+        # (dtype None / float64: exact arithmetic)
+        grp = Qr.reshape(B, Hkv, num_kv_groups, w, D)
+        if dtype in ("bfloat16", "float16", "float32"):
+            grp = grp.astype(np.float32)
+            acc = np.zeros(grp.shape[:2] + grp.shape[3:], np.float32)
+            for g in range(num_kv_groups):
+                acc = acc + grp[:, :, g]
+            Qr = round_to((acc * np.float32(1.0 / num_kv_groups)).astype(np.float64), dtype)
+        else:
+            Qr = grp.mean(axis=2)
     qn = np.sqrt((Qr ** 2).sum(axis=-2))                           # [B,Hkv,D]
     med = np.sort(qn, axis=-1)[..., (D - 1) // 2]                  # lower median
     qn = np.maximum(qn, 1e-3 * med[..., None])

@@ -222,7 +222,9 @@ __global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int
     a3 += src[(int64_t)(x + 3) * (kTiles * 256)];
   }
   for (; x < splits; ++x) a0 += src[(int64_t)x * (kTiles * 256)];
-  s_t[tid] = TT::to_f32(TT::from_f32((a0 + a1) + (a2 + a3)));
+  float sum = (a0 + a1) + (a2 + a3);  // fp32, then the key dtype (two roundings)
+  asm volatile("" : "+v"(sum));
+  s_t[tid] = TT::to_f32(TT::from_f32(sum));
   __syncthreads();
   const int i = tile_row(t), j = tile_col(t), m = tid >> 4, n = tid & 15;
   float* cb = cov + b * cs_b + (int64_t)h * cs_h;
@@ -484,7 +486,105 @@ __global__ void __launch_bounds__(128) gather_kernel(const void* R, int r_dtype,
   __syncthreads();
   float p = 0.f;
   for (int kk = 0; kk < k; ++kk) p += s_proj[kk] * TT::to_f32(s_rp[d][kk]);
-  dm[b * d_b + (int64_t)h * d_h + d * d_c] = TT::from_f32(s_mu[d] - p);
+  float dmu = s_mu[d] - p;           // fp32, then the key dtype (two roundings,
+  asm volatile("" : "+v"(dmu));      // as the reference; see qweight_kernel)
+  dm[b * d_b + (int64_t)h * d_h + d * d_c] = TT::from_f32(dmu);
+}
+
+// grid (B*H_kv), 256 threads: query-aware weighting of one covariance
+// (kv_pruning_utils.py:116-140).  q_norm[d] = || mean_g q[g, S-W+w, d] ||_2
+// over the last W queries, the group mean (over the G query heads of the KV
+// head) rounded to the query dtype as torch's bf16/fp16 mean is; floored at
+// 1e-3 x the lower median of the 128 norms; then
+//   out = 0.5 (C o (qn qn^T) + (C o (qn qn^T))^T) + max(1e-4 mean|diag|, 1e-6) I.
+// Thread (d, half) accumulates 16 of the W window rows of channel d; the two
+// halves are added in LDS.  out may alias cov.
+template <class TT>
+__global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t c_b, int64_t c_h, int64_t c_r,
+                                                      int64_t c_c, const uint16_t* q, int64_t q_b, int64_t q_h,
+                                                      int64_t q_s, int64_t q_d, int64_t S, int W, int G,
+                                                      float* out, int64_t o_b, int64_t o_h, int64_t o_r,
+                                                      int64_t o_c, int H) {
+  __shared__ float s_sq[2][128];
+  __shared__ float s_qn[128];
+  __shared__ float s_diag[128];
+  __shared__ float s_floor, s_ridge;
+  const int tid = threadIdx.x, d = tid & 127, half = tid >> 7;
+  const int bh = blockIdx.x, b = bh / H, kv = bh - b * H;
+  const float inv_g = 1.f / (float)G;
+  // window rows w = 16 half + i, i < 16 (rows past W are skipped)
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  const uint16_t* qb = q + b * q_b + (int64_t)(kv * G) * q_h + (S - W) * q_s + d * q_d;
+  for (int gg = 0; gg < G; ++gg) {
+    const uint16_t* qg = qb + (int64_t)gg * q_h;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int w = 16 * half + i;
+      acc[i] += w < W ? TT::to_f32(qg[(int64_t)min(w, W - 1) * q_s]) : 0.f;
+    }
+  }
+  float sq = 0.f;
+  {
+    // group mean in the query dtype: the fp32 product is rounded to fp32
+    // first and then to the dtype, as torch's MeanOps does.  The empty asm
+    // keeps the product in an fp32 register; otherwise the compiler fuses
+    // the multiply and the fp16 conversion into one v_fma_mixlo_f16, a
+    // single rounding of the exact product.
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float prod = acc[i] * inv_g;
+      asm volatile("" : "+v"(prod));
+      const float m = TT::to_f32(TT::from_f32(prod));
+      sq = fmaf(m, m, sq);
+    }
+  }
+  s_sq[half][d] = sq;
+  __syncthreads();
+  if (tid < 128) s_qn[d] = sqrtf(s_sq[0][d] + s_sq[1][d]);
+  __syncthreads();
+  if (tid < 128) {  // lower median: the element of rank 63 (ties by index)
+    const float v = s_qn[d];
+    int rank = 0;
+    for (int j = 0; j < 128; ++j) {
+      const float u = s_qn[j];
+      rank += (u < v) || (u == v && j < d);
+    }
+    if (rank == 63) s_floor = 1e-3f * v;
+  }
+  __syncthreads();
+  const float* C = cov + b * c_b + (int64_t)kv * c_h;
+  if (tid < 128) {
+    const float qd = fmaxf(s_qn[d], s_floor);
+    s_qn[d] = qd;
+    s_diag[d] = fabsf(C[d * c_r + d * c_c] * (qd * qd));
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sd = 0.f;
+    for (int j = 0; j < 128; ++j) sd += s_diag[j];
+    s_ridge = fmaxf(1e-4f * (sd * (1.f / 128.f)), 1e-6f);
+  }
+  __syncthreads();
+  // every output element reads its two mirrored inputs before the workgroup
+  // writes anything (out may alias cov)
+  const float ridge = s_ridge;
+  float res[64];
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const int e = tid + i * 256, r = e >> 7, c = e & 127;
+    const float wrc = s_qn[r] * s_qn[c], wcr = s_qn[c] * s_qn[r];
+    const float a = C[r * c_r + c * c_c] * wrc, bt = C[c * c_r + r * c_c] * wcr;
+    res[i] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
+  }
+  __syncthreads();
+  float* O = out + b * o_b + (int64_t)kv * o_h;
+#pragma unroll
+  for (int i = 0; i < 64; ++i) {
+    const int e = tid + i * 256, r = e >> 7, c = e & 127;
+    O[r * o_r + c * o_c] = res[i];
+  }
 }
 
 }  // namespace prefill
@@ -840,5 +940,40 @@ extern "C" int rk_gather_rotation(const rk_tensor* R_full, const rk_tensor* idx,
     go(rk::F16{});
   else
     go(rk::BF16{});
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+extern "C" int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, int64_t num_kv_groups,
+                               int32_t window, const rk_tensor* out, void* stream) {
+  if (!cov || !queries || !out) return RK_ERR_NULL;
+  int st;
+  if ((st = rk::check_desc(cov, 4)) || (st = rk::check_desc(queries, 4)) || (st = rk::check_desc(out, 4)))
+    return st;
+  if (cov->dtype != RK_F32 || out->dtype != RK_F32 || !rk::is_half(queries->dtype)) return RK_ERR_DTYPE;
+  const int64_t B = cov->shape[0], H = cov->shape[1];
+  if (cov->shape[2] != 128 || cov->shape[3] != 128 || queries->shape[3] != 128) return RK_ERR_HEAD_DIM;
+  for (int i = 0; i < 4; ++i)
+    if (out->shape[i] != cov->shape[i]) return RK_ERR_SHAPE;
+  if (num_kv_groups <= 0 || queries->shape[0] != B || queries->shape[1] != H * num_kv_groups) return RK_ERR_HEADS;
+  const int64_t S = queries->shape[2];
+  if (window <= 0 || window > 32) return RK_ERR_ARG;
+  const int W = (int)(S < window ? S : window);
+  if (B * H == 0) return RK_OK;
+  if (W == 0) return RK_ERR_SHAPE;
+  if (!cov->data || !queries->data || !out->data) return RK_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)(B * H));
+  if (queries->dtype == RK_F16)
+    hipLaunchKernelGGL((qweight_kernel<rk::F16>), grid, dim3(256), 0, s, (const float*)cov->data, cov->stride[0],
+                       cov->stride[1], cov->stride[2], cov->stride[3], (const uint16_t*)queries->data,
+                       queries->stride[0], queries->stride[1], queries->stride[2], queries->stride[3], S, W,
+                       (int)num_kv_groups, (float*)out->data, out->stride[0], out->stride[1], out->stride[2],
+                       out->stride[3], (int)H);
+  else
+    hipLaunchKernelGGL((qweight_kernel<rk::BF16>), grid, dim3(256), 0, s, (const float*)cov->data,
+                       cov->stride[0], cov->stride[1], cov->stride[2], cov->stride[3],
+                       (const uint16_t*)queries->data, queries->stride[0], queries->stride[1],
+                       queries->stride[2], queries->stride[3], S, W, (int)num_kv_groups, (float*)out->data,
+                       out->stride[0], out->stride[1], out->stride[2], out->stride[3], (int)H);
   return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
 }

@@ -13,9 +13,10 @@ Functional building blocks of ``ChannelPruner.update_rotatek``
 * ``gather_rotation``  ``R_partial = dtype(R[:, idx])`` and
                        ``delta_mu = dtype(mu - (mu R_partial) R_partial^T)``
                        (kv_pruning_utils.py:150-156)
+* ``query_weight``     query-aware weighting of the covariance
+                       (kv_pruning_utils.py:116-140)
 
-and, in torch on the device (small 128 x 128 matrices, as the reference):
-``query_weight`` (kv_pruning_utils.py:116-140) and ``eigen_rotation``
+and, in torch (LAPACK on the host, as the reference): ``eigen_rotation``
 (kv_pruning_utils.py:146-150).
 """
 from __future__ import annotations
@@ -107,24 +108,22 @@ def gather_rotation(R_full: torch.Tensor, idx: torch.Tensor, mean: torch.Tensor,
     return Rp, dmu
 
 
-def query_weight(cov: torch.Tensor, query_states: torch.Tensor, num_key_value_groups: int) -> torch.Tensor:
-    """Query-aware weighting of the covariance (kv_pruning_utils.py:116-140):
-    the last ``QUERY_WINDOW`` queries, group-mean H_q -> H_kv, per-channel L2
-    norm over tokens floored at 1e-3 x median, ``cov * outer(qn, qn)``,
-    symmetrised, plus a ridge of 1e-4 x mean|diag| (>= 1e-6) on the diagonal."""
-    bsz, num_kv_heads, _, head_dim = cov.shape
-    query_window = min(QUERY_WINDOW, query_states.shape[2])
-    queries_recent = query_states[..., -query_window:, :]
-    if queries_recent.shape[1] != num_kv_heads:
-        queries_recent = queries_recent.reshape(bsz, num_kv_heads, num_key_value_groups, query_window,
-                                                head_dim).mean(dim=2)
-    q_norm = queries_recent.float().norm(dim=-2, p=2)
-    q_floor = 1e-3 * q_norm.median(dim=-1, keepdim=True).values
-    q_norm = q_norm.clamp(min=q_floor)
-    cov = cov * (q_norm.unsqueeze(-1) * q_norm.unsqueeze(-2))
-    cov = 0.5 * (cov + cov.transpose(-1, -2))
-    ridge = 1e-4 * cov.diagonal(dim1=-2, dim2=-1).abs().mean(dim=-1, keepdim=True).clamp(min=1e-6).unsqueeze(-1)
-    return cov + ridge * torch.eye(head_dim, device=cov.device, dtype=cov.dtype)
+def query_weight(cov: torch.Tensor, query_states: torch.Tensor, num_key_value_groups: int,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """Query-aware weighting of the covariance (kv_pruning_utils.py:116-140)
+    in one HIP kernel (``rk_query_weight``): the last ``QUERY_WINDOW``
+    queries, group-mean H_q -> H_kv in the query dtype, per-channel L2 norm
+    over tokens floored at 1e-3 x the lower median, ``cov * outer(qn, qn)``,
+    symmetrised, plus a ridge of 1e-4 x mean|diag| (>= 1e-6) on the
+    diagonal.  ``out`` may be ``cov`` itself."""
+    _gpu(cov, "cov")
+    if out is None:
+        out = torch.empty_like(cov)
+    dc, dq, do = _lib.desc(cov), _lib.desc(query_states), _lib.desc(out)
+    _lib.check(_lib.load().rk_query_weight(ctypes.byref(dc), ctypes.byref(dq), int(num_key_value_groups),
+                                           QUERY_WINDOW, ctypes.byref(do), _lib.stream_handle(cov.device)),
+               "query_weight")
+    return out
 
 
 def eigen_rotation(cov: torch.Tensor, on_host: bool = True) -> torch.Tensor:

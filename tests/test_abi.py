@@ -274,3 +274,15 @@ def test_power_iteration_validation():
     o2 = _t((2, 4, 128, 8), _lib.RK_F32)
     assert lib.rk_power_iteration(r(cov), r(v0), r(o2), 5, 1e-4, None) == -4
     assert lib.rk_power_iteration(r(cov), r(v0), r(out), -1, 1e-4, None) == -10
+
+
+def test_query_weight_validation():
+    lib = _lib.load()
+    r = ctypes.byref
+    cov, out = _t((2, 4, 128, 128), _lib.RK_F32), _t((2, 4, 128, 128), _lib.RK_F32)
+    q = _t((2, 28, 50, 128), _lib.RK_BF16)
+    assert lib.rk_query_weight(r(cov), r(q), 7, 32, r(out), None) == -1      # no device memory
+    assert lib.rk_query_weight(r(cov), r(q), 5, 32, r(out), None) == -5      # H_q != H_kv * G
+    assert lib.rk_query_weight(r(cov), r(q), 7, 33, r(out), None) == -10     # window above 32
+    q32 = _t((2, 28, 50, 128), _lib.RK_F32)
+    assert lib.rk_query_weight(r(cov), r(q32), 7, 32, r(out), None) == -3

@@ -234,3 +234,24 @@ def test_update_rotatek_score_rule_and_edge_ratios():
         R = pr.current_rotatek_R_partial.float()
         eye = torch.eye(keep, device="cuda")
         assert (R.transpose(-1, -2) @ R - eye).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("G,S", [(7, 1200), (1, 40), (4, 9)])
+def test_query_weight_matches_oracle(dtype, G, S):
+    """HIP query weighting (window 32, or S when shorter) against the oracle
+    on the same covariance and queries; in place and out of place agree."""
+    from rotatek_amd import prefill
+    _say(f"query_weight {dtype} G={G} S={S}")
+    B, H = 2, 3
+    K = _lowrank_keys(B, H, 300, dtype, seed=G + S)
+    _, cov = prefill.key_covariance(K)
+    Q = (torch.randn(B, H * G, S, 128, device="cuda") * 1.5).to(dtype)
+    got = prefill.query_weight(cov, Q, G)
+    inplace = cov.clone()
+    prefill.query_weight(inplace, Q, G, out=inplace)
+    torch.cuda.synchronize()
+    assert torch.equal(got, inplace)
+    want = op.query_weight(_np(cov), _np(Q), G, dtype="bfloat16" if dtype == torch.bfloat16 else "float16")
+    scale = np.abs(want).max()
+    assert np.abs(_np(got) - want).max() <= 1e-5 * scale

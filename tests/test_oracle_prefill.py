@@ -218,3 +218,29 @@ def test_update_rotatek_score_rule_picks_outlier_channels():
     for h in range(H):
         assert {2, 9} <= set(r["keep_idx"][0, h].tolist())
     np.testing.assert_allclose(r["R_partial"][0, 0], np.eye(D)[:, r["keep_idx"][0, 0]])
+
+
+def test_query_weight_group_mean_uses_fp32_factor():
+    """The bf16 group mean is fp32(sum) * fp32(1/G), rounded (torch's MeanOps),
+    not the exact quotient: find a group of 7 bf16 values where the two
+    roundings differ and check the oracle takes the torch one."""
+    from oracle.numerics import round_bf16
+    rng = np.random.default_rng(11)
+    G, D = 7, 128
+    for _ in range(200):
+        vals = round_bf16(rng.standard_normal((G, D)) * 3).astype(np.float64)
+        s32 = vals.astype(np.float32).sum(axis=0, dtype=np.float32)
+        torch_like = round_bf16((s32 * np.float32(1.0 / G)).astype(np.float64))
+        exact = round_bf16(vals.sum(axis=0) / G)
+        if np.any(torch_like != exact):
+            break
+    else:
+        pytest.fail("no distinguishing group found")
+    q = np.zeros((1, G, 1, D))
+    q[0, :, 0, :] = vals
+    cov = np.eye(D)[None, None]
+    got = op.query_weight(cov, q, num_kv_groups=G, dtype="bfloat16")
+    qn = np.abs(torch_like).astype(np.float64)
+    qn = np.maximum(qn, 1e-3 * np.sort(qn)[(D - 1) // 2])
+    d = np.diag(got[0, 0])
+    np.testing.assert_allclose(d - max(1e-4 * (qn ** 2).mean(), 1e-6), qn ** 2, rtol=1e-12)
