@@ -401,15 +401,15 @@ decode_kernel(const DecodeArgs a) {
   const uint32_t krow0 = 8 * (n >> 2) + (n & 3), krow1 = krow0 + 4;
   const uint32_t rot_seed = ((uint32_t)u * 0x9E3779B1u) ^ ((uint32_t)x * 0x85EBCA77u);
 
-  // Prologue order: issue the prologue's own loads (q rows, and R / delta_mu
-  // or the mask bytes), then the first NBUF K/V blocks, and only then wait
-  // for the prologue data, so its latency hides under the first blocks.
+  // Prologue order: the first NBUF K/V blocks are requested, then the
+  // prologue's own loads (q rows; R / delta_mu or the mask bytes), and only
+  // then does anything wait, so one memory latency covers them all.  Loads
+  // are unconditional from clamped (in-bounds) addresses and masked after:
+  // a load under a divergent branch compiles to its own wait.
   constexpr int kQPer = (HMAX * 128 + kThreads - 1) / kThreads;
   float qv[kQPer];
-  // q rows: unconditional loads from clamped (in-bounds) rows, masked after,
-  // so every load of the prologue is in flight at once
-  // Fast layout: thread t loads channels 8 (t & 15) .. + 7 of head t >> 4
-  // (clamped to a valid head) with one 16-byte load.
+  // q rows, fast layout: thread t loads channels 8 (t & 15) .. + 7 of head
+  // t >> 4 (clamped to a valid head) with one 16-byte load.
   uint16_t qraw[kQPer];
   uint4 q16 = make_uint4(0u, 0u, 0u, 0u);
   // load_q issues the fast-layout load before the first K/V blocks; the
