@@ -18,6 +18,10 @@ LIB_PATH = os.path.join(HERE, "librotatek_hip.so")
 
 RK_F16, RK_BF16, RK_F32, RK_F64, RK_U8, RK_I32, RK_I64 = range(7)
 RK_POLICY_PAPER, RK_POLICY_GQA = 0, 1
+# rk_status (include/rotatek_hip.h)
+(RK_OK, RK_ERR_NULL, RK_ERR_RANK, RK_ERR_DTYPE, RK_ERR_SHAPE, RK_ERR_HEADS, RK_ERR_HEAD_DIM, RK_ERR_KEEP_DIM,
+ RK_ERR_STRIDE, RK_ERR_WORKSPACE, RK_ERR_ARG, RK_ERR_HIP, RK_ERR_NO_DEVICE) = (0, -1, -2, -3, -4, -5, -6, -7, -8,
+                                                                               -9, -10, -11, -12)
 
 _DTYPES = {
     torch.float16: RK_F16,
@@ -89,6 +93,19 @@ _SIGNATURES = {
     "rk_channel_scores": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rk_topk_channels": (ctypes.c_int, [_P, ctypes.c_int64, _P, _P, ctypes.c_void_p]),
     "rk_gather_rotation": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_void_p]),
+    "rk_think_score_and_compact_check": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P,
+                                                        ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
+    "rk_think_score_and_compact": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P,
+                                                  ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "rk_spark_prune_check": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P, _P,
+                                            ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
+    "rk_spark_prune": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P, _P,
+                                      ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "rk_think_recover_check": (ctypes.c_int, [_P, _P, _P, _P, _P]),
+    "rk_think_recover": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_void_p]),
+    "rk_spark_recover_check": (ctypes.c_int, [_P, _P, _P, _P, _P, _P]),
+    "rk_spark_recover": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, ctypes.c_void_p]),
+    "rk_channel_selection": (ctypes.c_int, [_P, _P, ctypes.c_void_p]),
 }
 
 _lib = None

@@ -1,0 +1,841 @@
+// rk_baselines.hip -- the ThinK and SparK Key channel-pruning baselines on
+// MI355X (gfx950): prefill scoring, selection and compaction, and the
+// decode-time recovery of full-width visual Keys that both baselines feed to
+// the dense decode kernel.
+//
+// ThinK (rotatek/baselines/think.py:15-58): one channel subset per KV head.
+//   sqsum_kernel         split-S fp32 partial sums of dtype(k^2) per channel
+//   think_select_kernel  keys_norm = dtype(sum * f_S), queries_norm =
+//                        dtype(mean over the group of dtype(mean over the
+//                        window of dtype(q^2))), score = dtype(qn * kn);
+//                        prune the prune_count smallest scores -> keep mask
+//                        and ascending kept indices
+//   compact_kernel       K_compact[..., j] = K[..., idx[j]]
+// SparK (rotatek/baselines/spark.py:15-60, with the group mean of the
+// queries from kv_pruning_utils.py:76-79): one channel subset per token.
+//   spark_qnorm_kernel   q_g = dtype(mean over the G query heads of a KV
+//                        head), q_norm = dtype(||q_g||_2 over the window)
+//   spark_kernel         one wave per token: score = dtype(dtype(k^2) qn);
+//                        keep the Dk largest by a radix select over
+//                        (score, channel) keys; writes K_compact, the
+//                        per-token mask and dtype(mean of the pruned values)
+// Recovery (llama_visionzip.py:216-233):
+//   recover_kernel       one wave per row of [prompt | visual | text]: the
+//                        visual rows get the kept channels from K_compact in
+//                        ascending channel order and 0 (ThinK) or the
+//                        token's pruned mean (SparK) elsewhere; prompt and
+//                        text rows are copied, so the caller's torch.cat of
+//                        the three spans is written by the same pass.
+//   selection_kernel     one-hot R[c][j] = (c is the j-th kept channel) from
+//                        a per-head mask, so the RotateK decode kernel can
+//                        run ThinK's zero-filled attention from K_compact.
+//
+// Mean factors: torch reduces a 16-bit mean as dtype(fp32 sum * f) with
+// f = float(n_out) / float(n_in) (ATen MeanOps); the host computes each f
+// that way and passes it in.  Ties: torch's GPU topk (largest=False) takes
+// equal values at the boundary in index order, so ThinK prunes the lower
+// channel first; the GPU sort behind argsort(descending) keeps equal values
+// in index order, so SparK keeps the lower channel first.  Both are encoded
+// in 23-bit keys (order-preserving 16-bit score << 7 | channel or
+// 127 - channel), which are distinct per head / token.
+#include <math.h>
+
+#include "rk_common.h"
+#include "rk_host.h"
+#include "rotatek_hip.h"
+
+namespace rk {
+namespace base {
+
+constexpr int kThreads = 256;
+constexpr int kD = 128;
+
+// [B, H, S, C] tensor of 16-bit elements, strides in elements.
+struct View {
+  const uint16_t* data;
+  int64_t sb, sh, ss, sc;
+  int64_t S;
+  int32_t H, C;
+};
+
+struct OutView {
+  uint16_t* data;
+  int64_t sb, sh, ss, sc;
+};
+
+struct MaskView {
+  uint8_t* data;
+  int64_t sb, sh, ss, sc;  // ss is 0 for a per-head mask
+};
+
+__device__ __forceinline__ int64_t head_off(int64_t sb, int64_t sh, int b, int h) {
+  return b * sb + (int64_t)h * sh;
+}
+
+// Keeps an fp32 result as fp32 so that the conversion which follows rounds
+// that fp32 value (fp32 op, then cast, as torch does) instead of being fused
+// with the op into one mixed-precision multiply-and-round.
+__device__ __forceinline__ float pin(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+template <class TT>
+__device__ __forceinline__ float rnd(float x) {
+  return TT::to_f32(TT::from_f32(x));
+}
+
+// Order-preserving key of a 16-bit float value: larger value -> larger key,
+// -0 == +0, every NaN above +inf (torch's sort and topk order NaN highest).
+template <class TT>
+__device__ __forceinline__ uint32_t order_key(float v) {
+  if (v != v) return 0xFFFFu;
+  uint32_t b = TT::from_f32(v);
+  if (v == 0.f) b = 0u;
+  return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+}
+
+template <bool VEC>
+__device__ __forceinline__ uint4 ld8(const uint16_t* base, int64_t ss, int64_t sc, int64_t t, int c0) {
+  if constexpr (VEC) {
+    return *(const uint4*)(base + t * ss + c0);
+  } else {
+    uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e >> 1] |= (uint32_t)base[t * ss + (c0 + e) * sc] << ((e & 1) * 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ------------------------------------------------------------------ ThinK
+// grid (splits, B*H): workgroup x sums dtype(k^2) over tokens
+// [x*chunk, (x+1)*chunk) of one head into part[bh][x][128].  Thread (row
+// group rg = t/16, channel chunk c8 = t%16) walks rows rg, rg+16, ...
+template <class TT, bool VEC>
+__global__ void __launch_bounds__(kThreads) sqsum_kernel(View k, int64_t chunk, int splits, float* part) {
+  __shared__ float s_sum[16][kD];
+  const int tid = threadIdx.x, rg = tid >> 4, c8 = tid & 15;
+  const int x = blockIdx.x, bh = blockIdx.y, b = bh / k.H, h = bh - b * k.H;
+  const uint16_t* base = k.data + head_off(k.sb, k.sh, b, h);
+  const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
+  const int64_t last = max(t1 - 1, (int64_t)0);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int64_t t = t0 + rg; t < t1; t += 64) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = ld8<VEC>(base, k.ss, k.sc, min(t + 16 * i, last), 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (t + 16 * i < t1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = TT::to_f32((uint16_t)(word(v[i], e >> 1) >> ((e & 1) * 16)));
+          acc[e] += rnd<TT>(f * f);  // f * f is exact in fp32
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_sum[rg][8 * c8 + e] = acc[e];
+  __syncthreads();
+  if (tid < kD) {
+    float s = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += s_sum[r][tid];
+    part[((int64_t)bh * splits + x) * kD + tid] = s;
+  }
+}
+
+struct ThinkArgs {
+  const float* part;
+  int splits;
+  View q;        // queries_recent [B, H_q, Q, 128]
+  int G;         // query heads per KV head
+  int keep;      // kept channels
+  int H;         // KV heads
+  float f_keys;  // mean factor over S_v
+  float f_win;   // mean factor over the Q window
+  float f_grp;   // mean factor over the G heads
+  MaskView mask;
+  int32_t* idx;  // [B*H][128] ascending kept channels
+};
+
+// grid (B*H), 128 threads (one per channel).
+template <class TT>
+__global__ void __launch_bounds__(kD) think_select_kernel(const ThinkArgs a) {
+  __shared__ uint32_t s_key[kD];
+  __shared__ int s_kept[kD];
+  const int c = threadIdx.x, bh = blockIdx.x, b = bh / a.H, h = bh - b * a.H;
+  float s = 0.f;
+  for (int x = 0; x < a.splits; ++x) s += a.part[((int64_t)bh * a.splits + x) * kD + c];
+  const float kn = rnd<TT>(pin(s * a.f_keys));
+  float qacc = 0.f;
+  for (int gi = 0; gi < a.G; ++gi) {
+    const uint16_t* qb = a.q.data + head_off(a.q.sb, a.q.sh, b, h * a.G + gi) + c * a.q.sc;
+    float w = 0.f;
+    for (int64_t t = 0; t < a.q.S; ++t) {
+      const float x = TT::to_f32(qb[t * a.q.ss]);
+      w += rnd<TT>(x * x);
+    }
+    qacc += rnd<TT>(pin(w * a.f_win));
+  }
+  const float qn = rnd<TT>(pin(qacc * a.f_grp));
+  const float score = rnd<TT>(qn * kn);  // product of two 16-bit values: exact in fp32
+  const uint32_t key = (order_key<TT>(score) << 7) | (uint32_t)c;
+  s_key[c] = key;
+  __syncthreads();
+  int above = 0;
+  for (int j = 0; j < kD; ++j) above += s_key[j] > key;
+  const int kept = above < a.keep;
+  s_kept[c] = kept;
+  a.mask.data[head_off(a.mask.sb, a.mask.sh, b, h) + c * a.mask.sc] = (uint8_t)kept;
+  __syncthreads();
+  if (kept) {
+    int pos = 0;
+    for (int j = 0; j < c; ++j) pos += s_kept[j];
+    a.idx[(int64_t)bh * kD + pos] = c;
+  }
+}
+
+// grid (splits, B*H): K_compact[b,h,t,j] = K[b,h,t,idx[j]].  Wave w of the
+// workgroup handles tokens t0 + w, t0 + w + 4, ...; lane l writes columns
+// 2l and 2l+1 (one dword store when OVEC).
+template <bool OVEC>
+__global__ void __launch_bounds__(kThreads) compact_kernel(View k, const int32_t* idx, int Dk, int64_t chunk,
+                                                           OutView o) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int x = blockIdx.x, bh = blockIdx.y, b = bh / k.H, h = bh - b * k.H;
+  const int j0 = 2 * lane, j1 = j0 + 1;
+  const bool v0 = j0 < Dk, v1 = j1 < Dk;
+  const int64_t s0 = v0 ? idx[(int64_t)bh * kD + j0] * k.sc : 0;
+  const int64_t s1 = v1 ? idx[(int64_t)bh * kD + j1] * k.sc : 0;
+  const uint16_t* base = k.data + head_off(k.sb, k.sh, b, h);
+  uint16_t* ob = o.data + head_off(o.sb, o.sh, b, h);
+  const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
+  for (int64_t t = t0 + w; t < t1; t += 4) {
+    const uint16_t e0 = v0 ? base[t * k.ss + s0] : (uint16_t)0;
+    const uint16_t e1 = v1 ? base[t * k.ss + s1] : (uint16_t)0;
+    if constexpr (OVEC) {
+      if (v1)
+        *(uint32_t*)(ob + t * o.ss + j0) = (uint32_t)e0 | ((uint32_t)e1 << 16);
+      else if (v0)
+        ob[t * o.ss + j0] = e0;
+    } else {
+      if (v0) ob[t * o.ss + j0 * o.sc] = e0;
+      if (v1) ob[t * o.ss + j1 * o.sc] = e1;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ SparK
+// grid (B*H), 128 threads: qn[bh][c] = dtype(sqrt(sum_t q_g[t][c]^2)) with
+// q_g[t][c] = dtype(sum over the G query heads * f_grp).
+template <class TT>
+__global__ void __launch_bounds__(kD) spark_qnorm_kernel(View q, int G, int H, float f_grp, float* qn) {
+  const int c = threadIdx.x, bh = blockIdx.x, b = bh / H, h = bh - b * H;
+  float acc = 0.f;
+  for (int64_t t = 0; t < q.S; ++t) {
+    float s = 0.f;
+    for (int gi = 0; gi < G; ++gi) s += TT::to_f32(q.data[head_off(q.sb, q.sh, b, h * G + gi) + t * q.ss + c * q.sc]);
+    const float g = rnd<TT>(pin(s * f_grp));
+    acc = fmaf(g, g, acc);  // g * g is exact, so fused or not gives the same sum
+  }
+  qn[(int64_t)bh * kD + c] = rnd<TT>(sqrtf(acc));
+}
+
+struct SparkArgs {
+  View k;
+  const float* qn;
+  int keep;
+  int64_t chunk;
+  float f_pruned;  // mean factor over the pruned channels
+  OutView kc;      // [B, H, S, Dk]
+  MaskView mask;   // [B, H, S, 128]
+  OutView pm;      // [B, H, S, 1]
+};
+
+// grid (splits, B*H); one wave per token, lane l owns channels 2l, 2l+1.
+template <class TT, bool KVEC>
+__global__ void __launch_bounds__(kThreads) spark_kernel(const SparkArgs a) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int x = blockIdx.x, bh = blockIdx.y, b = bh / a.k.H, h = bh - b * a.k.H;
+  const int c0 = 2 * lane, c1 = c0 + 1;
+  const float q0 = a.qn[(int64_t)bh * kD + c0], q1 = a.qn[(int64_t)bh * kD + c1];
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const uint16_t* kb = a.k.data + head_off(a.k.sb, a.k.sh, b, h);
+  uint16_t* cb = a.kc.data + head_off(a.kc.sb, a.kc.sh, b, h);
+  uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
+  uint16_t* pb = a.pm.data + head_off(a.pm.sb, a.pm.sh, b, h);
+  const int64_t t0 = (int64_t)x * a.chunk, t1 = min(a.k.S, t0 + a.chunk);
+  for (int64_t t = t0 + w; t < t1; t += 4) {  // wave-uniform loop
+    uint32_t raw;
+    if constexpr (KVEC) {
+      raw = *(const uint32_t*)(kb + t * a.k.ss + c0);
+    } else {
+      raw = (uint32_t)kb[t * a.k.ss + c0 * a.k.sc] | ((uint32_t)kb[t * a.k.ss + c1 * a.k.sc] << 16);
+    }
+    const uint16_t r0 = (uint16_t)raw, r1 = (uint16_t)(raw >> 16);
+    const float e0 = TT::to_f32(r0), e1 = TT::to_f32(r1);
+    const float s0 = rnd<TT>(rnd<TT>(e0 * e0) * q0), s1 = rnd<TT>(rnd<TT>(e1 * e1) * q1);
+    const uint32_t k0 = (order_key<TT>(s0) << 7) | (uint32_t)(127 - c0);
+    const uint32_t k1 = (order_key<TT>(s1) << 7) | (uint32_t)(127 - c1);
+    bool kept0, kept1;
+    if (a.keep >= kD) {
+      kept0 = kept1 = true;
+    } else if (a.keep <= 0) {
+      kept0 = kept1 = false;
+    } else {
+      // largest T with #{key >= T} >= keep, i.e. the keep-th largest key
+      uint32_t T = 0u;
+      for (int bit = 22; bit >= 0; --bit) {
+        const uint32_t cand = T | (1u << bit);
+        const int cnt = __popcll(__ballot(k0 >= cand)) + __popcll(__ballot(k1 >= cand));
+        if (cnt >= a.keep) T = cand;
+      }
+      kept0 = k0 >= T;
+      kept1 = k1 >= T;
+    }
+    const uint64_t m0 = __ballot(kept0), m1 = __ballot(kept1);
+    const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)kept0;
+    if (kept0) cb[t * a.kc.ss + p0 * a.kc.sc] = r0;
+    if (kept1) cb[t * a.kc.ss + p1 * a.kc.sc] = r1;
+    mb[t * a.mask.ss + c0 * a.mask.sc] = (uint8_t)kept0;
+    mb[t * a.mask.ss + c1 * a.mask.sc] = (uint8_t)kept1;
+    float p = (kept0 ? 0.f : e0) + (kept1 ? 0.f : e1);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) p += shfl_xor(p, off);
+    if (lane == 0) pb[t * a.pm.ss] = TT::from_f32(pin(p * a.f_pruned));
+  }
+}
+
+// ------------------------------------------------------------------ recovery
+struct RecoverArgs {
+  View pr;  // prompt rows (S = 0 when absent)
+  View kc;  // K_compact [B, H, S_v, Dk]
+  View tx;  // text rows (S = 0 when absent)
+  MaskView mask;         // ThinK [B, H, 128] (ss = 0) or SparK [B, H, S_v, 128]
+  const uint16_t* pm;    // SparK pruned mean [B, H, S_v, 1]
+  int64_t p_sb, p_sh, p_ss;
+  OutView out;           // [B, H, rows, 128]
+  int64_t rows, chunk;
+  int H;
+};
+
+// grid (splits, B*H); wave per output row, lane l writes channels 2l, 2l+1.
+// A visual row's kept channel of rank r (ascending channel order) takes
+// column r of K_compact; ranks >= Dk (a mask row with more than Dk kept
+// channels) are filled like pruned channels, so no read leaves the row.
+template <bool SPARK, bool OVEC>
+__global__ void __launch_bounds__(kThreads) recover_kernel(const RecoverArgs a) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int x = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh - b * a.H;
+  const int c0 = 2 * lane, c1 = c0 + 1;
+  const int Dk = a.kc.C;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const uint16_t* pb = a.pr.data + head_off(a.pr.sb, a.pr.sh, b, h);
+  const uint16_t* kb = a.kc.data + head_off(a.kc.sb, a.kc.sh, b, h);
+  const uint16_t* tb = a.tx.data + head_off(a.tx.sb, a.tx.sh, b, h);
+  const uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
+  uint16_t* ob = a.out.data + head_off(a.out.sb, a.out.sh, b, h);
+  int map0 = -1, map1 = -1;  // ThinK: K_compact column of channels c0, c1
+  if constexpr (!SPARK) {
+    const bool k0 = mb[c0 * a.mask.sc] != 0, k1 = mb[c1 * a.mask.sc] != 0;
+    const uint64_t m0 = __ballot(k0), m1 = __ballot(k1);
+    const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)k0;
+    map0 = (k0 && p0 < Dk) ? p0 : -1;
+    map1 = (k1 && p1 < Dk) ? p1 : -1;
+  }
+  const int64_t Sp = a.pr.S, Sv = a.kc.S;
+  const int64_t r0 = (int64_t)x * a.chunk, r1 = min(a.rows, r0 + a.chunk);
+  for (int64_t r = r0 + w; r < r1; r += 4) {  // wave-uniform loop
+    uint16_t e0, e1;
+    if (r < Sp) {
+      e0 = pb[r * a.pr.ss + c0 * a.pr.sc];
+      e1 = pb[r * a.pr.ss + c1 * a.pr.sc];
+    } else if (r < Sp + Sv) {
+      const int64_t t = r - Sp;
+      int s0 = map0, s1 = map1;
+      uint16_t fill = 0;
+      if constexpr (SPARK) {
+        const bool k0 = mb[t * a.mask.ss + c0 * a.mask.sc] != 0, k1 = mb[t * a.mask.ss + c1 * a.mask.sc] != 0;
+        const uint64_t m0 = __ballot(k0), m1 = __ballot(k1);
+        const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)k0;
+        s0 = (k0 && p0 < Dk) ? p0 : -1;
+        s1 = (k1 && p1 < Dk) ? p1 : -1;
+        fill = a.pm[head_off(a.p_sb, a.p_sh, b, h) + t * a.p_ss];
+      }
+      e0 = s0 >= 0 ? kb[t * a.kc.ss + s0 * a.kc.sc] : fill;
+      e1 = s1 >= 0 ? kb[t * a.kc.ss + s1 * a.kc.sc] : fill;
+    } else {
+      const int64_t t = r - Sp - Sv;
+      e0 = tb[t * a.tx.ss + c0 * a.tx.sc];
+      e1 = tb[t * a.tx.ss + c1 * a.tx.sc];
+    }
+    if constexpr (OVEC) {
+      *(uint32_t*)(ob + r * a.out.ss + c0) = (uint32_t)e0 | ((uint32_t)e1 << 16);
+    } else {
+      ob[r * a.out.ss + c0 * a.out.sc] = e0;
+      ob[r * a.out.ss + c1 * a.out.sc] = e1;
+    }
+  }
+}
+
+// grid (B*H), 128 threads: R[b,h,c,j] = 1 if c is the j-th kept channel of
+// the head's mask (ascending), else 0; `one` is 1.0 in R's dtype.
+template <class E>
+__global__ void __launch_bounds__(kD) selection_kernel(MaskView m, int H, int Dk, E* R, int64_t r_sb, int64_t r_sh,
+                                                       int64_t r_sr, int64_t r_sc, E one) {
+  __shared__ int s_kept[kD];
+  const int c = threadIdx.x, bh = blockIdx.x, b = bh / H, h = bh - b * H;
+  const int kept = m.data[head_off(m.sb, m.sh, b, h) + c * m.sc] != 0;
+  s_kept[c] = kept;
+  __syncthreads();
+  int pos = 0;
+  for (int j = 0; j < c; ++j) pos += s_kept[j];
+  E* row = R + head_off(r_sb, r_sh, b, h) + c * r_sr;
+  for (int j = 0; j < Dk; ++j) row[j * r_sc] = (kept && pos == j) ? one : (E)0;
+}
+
+}  // namespace base
+}  // namespace rk
+
+// =====================================================================
+// host side
+// =====================================================================
+namespace {
+
+using namespace rk::base;
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+// torch's mean factor float(n_out) / float(n_in) (ATen MeanOps).
+float mean_factor(int64_t n_out, int64_t n_in) { return static_cast<float>(n_out) / static_cast<float>(n_in); }
+
+// [B, H, S, C] descriptor of a 16-bit float tensor with C == want_c (or any
+// C <= 128 when want_c < 0).
+int view_of(const rk_tensor* t, int want_c, View* v) {
+  int st = rk::check_desc(t, 4);
+  if (st) return st;
+  if (!rk::is_half(t->dtype)) return RK_ERR_DTYPE;
+  if (want_c >= 0 ? t->shape[3] != want_c : t->shape[3] > 128) return want_c == 128 ? RK_ERR_HEAD_DIM : RK_ERR_SHAPE;
+  if (t->shape[1] > (INT64_C(1) << 30) || t->shape[0] * t->shape[1] > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
+  v->data = (const uint16_t*)t->data;
+  v->sb = t->stride[0];
+  v->sh = t->stride[1];
+  v->ss = t->stride[2];
+  v->sc = t->stride[3];
+  v->S = t->shape[2];
+  v->H = (int32_t)t->shape[1];
+  v->C = (int32_t)t->shape[3];
+  return RK_OK;
+}
+
+OutView out_of(const rk_tensor* t) {
+  OutView o;
+  o.data = (uint16_t*)t->data;
+  o.sb = t->stride[0];
+  o.sh = t->stride[1];
+  o.ss = t->stride[2];
+  o.sc = t->stride[3];
+  return o;
+}
+
+// Per-head [B, H, 128] or per-token [B, H, S, 128] bool/uint8 mask.
+int mask_of(const rk_tensor* t, int64_t B, int64_t H, int64_t S, bool per_token, MaskView* m) {
+  int st = rk::check_desc(t, per_token ? 4 : 3);
+  if (st) return st;
+  if (t->dtype != RK_U8) return RK_ERR_DTYPE;
+  if (t->shape[0] != B || t->shape[1] != H) return RK_ERR_SHAPE;
+  if (per_token ? (t->shape[2] != S || t->shape[3] != 128) : t->shape[2] != 128) return RK_ERR_SHAPE;
+  m->data = (uint8_t*)t->data;
+  m->sb = t->stride[0];
+  m->sh = t->stride[1];
+  m->ss = per_token ? t->stride[2] : 0;
+  m->sc = per_token ? t->stride[3] : t->stride[2];
+  return RK_OK;
+}
+
+bool same_bhs(const rk_tensor* t, int64_t B, int64_t H, int64_t S) {
+  return t->shape[0] == B && t->shape[1] == H && t->shape[2] == S;
+}
+
+// 16-byte row loads: unit channel stride, 8-element aligned rows and base.
+bool rows16(const rk_tensor* t) { return rk::vec_ok(t); }
+
+// 4-byte row stores / loads of channel pairs: unit channel stride, even row
+// strides, 4-byte aligned base.
+bool pairs4(const rk_tensor* t) {
+  if (t->stride[3] != 1) return false;
+  for (int i = 0; i < 3; ++i)
+    if (t->shape[i] > 1 && (t->stride[i] & 1)) return false;
+  return (((uintptr_t)t->data) & 3) == 0;
+}
+
+// Token split: about `per_cu` workgroups per CU over all heads, at least
+// `min_tokens` tokens per workgroup.
+int token_splits(int64_t bh, int64_t S, int cus, int per_cu, int64_t min_tokens) {
+  if (S <= 0 || bh <= 0) return 1;
+  int64_t want = cdiv((int64_t)per_cu * cus, bh);
+  const int64_t cap = cdiv(S, min_tokens);
+  if (want > cap) want = cap;
+  if (want < 1) want = 1;
+  if (want > 65535) want = 65535;
+  return (int)want;
+}
+
+int resolve_cus(int32_t num_cus, int* st) {
+  *st = RK_OK;
+  if (num_cus > 0) return num_cus;
+  int dev = 0;
+  const int cus = rk::current_device_cus(&dev);
+  if (cus <= 0) *st = RK_ERR_NO_DEVICE;
+  return cus;
+}
+
+struct ThinkPlan {
+  int splits;
+  int64_t chunk;
+  size_t off_part, off_idx, total;
+};
+
+ThinkPlan think_plan(int64_t bh, int64_t S, int cus) {
+  ThinkPlan p;
+  p.splits = token_splits(bh, S, cus, 2, 256);
+  p.chunk = cdiv(S > 0 ? S : 1, p.splits);
+  p.off_part = 0;
+  p.off_idx = align256((size_t)bh * p.splits * kD * sizeof(float));
+  p.total = p.off_idx + align256((size_t)bh * kD * sizeof(int32_t));
+  return p;
+}
+
+// Shapes of ThinK's inputs and outputs; sets the views and B, H, keep.
+int think_check(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_heads, int64_t prune_count,
+                const rk_tensor* kc_out, const rk_tensor* mask_out, View* kv, View* qv, MaskView* mv,
+                int64_t* keep) {
+  if (!keys || !queries || !kc_out || !mask_out) return RK_ERR_NULL;
+  int st;
+  if ((st = view_of(keys, 128, kv)) || (st = view_of(queries, 128, qv))) return st;
+  if (queries->dtype != keys->dtype) return RK_ERR_DTYPE;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  if (queries->shape[0] != B) return RK_ERR_SHAPE;
+  if (num_kv_heads != H || H < 1 || queries->shape[1] % H != 0) return RK_ERR_HEADS;
+  if (prune_count < 0 || prune_count > 128) return RK_ERR_KEEP_DIM;
+  *keep = 128 - prune_count;
+  if ((st = rk::check_desc(kc_out, 4))) return st;
+  if (kc_out->dtype != keys->dtype) return RK_ERR_DTYPE;
+  if (!same_bhs(kc_out, B, H, keys->shape[2]) || kc_out->shape[3] != *keep) return RK_ERR_SHAPE;
+  if ((st = mask_of(mask_out, B, H, 0, false, mv))) return st;
+  return RK_OK;
+}
+
+template <class TT>
+hipError_t launch_think(const View& kv, bool kvec, const View& qv, int G, int keep, const ThinkPlan& p, int64_t B,
+                        float f_keys, float f_win, float f_grp, const MaskView& mv, const rk_tensor* kc_out,
+                        void* ws, hipStream_t s) {
+  const int64_t bh = B * kv.H;
+  float* part = (float*)((char*)ws + p.off_part);
+  int32_t* idx = (int32_t*)((char*)ws + p.off_idx);
+  const dim3 grid((unsigned)p.splits, (unsigned)bh);
+  if (kvec)
+    hipLaunchKernelGGL((sqsum_kernel<TT, true>), grid, dim3(kThreads), 0, s, kv, p.chunk, p.splits, part);
+  else
+    hipLaunchKernelGGL((sqsum_kernel<TT, false>), grid, dim3(kThreads), 0, s, kv, p.chunk, p.splits, part);
+  ThinkArgs a;
+  a.part = part;
+  a.splits = p.splits;
+  a.q = qv;
+  a.G = G;
+  a.keep = keep;
+  a.H = kv.H;
+  a.f_keys = f_keys;
+  a.f_win = f_win;
+  a.f_grp = f_grp;
+  a.mask = mv;
+  a.idx = idx;
+  hipLaunchKernelGGL((think_select_kernel<TT>), dim3((unsigned)bh), dim3(kD), 0, s, a);
+  if (keep > 0 && kv.S > 0) {
+    const OutView o = out_of(kc_out);
+    if (pairs4(kc_out))
+      hipLaunchKernelGGL((compact_kernel<true>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
+    else
+      hipLaunchKernelGGL((compact_kernel<false>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
+  }
+  return hipGetLastError();
+}
+
+struct SparkPlan {
+  int splits;
+  int64_t chunk;
+  size_t total;
+};
+
+SparkPlan spark_plan(int64_t bh, int64_t S, int cus) {
+  SparkPlan p;
+  p.splits = token_splits(bh, S, cus, 8, 64);
+  p.chunk = cdiv(S > 0 ? S : 1, p.splits);
+  p.total = align256((size_t)bh * kD * sizeof(float));
+  return p;
+}
+
+int spark_check(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_groups, int64_t prune_count,
+                const rk_tensor* kc_out, const rk_tensor* mask_out, const rk_tensor* pm_out, View* kv, View* qv,
+                MaskView* mv, int64_t* keep) {
+  if (!keys || !queries || !kc_out || !mask_out || !pm_out) return RK_ERR_NULL;
+  int st;
+  if ((st = view_of(keys, 128, kv)) || (st = view_of(queries, 128, qv))) return st;
+  if (queries->dtype != keys->dtype) return RK_ERR_DTYPE;
+  const int64_t B = keys->shape[0], H = keys->shape[1], S = keys->shape[2];
+  if (queries->shape[0] != B) return RK_ERR_SHAPE;
+  if (num_kv_groups < 1 || queries->shape[1] != H * num_kv_groups) return RK_ERR_HEADS;
+  if (prune_count < 0 || prune_count > 128) return RK_ERR_KEEP_DIM;
+  *keep = 128 - prune_count;
+  if ((st = rk::check_desc(kc_out, 4)) || (st = rk::check_desc(pm_out, 4))) return st;
+  if (kc_out->dtype != keys->dtype || pm_out->dtype != keys->dtype) return RK_ERR_DTYPE;
+  if (!same_bhs(kc_out, B, H, S) || kc_out->shape[3] != *keep) return RK_ERR_SHAPE;
+  if (!same_bhs(pm_out, B, H, S) || pm_out->shape[3] != 1) return RK_ERR_SHAPE;
+  if ((st = mask_of(mask_out, B, H, S, true, mv))) return st;
+  return RK_OK;
+}
+
+template <class TT>
+hipError_t launch_spark(const View& kv, bool kvec, const View& qv, int G, int keep, const SparkPlan& p, int64_t B,
+                        float f_grp, float f_pruned, const MaskView& mv, const rk_tensor* kc_out,
+                        const rk_tensor* pm_out, void* ws, hipStream_t s) {
+  const int64_t bh = B * kv.H;
+  float* qn = (float*)ws;
+  hipLaunchKernelGGL((spark_qnorm_kernel<TT>), dim3((unsigned)bh), dim3(kD), 0, s, qv, G, kv.H, f_grp, qn);
+  if (kv.S == 0) return hipGetLastError();
+  SparkArgs a;
+  a.k = kv;
+  a.qn = qn;
+  a.keep = keep;
+  a.chunk = p.chunk;
+  a.f_pruned = f_pruned;
+  a.kc = out_of(kc_out);
+  a.mask = mv;
+  a.pm = out_of(pm_out);
+  const dim3 grid((unsigned)p.splits, (unsigned)bh);
+  if (kvec)
+    hipLaunchKernelGGL((spark_kernel<TT, true>), grid, dim3(kThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((spark_kernel<TT, false>), grid, dim3(kThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+// Optional prompt / text spans of the recovery: NULL -> an empty view.
+int span_of(const rk_tensor* t, const rk_tensor* kc, View* v) {
+  if (!t) {
+    *v = View{nullptr, 0, 0, 0, 0, 0, (int32_t)kc->shape[1], 128};
+    return RK_OK;
+  }
+  int st = view_of(t, 128, v);
+  if (st) return st;
+  if (t->dtype != kc->dtype) return RK_ERR_DTYPE;
+  if (t->shape[0] != kc->shape[0] || t->shape[1] != kc->shape[1]) return RK_ERR_SHAPE;
+  return RK_OK;
+}
+
+int recover(bool spark, const rk_tensor* k_prompt, const rk_tensor* k_pruned, const rk_tensor* k_text,
+            const rk_tensor* mask, const rk_tensor* pruned_mean, const rk_tensor* out, int32_t num_cus,
+            void* stream, bool launch) {
+  if (!k_pruned || !mask || !out || (spark && !pruned_mean)) return RK_ERR_NULL;
+  RecoverArgs a;
+  int st;
+  if ((st = view_of(k_pruned, -1, &a.kc))) return st;
+  const int64_t B = k_pruned->shape[0], H = k_pruned->shape[1], Sv = k_pruned->shape[2];
+  if ((st = span_of(k_prompt, k_pruned, &a.pr)) || (st = span_of(k_text, k_pruned, &a.tx))) return st;
+  if ((st = mask_of(mask, B, H, Sv, spark, &a.mask))) return st;
+  a.pm = nullptr;
+  a.p_sb = a.p_sh = a.p_ss = 0;
+  if (spark) {
+    if ((st = rk::check_desc(pruned_mean, 4))) return st;
+    if (pruned_mean->dtype != k_pruned->dtype) return RK_ERR_DTYPE;
+    if (!same_bhs(pruned_mean, B, H, Sv) || pruned_mean->shape[3] != 1) return RK_ERR_SHAPE;
+    a.pm = (const uint16_t*)pruned_mean->data;
+    a.p_sb = pruned_mean->stride[0];
+    a.p_sh = pruned_mean->stride[1];
+    a.p_ss = pruned_mean->stride[2];
+  }
+  if ((st = rk::check_desc(out, 4))) return st;
+  if (out->dtype != k_pruned->dtype) return RK_ERR_DTYPE;
+  a.rows = a.pr.S + Sv + a.tx.S;
+  if (!same_bhs(out, B, H, a.rows)) return RK_ERR_SHAPE;
+  if (out->shape[3] != 128) return RK_ERR_HEAD_DIM;
+  if (!launch) return RK_OK;
+  if (B * H == 0 || a.rows == 0) return RK_OK;
+  if (!out->data || (Sv > 0 && !mask->data) || (Sv > 0 && a.kc.C > 0 && !k_pruned->data) ||
+      (spark && Sv > 0 && !pruned_mean->data) || (a.pr.S > 0 && !a.pr.data) || (a.tx.S > 0 && !a.tx.data) ||
+      (!spark && !mask->data))
+    return RK_ERR_NULL;
+  const int cus = resolve_cus(num_cus, &st);
+  if (st) return st;
+  a.out = out_of(out);
+  a.H = (int)H;
+  const int splits = token_splits(B * H, a.rows, cus, 4, 64);
+  a.chunk = cdiv(a.rows, splits);
+  const dim3 grid((unsigned)splits, (unsigned)(B * H));
+  hipStream_t s = (hipStream_t)stream;
+  const bool ovec = pairs4(out);
+  if (spark) {
+    if (ovec)
+      hipLaunchKernelGGL((recover_kernel<true, true>), grid, dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((recover_kernel<true, false>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    if (ovec)
+      hipLaunchKernelGGL((recover_kernel<false, true>), grid, dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((recover_kernel<false, false>), grid, dim3(kThreads), 0, s, a);
+  }
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int rk_think_score_and_compact_check(const rk_tensor* keys_vision, const rk_tensor* queries_recent,
+                                                int64_t num_kv_heads, int64_t prune_count,
+                                                const rk_tensor* k_compact_out, const rk_tensor* keep_mask_out,
+                                                int32_t num_cus, size_t* workspace_bytes) {
+  View kv, qv;
+  MaskView mv;
+  int64_t keep;
+  int st = think_check(keys_vision, queries_recent, num_kv_heads, prune_count, k_compact_out, keep_mask_out, &kv,
+                       &qv, &mv, &keep);
+  if (st) return st;
+  const int cus = resolve_cus(num_cus, &st);
+  if (st) return st;
+  if (workspace_bytes) *workspace_bytes = think_plan(keys_vision->shape[0] * kv.H, kv.S, cus).total;
+  return RK_OK;
+}
+
+extern "C" int rk_think_score_and_compact(const rk_tensor* keys_vision, const rk_tensor* queries_recent,
+                                          int64_t num_kv_heads, int64_t prune_count,
+                                          const rk_tensor* k_compact_out, const rk_tensor* keep_mask_out,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  View kv, qv;
+  MaskView mv;
+  int64_t keep;
+  int st = think_check(keys_vision, queries_recent, num_kv_heads, prune_count, k_compact_out, keep_mask_out, &kv,
+                       &qv, &mv, &keep);
+  if (st) return st;
+  const int64_t B = keys_vision->shape[0], H = kv.H, Hq = queries_recent->shape[1];
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  const ThinkPlan p = think_plan(B * H, kv.S, cus);
+  if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < p.total) return RK_ERR_WORKSPACE;
+  if (B * H == 0) return RK_OK;
+  if ((kv.S > 0 && !kv.data) || (qv.S > 0 && !qv.data) || !mv.data || (keep > 0 && kv.S > 0 && !k_compact_out->data))
+    return RK_ERR_NULL;
+  const int G = (int)(Hq / H);
+  const float f_keys = mean_factor(B * H * 128, B * H * kv.S * 128);
+  const float f_win = mean_factor(B * Hq * 128, B * Hq * qv.S * 128);
+  const float f_grp = mean_factor(B * H * 128, B * Hq * 128);
+  const bool kvec = rows16(keys_vision);
+  hipStream_t s = (hipStream_t)stream;
+  const hipError_t e = keys_vision->dtype == RK_F16
+                           ? launch_think<rk::F16>(kv, kvec, qv, G, (int)keep, p, B, f_keys, f_win, f_grp, mv,
+                                                   k_compact_out, workspace, s)
+                           : launch_think<rk::BF16>(kv, kvec, qv, G, (int)keep, p, B, f_keys, f_win, f_grp, mv,
+                                                    k_compact_out, workspace, s);
+  return e == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+extern "C" int rk_spark_prune_check(const rk_tensor* keys_vision, const rk_tensor* queries, int64_t num_kv_groups,
+                                    int64_t prune_count, const rk_tensor* k_compact_out,
+                                    const rk_tensor* keep_mask_out, const rk_tensor* pruned_mean_out,
+                                    int32_t num_cus, size_t* workspace_bytes) {
+  View kv, qv;
+  MaskView mv;
+  int64_t keep;
+  int st = spark_check(keys_vision, queries, num_kv_groups, prune_count, k_compact_out, keep_mask_out,
+                       pruned_mean_out, &kv, &qv, &mv, &keep);
+  if (st) return st;
+  const int cus = resolve_cus(num_cus, &st);
+  if (st) return st;
+  if (workspace_bytes) *workspace_bytes = spark_plan(keys_vision->shape[0] * kv.H, kv.S, cus).total;
+  return RK_OK;
+}
+
+extern "C" int rk_spark_prune(const rk_tensor* keys_vision, const rk_tensor* queries, int64_t num_kv_groups,
+                              int64_t prune_count, const rk_tensor* k_compact_out, const rk_tensor* keep_mask_out,
+                              const rk_tensor* pruned_mean_out, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  View kv, qv;
+  MaskView mv;
+  int64_t keep;
+  int st = spark_check(keys_vision, queries, num_kv_groups, prune_count, k_compact_out, keep_mask_out,
+                       pruned_mean_out, &kv, &qv, &mv, &keep);
+  if (st) return st;
+  const int64_t B = keys_vision->shape[0], H = kv.H;
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  const SparkPlan p = spark_plan(B * H, kv.S, cus);
+  if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < p.total) return RK_ERR_WORKSPACE;
+  if (B * H == 0) return RK_OK;
+  if ((kv.S > 0 && (!kv.data || !mv.data || !pruned_mean_out->data || (keep > 0 && !k_compact_out->data))) ||
+      (qv.S > 0 && !qv.data))
+    return RK_ERR_NULL;
+  const int64_t W = qv.S;
+  const float f_grp = mean_factor(B * H * W * 128, B * H * num_kv_groups * W * 128);
+  const float f_pruned = mean_factor(B * H * kv.S, B * H * kv.S * prune_count);
+  const bool kvec = pairs4(keys_vision);
+  hipStream_t s = (hipStream_t)stream;
+  const hipError_t e =
+      keys_vision->dtype == RK_F16
+          ? launch_spark<rk::F16>(kv, kvec, qv, (int)num_kv_groups, (int)keep, p, B, f_grp, f_pruned, mv,
+                                  k_compact_out, pruned_mean_out, workspace, s)
+          : launch_spark<rk::BF16>(kv, kvec, qv, (int)num_kv_groups, (int)keep, p, B, f_grp, f_pruned, mv,
+                                   k_compact_out, pruned_mean_out, workspace, s);
+  return e == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+extern "C" int rk_think_recover_check(const rk_tensor* k_prompt, const rk_tensor* k_pruned,
+                                      const rk_tensor* k_text, const rk_tensor* think_mask,
+                                      const rk_tensor* out) {
+  return recover(false, k_prompt, k_pruned, k_text, think_mask, nullptr, out, 1, nullptr, false);
+}
+
+extern "C" int rk_think_recover(const rk_tensor* k_prompt, const rk_tensor* k_pruned, const rk_tensor* k_text,
+                                const rk_tensor* think_mask, const rk_tensor* out, void* stream) {
+  return recover(false, k_prompt, k_pruned, k_text, think_mask, nullptr, out, 0, stream, true);
+}
+
+extern "C" int rk_spark_recover_check(const rk_tensor* k_prompt, const rk_tensor* k_pruned,
+                                      const rk_tensor* k_text, const rk_tensor* spark_mask,
+                                      const rk_tensor* pruned_mean, const rk_tensor* out) {
+  return recover(true, k_prompt, k_pruned, k_text, spark_mask, pruned_mean, out, 1, nullptr, false);
+}
+
+extern "C" int rk_spark_recover(const rk_tensor* k_prompt, const rk_tensor* k_pruned, const rk_tensor* k_text,
+                                const rk_tensor* spark_mask, const rk_tensor* pruned_mean, const rk_tensor* out,
+                                void* stream) {
+  return recover(true, k_prompt, k_pruned, k_text, spark_mask, pruned_mean, out, 0, stream, true);
+}
+
+extern "C" int rk_channel_selection(const rk_tensor* keep_mask, const rk_tensor* R_out, void* stream) {
+  if (!keep_mask || !R_out) return RK_ERR_NULL;
+  int st = rk::check_desc(R_out, 4);
+  if (st) return st;
+  if (!rk::is_float_param(R_out->dtype)) return RK_ERR_DTYPE;
+  const int64_t B = R_out->shape[0], H = R_out->shape[1], Dk = R_out->shape[3];
+  if (R_out->shape[2] != 128) return RK_ERR_HEAD_DIM;
+  if (Dk < 1 || Dk > 128) return RK_ERR_KEEP_DIM;
+  if (H > (INT64_C(1) << 30) || B * H > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
+  MaskView m;
+  if ((st = mask_of(keep_mask, B, H, 0, false, &m))) return st;
+  if (B * H == 0) return RK_OK;
+  if (!m.data || !R_out->data) return RK_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)(B * H));
+  const int64_t* rs = R_out->stride;
+  if (R_out->dtype == RK_F32) {
+    hipLaunchKernelGGL((selection_kernel<float>), grid, dim3(kD), 0, s, m, (int)H, (int)Dk, (float*)R_out->data,
+                       rs[0], rs[1], rs[2], rs[3], 1.0f);
+  } else {
+    const uint16_t one = R_out->dtype == RK_F16 ? (uint16_t)0x3C00 : (uint16_t)0x3F80;
+    hipLaunchKernelGGL((selection_kernel<uint16_t>), grid, dim3(kD), 0, s, m, (int)H, (int)Dk,
+                       (uint16_t*)R_out->data, rs[0], rs[1], rs[2], rs[3], one);
+  }
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+}

@@ -286,3 +286,78 @@ def test_query_weight_validation():
     assert lib.rk_query_weight(r(cov), r(q), 7, 33, r(out), None) == -10     # window above 32
     q32 = _t((2, 28, 50, 128), _lib.RK_F32)
     assert lib.rk_query_weight(r(cov), r(q32), 7, 32, r(out), None) == -3
+
+
+def test_think_validation():
+    lib = _lib.load()
+    need = ctypes.c_size_t(0)
+
+    def chk(keys=(2, 4, 50, 128), q=(2, 8, 32, 128), heads=4, prune=96, kc=None, mask=(2, 4, 128),
+            kdt=_lib.RK_BF16, qdt=_lib.RK_BF16, mdt=_lib.RK_U8):
+        kc = kc or (keys[0], keys[1], keys[2], 128 - prune)
+        d = [_t(keys, kdt), _t(q, qdt), _t(kc, kdt), _t(mask, mdt)]
+        return lib.rk_think_score_and_compact_check(ctypes.byref(d[0]), ctypes.byref(d[1]), heads, prune,
+                                                    ctypes.byref(d[2]), ctypes.byref(d[3]), 256,
+                                                    ctypes.byref(need))
+
+    assert chk() == 0 and need.value > 0
+    assert chk(prune=0) == 0 and chk(prune=128) == 0
+    assert chk(prune=129, kc=(2, 4, 50, 1)) == _lib.RK_ERR_KEEP_DIM
+    assert chk(heads=3) == _lib.RK_ERR_HEADS
+    assert chk(q=(2, 6, 32, 128), heads=4) == _lib.RK_ERR_HEADS
+    assert chk(keys=(2, 4, 50, 64)) == _lib.RK_ERR_HEAD_DIM
+    assert chk(qdt=_lib.RK_F16) == _lib.RK_ERR_DTYPE
+    assert chk(kc=(2, 4, 50, 33)) == _lib.RK_ERR_SHAPE
+    assert chk(mask=(2, 4, 127)) == _lib.RK_ERR_SHAPE
+    assert chk(mdt=_lib.RK_I32) == _lib.RK_ERR_DTYPE
+    assert chk(kdt=_lib.RK_F32, qdt=_lib.RK_F32) == _lib.RK_ERR_DTYPE
+
+
+def test_spark_validation():
+    lib = _lib.load()
+    need = ctypes.c_size_t(0)
+
+    def chk(keys=(2, 4, 50, 128), q=(2, 28, 32, 128), groups=7, prune=96, kc=None, mask=None, pm=None,
+            dt=_lib.RK_F16):
+        B, H, S = keys[:3]
+        kc = kc or (B, H, S, 128 - prune)
+        mask = mask or (B, H, S, 128)
+        pm = pm or (B, H, S, 1)
+        d = [_t(keys, dt), _t(q, dt), _t(kc, dt), _t(mask, _lib.RK_U8), _t(pm, dt)]
+        return lib.rk_spark_prune_check(ctypes.byref(d[0]), ctypes.byref(d[1]), groups, prune,
+                                        *[ctypes.byref(x) for x in d[2:]], 256, ctypes.byref(need))
+
+    assert chk() == 0 and need.value > 0
+    assert chk(groups=1, q=(2, 4, 32, 128)) == 0
+    assert chk(groups=6) == _lib.RK_ERR_HEADS
+    assert chk(groups=0) == _lib.RK_ERR_HEADS
+    assert chk(prune=-1, kc=(2, 4, 50, 129)) == _lib.RK_ERR_KEEP_DIM
+    assert chk(mask=(2, 4, 50, 64)) == _lib.RK_ERR_SHAPE
+    assert chk(mask=(2, 4, 128)) == _lib.RK_ERR_RANK
+    assert chk(pm=(2, 4, 50, 2)) == _lib.RK_ERR_SHAPE
+    assert chk(kc=(2, 4, 49, 32)) == _lib.RK_ERR_SHAPE
+    assert chk(dt=_lib.RK_F32) == _lib.RK_ERR_DTYPE
+
+
+def test_recover_validation():
+    lib = _lib.load()
+    B, H, Sp, Sv, St, Dk = 2, 4, 5, 40, 3, 32
+    kp, kc, kt = _t((B, H, Sp, 128)), _t((B, H, Sv, Dk)), _t((B, H, St, 128))
+    tm, sm, pm = _t((B, H, 128), _lib.RK_U8), _t((B, H, Sv, 128), _lib.RK_U8), _t((B, H, Sv, 1))
+    out, vis = _t((B, H, Sp + Sv + St, 128)), _t((B, H, Sv, 128))
+    r = ctypes.byref
+    assert lib.rk_think_recover_check(r(kp), r(kc), r(kt), r(tm), r(out)) == 0
+    assert lib.rk_think_recover_check(None, r(kc), None, r(tm), r(vis)) == 0
+    assert lib.rk_think_recover_check(None, r(kc), None, r(tm), r(out)) == _lib.RK_ERR_SHAPE
+    assert lib.rk_think_recover_check(r(kp), r(kc), r(kt), r(sm), r(out)) == _lib.RK_ERR_RANK
+    assert lib.rk_spark_recover_check(r(kp), r(kc), r(kt), r(sm), r(pm), r(out)) == 0
+    assert lib.rk_spark_recover_check(None, r(kc), None, r(sm), r(pm), r(vis)) == 0
+    assert lib.rk_spark_recover_check(None, r(kc), None, r(sm), None, r(vis)) == _lib.RK_ERR_NULL
+    bad_pm = _t((B, H, Sv, 1), _lib.RK_BF16)
+    assert lib.rk_spark_recover_check(None, r(kc), None, r(sm), r(bad_pm), r(vis)) == _lib.RK_ERR_DTYPE
+    wide = _t((B, H, Sv, 129))
+    assert lib.rk_think_recover_check(None, wide, None, r(tm), r(vis)) == _lib.RK_ERR_SHAPE
+    sel = _t((B, H, 128, Dk), _lib.RK_F32)
+    assert lib.rk_channel_selection(r(tm), r(_t((B, H, 128, 0), _lib.RK_F32)), None) == _lib.RK_ERR_KEEP_DIM
+    assert lib.rk_channel_selection(r(tm), r(_t((B, H, 64, Dk), _lib.RK_F32)), None) == _lib.RK_ERR_HEAD_DIM
+    assert lib.rk_channel_selection(r(sm), r(sel), None) == _lib.RK_ERR_RANK
