@@ -95,6 +95,39 @@ def _time_graph(fn, steps, warmup, per_graph=1):
     return s.elapsed_time(e) / (reps * per_graph) * 1e3
 
 
+def _timed(fn, reps, graph=True):
+    """(result, device us per call, wall us per call) over ``reps`` calls.
+    Device-only stages are replayed from a HIP graph, so small kernels are not
+    timed at the speed of the Python call that launches them."""
+    import torch
+    out = fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                for _ in range(reps):
+                    fn()
+        torch.cuda.current_stream().wait_stream(side)
+        g.replay()
+        torch.cuda.synchronize()
+        run = g.replay
+    else:
+        def run():
+            for _ in range(reps):
+                fn()
+    t0 = time.perf_counter()
+    e0.record()
+    run()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / reps * 1e6
+    return out, e0.elapsed_time(e1) * 1e3 / reps, wall
+
+
 def _cpu_baseline(inp, cfg, budget_s=12.0):
     """CPU oracle (numpy fp32) over whole batch elements of the same inputs,
     cycling over the batch until ~budget_s of CPU work; returns us per full
@@ -299,35 +332,7 @@ def run_prefill(args):
     rows = []
 
     def timed(fn, graph=True):
-        """(result, device us per call, wall us per call).  Device-only stages
-        are replayed from a HIP graph, so small kernels are not timed at the
-        speed of the Python call that launches them."""
-        out = fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        if graph:
-            g = torch.cuda.CUDAGraph()
-            side = torch.cuda.Stream()
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                with torch.cuda.graph(g, stream=side):
-                    for _ in range(reps):
-                        fn()
-            torch.cuda.current_stream().wait_stream(side)
-            g.replay()
-            torch.cuda.synchronize()
-            run = g.replay
-        else:
-            def run():
-                for _ in range(reps):
-                    fn()
-        t0 = time.perf_counter()
-        e0.record()
-        run()
-        e1.record()
-        torch.cuda.synchronize()
-        wall = (time.perf_counter() - t0) / reps * 1e6
-        return out, e0.elapsed_time(e1) * 1e3 / reps, wall
+        return _timed(fn, reps, graph)
 
     for S_v in c.visual:
         st = synth.make_flow_layer(c, S_v, seed=S_v, device=dev)
@@ -363,6 +368,83 @@ def run_prefill(args):
     print(json.dumps(line), flush=True)
 
 
+def run_baselines(args):
+    """ThinK and SparK (kv_pruning_utils.py:44-90, llama_visionzip.py:216-241)
+    at a decode configuration (default config 2) on one GPU: the prefill
+    selection of each over the visual Keys, the decode-time recovery (the
+    recovered visual rows and the full-width span written by one launch) and
+    the decode step (recovery + dense decode), next to ThinK's attention on
+    the RotateK kernel (one-hot R, no recovery) and the RotateK step on the
+    same data.  Every stage is >= 100 us at config 2, so it is timed eagerly
+    with HIP events over ``--steps`` calls; bytes are algorithmic."""
+    import torch
+
+    from rotatek_amd import synth
+    from rotatek_amd.baselines import (recover_spark, recover_think, selection_rotation, spark_prune,
+                                       think_score_and_compact)
+    from rotatek_amd.kernels.full_channel_flash_decoding import full_channel_decode
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+
+    cfg = synth.CONFIGS[args.config]
+    torch.cuda.set_device(0)
+    reps = args.steps if args.steps_given else 20
+    inp = synth.make_decode_inputs(cfg, "cuda", seed=0, with_raw=True)
+    B, Hq, H, S_v, S_f, keep, G = cfg.B, cfg.H_q, cfg.H_kv, cfg.S_v, cfg.S_f, cfg.keep, cfg.G
+    prune, e, heads, rows = 128 - keep, 2, cfg.B * cfg.H_kv, cfg.S_v + cfg.S_f
+    g = torch.Generator(device="cuda").manual_seed(1)
+    Kv, q, kf, V = inp["k_vis_raw"], inp["q_full"], inp["k_full"], inp["V"]   # V rows: [visual | full]
+    Qw = torch.randn(B, Hq, 32, 128, generator=g, device="cuda").to(cfg.dtype)
+    stage = torch.empty(B, H, rows, 128, device="cuda", dtype=cfg.dtype)
+    _log(f"[baselines] {torch.cuda.get_device_name(0)}; {cfg}")
+
+    def timed(fn):
+        return _timed(fn, reps, graph=False)
+
+    r = {}
+    kbytes = heads * S_v * 128 * e
+    (Kc_t, tm), t, _ = timed(lambda: think_score_and_compact(Kv, Qw, H, prune))
+    r["think_prefill_us"] = t
+    r["think_prefill_gbps"] = (2 * kbytes + heads * S_v * keep * e) / t / 1e3   # two passes over K
+    (Kc_s, sm, pm), t, _ = timed(lambda: spark_prune(Kv, Qw, G, prune))
+    r["spark_prefill_us"] = t
+    r["spark_prefill_gbps"] = (kbytes + heads * S_v * (keep * e + 128 + e)) / t / 1e3
+    full_bytes = heads * S_f * 128 * e + heads * rows * 128 * e               # read the full span, write all rows
+    _, t, _ = timed(lambda: recover_think(Kc_t, tm, out=stage, k_text=kf))
+    r["think_recover_us"] = t
+    r["think_recover_gbps"] = (heads * S_v * keep * e + full_bytes) / t / 1e3
+    _, t, _ = timed(lambda: recover_spark(Kc_s, sm, pm, out=stage, k_text=kf))
+    r["spark_recover_us"] = t
+    r["spark_recover_gbps"] = (heads * S_v * (keep * e + 128 + e) + full_bytes) / t / 1e3
+
+    def think_step():
+        recover_think(Kc_t, tm, out=stage, k_text=kf)
+        return full_channel_decode(q, stage, V, G)
+
+    def spark_step():
+        recover_spark(Kc_s, sm, pm, out=stage, k_text=kf)
+        return full_channel_decode(q, stage, V, G)
+
+    da = synth.decode_args(inp)
+    R_sel = selection_rotation(tm, keep, cfg.dtype)
+    think_fused_args = dict(da, R_partial=R_sel, delta_mu=None, k_sparse=Kc_t)
+    for name, fn in (("think_decode_step", think_step), ("spark_decode_step", spark_step),
+                     ("think_fused_decode", lambda: rotatek_decode_fused(**think_fused_args)),
+                     ("rotatek_decode", lambda: rotatek_decode_fused(**da))):
+        _, t, _ = timed(fn)
+        r[name + "_us"] = t
+    r = {k: round(v, 2) for k, v in r.items()}
+    _log("[baselines] " + ", ".join(f"{k}={v}" for k, v in r.items()))
+    line = {"metric": "ThinK / SparK baselines on HIP: prefill per layer and decode step (us, HIP events)",
+            "value": r["think_decode_step_us"], "unit": "us", "n_gpus": 1, "steps": reps, "warmup": 1,
+            "higher_is_better": False, "dtype": "fp16" if cfg.dtype == torch.float16 else "bf16",
+            "data": "synthetic: the decode inputs of the configuration, full-width visual Keys, N(0,1) "
+                    "query window of 32",
+            "config": {"workload": f"{cfg.name} baselines: B={B}, H_q={Hq}, H_kv={H}, S_v={S_v}, S_f={S_f}, "
+                                   f"keep {keep}; value = ThinK decode step (recover + dense decode)",
+                       "stages": r}}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -374,6 +456,8 @@ def main():
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--prefill-only", action="store_true", help="config 4: time the prefill stages")
+    ap.add_argument("--baselines", action="store_true",
+                    help="time the ThinK / SparK prefill, recovery and decode at --config")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc passes (no GPU needed)")
@@ -388,6 +472,12 @@ def main():
         return
     if args.pmc_summary:
         pmc_summary(args.pmc_summary[0], args.pmc_summary[1], args.copy_calibration, args.steps, args.config)
+        return
+    if args.baselines:
+        if args.gpus != 1:
+            print("bench.py measures one GPU only", file=sys.stderr)
+            sys.exit(2)
+        run_baselines(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the RotateK decode "

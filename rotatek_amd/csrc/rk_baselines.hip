@@ -10,22 +10,25 @@
 //                        window of dtype(q^2))), score = dtype(qn * kn);
 //                        prune the prune_count smallest scores -> keep mask
 //                        and ascending kept indices
-//   compact_kernel       K_compact[..., j] = K[..., idx[j]]
+//   compact_kernel       K_compact[..., j] = K[..., idx[j]] over 64-token
+//                        tiles staged in LDS
 // SparK (rotatek/baselines/spark.py:15-60, with the group mean of the
 // queries from kv_pruning_utils.py:76-79): one channel subset per token.
 //   spark_qnorm_kernel   q_g = dtype(mean over the G query heads of a KV
 //                        head), q_norm = dtype(||q_g||_2 over the window)
 //   spark_kernel         one wave per token: score = dtype(dtype(k^2) qn);
-//                        keep the Dk largest by a radix select over
-//                        (score, channel) keys; writes K_compact, the
-//                        per-token mask and dtype(mean of the pruned values)
+//                        keep the Dk largest (bitwise search for the
+//                        threshold score, lowest channels among the ties);
+//                        writes K_compact, the per-token mask and
+//                        dtype(mean of the pruned values)
 // Recovery (llama_visionzip.py:216-233):
-//   recover_kernel       one wave per row of [prompt | visual | text]: the
-//                        visual rows get the kept channels from K_compact in
-//                        ascending channel order and 0 (ThinK) or the
-//                        token's pruned mean (SparK) elsewhere; prompt and
-//                        text rows are copied, so the caller's torch.cat of
-//                        the three spans is written by the same pass.
+//   recover_kernel       64-row tiles of [prompt | visual | text]: the
+//                        visual rows get the kept channels from K_compact
+//                        (staged in LDS) in ascending channel order and 0
+//                        (ThinK) or the token's pruned mean (SparK)
+//                        elsewhere; prompt and text rows are copied, so the
+//                        caller's torch.cat of the three spans is written by
+//                        the same pass.
 //   selection_kernel     one-hot R[c][j] = (c is the j-th kept channel) from
 //                        a per-head mask, so the RotateK decode kernel can
 //                        run ThinK's zero-filled attention from K_compact.
@@ -35,9 +38,8 @@
 // that way and passes it in.  Ties: torch's GPU topk (largest=False) takes
 // equal values at the boundary in index order, so ThinK prunes the lower
 // channel first; the GPU sort behind argsort(descending) keeps equal values
-// in index order, so SparK keeps the lower channel first.  Both are encoded
-// in 23-bit keys (order-preserving 16-bit score << 7 | channel or
-// 127 - channel), which are distinct per head / token.
+// in index order, so SparK keeps the lower channel first.  Scores are compared
+// through order-preserving 16-bit keys (NaN highest, -0 == +0).
 #include <math.h>
 
 #include "rk_common.h"
@@ -106,6 +108,48 @@ __device__ __forceinline__ uint4 ld8(const uint16_t* base, int64_t ss, int64_t s
     return make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
+
+template <bool VEC>
+__device__ __forceinline__ void st8(uint16_t* base, int64_t ss, int64_t sc, int64_t t, int c0, const uint4& v) {
+  if constexpr (VEC) {
+    *(uint4*)(base + t * ss + c0) = v;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) base[t * ss + (c0 + e) * sc] = (uint16_t)(word(v, e >> 1) >> ((e & 1) * 16));
+  }
+}
+
+// Kept flags of the eight mask bytes p[0], p[sc], ..., p[7 sc] (bit e set
+// when byte e is non-zero); VEC: one 8-byte load (sc == 1, 8-byte aligned).
+template <bool VEC>
+__device__ __forceinline__ uint32_t mask8(const uint8_t* p, int64_t sc) {
+  uint32_t f = 0u;
+  if constexpr (VEC) {
+    const uint64_t m = *(const uint64_t*)p;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f |= (((m >> (8 * e)) & 0xFFu) != 0u ? 1u : 0u) << e;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f |= (p[e * sc] != 0 ? 1u : 0u) << e;
+  }
+  return f;
+}
+
+// Exclusive prefix sum of v over the 16 lanes of this lane's row of the
+// wave (every lane of the row must call it).
+__device__ __forceinline__ int prefix16(int v) {
+  const int l16 = threadIdx.x & 15;
+  int incl = v;
+#pragma unroll
+  for (int d = 1; d < 16; d <<= 1) {
+    const int y = __shfl_up(incl, d, 16);
+    if (l16 >= d) incl += y;
+  }
+  return incl - v;
+}
+
+constexpr int kTile = 64;     // token rows per workgroup tile
+constexpr int kTilePad = 8;   // LDS row padding (elements): 16-byte aligned rows
 
 // ------------------------------------------------------------------ ThinK
 // grid (splits, B*H): workgroup x sums dtype(k^2) over tokens
@@ -197,33 +241,49 @@ __global__ void __launch_bounds__(kD) think_select_kernel(const ThinkArgs a) {
   }
 }
 
-// grid (splits, B*H): K_compact[b,h,t,j] = K[b,h,t,idx[j]].  Wave w of the
-// workgroup handles tokens t0 + w, t0 + w + 4, ...; lane l writes columns
-// 2l and 2l+1 (one dword store when OVEC).
-template <bool OVEC>
+// grid (splits, B*H): K_compact[b,h,t,j] = K[b,h,t,idx[j]].  Tiles of 64
+// tokens are staged in LDS with 16-byte loads (thread t loads channels
+// 8(t%16).. of rows t/16 + 16i); thread t then gathers output columns
+// 8(t%16)..+7 of the same rows from LDS (threads past Dk idle).  OVEC: one
+// 16-byte store per chunk (unit stride, aligned rows, Dk % 8 == 0).
+template <bool VEC, bool OVEC>
 __global__ void __launch_bounds__(kThreads) compact_kernel(View k, const int32_t* idx, int Dk, int64_t chunk,
                                                            OutView o) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ __align__(16) uint16_t s_k[kTile * (kD + kTilePad)];
+  const int tid = threadIdx.x, c8 = tid & 15, rq = tid >> 4;
   const int x = blockIdx.x, bh = blockIdx.y, b = bh / k.H, h = bh - b * k.H;
-  const int j0 = 2 * lane, j1 = j0 + 1;
-  const bool v0 = j0 < Dk, v1 = j1 < Dk;
-  const int64_t s0 = v0 ? idx[(int64_t)bh * kD + j0] * k.sc : 0;
-  const int64_t s1 = v1 ? idx[(int64_t)bh * kD + j1] * k.sc : 0;
+  int src[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) src[e] = 8 * c8 + e < Dk ? idx[(int64_t)bh * kD + 8 * c8 + e] : 0;
   const uint16_t* base = k.data + head_off(k.sb, k.sh, b, h);
   uint16_t* ob = o.data + head_off(o.sb, o.sh, b, h);
   const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
-  for (int64_t t = t0 + w; t < t1; t += 4) {
-    const uint16_t e0 = v0 ? base[t * k.ss + s0] : (uint16_t)0;
-    const uint16_t e1 = v1 ? base[t * k.ss + s1] : (uint16_t)0;
-    if constexpr (OVEC) {
-      if (v1)
-        *(uint32_t*)(ob + t * o.ss + j0) = (uint32_t)e0 | ((uint32_t)e1 << 16);
-      else if (v0)
-        ob[t * o.ss + j0] = e0;
-    } else {
-      if (v0) ob[t * o.ss + j0 * o.sc] = e0;
-      if (v1) ob[t * o.ss + j1 * o.sc] = e1;
+  for (int64_t tile = t0; tile < t1; tile += kTile) {
+#pragma unroll
+    for (int i = 0; i < kTile / 16; ++i) {
+      const int64_t t = tile + rq + 16 * i;
+      if (t < t1) *(uint4*)(s_k + (rq + 16 * i) * (kD + kTilePad) + 8 * c8) = ld8<VEC>(base, k.ss, k.sc, t, 8 * c8);
     }
+    __syncthreads();
+    if (8 * c8 < Dk) {
+#pragma unroll
+      for (int i = 0; i < kTile / 16; ++i) {
+        const int64_t t = tile + rq + 16 * i;
+        if (t >= t1) continue;
+        const uint16_t* row = s_k + (rq + 16 * i) * (kD + kTilePad);
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w[e >> 1] |= (uint32_t)row[src[e]] << ((e & 1) * 16);
+        if constexpr (OVEC) {
+          *(uint4*)(ob + t * o.ss + 8 * c8) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            if (8 * c8 + e < Dk) ob[t * o.ss + (8 * c8 + e) * o.sc] = (uint16_t)(w[e >> 1] >> ((e & 1) * 16));
+        }
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -255,8 +315,14 @@ struct SparkArgs {
 };
 
 // grid (splits, B*H); one wave per token, lane l owns channels 2l, 2l+1.
+// Wave w of the workgroup takes groups of 8 consecutive tokens (w, w + 4,
+// ...) and loads the next group while it selects the current one.
+// Selection: the keep-th largest 16-bit score key T by a bitwise search over
+// wave-wide counts, then every channel above T and, of those equal to T, the
+// lowest channels up to keep (a prefix count over the channel order).
 template <class TT, bool KVEC>
 __global__ void __launch_bounds__(kThreads) spark_kernel(const SparkArgs a) {
+  constexpr int NT = 8;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int x = blockIdx.x, bh = blockIdx.y, b = bh / a.k.H, h = bh - b * a.k.H;
   const int c0 = 2 * lane, c1 = c0 + 1;
@@ -267,44 +333,65 @@ __global__ void __launch_bounds__(kThreads) spark_kernel(const SparkArgs a) {
   uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
   uint16_t* pb = a.pm.data + head_off(a.pm.sb, a.pm.sh, b, h);
   const int64_t t0 = (int64_t)x * a.chunk, t1 = min(a.k.S, t0 + a.chunk);
-  for (int64_t t = t0 + w; t < t1; t += 4) {  // wave-uniform loop
-    uint32_t raw;
-    if constexpr (KVEC) {
-      raw = *(const uint32_t*)(kb + t * a.k.ss + c0);
-    } else {
-      raw = (uint32_t)kb[t * a.k.ss + c0 * a.k.sc] | ((uint32_t)kb[t * a.k.ss + c1 * a.k.sc] << 16);
-    }
-    const uint16_t r0 = (uint16_t)raw, r1 = (uint16_t)(raw >> 16);
-    const float e0 = TT::to_f32(r0), e1 = TT::to_f32(r1);
-    const float s0 = rnd<TT>(rnd<TT>(e0 * e0) * q0), s1 = rnd<TT>(rnd<TT>(e1 * e1) * q1);
-    const uint32_t k0 = (order_key<TT>(s0) << 7) | (uint32_t)(127 - c0);
-    const uint32_t k1 = (order_key<TT>(s1) << 7) | (uint32_t)(127 - c1);
-    bool kept0, kept1;
-    if (a.keep >= kD) {
-      kept0 = kept1 = true;
-    } else if (a.keep <= 0) {
-      kept0 = kept1 = false;
-    } else {
-      // largest T with #{key >= T} >= keep, i.e. the keep-th largest key
-      uint32_t T = 0u;
-      for (int bit = 22; bit >= 0; --bit) {
-        const uint32_t cand = T | (1u << bit);
-        const int cnt = __popcll(__ballot(k0 >= cand)) + __popcll(__ballot(k1 >= cand));
-        if (cnt >= a.keep) T = cand;
-      }
-      kept0 = k0 >= T;
-      kept1 = k1 >= T;
-    }
-    const uint64_t m0 = __ballot(kept0), m1 = __ballot(kept1);
-    const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)kept0;
-    if (kept0) cb[t * a.kc.ss + p0 * a.kc.sc] = r0;
-    if (kept1) cb[t * a.kc.ss + p1 * a.kc.sc] = r1;
-    mb[t * a.mask.ss + c0 * a.mask.sc] = (uint8_t)kept0;
-    mb[t * a.mask.ss + c1 * a.mask.sc] = (uint8_t)kept1;
-    float p = (kept0 ? 0.f : e0) + (kept1 ? 0.f : e1);
+  const int keep = a.keep;
+
+  auto load_group = [&](int64_t tg, uint32_t (&raw)[NT]) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) p += shfl_xor(p, off);
-    if (lane == 0) pb[t * a.pm.ss] = TT::from_f32(pin(p * a.f_pruned));
+    for (int j = 0; j < NT; ++j) {
+      const int64_t t = min(tg + j, t1 - 1);
+      if constexpr (KVEC) {
+        raw[j] = *(const uint32_t*)(kb + t * a.k.ss + c0);
+      } else {
+        raw[j] = (uint32_t)kb[t * a.k.ss + c0 * a.k.sc] | ((uint32_t)kb[t * a.k.ss + c1 * a.k.sc] << 16);
+      }
+    }
+  };
+
+  uint32_t cur[NT], nxt[NT];
+  int64_t tg = t0 + (int64_t)NT * w;
+  if (tg < t1) load_group(tg, nxt);
+  for (; tg < t1; tg += NT * 4) {  // wave-uniform loop
+#pragma unroll
+    for (int j = 0; j < NT; ++j) cur[j] = nxt[j];
+    if (tg + NT * 4 < t1) load_group(tg + NT * 4, nxt);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t t = tg + j;
+      if (t >= t1) break;
+      const uint16_t r0 = (uint16_t)cur[j], r1 = (uint16_t)(cur[j] >> 16);
+      const float e0 = TT::to_f32(r0), e1 = TT::to_f32(r1);
+      const uint32_t k0 = order_key<TT>(rnd<TT>(rnd<TT>(e0 * e0) * q0));
+      const uint32_t k1 = order_key<TT>(rnd<TT>(rnd<TT>(e1 * e1) * q1));
+      bool kept0, kept1;
+      if (keep >= kD) {
+        kept0 = kept1 = true;
+      } else if (keep <= 0) {
+        kept0 = kept1 = false;
+      } else {
+        uint32_t T = 0u;  // largest T with #{key >= T} >= keep
+        for (int bit = 15; bit >= 0; --bit) {
+          const uint32_t cand = T | (1u << bit);
+          const int cnt = __popcll(__ballot(k0 >= cand)) + __popcll(__ballot(k1 >= cand));
+          if (cnt >= keep) T = cand;
+        }
+        const int need = keep - (__popcll(__ballot(k0 > T)) + __popcll(__ballot(k1 > T)));
+        const bool eq0 = k0 == T, eq1 = k1 == T;
+        const uint64_t q0m = __ballot(eq0), q1m = __ballot(eq1);
+        const int er0 = __popcll(q0m & below) + __popcll(q1m & below), er1 = er0 + (int)eq0;
+        kept0 = k0 > T || (eq0 && er0 < need);
+        kept1 = k1 > T || (eq1 && er1 < need);
+      }
+      const uint64_t m0 = __ballot(kept0), m1 = __ballot(kept1);
+      const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)kept0;
+      if (kept0) cb[t * a.kc.ss + p0 * a.kc.sc] = r0;
+      if (kept1) cb[t * a.kc.ss + p1 * a.kc.sc] = r1;
+      mb[t * a.mask.ss + c0 * a.mask.sc] = (uint8_t)kept0;
+      mb[t * a.mask.ss + c1 * a.mask.sc] = (uint8_t)kept1;
+      float p = (kept0 ? 0.f : e0) + (kept1 ? 0.f : e1);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) p += shfl_xor(p, off);
+      if (lane == 0) pb[t * a.pm.ss] = TT::from_f32(pin(p * a.f_pruned));
+    }
   }
 }
 
@@ -321,62 +408,91 @@ struct RecoverArgs {
   int H;
 };
 
-// grid (splits, B*H); wave per output row, lane l writes channels 2l, 2l+1.
-// A visual row's kept channel of rank r (ascending channel order) takes
-// column r of K_compact; ranks >= Dk (a mask row with more than Dk kept
-// channels) are filled like pruned channels, so no read leaves the row.
-template <bool SPARK, bool OVEC>
+// grid (splits, B*H); tiles of 64 output rows.  The tile's compact rows are
+// staged in LDS (4 threads per row), then thread t writes channels
+// 8(t%16)..+7 of rows t/16 + 16i: prompt / text rows are copied, a visual
+// row's kept channel of rank r (ascending channel order) takes column r of
+// K_compact and the others 0 (ThinK) or the row's pruned mean (SparK).
+// Ranks come from 16-lane prefix sums of the mask popcounts; ranks >= Dk (a
+// mask row with more than Dk kept channels) are filled like pruned channels,
+// so no read leaves the row.  FAST: 16-byte loads and stores of every span
+// (unit channel stride, aligned rows), 8-byte mask loads, Dk % 8 == 0.
+template <bool SPARK, bool FAST>
 __global__ void __launch_bounds__(kThreads) recover_kernel(const RecoverArgs a) {
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ __align__(16) uint16_t s_c[kTile * kD];
+  const int tid = threadIdx.x, c8 = tid & 15, rq = tid >> 4;
   const int x = blockIdx.x, bh = blockIdx.y, b = bh / a.H, h = bh - b * a.H;
-  const int c0 = 2 * lane, c1 = c0 + 1;
   const int Dk = a.kc.C;
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int64_t Sp = a.pr.S, Sv = a.kc.S;
   const uint16_t* pb = a.pr.data + head_off(a.pr.sb, a.pr.sh, b, h);
   const uint16_t* kb = a.kc.data + head_off(a.kc.sb, a.kc.sh, b, h);
   const uint16_t* tb = a.tx.data + head_off(a.tx.sb, a.tx.sh, b, h);
   const uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
+  const uint16_t* fb = SPARK ? a.pm + head_off(a.p_sb, a.p_sh, b, h) : nullptr;
   uint16_t* ob = a.out.data + head_off(a.out.sb, a.out.sh, b, h);
-  int map0 = -1, map1 = -1;  // ThinK: K_compact column of channels c0, c1
+  int map[8];  // ThinK: K_compact column of channel 8 c8 + e, -1 = pruned
   if constexpr (!SPARK) {
-    const bool k0 = mb[c0 * a.mask.sc] != 0, k1 = mb[c1 * a.mask.sc] != 0;
-    const uint64_t m0 = __ballot(k0), m1 = __ballot(k1);
-    const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)k0;
-    map0 = (k0 && p0 < Dk) ? p0 : -1;
-    map1 = (k1 && p1 < Dk) ? p1 : -1;
+    const uint32_t f = mask8<false>(mb + 8 * c8 * a.mask.sc, a.mask.sc);
+    int rank = prefix16(__popc(f));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool kept = (f >> e) & 1u;
+      map[e] = (kept && rank < Dk) ? rank : -1;
+      rank += kept;
+    }
   }
-  const int64_t Sp = a.pr.S, Sv = a.kc.S;
   const int64_t r0 = (int64_t)x * a.chunk, r1 = min(a.rows, r0 + a.chunk);
-  for (int64_t r = r0 + w; r < r1; r += 4) {  // wave-uniform loop
-    uint16_t e0, e1;
-    if (r < Sp) {
-      e0 = pb[r * a.pr.ss + c0 * a.pr.sc];
-      e1 = pb[r * a.pr.ss + c1 * a.pr.sc];
-    } else if (r < Sp + Sv) {
-      const int64_t t = r - Sp;
-      int s0 = map0, s1 = map1;
-      uint16_t fill = 0;
-      if constexpr (SPARK) {
-        const bool k0 = mb[t * a.mask.ss + c0 * a.mask.sc] != 0, k1 = mb[t * a.mask.ss + c1 * a.mask.sc] != 0;
-        const uint64_t m0 = __ballot(k0), m1 = __ballot(k1);
-        const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)k0;
-        s0 = (k0 && p0 < Dk) ? p0 : -1;
-        s1 = (k1 && p1 < Dk) ? p1 : -1;
-        fill = a.pm[head_off(a.p_sb, a.p_sh, b, h) + t * a.p_ss];
+  for (int64_t tile = r0; tile < r1; tile += kTile) {
+    const int64_t v0 = max(tile, Sp), v1 = min(min(tile + kTile, r1), Sp + Sv);
+    if (v0 < v1) {  // stage the tile's visual rows (workgroup-uniform)
+      const int row = tid >> 2, nrow = (int)(v1 - v0), off = (int)(v0 - tile);
+      if (row < nrow) {
+        const uint16_t* src = kb + (v0 - Sp + row) * a.kc.ss;
+        uint16_t* dst = s_c + (off + row) * kD;
+        if constexpr (FAST) {
+          for (int cc = tid & 3; cc < (Dk >> 3); cc += 4) *(uint4*)(dst + 8 * cc) = *(const uint4*)(src + 8 * cc);
+        } else {
+          for (int cc = tid & 3; cc < Dk; cc += 4) dst[cc] = src[cc * a.kc.sc];
+        }
       }
-      e0 = s0 >= 0 ? kb[t * a.kc.ss + s0 * a.kc.sc] : fill;
-      e1 = s1 >= 0 ? kb[t * a.kc.ss + s1 * a.kc.sc] : fill;
-    } else {
-      const int64_t t = r - Sp - Sv;
-      e0 = tb[t * a.tx.ss + c0 * a.tx.sc];
-      e1 = tb[t * a.tx.ss + c1 * a.tx.sc];
     }
-    if constexpr (OVEC) {
-      *(uint32_t*)(ob + r * a.out.ss + c0) = (uint32_t)e0 | ((uint32_t)e1 << 16);
-    } else {
-      ob[r * a.out.ss + c0 * a.out.sc] = e0;
-      ob[r * a.out.ss + c1 * a.out.sc] = e1;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kTile / 16; ++i) {
+      const int64_t r = tile + rq + 16 * i;
+      const bool live = r < r1, vis = live && r >= Sp && r < Sp + Sv;
+      uint32_t f = 0u;
+      if constexpr (SPARK) {
+        if (vis) f = mask8<FAST>(mb + (r - Sp) * a.mask.ss + 8 * c8 * a.mask.sc, a.mask.sc);
+      }
+      int rank = SPARK ? prefix16(__popc(f)) : 0;  // every lane of the row takes part
+      if (!live) continue;
+      uint4 v;
+      if (r < Sp) {
+        v = ld8<FAST>(pb, a.pr.ss, a.pr.sc, r, 8 * c8);
+      } else if (vis) {
+        const uint16_t* row = s_c + (r - tile) * kD;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if constexpr (SPARK) {
+          const uint32_t fill = fb[(r - Sp) * a.p_ss];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const bool kept = (f >> e) & 1u;
+            const uint32_t val = (kept && rank < Dk) ? (uint32_t)row[rank] : fill;
+            rank += kept;
+            w[e >> 1] |= val << ((e & 1) * 16);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) w[e >> 1] |= (map[e] >= 0 ? (uint32_t)row[map[e]] : 0u) << ((e & 1) * 16);
+        }
+        v = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        v = ld8<FAST>(tb, a.tx.ss, a.tx.sc, r - Sp - Sv, 8 * c8);
+      }
+      st8<FAST>(ob, a.out.ss, a.out.sc, r, 8 * c8, v);
     }
+    __syncthreads();
   }
 }
 
@@ -502,7 +618,8 @@ struct ThinkPlan {
 ThinkPlan think_plan(int64_t bh, int64_t S, int cus) {
   ThinkPlan p;
   p.splits = token_splits(bh, S, cus, 2, 256);
-  p.chunk = cdiv(S > 0 ? S : 1, p.splits);
+  p.chunk = cdiv(cdiv(S > 0 ? S : 1, p.splits), kTile) * kTile;
+  p.splits = (int)cdiv(S > 0 ? S : 1, p.chunk);
   p.off_part = 0;
   p.off_idx = align256((size_t)bh * p.splits * kD * sizeof(float));
   p.total = p.off_idx + align256((size_t)bh * kD * sizeof(int32_t));
@@ -556,10 +673,15 @@ hipError_t launch_think(const View& kv, bool kvec, const View& qv, int G, int ke
   hipLaunchKernelGGL((think_select_kernel<TT>), dim3((unsigned)bh), dim3(kD), 0, s, a);
   if (keep > 0 && kv.S > 0) {
     const OutView o = out_of(kc_out);
-    if (pairs4(kc_out))
-      hipLaunchKernelGGL((compact_kernel<true>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
+    const bool ovec = rows16(kc_out) && keep % 8 == 0;
+    if (kvec && ovec)
+      hipLaunchKernelGGL((compact_kernel<true, true>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
+    else if (kvec)
+      hipLaunchKernelGGL((compact_kernel<true, false>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
+    else if (ovec)
+      hipLaunchKernelGGL((compact_kernel<false, true>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
     else
-      hipLaunchKernelGGL((compact_kernel<false>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
+      hipLaunchKernelGGL((compact_kernel<false, false>), grid, dim3(kThreads), 0, s, kv, idx, keep, p.chunk, o);
   }
   return hipGetLastError();
 }
@@ -672,18 +794,24 @@ int recover(bool spark, const rk_tensor* k_prompt, const rk_tensor* k_pruned, co
   if (st) return st;
   a.out = out_of(out);
   a.H = (int)H;
-  const int splits = token_splits(B * H, a.rows, cus, 4, 64);
-  a.chunk = cdiv(a.rows, splits);
+  int splits = token_splits(B * H, a.rows, cus, 8, kTile);
+  a.chunk = cdiv(cdiv(a.rows, splits), kTile) * kTile;
+  splits = (int)cdiv(a.rows, a.chunk);
   const dim3 grid((unsigned)splits, (unsigned)(B * H));
   hipStream_t s = (hipStream_t)stream;
-  const bool ovec = pairs4(out);
+  // 16-byte rows everywhere, 8-byte mask rows (SparK)
+  bool fast = rows16(out) && (!k_prompt || rows16(k_prompt)) && (!k_text || rows16(k_text)) &&
+              a.kc.C % 8 == 0 && (a.kc.C == 0 || rows16(k_pruned));
+  if (spark)
+    fast = fast && mask->stride[3] == 1 && mask->stride[0] % 8 == 0 && mask->stride[1] % 8 == 0 &&
+           mask->stride[2] % 8 == 0 && (((uintptr_t)mask->data) & 7) == 0;
   if (spark) {
-    if (ovec)
+    if (fast)
       hipLaunchKernelGGL((recover_kernel<true, true>), grid, dim3(kThreads), 0, s, a);
     else
       hipLaunchKernelGGL((recover_kernel<true, false>), grid, dim3(kThreads), 0, s, a);
   } else {
-    if (ovec)
+    if (fast)
       hipLaunchKernelGGL((recover_kernel<false, true>), grid, dim3(kThreads), 0, s, a);
     else
       hipLaunchKernelGGL((recover_kernel<false, false>), grid, dim3(kThreads), 0, s, a);
