@@ -23,14 +23,21 @@ __all__ = ["full_channel_decode", "rotatek_decode", "power_iteration_gpu", "inst
 
 def install_as_rotatek() -> None:
     """Alias this package as ``rotatek`` / ``rotatek.kernels`` /
-    ``rotatek.rotation`` (and the kernel submodules) in ``sys.modules``."""
+    ``rotatek.rotation`` / ``rotatek.baselines`` (and their submodules) in
+    ``sys.modules``."""
     import rotatek_amd
     import rotatek_amd.kernels as k
     import rotatek_amd.kernels.fused_decode as fd
     import rotatek_amd.kernels.full_channel_flash_decoding as fc
     import rotatek_amd.kernels.gqa_decode as gd
+    import rotatek_amd.baselines as bl
+    import rotatek_amd.baselines.spark as bs
+    import rotatek_amd.baselines.think as bt
     import rotatek_amd.rotation as rot
     sys.modules["rotatek"] = rotatek_amd
+    sys.modules["rotatek.baselines"] = bl
+    sys.modules["rotatek.baselines.think"] = bt
+    sys.modules["rotatek.baselines.spark"] = bs
     sys.modules["rotatek.kernels"] = k
     sys.modules["rotatek.kernels.fused_decode"] = fd
     sys.modules["rotatek.kernels.full_channel_flash_decoding"] = fc

@@ -16,7 +16,7 @@
 // queries from kv_pruning_utils.py:76-79): one channel subset per token.
 //   spark_qnorm_kernel   q_g = dtype(mean over the G query heads of a KV
 //                        head), q_norm = dtype(||q_g||_2 over the window)
-//   spark_kernel         one wave per token: score = dtype(dtype(k^2) qn);
+//   spark_kernel         16 lanes per token: score = dtype(dtype(k^2) qn);
 //                        keep the Dk largest (bitwise search for the
 //                        threshold score, lowest channels among the ties);
 //                        writes K_compact, the per-token mask and
@@ -146,6 +146,40 @@ __device__ __forceinline__ int prefix16(int v) {
     if (l16 >= d) incl += y;
   }
   return incl - v;
+}
+
+// Sum of v over the 16 lanes of this lane's row, in every lane of the row
+// (DPP row rotations by 8, 4, 2, 1).
+__device__ __forceinline__ int sum16(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x122, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x121, 0xF, 0xF, false);
+  return v;
+}
+
+template <int CTL>
+__device__ __forceinline__ float fdpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float fsum16(float v) {
+  v += fdpp<0x128>(v);
+  v += fdpp<0x124>(v);
+  v += fdpp<0x122>(v);
+  v += fdpp<0x121>(v);
+  return v;
+}
+
+// Exclusive prefix sum of v over the 16 lanes of this lane's row (DPP row
+// shifts by 1, 2, 4, 8 with zero fill).
+__device__ __forceinline__ int scan16(int v) {
+  int x = v;
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);
+  return x - v;
 }
 
 constexpr int kTile = 64;     // token rows per workgroup tile
@@ -314,83 +348,112 @@ struct SparkArgs {
   OutView pm;      // [B, H, S, 1]
 };
 
-// grid (splits, B*H); one wave per token, lane l owns channels 2l, 2l+1.
-// Wave w of the workgroup takes groups of 8 consecutive tokens (w, w + 4,
-// ...) and loads the next group while it selects the current one.
-// Selection: the keep-th largest 16-bit score key T by a bitwise search over
-// wave-wide counts, then every channel above T and, of those equal to T, the
-// lowest channels up to keep (a prefix count over the channel order).
-template <class TT, bool KVEC>
+// grid (splits, B*H).  Each 16-lane row of a wave owns one token (lane n:
+// channels 8n..8n+7, one 16-byte load), so a wave selects four tokens at
+// once and a workgroup sixteen; rows are prefetched two iterations ahead.
+// Selection per row: the keep-th largest 16-bit score key T by a bitwise
+// search over 16-lane counts, then every channel above T and, of those equal
+// to T, the lowest channels up to keep.  MVEC: 8-byte mask stores.
+template <class TT, bool KVEC, bool MVEC, bool CVEC>
 __global__ void __launch_bounds__(kThreads) spark_kernel(const SparkArgs a) {
-  constexpr int NT = 8;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ __align__(16) uint16_t s_row[kThreads / 64][4][kD];  // per wave: its four compact rows
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
   const int x = blockIdx.x, bh = blockIdx.y, b = bh / a.k.H, h = bh - b * a.k.H;
-  const int c0 = 2 * lane, c1 = c0 + 1;
-  const float q0 = a.qn[(int64_t)bh * kD + c0], q1 = a.qn[(int64_t)bh * kD + c1];
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  float qv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) qv[e] = a.qn[(int64_t)bh * kD + 8 * n + e];
   const uint16_t* kb = a.k.data + head_off(a.k.sb, a.k.sh, b, h);
   uint16_t* cb = a.kc.data + head_off(a.kc.sb, a.kc.sh, b, h);
   uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
   uint16_t* pb = a.pm.data + head_off(a.pm.sb, a.pm.sh, b, h);
   const int64_t t0 = (int64_t)x * a.chunk, t1 = min(a.k.S, t0 + a.chunk);
   const int keep = a.keep;
+  auto load = [&](int64_t t) { return ld8<KVEC>(kb, a.k.ss, a.k.sc, min(t, t1 - 1), 8 * n); };
 
-  auto load_group = [&](int64_t tg, uint32_t (&raw)[NT]) {
+  const int64_t first = t0 + 4 * w;  // this wave's first group; groups advance by 16 tokens
+  uint4 b0 = make_uint4(0, 0, 0, 0), b1 = b0;
+  if (first < t1) b0 = load(first + g);
+  if (first + 16 < t1) b1 = load(first + 16 + g);
+  for (int64_t tb = first; tb < t1; tb += 16) {  // wave-uniform loop
+    const uint4 cur = b0;
+    b0 = b1;
+    if (tb + 32 < t1) b1 = load(tb + 32 + g);
+    const int64_t t = tb + g;
+    float ev[8];
+    uint32_t kk[8];
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int64_t t = min(tg + j, t1 - 1);
-      if constexpr (KVEC) {
-        raw[j] = *(const uint32_t*)(kb + t * a.k.ss + c0);
-      } else {
-        raw[j] = (uint32_t)kb[t * a.k.ss + c0 * a.k.sc] | ((uint32_t)kb[t * a.k.ss + c1 * a.k.sc] << 16);
+    for (int e = 0; e < 8; ++e) {
+      ev[e] = TT::to_f32((uint16_t)(word(cur, e >> 1) >> ((e & 1) * 16)));
+      kk[e] = order_key<TT>(rnd<TT>(rnd<TT>(ev[e] * ev[e]) * qv[e]));
+    }
+    uint32_t kept = 0u;  // bit e: channel 8n + e kept
+    if (keep >= kD) {
+      kept = 0xFFu;
+    } else if (keep > 0) {
+      uint32_t T = 0u;  // largest T with #{key >= T} >= keep in this row
+      for (int bit = 15; bit >= 0; --bit) {
+        const uint32_t cand = T | (1u << bit);
+        int c = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c += kk[e] >= cand;
+        T = sum16(c) >= keep ? cand : T;
+      }
+      int gt = 0, eq = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        gt += kk[e] > T;
+        eq += kk[e] == T;
+      }
+      const int need = keep - sum16(gt);
+      int er = scan16(eq);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool tie = kk[e] == T;
+        kept |= (kk[e] > T || (tie && er < need) ? 1u : 0u) << e;
+        er += tie;
       }
     }
-  };
-
-  uint32_t cur[NT], nxt[NT];
-  int64_t tg = t0 + (int64_t)NT * w;
-  if (tg < t1) load_group(tg, nxt);
-  for (; tg < t1; tg += NT * 4) {  // wave-uniform loop
+    int pos = scan16(__popc(kept));
+    float p = 0.f;
 #pragma unroll
-    for (int j = 0; j < NT; ++j) cur[j] = nxt[j];
-    if (tg + NT * 4 < t1) load_group(tg + NT * 4, nxt);
+    for (int e = 0; e < 8; ++e) p += ((kept >> e) & 1u) ? 0.f : ev[e];
+    p = fsum16(p);
+    // the row's kept values in channel order, assembled in LDS and written
+    // as 16-byte chunks (lane n: columns 8n..8n+7)
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int64_t t = tg + j;
-      if (t >= t1) break;
-      const uint16_t r0 = (uint16_t)cur[j], r1 = (uint16_t)(cur[j] >> 16);
-      const float e0 = TT::to_f32(r0), e1 = TT::to_f32(r1);
-      const uint32_t k0 = order_key<TT>(rnd<TT>(rnd<TT>(e0 * e0) * q0));
-      const uint32_t k1 = order_key<TT>(rnd<TT>(rnd<TT>(e1 * e1) * q1));
-      bool kept0, kept1;
-      if (keep >= kD) {
-        kept0 = kept1 = true;
-      } else if (keep <= 0) {
-        kept0 = kept1 = false;
-      } else {
-        uint32_t T = 0u;  // largest T with #{key >= T} >= keep
-        for (int bit = 15; bit >= 0; --bit) {
-          const uint32_t cand = T | (1u << bit);
-          const int cnt = __popcll(__ballot(k0 >= cand)) + __popcll(__ballot(k1 >= cand));
-          if (cnt >= keep) T = cand;
-        }
-        const int need = keep - (__popcll(__ballot(k0 > T)) + __popcll(__ballot(k1 > T)));
-        const bool eq0 = k0 == T, eq1 = k1 == T;
-        const uint64_t q0m = __ballot(eq0), q1m = __ballot(eq1);
-        const int er0 = __popcll(q0m & below) + __popcll(q1m & below), er1 = er0 + (int)eq0;
-        kept0 = k0 > T || (eq0 && er0 < need);
-        kept1 = k1 > T || (eq1 && er1 < need);
+    for (int e = 0; e < 8; ++e) {
+      if ((kept >> e) & 1u) {
+        s_row[w][g][pos] = (uint16_t)(word(cur, e >> 1) >> ((e & 1) * 16));
+        ++pos;
       }
-      const uint64_t m0 = __ballot(kept0), m1 = __ballot(kept1);
-      const int p0 = __popcll(m0 & below) + __popcll(m1 & below), p1 = p0 + (int)kept0;
-      if (kept0) cb[t * a.kc.ss + p0 * a.kc.sc] = r0;
-      if (kept1) cb[t * a.kc.ss + p1 * a.kc.sc] = r1;
-      mb[t * a.mask.ss + c0 * a.mask.sc] = (uint8_t)kept0;
-      mb[t * a.mask.ss + c1 * a.mask.sc] = (uint8_t)kept1;
-      float p = (kept0 ? 0.f : e0) + (kept1 ? 0.f : e1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (t < t1 && 8 * n < keep) {
+      const uint16_t* src = &s_row[w][g][8 * n];
+      if constexpr (CVEC) {
+        *(uint4*)(cb + t * a.kc.ss + 8 * n) = *(const uint4*)src;
+      } else {
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) p += shfl_xor(p, off);
-      if (lane == 0) pb[t * a.pm.ss] = TT::from_f32(pin(p * a.f_pruned));
+        for (int e = 0; e < 8; ++e)
+          if (8 * n + e < keep) cb[t * a.kc.ss + (8 * n + e) * a.kc.sc] = src[e];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (t < t1) {
+      if constexpr (MVEC) {
+        uint64_t m = 0ull;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) m |= (uint64_t)((kept >> e) & 1u) << (8 * e);
+        *(uint64_t*)(mb + t * a.mask.ss + 8 * n) = m;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mb[t * a.mask.ss + (8 * n + e) * a.mask.sc] = (uint8_t)((kept >> e) & 1u);
+      }
+      if (n == 0) pb[t * a.pm.ss] = TT::from_f32(pin(p * a.f_pruned));
     }
   }
 }
@@ -695,7 +758,8 @@ struct SparkPlan {
 SparkPlan spark_plan(int64_t bh, int64_t S, int cus) {
   SparkPlan p;
   p.splits = token_splits(bh, S, cus, 8, 64);
-  p.chunk = cdiv(S > 0 ? S : 1, p.splits);
+  p.chunk = cdiv(cdiv(S > 0 ? S : 1, p.splits), 16) * 16;
+  p.splits = (int)cdiv(S > 0 ? S : 1, p.chunk);
   p.total = align256((size_t)bh * kD * sizeof(float));
   return p;
 }
@@ -721,7 +785,8 @@ int spark_check(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_
 }
 
 template <class TT>
-hipError_t launch_spark(const View& kv, bool kvec, const View& qv, int G, int keep, const SparkPlan& p, int64_t B,
+hipError_t launch_spark(const View& kv, bool kvec, bool mvec, const View& qv, int G, int keep, const SparkPlan& p,
+                        int64_t B,
                         float f_grp, float f_pruned, const MaskView& mv, const rk_tensor* kc_out,
                         const rk_tensor* pm_out, void* ws, hipStream_t s) {
   const int64_t bh = B * kv.H;
@@ -738,10 +803,13 @@ hipError_t launch_spark(const View& kv, bool kvec, const View& qv, int G, int ke
   a.mask = mv;
   a.pm = out_of(pm_out);
   const dim3 grid((unsigned)p.splits, (unsigned)bh);
-  if (kvec)
-    hipLaunchKernelGGL((spark_kernel<TT, true>), grid, dim3(kThreads), 0, s, a);
+  const bool cvec = keep % 8 == 0 && rows16(kc_out);
+  if (kvec && mvec && cvec)
+    hipLaunchKernelGGL((spark_kernel<TT, true, true, true>), grid, dim3(kThreads), 0, s, a);
+  else if (kvec && mvec)
+    hipLaunchKernelGGL((spark_kernel<TT, true, true, false>), grid, dim3(kThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((spark_kernel<TT, false>), grid, dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((spark_kernel<TT, false, false, false>), grid, dim3(kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -907,13 +975,16 @@ extern "C" int rk_spark_prune(const rk_tensor* keys_vision, const rk_tensor* que
   const int64_t W = qv.S;
   const float f_grp = mean_factor(B * H * W * 128, B * H * num_kv_groups * W * 128);
   const float f_pruned = mean_factor(B * H * kv.S, B * H * kv.S * prune_count);
-  const bool kvec = pairs4(keys_vision);
+  const bool kvec = rows16(keys_vision);
+  const bool mvec = keep_mask_out->stride[3] == 1 && keep_mask_out->stride[0] % 8 == 0 &&
+                    keep_mask_out->stride[1] % 8 == 0 && keep_mask_out->stride[2] % 8 == 0 &&
+                    (((uintptr_t)keep_mask_out->data) & 7) == 0;
   hipStream_t s = (hipStream_t)stream;
   const hipError_t e =
       keys_vision->dtype == RK_F16
-          ? launch_spark<rk::F16>(kv, kvec, qv, (int)num_kv_groups, (int)keep, p, B, f_grp, f_pruned, mv,
+          ? launch_spark<rk::F16>(kv, kvec, mvec, qv, (int)num_kv_groups, (int)keep, p, B, f_grp, f_pruned, mv,
                                   k_compact_out, pruned_mean_out, workspace, s)
-          : launch_spark<rk::BF16>(kv, kvec, qv, (int)num_kv_groups, (int)keep, p, B, f_grp, f_pruned, mv,
+          : launch_spark<rk::BF16>(kv, kvec, mvec, qv, (int)num_kv_groups, (int)keep, p, B, f_grp, f_pruned, mv,
                                    k_compact_out, pruned_mean_out, workspace, s);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
