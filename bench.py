@@ -226,7 +226,7 @@ def pmc_summary(fetch_csv, write_csv, calib_bytes, calib_copies, cfg_name):
 
 def run_flow(args):
     """Config 4: per (visual length, keep) point, prefill a 28-layer stack
-    (HIP covariance -> eigh -> head-wise channel top-k -> truncated Key
+    (HIP covariance -> device eigh -> head-wise channel top-k -> truncated Key
     write into the span cache), then time ``--steps`` decode steps, each one
     replay of a HIP graph that appends a token and runs the RotateK decode
     for every layer."""
@@ -315,8 +315,9 @@ def run_prefill(args):
     """Config 4 prefill, one layer per visual length, each stage timed on
     the device (HIP events over ``--steps`` repetitions, replayed from a HIP
     graph where the stage is device-only): key covariance
-    (mean pass + MFMA covariance pass + finalize), query weighting (torch),
-    eigh (torch, on the host as the reference), the HIP subspace iteration
+    (mean pass + MFMA covariance pass + finalize), query weighting (HIP),
+    eigh (torch, on the host as the reference and on the device, the
+    default here), the HIP subspace iteration
     (the reference's default solver), channel scores, top-k, R_partial /
     delta_mu gather and the truncated Key write."""
     import torch
@@ -339,7 +340,8 @@ def run_prefill(args):
         kv = st["K"][:, :, c.prompt:c.prompt + S_v]
         (mean, cov), t_cov, _ = timed(lambda: prefill.key_covariance(kv))
         covw, t_qw, _ = timed(lambda: prefill.query_weight(cov, st["Q"], c.G))
-        R_full, _, w_eigh = timed(lambda: prefill.eigen_rotation(covw), graph=False)
+        _, _, w_eigh = timed(lambda: prefill.eigen_rotation(covw, on_host=True), graph=False)
+        R_full, _, w_eigh_dev = timed(lambda: prefill.eigen_rotation(covw, on_host=False), graph=False)
         _, t_pi, _ = timed(lambda: power_iteration_gpu(covw, keep, num_iters=5, seed=0), graph=False)
         scores, t_sc, _ = timed(lambda: prefill.channel_scores(kv, R_full))
         (idx, mask), t_tk, _ = timed(lambda: prefill.topk_channels(scores, keep))
@@ -353,6 +355,7 @@ def run_prefill(args):
                "covariance_gbps_two_passes": round(2 * kbytes / t_cov / 1e3, 1),
                "covariance_mfma_tflops": round(cov_flops / t_cov / 1e6, 2),
                "query_weight_us": round(t_qw, 2), "eigh_host_us": round(w_eigh, 1),
+               "eigh_device_us": round(w_eigh_dev, 1),
                "power_iteration_us": round(t_pi, 2),
                "channel_scores_us": round(t_sc, 2), "topk_us": round(t_tk, 2),
                "gather_us": round(t_ga, 2), "rotate_write_us": round(t_rot, 2),
