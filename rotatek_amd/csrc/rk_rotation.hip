@@ -11,7 +11,7 @@
 //   G = W^T W     thread tile (KP/16) x (KP/16)
 //   Cholesky      wave 0, lane i holds row i of G in registers; the pivot
 //                 and column entries are read across lanes (readlane)
-//   V = W L^-T    forward substitution per row (threads 0..127)
+//   V = W L^-T    right-looking forward substitution per row (threads 0..127)
 // The start block V0 comes from the caller (the reference draws it with
 // torch.randn from a seeded device generator, rotation.py:88-90).  Columns
 // k..KP-1 are zero padding; their G block is set to the identity so they
@@ -47,13 +47,37 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
   const float* C = cov + b * c_sb + (int64_t)h * c_sh;
   const float* V0 = v0 + b * v_sb + (int64_t)h * v_sh;
 
-  for (int e = tid; e < kD * kD; e += kThreads) {
-    const int r = e >> 7, c = e & 127;
-    sC[r * kCPad + c] = C[r * c_sr + c * c_sc];
+  // Stage C and V0 in LDS.  The loads of a batch are all issued before any
+  // of them is stored, so the copy costs a few memory round trips rather
+  // than one per element.
+  constexpr int kCB = 16;  // elements per thread per batch
+  for (int e0 = 0; e0 < kD * kD; e0 += kThreads * kCB) {
+    float v[kCB];
+#pragma unroll
+    for (int i = 0; i < kCB; ++i) {
+      const int e = e0 + i * kThreads + tid, r = e >> 7, c = e & 127;
+      v[i] = C[r * c_sr + c * c_sc];
+    }
+#pragma unroll
+    for (int i = 0; i < kCB; ++i) {
+      const int e = e0 + i * kThreads + tid;
+      sC[(e >> 7) * kCPad + (e & 127)] = v[i];
+    }
   }
-  for (int e = tid; e < kD * KP; e += kThreads) {
-    const int r = e / KP, c = e - (e / KP) * KP;
-    sV[r * SP + c] = c < k ? V0[r * v_sr + c * v_sc] : 0.f;
+  constexpr int kVB = kD * KP / kThreads < kCB ? kD * KP / kThreads : kCB;  // divides kD * KP / kThreads
+  static_assert((kD * kD) % (kThreads * kCB) == 0 && (kD * KP) % (kThreads * kVB) == 0, "whole batches");
+  for (int e0 = 0; e0 < kD * KP; e0 += kThreads * kVB) {
+    float v[kVB];
+#pragma unroll
+    for (int i = 0; i < kVB; ++i) {
+      const int e = e0 + i * kThreads + tid, r = e / KP, c = e - r * KP;
+      v[i] = c < k ? V0[r * v_sr + c * v_sc] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kVB; ++i) {
+      const int e = e0 + i * kThreads + tid, r = e / KP;
+      sV[r * SP + (e - r * KP)] = v[i];
+    }
   }
   __syncthreads();
 
@@ -66,6 +90,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int c = 0; c < TC; ++c) w[i][c] = 0.f;
+#pragma unroll 8
     for (int d = 0; d < kD; ++d) {
       float cv[4], vv[TC];
 #pragma unroll
@@ -91,6 +116,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
       for (int i = 0; i < GT; ++i)
 #pragma unroll
         for (int j = 0; j < GT; ++j) g[i][j] = 0.f;
+#pragma unroll 8
       for (int r = 0; r < kD; ++r) {
         float a[GT], bb[GT];
 #pragma unroll
@@ -142,17 +168,18 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     }
     __syncthreads();
 
-    // ---- V = W L^-T: row r solves L x^T = w^T by forward substitution
+    // ---- V = W L^-T: row r solves L x^T = w^T by forward substitution,
+    // right-looking (x_j final, then subtracted from every later unknown), so
+    // the dependency chain is two operations per column rather than j
     if (tid < kD) {
       float x[KP];
 #pragma unroll
       for (int j = 0; j < KP; ++j) x[j] = sV[tid * SP + j];
 #pragma unroll
       for (int j = 0; j < KP; ++j) {
-        float acc = x[j];
+        x[j] = x[j] / sG[j * GP + j];
 #pragma unroll
-        for (int p = 0; p < j; ++p) acc = fmaf(-sG[j * GP + p], x[p], acc);
-        x[j] = acc / sG[j * GP + j];
+        for (int i = j + 1; i < KP; ++i) x[i] = fmaf(-sG[i * GP + j], x[j], x[i]);
       }
 #pragma unroll
       for (int j = 0; j < KP; ++j) sV[tid * SP + j] = x[j];
