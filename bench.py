@@ -387,8 +387,13 @@ def run_baselines(args):
                                        think_score_and_compact)
     from rotatek_amd.kernels.full_channel_flash_decoding import full_channel_decode
     from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    from rotatek_amd.kernels.gqa_decode import full_channel_decode_gqa, rotatek_decode_gqa
 
     cfg = synth.CONFIGS[args.config]
+    # GQA shapes default to the gqa family (each K/V tile shared by the group)
+    family = args.family if args.family_given else ("gqa" if cfg.G > 1 else "paper")
+    rot = rotatek_decode_gqa if family == "gqa" else rotatek_decode_fused
+    dense = full_channel_decode_gqa if family == "gqa" else full_channel_decode
     torch.cuda.set_device(0)
     reps = args.steps if args.steps_given else 20
     inp = synth.make_decode_inputs(cfg, "cuda", seed=0, with_raw=True)
@@ -421,18 +426,18 @@ def run_baselines(args):
 
     def think_step():
         recover_think(Kc_t, tm, out=stage, k_text=kf)
-        return full_channel_decode(q, stage, V, G)
+        return dense(q, stage, V, G)
 
     def spark_step():
         recover_spark(Kc_s, sm, pm, out=stage, k_text=kf)
-        return full_channel_decode(q, stage, V, G)
+        return dense(q, stage, V, G)
 
     da = synth.decode_args(inp)
     R_sel = selection_rotation(tm, keep, cfg.dtype)
     think_fused_args = dict(da, R_partial=R_sel, delta_mu=None, k_sparse=Kc_t)
     for name, fn in (("think_decode_step", think_step), ("spark_decode_step", spark_step),
-                     ("think_fused_decode", lambda: rotatek_decode_fused(**think_fused_args)),
-                     ("rotatek_decode", lambda: rotatek_decode_fused(**da))):
+                     ("think_fused_decode", lambda: rot(**think_fused_args)),
+                     ("rotatek_decode", lambda: rot(**da))):
         _, t, _ = timed(fn)
         r[name + "_us"] = t
     r = {k: round(v, 2) for k, v in r.items()}
@@ -443,7 +448,8 @@ def run_baselines(args):
             "data": "synthetic: the decode inputs of the configuration, full-width visual Keys, N(0,1) "
                     "query window of 32",
             "config": {"workload": f"{cfg.name} baselines: B={B}, H_q={Hq}, H_kv={H}, S_v={S_v}, S_f={S_f}, "
-                                   f"keep {keep}; value = ThinK decode step (recover + dense decode)",
+                                   f"keep {keep}, family={family}; value = ThinK decode step (recover + dense "
+                                   f"decode)",
                        "stages": r}}
     print(json.dumps(line), flush=True)
 
