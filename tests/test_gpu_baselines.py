@@ -333,7 +333,8 @@ def test_cache_decode_over_recovered_keys(dtype, method):
         err = np.abs(_np(got) - want).max()
         assert err <= TOL[dtype], (step, err)
         if method == "think":
-            fused, _, _ = cache.decode_think_fused(qd, 0, G)
-            torch.cuda.synchronize()
-            err = np.abs(_np(fused) - want).max()
-            assert err <= TOL[dtype], ("fused", step, err)
+            for policy in (0, 1):  # paper, gqa
+                fused, _, _ = cache.decode_think_fused(qd, 0, G, policy=policy)
+                torch.cuda.synchronize()
+                err = np.abs(_np(fused) - want).max()
+                assert err <= TOL[dtype], ("fused", policy, step, err)
