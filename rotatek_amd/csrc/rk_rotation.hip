@@ -5,13 +5,15 @@
 // Per iteration, as the reference:
 //   W = C V;  G = W^T W;  G += eps * mean(diag G) * I;  G = L L^T;  V = W L^-T
 // One 256-thread workgroup owns one matrix and keeps everything in LDS
-// (C 128 x 129, V/W 128 x (KP+1), G/L KP x (KP+1), padded rows: ~116 KB at
-// KP = 64):
-//   W = C V       thread tile 4 rows x KP/8 columns, fp32 FMA
-//   G = W^T W     thread tile (KP/16) x (KP/16)
-//   Cholesky      wave 0, lane i holds row i of G in registers; the pivot
-//                 and column entries are read across lanes (readlane)
-//   V = W L^-T    right-looking forward substitution per row (threads 0..127)
+// (C 128 x 132, V/W 128 x (KP+16), G/L KP x (KP+1), (L^-1)^T KP x (KP+16):
+// ~146 KB at KP = 64).  The three products run on v_mfma_f32_16x16x4_f32:
+//   W = C V            8 x KP/16 tiles of 16 x 16 over the four waves
+//   G = W^T W          (KP/16)^2 tiles
+//   Cholesky + L^-1    wave 0 in one pass: lane i holds row i of G, column
+//                      j of L goes through LDS and serves both the row
+//                      updates and step j of the substitution L x = e_c
+//                      that lane c runs for column c of L^-1
+//   V = W (L^-1)^T     8 x KP/16 tiles
 // The start block V0 comes from the caller (the reference draws it with
 // torch.randn from a seeded device generator, rotation.py:88-90).  Columns
 // k..KP-1 are zero padding; their G block is set to the identity so they
@@ -25,24 +27,45 @@
 namespace rk {
 namespace rot {
 
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+
 constexpr int kD = 128;
 constexpr int kThreads = 256;
-constexpr int kCPad = kD + 1;
+constexpr int kCPad = kD + 4;  // C row stride: MFMA A reads (row n, column g) hit banks 4n + g
+
+// D = A B + D on v_mfma_f32_16x16x4_f32 (A 16x4, B 4x16): lane (g, n) supplies
+// A[n][g] and B[g][n] and holds D[4g + i][n], i = 0..3.
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 d) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, d, 0, 0, 0);
+}
+
+// The LDS address of p, through an empty asm the compiler cannot see into.
+__device__ __forceinline__ lds_f32* opaque_lds(float* p) {
+  unsigned a = (unsigned)(uintptr_t)(lds_f32*)p;
+  asm volatile("" : "+v"(a));
+  return (lds_f32*)(uintptr_t)a;
+}
 
 template <int KP>
 __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     const float* cov, int64_t c_sb, int64_t c_sh, int64_t c_sr, int64_t c_sc, const float* v0, int64_t v_sb,
     int64_t v_sh, int64_t v_sr, int64_t v_sc, float* out, int64_t o_sb, int64_t o_sh, int64_t o_sr,
     int64_t o_sc, int H, int k, int iters, float eps) {
-  constexpr int TC = KP / 8;    // W tile columns per thread
-  constexpr int GT = KP / 16;   // G tile edge per thread
-  constexpr int GP = KP + 1;    // padded G row
-  constexpr int SP = KP + 1;    // padded V row (row-per-thread access in the solve)
+  constexpr int SP = KP + 16;       // V / W row stride: MFMA reads (row g, column n) hit banks 16g + n
+  constexpr int GP = KP + 1;        // G / L row (row per lane in the Cholesky)
+  constexpr int LP = KP + 16;       // (L^-1)^T row stride
+  constexpr int NTJ = KP / 16;      // 16-column tiles of W / V
+  constexpr int TPW = 8 * NTJ / 4;  // 16 x 16 tiles of W per wave
+  constexpr int NG = NTJ * NTJ;     // 16 x 16 tiles of G
+  constexpr int TPG = NG >= 4 ? NG / 4 : 1;
   __shared__ float sC[kD * kCPad];
   __shared__ float sV[kD * SP];
-  __shared__ float sG[KP * GP];
+  // G, then L by columns; the tail takes the idle lanes' last column writes
+  __shared__ __align__(16) float sG[KP * GP > KP * KP + 64 ? KP * GP : KP * KP + 64];
+  __shared__ float sLt[64 * LP];  // rows >= KP: scratch for the idle lanes of wave 0
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
   const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
   const float* C = cov + b * c_sb + (int64_t)h * c_sh;
   const float* V0 = v0 + b * v_sb + (int64_t)h * v_sh;
@@ -81,108 +104,167 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
   }
   __syncthreads();
 
-  const int rg = tid >> 3, cg = tid & 7;           // W tile: rows 4 rg.., columns TC cg..
-  const int gi = tid >> 4, gj = tid & 15;          // G tile: rows GT gi.., columns GT gj..
+  // Wave w owns the 16 x 16 output tiles w, w + 4, w + 8, ... of each
+  // product.  With NTJ column tiles (NTJ divides 4) tile w + 4t sits at row
+  // tile ti0 + t * RS and column tile tj0.
+  constexpr int RS = 4 / NTJ;
+  const int ti0 = wave / NTJ, tj0 = wave - (wave / NTJ) * NTJ;
+
   for (int it = 0; it < iters; ++it) {
-    // ---- W = C V (registers), then back into sV
-    float w[4][TC];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int c = 0; c < TC; ++c) w[i][c] = 0.f;
-#pragma unroll 8
-    for (int d = 0; d < kD; ++d) {
-      float cv[4], vv[TC];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cv[i] = sC[(4 * rg + i) * kCPad + d];
-#pragma unroll
-      for (int c = 0; c < TC; ++c) vv[c] = sV[d * SP + TC * cg + c];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int c = 0; c < TC; ++c) w[i][c] = fmaf(cv[i], vv[c], w[i][c]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int c = 0; c < TC; ++c) sV[(4 * rg + i) * SP + TC * cg + c] = w[i][c];
-    __syncthreads();
+    // LDS bases, opaque to the compiler once per iteration: every access
+    // below is one of these plus a lane part plus an immediate offset
+    // (< 64 KB), so no per-access address is kept in a register across
+    // iterations
+    lds_f32* const lC = opaque_lds(sC);
+    lds_f32* const lV = opaque_lds(sV);
+    lds_f32* const lG = opaque_lds(sG);
+    lds_f32* const lLt = opaque_lds(sLt);
 
-    // ---- G = W^T W
+    // ---- W = C V on the MFMA, k = 128 in steps of 4
     {
-      float g[GT][GT];
+      const lds_f32* pa = lC + (16 * ti0 + n) * kCPad + g;  // C[16 ti + n][4 ks + g]
+      const lds_f32* pb = lV + g * SP + 16 * tj0 + n;       // V[4 ks + g][16 tj + n]
+      f32x4 acc[TPW];
 #pragma unroll
-      for (int i = 0; i < GT; ++i)
+      for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int ks = 0; ks < kD / 4; ++ks) {
+        const float bv = pb[4 * ks * SP];
 #pragma unroll
-        for (int j = 0; j < GT; ++j) g[i][j] = 0.f;
-#pragma unroll 8
-      for (int r = 0; r < kD; ++r) {
-        float a[GT], bb[GT];
-#pragma unroll
-        for (int i = 0; i < GT; ++i) a[i] = sV[r * SP + GT * gi + i];
-#pragma unroll
-        for (int j = 0; j < GT; ++j) bb[j] = sV[r * SP + GT * gj + j];
-#pragma unroll
-        for (int i = 0; i < GT; ++i)
-#pragma unroll
-          for (int j = 0; j < GT; ++j) g[i][j] = fmaf(a[i], bb[j], g[i][j]);
+        for (int t = 0; t < TPW; ++t) acc[t] = mfma4(pa[16 * RS * t * kCPad + 4 * ks], bv, acc[t]);
       }
+      __syncthreads();
+      lds_f32* pw = lV + (16 * ti0 + 4 * g) * SP + 16 * tj0 + n;
 #pragma unroll
-      for (int i = 0; i < GT; ++i)
+      for (int t = 0; t < TPW; ++t)
 #pragma unroll
-        for (int j = 0; j < GT; ++j) sG[(GT * gi + i) * GP + GT * gj + j] = g[i][j];
+        for (int i = 0; i < 4; ++i) pw[(16 * RS * t + i) * SP] = acc[t][i];
     }
     __syncthreads();
 
-    // ---- ridge and Cholesky (wave 0; lane i owns row i)
+    // ---- G = W^T W on the MFMA (NTJ x NTJ tiles; at NTJ = 1 wave 0 alone);
+    // two accumulators per tile (even / odd k steps) so consecutive MFMAs
+    // do not wait on each other
+    if (wave < NG) {  // wave-uniform
+      const lds_f32* pa = lV + g * SP + 16 * ti0 + n;  // W[4 ks + g][16 ti + n]
+      const lds_f32* pb = lV + g * SP + 16 * tj0 + n;  // W[4 ks + g][16 tj + n]
+      f32x4 acc[TPG][2];
+#pragma unroll
+      for (int t = 0; t < TPG; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+      for (int ks = 0; ks < kD / 4; ks += 2) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const float bv = pb[4 * (ks + h2) * SP];
+#pragma unroll
+          for (int t = 0; t < TPG; ++t) acc[t][h2] = mfma4(pa[4 * (ks + h2) * SP + 16 * RS * t], bv, acc[t][h2]);
+        }
+      }
+      lds_f32* pg = lG + (16 * ti0 + 4 * g) * GP + 16 * tj0 + n;
+#pragma unroll
+      for (int t = 0; t < TPG; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pg[(16 * RS * t + i) * GP] = acc[t][0][i] + acc[t][1][i];
+    }
+    __syncthreads();
+
+    // ---- ridge, Cholesky G = L L^T and L^-1, one pass in wave 0.
+    // Lane i holds row i of G.  Step j takes the pivot from lane j, scales
+    // column j by r_j = 1/sqrt(pivot) and publishes it to LDS (column j of
+    // L, with r_j in place of L_jj); every lane reads the column back as
+    // 16-byte broadcasts and uses it twice: the right-looking update of its
+    // row of G, and step j of the forward substitution L x = e_c that lane
+    // c runs for column c of L^-1.  Rows of finished lanes (lane <= j) keep
+    // being updated in their upper triangle, which is never read.
     if (wave == 0) {
-      float dg = lane < k ? sG[lane * GP + lane] : 0.f;
+      // the lane index, opaque to the compiler, so that the per-column lane
+      // masks below are formed where they are used instead of being hoisted
+      // out of the iteration loop (where they would not fit in registers)
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int lr = min(ln, KP - 1);  // lanes >= KP compute on a copy of row KP-1 and store nothing
+      const lds_f32* prow = lG + lr * GP;
+      const float dii = prow[lr];
+      float dg = ln < k ? dii : 0.f;
 #pragma unroll
       for (int off = 32; off > 0; off >>= 1) dg += shfl_xor(dg, off);
       const float ridge = eps * (dg / (float)k);
-      float row[KP];
+      // the padding rows and columns of G are zero (V's padding columns
+      // are): a unit diagonal there makes them the identity
+      if (ln < KP) lG[ln * GP + ln] = ln < k ? dii + ridge : 1.f;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      float row[KP], x[KP];
 #pragma unroll
       for (int m = 0; m < KP; ++m) {
-        float x = lane < KP ? sG[min(lane, KP - 1) * GP + m] : 0.f;
-        if (lane >= k || m >= k) x = (lane == m) ? 1.f : 0.f;  // identity on the padding
-        else if (lane == m) x += ridge;
-        row[m] = x;
+        row[m] = prow[m];
+        x[m] = ln == m ? 1.f : 0.f;
       }
+      // G's storage is rewritten below as L by columns (sL[j * KP + m] =
+      // L_mj), after every lane's loads above
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      lds_f32* const sL = lG;
+      // column j is written unconditionally (a guarded store per step would
+      // split the pass into blocks and let the compiler sink the
+      // substitution to the end): lanes >= KP write past column j, into
+      // columns that are rewritten before they are read, or into the tail
+      // of the array
+      lds_f32* const pl = lG + ln;
 #pragma unroll
       for (int j = 0; j < KP; ++j) {
-        const float ljj =
-            sqrtf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, row[j]), j)));
-        const float lij = lane > j ? row[j] / ljj : (lane == j ? ljj : row[j]);
-        row[j] = lij;
+        const float piv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, row[j]), j));
+        const float rj = __builtin_amdgcn_rsqf(piv);
+        const float lij = ln > j ? row[j] * rj : (ln == j ? rj : 0.f);
+        pl[j * KP] = lij;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        x[j] *= rj;
 #pragma unroll
-        for (int m = j + 1; m < KP; ++m) {
-          const float lmj = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lij), m));
-          if (lane >= m) row[m] = fmaf(-lij, lmj, row[m]);
+        for (int m4 = (j + 1) & ~3; m4 < KP; m4 += 4) {
+          const f32x4 col = *(const lds_f32x4*)&sL[j * KP + m4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int m = m4 + q;
+            if (m > j) {  // compile-time
+              row[m] = fmaf(-lij, col[q], row[m]);
+              x[m] = fmaf(-col[q], x[j], x[m]);
+            }
+          }
         }
       }
-      if (lane < KP) {
+      // unconditional (rows KP..63 of the array take the idle lanes'
+      // values and are never read): a guarded store would let the compiler
+      // sink the whole substitution into it, holding every column read
+      // above in registers until the end
+      lds_f32* px = lLt + ln * LP;
 #pragma unroll
-        for (int m = 0; m < KP; ++m) sG[lane * GP + m] = m <= lane ? row[m] : 0.f;
-      }
+      for (int i = 0; i < KP; ++i) px[i] = x[i];
     }
     __syncthreads();
 
-    // ---- V = W L^-T: row r solves L x^T = w^T by forward substitution,
-    // right-looking (x_j final, then subtracted from every later unknown), so
-    // the dependency chain is two operations per column rather than j
-    if (tid < kD) {
-      float x[KP];
+    // ---- V = W (L^-1)^T on the MFMA: V[r][j] = sum_m W[r][m] (L^-1)^T[m][j]
+    {
+      const lds_f32* pa = lV + (16 * ti0 + n) * SP + g;  // W[16 ti + n][4 ks + g]
+      const lds_f32* pb = lLt + g * LP + 16 * tj0 + n;   // (L^-1)^T[4 ks + g][16 tj + n]
+      f32x4 acc[TPW];
 #pragma unroll
-      for (int j = 0; j < KP; ++j) x[j] = sV[tid * SP + j];
+      for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < KP; ++j) {
-        x[j] = x[j] / sG[j * GP + j];
+      for (int ks = 0; ks < KP / 4; ++ks) {
+        const float bv = pb[4 * ks * LP];
 #pragma unroll
-        for (int i = j + 1; i < KP; ++i) x[i] = fmaf(-sG[i * GP + j], x[j], x[i]);
+        for (int t = 0; t < TPW; ++t) acc[t] = mfma4(pa[16 * RS * t * SP + 4 * ks], bv, acc[t]);
       }
+      __syncthreads();
+      lds_f32* pw = lV + (16 * ti0 + 4 * g) * SP + 16 * tj0 + n;
 #pragma unroll
-      for (int j = 0; j < KP; ++j) sV[tid * SP + j] = x[j];
+      for (int t = 0; t < TPW; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pw[(16 * RS * t + i) * SP] = acc[t][i];
     }
     __syncthreads();
   }
