@@ -32,7 +32,8 @@ typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 
 constexpr int kD = 128;
 constexpr int kThreads = 256;
-constexpr int kCPad = kD + 4;  // C row stride: MFMA A reads (row n, column g) hit banks 4n + g
+constexpr int kCPad = kD + 4;  // C row stride: 16-byte reads of rows n = 0..15 cover all 64 banks
+constexpr int kLook = 3;       // Cholesky: column entries passed by readlane ahead of the LDS broadcast
 
 // D = A B + D on v_mfma_f32_16x16x4_f32 (A 16x4, B 4x16): lane (g, n) supplies
 // A[n][g] and B[g][n] and holds D[4g + i][n], i = 0..3.
@@ -52,15 +53,18 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     const float* cov, int64_t c_sb, int64_t c_sh, int64_t c_sr, int64_t c_sc, const float* v0, int64_t v_sb,
     int64_t v_sh, int64_t v_sr, int64_t v_sc, float* out, int64_t o_sb, int64_t o_sh, int64_t o_sr,
     int64_t o_sc, int H, int k, int iters, float eps) {
-  constexpr int SP = KP + 16;       // V / W row stride: MFMA reads (row g, column n) hit banks 16g + n
-  constexpr int GP = KP + 1;        // G / L row (row per lane in the Cholesky)
-  constexpr int LP = KP + 16;       // (L^-1)^T row stride
+  // V / W and (L^-1)^T row stride, 4 mod 16: reads of rows 4g + r (r fixed)
+  // at columns n = 0..15 hit banks 16g + n, and 16-byte reads of rows n at
+  // column 4g cover all 64 banks
+  constexpr int SP = KP + 4;
+  constexpr int LP = KP + 4;
+  constexpr int GP = KP + 1;        // G row (row per lane in the Cholesky)
   constexpr int NTJ = KP / 16;      // 16-column tiles of W / V
   constexpr int TPW = 8 * NTJ / 4;  // 16 x 16 tiles of W per wave
   constexpr int NG = NTJ * NTJ;     // 16 x 16 tiles of G
   constexpr int TPG = NG >= 4 ? NG / 4 : 1;
-  __shared__ float sC[kD * kCPad];
-  __shared__ float sV[kD * SP];
+  __shared__ __align__(16) float sC[kD * kCPad];
+  __shared__ __align__(16) float sV[kD * SP];
   // G, then L by columns; the tail takes the idle lanes' last column writes
   __shared__ __align__(16) float sG[KP * GP > KP * KP + 64 ? KP * GP : KP * KP + 64];
   __shared__ float sLt[64 * LP];  // rows >= KP: scratch for the idle lanes of wave 0
@@ -120,18 +124,34 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     lds_f32* const lG = opaque_lds(sG);
     lds_f32* const lLt = opaque_lds(sLt);
 
-    // ---- W = C V on the MFMA, k = 128 in steps of 4
+    // ---- W = C V on the MFMA.  In the four MFMA steps of k-group q, lane
+    // (g, n) supplies k = 16q + 4g + r, r = 0..3 (any assignment of k to
+    // (step, g) sums the same products), so one 16-byte read of C's row
+    // feeds all four; group q + 1 is read while group q computes
     {
-      const lds_f32* pa = lC + (16 * ti0 + n) * kCPad + g;  // C[16 ti + n][4 ks + g]
-      const lds_f32* pb = lV + g * SP + 16 * tj0 + n;       // V[4 ks + g][16 tj + n]
-      f32x4 acc[TPW];
+      const lds_f32* pa = lC + (16 * ti0 + n) * kCPad + 4 * g;  // C[16 ti + n][16 q + 4 g + r]
+      const lds_f32* pb = lV + 4 * g * SP + 16 * tj0 + n;       // V[16 q + 4 g + r][16 tj + n]
+      f32x4 acc[TPW], a[2][TPW];
+      float bv[2][4];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int ks = 0; ks < kD / 4; ++ks) {
-        const float bv = pb[4 * ks * SP];
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) acc[t] = mfma4(pa[16 * RS * t * kCPad + 4 * ks], bv, acc[t]);
+      for (int t = 0; t < TPW; ++t) a[0][t] = *(const lds_f32x4*)&pa[16 * RS * t * kCPad];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bv[0][r] = pb[r * SP];
+#pragma unroll
+      for (int q = 0; q < kD / 16; ++q) {
+        const int cur = q & 1, nxt = cur ^ 1;
+        if (q + 1 < kD / 16) {
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) a[nxt][t] = *(const lds_f32x4*)&pa[16 * RS * t * kCPad + 16 * (q + 1)];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bv[nxt][r] = pb[(16 * (q + 1) + r) * SP];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) acc[t] = mfma4(a[cur][t][r], bv[cur][r], acc[t]);
       }
       __syncthreads();
       lds_f32* pw = lV + (16 * ti0 + 4 * g) * SP + 16 * tj0 + n;
@@ -142,22 +162,24 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     }
     __syncthreads();
 
-    // ---- G = W^T W on the MFMA (NTJ x NTJ tiles; at NTJ = 1 wave 0 alone);
-    // two accumulators per tile (even / odd k steps) so consecutive MFMAs
-    // do not wait on each other
+    // ---- G = W^T W on the MFMA (NTJ x NTJ tiles; at NTJ = 1 wave 0 alone),
+    // k assigned as in C V (lane (g, n) takes rows 16q + 4g + r); two
+    // accumulators per tile (even / odd r) so consecutive MFMAs do not wait
+    // on each other
     if (wave < NG) {  // wave-uniform
-      const lds_f32* pa = lV + g * SP + 16 * ti0 + n;  // W[4 ks + g][16 ti + n]
-      const lds_f32* pb = lV + g * SP + 16 * tj0 + n;  // W[4 ks + g][16 tj + n]
+      const lds_f32* pa = lV + 4 * g * SP + 16 * ti0 + n;  // W[16 q + 4 g + r][16 ti + n]
+      const lds_f32* pb = lV + 4 * g * SP + 16 * tj0 + n;  // W[16 q + 4 g + r][16 tj + n]
       f32x4 acc[TPG][2];
 #pragma unroll
       for (int t = 0; t < TPG; ++t) acc[t][0] = acc[t][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-      for (int ks = 0; ks < kD / 4; ks += 2) {
+#pragma unroll 2
+      for (int q = 0; q < kD / 16; ++q) {
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          const float bv = pb[4 * (ks + h2) * SP];
+        for (int r = 0; r < 4; ++r) {
+          const float bv = pb[(16 * q + r) * SP];
 #pragma unroll
-          for (int t = 0; t < TPG; ++t) acc[t][h2] = mfma4(pa[4 * (ks + h2) * SP + 16 * RS * t], bv, acc[t][h2]);
+          for (int t = 0; t < TPG; ++t)
+            acc[t][r & 1] = mfma4(pa[(16 * q + r) * SP + 16 * RS * t], bv, acc[t][r & 1]);
         }
       }
       lds_f32* pg = lG + (16 * ti0 + 4 * g) * GP + 16 * tj0 + n;
@@ -219,17 +241,28 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
         const float rj = __builtin_amdgcn_rsqf(piv);
         const float lij = ln > j ? row[j] * rj : (ln == j ? rj : 0.f);
         pl[j * KP] = lij;
+        x[j] *= rj;
+        // the entries the next kLook pivots depend on, L_{j+1..j+kLook, j},
+        // come straight from their lanes; the rest of the column goes
+        // through LDS, whose round trip then has kLook steps to complete
+#pragma unroll
+        for (int d = 1; d <= kLook; ++d) {
+          if (j + d < KP) {  // compile-time
+            const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lij), j + d));
+            row[j + d] = fmaf(-lij, c, row[j + d]);
+            x[j + d] = fmaf(-c, x[j], x[j + d]);
+          }
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        x[j] *= rj;
 #pragma unroll
-        for (int m4 = (j + 1) & ~3; m4 < KP; m4 += 4) {
+        for (int m4 = (j + kLook + 1) & ~3; m4 < KP; m4 += 4) {
           const f32x4 col = *(const lds_f32x4*)&sL[j * KP + m4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int m = m4 + q;
-            if (m > j) {  // compile-time
+            if (m > j + kLook) {  // compile-time
               row[m] = fmaf(-lij, col[q], row[m]);
               x[m] = fmaf(-col[q], x[j], x[m]);
             }
@@ -246,18 +279,32 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     }
     __syncthreads();
 
-    // ---- V = W (L^-1)^T on the MFMA: V[r][j] = sum_m W[r][m] (L^-1)^T[m][j]
+    // ---- V = W (L^-1)^T on the MFMA: V[r][j] = sum_m W[r][m] (L^-1)^T[m][j],
+    // k assigned as in C V, so one 16-byte read of W's row feeds four steps
     {
-      const lds_f32* pa = lV + (16 * ti0 + n) * SP + g;  // W[16 ti + n][4 ks + g]
-      const lds_f32* pb = lLt + g * LP + 16 * tj0 + n;   // (L^-1)^T[4 ks + g][16 tj + n]
-      f32x4 acc[TPW];
+      const lds_f32* pa = lV + (16 * ti0 + n) * SP + 4 * g;  // W[16 ti + n][16 q + 4 g + r]
+      const lds_f32* pb = lLt + 4 * g * LP + 16 * tj0 + n;   // (L^-1)^T[16 q + 4 g + r][16 tj + n]
+      f32x4 acc[TPW], a[2][TPW];
+      float bv[2][4];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < KP / 4; ++ks) {
-        const float bv = pb[4 * ks * LP];
+      for (int t = 0; t < TPW; ++t) a[0][t] = *(const lds_f32x4*)&pa[16 * RS * t * SP];
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) acc[t] = mfma4(pa[16 * RS * t * SP + 4 * ks], bv, acc[t]);
+      for (int r = 0; r < 4; ++r) bv[0][r] = pb[r * LP];
+#pragma unroll
+      for (int q = 0; q < KP / 16; ++q) {
+        const int cur = q & 1, nxt = cur ^ 1;
+        if (q + 1 < KP / 16) {
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) a[nxt][t] = *(const lds_f32x4*)&pa[16 * RS * t * SP + 16 * (q + 1)];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bv[nxt][r] = pb[(16 * (q + 1) + r) * LP];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int t = 0; t < TPW; ++t) acc[t] = mfma4(a[cur][t][r], bv[cur][r], acc[t]);
       }
       __syncthreads();
       lds_f32* pw = lV + (16 * ti0 + 4 * g) * SP + 16 * tj0 + n;
