@@ -5,8 +5,8 @@
 // Per iteration, as the reference:
 //   W = C V;  G = W^T W;  G += eps * mean(diag G) * I;  G = L L^T;  V = W L^-T
 // One 256-thread workgroup owns one matrix and keeps everything in LDS
-// (C 128 x 132, V/W 128 x (KP+16), G/L KP x (KP+1), (L^-1)^T KP x (KP+16):
-// ~146 KB at KP = 64).  The three products run on v_mfma_f32_16x16x4_f32:
+// (C 128 x 132, V/W 128 x (KP+4), G/L KP x (KP+1), (L^-1)^T 64 x (KP+4):
+// 136 KB at KP = 64).  The three products run on v_mfma_f32_16x16x4_f32:
 //   W = C V            8 x KP/16 tiles of 16 x 16 over the four waves
 //   G = W^T W          (KP/16)^2 tiles
 //   Cholesky + L^-1    wave 0 in one pass: lane i holds row i of G, column
@@ -14,10 +14,10 @@
 //                      updates and step j of the substitution L x = e_c
 //                      that lane c runs for column c of L^-1
 //   V = W (L^-1)^T     8 x KP/16 tiles
+// Padding columns of V are zero, so their rows and columns of G are too: a
+// unit diagonal there makes that block the identity, and V keeps them zero.
 // The start block V0 comes from the caller (the reference draws it with
-// torch.randn from a seeded device generator, rotation.py:88-90).  Columns
-// k..KP-1 are zero padding; their G block is set to the identity so they
-// stay zero.
+// torch.randn from a seeded device generator, rotation.py:88-90).
 #include <math.h>
 
 #include "rk_common.h"
