@@ -83,3 +83,49 @@ def test_power_iteration_gpu_uses_hip_and_zero_iterations():
     zero = rotation.power_iteration_hip(cov, V0, 0)
     torch.cuda.synchronize()
     assert torch.equal(zero, V0)
+
+
+def test_power_iteration_many_matrices_strided_views():
+    """300 matrices (more workgroups than CUs); covariance, start block and
+    output as permuted / transposed views, so every stride is non-trivial."""
+    from rotatek_amd.rotation import power_iteration_hip
+    _say("power iteration 6 x 50 matrices, strided views, k=24")
+    B, H, k = 6, 50, 24
+    cov = _cov(H, B, seed=5).permute(1, 0, 2, 3)                  # [B,H,128,128], batch stride < head stride
+    g = torch.Generator(device="cuda").manual_seed(1)
+    V0 = torch.randn(B, H, k, 128, generator=g, device="cuda").transpose(-1, -2)   # column stride 128
+    assert not cov.is_contiguous() and not V0.is_contiguous()
+    got = power_iteration_hip(cov, V0, 5, 1e-4)
+    torch.cuda.synchronize()
+    want = op.power_iteration(cov.double().cpu().numpy(), V0.double().cpu().numpy(), 5, 1e-4)
+    assert np.abs(got.double().cpu().numpy() - want).max() < 2e-3 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("iters", [1, 10])
+def test_power_iteration_iteration_counts(iters):
+    from rotatek_amd.rotation import power_iteration_hip
+    _say(f"power iteration iters={iters} k=48")
+    cov = _cov(2, 2, seed=iters)
+    g = torch.Generator(device="cuda").manual_seed(2)
+    V0 = torch.randn(2, 2, 128, 48, generator=g, device="cuda")
+    got = power_iteration_hip(cov, V0, iters, 1e-4)
+    torch.cuda.synchronize()
+    want = op.power_iteration(cov.double().cpu().numpy(), V0.double().cpu().numpy(), iters, 1e-4)
+    assert np.abs(got.double().cpu().numpy() - want).max() < 2e-3 * max(1.0, np.abs(want).max())
+
+
+def test_power_iteration_rank_deficient_covariance():
+    """Rank 8 covariance, k = 16: the Gram matrix is singular but for the
+    ridge, which alone keeps the Cholesky defined (rotation.py:36-50)."""
+    from rotatek_amd.rotation import power_iteration_hip
+    _say("power iteration rank-8 covariance, k=16")
+    g = torch.Generator(device="cuda").manual_seed(7)
+    X = torch.randn(2, 3, 128, 8, generator=g, device="cuda", dtype=torch.float64)
+    cov = (X @ X.transpose(-1, -2) / 8).float().contiguous()
+    V0 = torch.randn(2, 3, 128, 16, generator=g, device="cuda")
+    got = power_iteration_hip(cov, V0, 5, 1e-4)
+    torch.cuda.synchronize()
+    want = op.power_iteration(cov.double().cpu().numpy(), V0.double().cpu().numpy(), 5, 1e-4)
+    g_np = got.double().cpu().numpy()
+    assert np.isfinite(g_np).all()
+    assert np.abs(g_np - want).max() < 2e-3 * max(1.0, np.abs(want).max())
