@@ -73,7 +73,8 @@ def query_weight(cov, queries, num_kv_groups: int, window: int = QUERY_WINDOW,
     H_q -> H_kv (the group mean is stored in the query ``dtype`` before the
     fp32 norm, as torch's ``mean`` on a bf16 tensor is), weights cov by outer(||q||, ||q||) with a floor of
     1e-3 * median (lower middle element for an even count, as torch.median),
-    symmetrises and adds ridge = max(1e-4 * mean|diag|, 1e-6) * I.
+    symmetrises and adds ridge = 1e-4 * max(mean|diag|, 1e-6) * I (the clamp
+    applies to the mean, kv_pruning_utils.py:137-139).
     """
     cov = np.asarray(cov, np.float64)
     Q = np.asarray(queries, np.float64)
@@ -100,7 +101,7 @@ def query_weight(cov, queries, num_kv_groups: int, window: int = QUERY_WINDOW,
     qn = np.maximum(qn, 1e-3 * med[..., None])
     cov = cov * (qn[..., :, None] * qn[..., None, :])
     cov = 0.5 * (cov + np.swapaxes(cov, -1, -2))
-    ridge = np.maximum(1e-4 * np.abs(np.diagonal(cov, axis1=-2, axis2=-1)).mean(axis=-1), 1e-6)
+    ridge = 1e-4 * np.maximum(np.abs(np.diagonal(cov, axis1=-2, axis2=-1)).mean(axis=-1), 1e-6)
     return cov + ridge[..., None, None] * np.eye(D)
 
 

@@ -111,9 +111,23 @@ __global__ void __launch_bounds__(kThreads) mean_kernel(KeyView k, int64_t chunk
 
 // mean of one head from the pass-1 partials (fixed summation order, so every
 // kernel that needs mu gets the same bits).
-__device__ __forceinline__ float head_mean(const float* part, int bh, int splits, int c, int64_t S) {
+// Sum of n strided fp32 values, kSumBatch loads issued before any is
+// added (the adds keep their index order).
+constexpr int kSumBatch = 16;
+__device__ __forceinline__ float strided_sum(const float* p, int n, int64_t stride) {
   float s = 0.f;
-  for (int x = 0; x < splits; ++x) s += part[((int64_t)bh * splits + x) * 128 + c];
+  for (int x0 = 0; x0 < n; x0 += kSumBatch) {
+    float v[kSumBatch];
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) v[u] = x0 + u < n ? p[(int64_t)(x0 + u) * stride] : 0.f;
+#pragma unroll
+    for (int u = 0; u < kSumBatch; ++u) s += v[u];
+  }
+  return s;
+}
+
+__device__ __forceinline__ float head_mean(const float* part, int bh, int splits, int c, int64_t S) {
+  const float s = strided_sum(part + (int64_t)bh * splits * 128 + c, splits, 128);
   return S > 0 ? s / (float)S : 0.f;
 }
 
@@ -213,16 +227,7 @@ __global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int
   const int tid = threadIdx.x, t = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
   const float* src = part + (int64_t)bh * splits * (kTiles * 256) + t * 256 + tid;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  int x = 0;
-  for (; x + 4 <= splits; x += 4) {
-    a0 += src[(int64_t)(x + 0) * (kTiles * 256)];
-    a1 += src[(int64_t)(x + 1) * (kTiles * 256)];
-    a2 += src[(int64_t)(x + 2) * (kTiles * 256)];
-    a3 += src[(int64_t)(x + 3) * (kTiles * 256)];
-  }
-  for (; x < splits; ++x) a0 += src[(int64_t)x * (kTiles * 256)];
-  float sum = (a0 + a1) + (a2 + a3);  // fp32, then the key dtype (two roundings)
+  float sum = strided_sum(src, splits, kTiles * 256);  // fp32, then the key dtype (two roundings)
   asm volatile("" : "+v"(sum));
   s_t[tid] = TT::to_f32(TT::from_f32(sum));
   __syncthreads();
@@ -496,94 +501,169 @@ __global__ void __launch_bounds__(128) gather_kernel(const void* R, int r_dtype,
 // over the last W queries, the group mean (over the G query heads of the KV
 // head) rounded to the query dtype as torch's bf16/fp16 mean is; floored at
 // 1e-3 x the lower median of the 128 norms; then
-//   out = 0.5 (C o (qn qn^T) + (C o (qn qn^T))^T) + max(1e-4 mean|diag|, 1e-6) I.
-// Thread (d, half) accumulates 16 of the W window rows of channel d; the two
-// halves are added in LDS.  out may alias cov.
-template <class TT>
+//   out = 0.5 (C o (qn qn^T) + (C o (qn qn^T))^T) + 1e-4 max(mean|diag|, 1e-6) I
+// (the clamp binds to the mean).  Every global load (the covariance and the
+// G x W query rows) is issued before the first is used, so the kernel costs
+// one memory latency plus its LDS work.  Thread (slot rs = t/16, chunk
+// c8 = t%16) owns window rows rs and rs + 16 of channels 8 c8..8 c8+7 for all
+// G heads.  The covariance goes through LDS (rows padded to 129), so the
+// transposed read is conflict-free; out may alias cov.  CV / QV: 16-byte
+// row loads of the covariance / the queries (unit inner stride, aligned).
+constexpr int kQHeads = 8;  // query heads whose window rows are loaded together (G <= 8: one batch)
+template <class TT, bool CV, bool QV>
 __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t c_b, int64_t c_h, int64_t c_r,
                                                       int64_t c_c, const uint16_t* q, int64_t q_b, int64_t q_h,
                                                       int64_t q_s, int64_t q_d, int64_t S, int W, int G,
                                                       float* out, int64_t o_b, int64_t o_h, int64_t o_r,
                                                       int64_t o_c, int H) {
-  __shared__ float s_sq[2][128];
-  __shared__ float s_qn[128];
-  __shared__ float s_diag[128];
-  __shared__ float s_floor, s_ridge;
-  const int tid = threadIdx.x, d = tid & 127, half = tid >> 7;
+  constexpr int CP = 129;
+  __shared__ float s_C[128 * CP];
+  __shared__ float s_part[16][128];
+  __shared__ __align__(16) float s_qn[128];
+  __shared__ float s_wsum[2];
+  __shared__ float s_floor;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int bh = blockIdx.x, b = bh / H, kv = bh - b * H;
+  const float* C = cov + b * c_b + (int64_t)kv * c_h;
+
+  // ---- covariance loads (64 floats per thread)
+  float cv[64];
+  if constexpr (CV) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e4 = tid + 256 * i, r = e4 >> 5, c = (e4 & 31) * 4;
+      const float4 v = *(const float4*)(C + r * c_r + c);
+      cv[4 * i] = v.x, cv[4 * i + 1] = v.y, cv[4 * i + 2] = v.z, cv[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int e = tid + 256 * i;
+      cv[i] = C[(e >> 7) * c_r + (e & 127) * c_c];
+    }
+  }
+
+  // ---- query rows: group sums in fp32, G in order, kQHeads heads' loads at a time
+  const int rs = tid >> 4, c8 = tid & 15;
+  const int w0 = rs, w1 = rs + 16;
+  const uint16_t* qb = q + b * q_b + (int64_t)(kv * G) * q_h + (S - W) * q_s + (int64_t)(8 * c8) * q_d;
+  float acc[2][8];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+  for (int g0 = 0; g0 < G; g0 += kQHeads) {
+    uint4 v[kQHeads][2];
+#pragma unroll
+    for (int u = 0; u < kQHeads; ++u)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int w = j ? w1 : w0;
+        v[u][j] = make_uint4(0u, 0u, 0u, 0u);
+        if (g0 + u < G && w < W) {
+          const uint16_t* p = qb + (int64_t)(g0 + u) * q_h + (int64_t)w * q_s;
+          if constexpr (QV) {
+            v[u][j] = *(const uint4*)p;
+          } else {
+            uint32_t wd[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wd[e >> 1] |= (uint32_t)p[e * q_d] << ((e & 1) * 16);
+            v[u][j] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+          }
+        }
+      }
+#pragma unroll
+    for (int u = 0; u < kQHeads; ++u)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (g0 + u < G) {
+          float f[8];
+          unpack8<TT>(v[u][j], f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j][e] += f[e];
+        }
+      }
+  }
+
+  // ---- the covariance into LDS
+  if constexpr (CV) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e4 = tid + 256 * i, r = e4 >> 5, c = (e4 & 31) * 4;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s_C[r * CP + c + u] = cv[4 * i + u];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int e = tid + 256 * i;
+      s_C[(e >> 7) * CP + (e & 127)] = cv[i];
+    }
+  }
+
+  // ---- group mean in the query dtype, then the squares.  The fp32 product
+  // is rounded to fp32 first and then to the dtype, as torch's MeanOps does;
+  // the empty asm keeps the product in an fp32 register (otherwise the
+  // multiply and the conversion fuse into one v_fma_mix, a single rounding)
   const float inv_g = 1.f / (float)G;
-  // window rows w = 16 half + i, i < 16 (rows past W are skipped)
-  float acc[16];
+  float sq[8];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-  const uint16_t* qb = q + b * q_b + (int64_t)(kv * G) * q_h + (S - W) * q_s + d * q_d;
-  for (int gg = 0; gg < G; ++gg) {
-    const uint16_t* qg = qb + (int64_t)gg * q_h;
+  for (int e = 0; e < 8; ++e) sq[e] = 0.f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int w = 16 * half + i;
-      acc[i] += w < W ? TT::to_f32(qg[(int64_t)min(w, W - 1) * q_s]) : 0.f;
+  for (int j = 0; j < 2; ++j) {
+    if ((j ? w1 : w0) < W) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float prod = acc[j][e] * inv_g;
+        asm volatile("" : "+v"(prod));
+        const float m = TT::to_f32(TT::from_f32(prod));
+        sq[e] = fmaf(m, m, sq[e]);
+      }
     }
   }
-  float sq = 0.f;
-  {
-    // group mean in the query dtype: the fp32 product is rounded to fp32
-    // first and then to the dtype, as torch's MeanOps does.  The empty asm
-    // keeps the product in an fp32 register; otherwise the compiler fuses
-    // the multiply and the fp16 conversion into one v_fma_mixlo_f16, a
-    // single rounding of the exact product.
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float prod = acc[i] * inv_g;
-      asm volatile("" : "+v"(prod));
-      const float m = TT::to_f32(TT::from_f32(prod));
-      sq = fmaf(m, m, sq);
-    }
+  for (int e = 0; e < 8; ++e) s_part[rs][8 * c8 + e] = sq[e];
+  __syncthreads();
+  if (tid < 128) {
+    float t = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) t += s_part[r][tid];
+    s_qn[tid] = sqrtf(t);
   }
-  s_sq[half][d] = sq;
   __syncthreads();
-  if (tid < 128) s_qn[d] = sqrtf(s_sq[0][d] + s_sq[1][d]);
-  __syncthreads();
-  if (tid < 128) {  // lower median: the element of rank 63 (ties by index)
-    const float v = s_qn[d];
+  // ---- lower median: the norm of rank 63 (ties by index)
+  if (tid < 128) {
+    const float v = s_qn[tid];
     int rank = 0;
-    for (int j = 0; j < 128; ++j) {
-      const float u = s_qn[j];
-      rank += (u < v) || (u == v && j < d);
+#pragma unroll
+    for (int j4 = 0; j4 < 32; ++j4) {
+      const float4 u = *(const float4*)&s_qn[4 * j4];
+      const float uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) rank += (uu[e] < v) || (uu[e] == v && 4 * j4 + e < tid);
     }
     if (rank == 63) s_floor = 1e-3f * v;
   }
   __syncthreads();
-  const float* C = cov + b * c_b + (int64_t)kv * c_h;
+  // ---- floored norms and mean |diag| of the weighted matrix (waves 0, 1)
   if (tid < 128) {
-    const float qd = fmaxf(s_qn[d], s_floor);
-    s_qn[d] = qd;
-    s_diag[d] = fabsf(C[d * c_r + d * c_c] * (qd * qd));
-  }
-  __syncthreads();
-  if (tid == 0) {
-    float sd = 0.f;
-    for (int j = 0; j < 128; ++j) sd += s_diag[j];
-    s_ridge = fmaxf(1e-4f * (sd * (1.f / 128.f)), 1e-6f);
-  }
-  __syncthreads();
-  // every output element reads its two mirrored inputs before the workgroup
-  // writes anything (out may alias cov)
-  const float ridge = s_ridge;
-  float res[64];
+    const float qd = fmaxf(s_qn[tid], s_floor);
+    float dg = fabsf(s_C[tid * CP + tid] * (qd * qd));
 #pragma unroll
-  for (int i = 0; i < 64; ++i) {
-    const int e = tid + i * 256, r = e >> 7, c = e & 127;
-    const float wrc = s_qn[r] * s_qn[c], wcr = s_qn[c] * s_qn[r];
-    const float a = C[r * c_r + c * c_c] * wrc, bt = C[c * c_r + r * c_c] * wcr;
-    res[i] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
+    for (int off = 32; off > 0; off >>= 1) dg += shfl_xor(dg, off);
+    if (lane == 0) s_wsum[wave] = dg;
+    s_qn[tid] = qd;
   }
   __syncthreads();
+  const float ridge = 1e-4f * fmaxf((s_wsum[0] + s_wsum[1]) * (1.f / 128.f), 1e-6f);
+  // ---- out[r][c] = 0.5 (C[r][c] w + C[c][r] w) + ridge [r == c], w = qn[r] qn[c]
   float* O = out + b * o_b + (int64_t)kv * o_h;
-#pragma unroll
+#pragma unroll 8
   for (int i = 0; i < 64; ++i) {
-    const int e = tid + i * 256, r = e >> 7, c = e & 127;
-    O[r * o_r + c * o_c] = res[i];
+    const int e = tid + 256 * i, r = e >> 7, c = e & 127;
+    const float w = s_qn[r] * s_qn[c];
+    const float a = s_C[r * CP + c] * w, bt = s_C[c * CP + r] * w;
+    O[r * o_r + c * o_c] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
   }
 }
 
@@ -963,17 +1043,27 @@ extern "C" int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, i
   if (!cov->data || !queries->data || !out->data) return RK_ERR_NULL;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)(B * H));
-  if (queries->dtype == RK_F16)
-    hipLaunchKernelGGL((qweight_kernel<rk::F16>), grid, dim3(256), 0, s, (const float*)cov->data, cov->stride[0],
-                       cov->stride[1], cov->stride[2], cov->stride[3], (const uint16_t*)queries->data,
-                       queries->stride[0], queries->stride[1], queries->stride[2], queries->stride[3], S, W,
-                       (int)num_kv_groups, (float*)out->data, out->stride[0], out->stride[1], out->stride[2],
-                       out->stride[3], (int)H);
-  else
-    hipLaunchKernelGGL((qweight_kernel<rk::BF16>), grid, dim3(256), 0, s, (const float*)cov->data,
-                       cov->stride[0], cov->stride[1], cov->stride[2], cov->stride[3],
-                       (const uint16_t*)queries->data, queries->stride[0], queries->stride[1],
-                       queries->stride[2], queries->stride[3], S, W, (int)num_kv_groups, (float*)out->data,
-                       out->stride[0], out->stride[1], out->stride[2], out->stride[3], (int)H);
+  // 16-byte loads: unit inner stride, rows (and the bases) 16-byte aligned
+  const bool cvec = cov->stride[3] == 1 && cov->stride[2] % 4 == 0 && cov->stride[1] % 4 == 0 &&
+                    cov->stride[0] % 4 == 0 && ((uintptr_t)cov->data & 15) == 0;
+  const bool qvec = queries->stride[3] == 1 && queries->stride[2] % 8 == 0 && queries->stride[1] % 8 == 0 &&
+                    queries->stride[0] % 8 == 0 && ((uintptr_t)queries->data & 15) == 0;
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, (const float*)cov->data, cov->stride[0], cov->stride[1],
+                       cov->stride[2], cov->stride[3], (const uint16_t*)queries->data, queries->stride[0],
+                       queries->stride[1], queries->stride[2], queries->stride[3], S, W, (int)num_kv_groups,
+                       (float*)out->data, out->stride[0], out->stride[1], out->stride[2], out->stride[3], (int)H);
+  };
+  if (queries->dtype == RK_F16) {
+    if (cvec && qvec) go(qweight_kernel<rk::F16, true, true>);
+    else if (cvec) go(qweight_kernel<rk::F16, true, false>);
+    else if (qvec) go(qweight_kernel<rk::F16, false, true>);
+    else go(qweight_kernel<rk::F16, false, false>);
+  } else {
+    if (cvec && qvec) go(qweight_kernel<rk::BF16, true, true>);
+    else if (cvec) go(qweight_kernel<rk::BF16, true, false>);
+    else if (qvec) go(qweight_kernel<rk::BF16, false, true>);
+    else go(qweight_kernel<rk::BF16, false, false>);
+  }
   return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
 }

@@ -255,3 +255,24 @@ def test_query_weight_matches_oracle(dtype, G, S):
     want = op.query_weight(_np(cov), _np(Q), G, dtype="bfloat16" if dtype == torch.bfloat16 else "float16")
     scale = np.abs(want).max()
     assert np.abs(_np(got) - want).max() <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("cscale", [1e-4, 1e-9])
+def test_query_weight_small_covariance_ridge(cscale):
+    """mean|diag| of the weighted matrix below 1e-2 (and below 1e-6): the
+    ridge is 1e-4 * mean|diag|.clamp(min=1e-6) (kv_pruning_utils.py:137-139),
+    checked on the diagonal, where it is not lost against the entries."""
+    from rotatek_amd import prefill
+    _say(f"query_weight small covariance x{cscale}")
+    B, H, G = 1, 2, 4
+    K = _lowrank_keys(B, H, 300, torch.bfloat16, seed=3)
+    _, cov = prefill.key_covariance(K)
+    cov = (cov * (cscale / cov.diagonal(dim1=-2, dim2=-1).abs().mean())).contiguous()
+    Q = (torch.randn(B, H * G, 64, 128, device="cuda") * 0.05).to(torch.bfloat16)
+    got = prefill.query_weight(cov, Q, G)
+    torch.cuda.synchronize()
+    want = op.query_weight(_np(cov), _np(Q), G, dtype="bfloat16")
+    dg = np.diagonal(_np(got), axis1=-2, axis2=-1)
+    dw = np.diagonal(want, axis1=-2, axis2=-1)
+    assert np.abs(dg - dw).max() <= 1e-5 * np.abs(dw).max()
+    assert np.abs(_np(got) - want).max() <= 1e-5 * np.abs(want).max()

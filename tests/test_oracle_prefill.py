@@ -95,8 +95,21 @@ def test_query_weight_hand_case():
     got = op.query_weight(cov, q, num_kv_groups=1)
     qn = np.array([4.0, 2e-3, 2.0, 3.0])
     diag = qn ** 2
-    ridge = max(1e-4 * diag.mean(), 1e-6)
+    ridge = 1e-4 * max(diag.mean(), 1e-6)
     np.testing.assert_allclose(got[0, 0], np.diag(diag + ridge), rtol=1e-12, atol=1e-15)
+
+
+@pytest.mark.parametrize("scale,ridge", [(1e-3, 1e-7), (1e-8, 1e-10), (2.0, 2e-4)])
+def test_query_weight_ridge_clamps_the_mean(scale, ridge):
+    """ridge = 1e-4 * mean|diag|.clamp(min=1e-6) (kv_pruning_utils.py:137-139:
+    the clamp binds to the mean, before the product).  With unit query norms
+    the weighted diagonal is ``scale``; the numbers are written out, so a
+    clamp moved outside the product (max(1e-4 m, 1e-6)) fails the first two."""
+    D = 4
+    q = np.zeros((1, 1, 1, D))
+    q[0, 0, 0] = 1.0
+    got = op.query_weight(scale * np.eye(D)[None, None], q, num_kv_groups=1)
+    np.testing.assert_allclose(np.diag(got[0, 0]), np.full(D, scale + ridge), rtol=1e-12)
 
 
 def test_query_weight_window_and_group_mean():
@@ -110,7 +123,7 @@ def test_query_weight_window_and_group_mean():
         qn = np.sqrt((grp ** 2).sum(axis=0))
         qn = np.maximum(qn, 1e-3 * np.sort(qn)[(D - 1) // 2])
         diag = qn ** 2
-        np.testing.assert_allclose(np.diag(got[0, h]), diag + max(1e-4 * diag.mean(), 1e-6), rtol=1e-12)
+        np.testing.assert_allclose(np.diag(got[0, h]), diag + 1e-4 * max(diag.mean(), 1e-6), rtol=1e-12)
         off = got[0, h] - np.diag(np.diag(got[0, h]))
         assert np.all(off == 0.0)
 
@@ -243,4 +256,4 @@ def test_query_weight_group_mean_uses_fp32_factor():
     qn = np.abs(torch_like).astype(np.float64)
     qn = np.maximum(qn, 1e-3 * np.sort(qn)[(D - 1) // 2])
     d = np.diag(got[0, 0])
-    np.testing.assert_allclose(d - max(1e-4 * (qn ** 2).mean(), 1e-6), qn ** 2, rtol=1e-12)
+    np.testing.assert_allclose(d - 1e-4 * max((qn ** 2).mean(), 1e-6), qn ** 2, rtol=1e-12)
