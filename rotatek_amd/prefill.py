@@ -115,8 +115,9 @@ def query_weight(cov: torch.Tensor, query_states: torch.Tensor, num_key_value_gr
     in one HIP kernel (``rk_query_weight``): the last ``QUERY_WINDOW``
     queries, group-mean H_q -> H_kv in the query dtype, per-channel L2 norm
     over tokens floored at 1e-3 x the lower median, ``cov * outer(qn, qn)``,
-    symmetrised, plus a ridge of 1e-4 x mean|diag| (>= 1e-6) on the
-    diagonal.  ``out`` may be ``cov`` itself."""
+    symmetrised, plus a ridge of 1e-4 x max(mean|diag|, 1e-6) on the
+    diagonal (the clamp binds to the mean, kv_pruning_utils.py:137-139).
+    ``out`` may be ``cov`` itself."""
     _gpu(cov, "cov")
     if out is None:
         out = torch.empty_like(cov)
