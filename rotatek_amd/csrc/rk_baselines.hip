@@ -592,8 +592,7 @@ using namespace rk::base;
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// torch's mean factor float(n_out) / float(n_in) (ATen MeanOps).
-float mean_factor(int64_t n_out, int64_t n_in) { return static_cast<float>(n_out) / static_cast<float>(n_in); }
+using rk::mean_factor;
 
 // [B, H, S, C] descriptor of a 16-bit float tensor with C == want_c (or any
 // C <= 128 when want_c < 0).

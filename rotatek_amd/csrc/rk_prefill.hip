@@ -126,9 +126,10 @@ __device__ __forceinline__ float strided_sum(const float* p, int n, int64_t stri
   return s;
 }
 
-__device__ __forceinline__ float head_mean(const float* part, int bh, int splits, int c, int64_t S) {
-  const float s = strided_sum(part + (int64_t)bh * splits * 128 + c, splits, 128);
-  return S > 0 ? s / (float)S : 0.f;
+// fp32 mean of channel c of head bh: the fp32 sum of the split partials
+// times torch's mean factor (fp32 1/S), as torch's fp32 mean forms it.
+__device__ __forceinline__ float head_mean(const float* part, int bh, int splits, int c, float mfac) {
+  return strided_sum(part + (int64_t)bh * splits * 128 + c, splits, 128) * mfac;
 }
 
 // ------------------------------------------------------------------ pass 2
@@ -146,7 +147,8 @@ __host__ __device__ constexpr int tile_col(int t) { return tile_row(t) + t - til
 // and the workgroup writes one [36][256] partial.
 template <class TT, bool VEC>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mean_splits, float* part) {
+cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mean_splits, float mfac,
+           float* part) {
   __shared__ float s_c[128];
   __shared__ float s_red[kTiles * 256];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
@@ -154,7 +156,7 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
   const uint16_t* base = head_base(k, bh);
   if (tid < 128) {
     // centre = mean rounded to the key dtype (kv_pruning_utils.py:113)
-    s_c[tid] = TT::to_f32(TT::from_f32(head_mean(mean_part, bh, mean_splits, tid, k.S)));
+    s_c[tid] = TT::to_f32(TT::from_f32(head_mean(mean_part, bh, mean_splits, tid, mfac)));
   }
   __syncthreads();
   float cen[8];
@@ -220,7 +222,7 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
 template <class TT>
 __global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int splits,
                                                           const float* mean_part, int mean_splits,
-                                                          int64_t S, float* cov, int64_t cs_b, int64_t cs_h,
+                                                          float mfac, float* cov, int64_t cs_b, int64_t cs_h,
                                                           int64_t cs_r, int64_t cs_c, float* mu, int64_t ms_b,
                                                           int64_t ms_h, int64_t ms_c, int H) {
   __shared__ float s_t[256];
@@ -239,7 +241,7 @@ __global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int
   cb[r * cs_r + c * cs_c] = 0.5f * (rc + cr);
   if (i != j) cb[c * cs_r + r * cs_c] = 0.5f * (cr + rc);
   if (t == 0 && tid < 128 && mu)
-    mu[b * ms_b + (int64_t)h * ms_h + tid * ms_c] = head_mean(mean_part, bh, mean_splits, tid, S);
+    mu[b * ms_b + (int64_t)h * ms_h + tid * ms_c] = head_mean(mean_part, bh, mean_splits, tid, mfac);
 }
 
 // ------------------------------------------------------------------ rotate / score
@@ -514,8 +516,8 @@ template <class TT, bool CV, bool QV>
 __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t c_b, int64_t c_h, int64_t c_r,
                                                       int64_t c_c, const uint16_t* q, int64_t q_b, int64_t q_h,
                                                       int64_t q_s, int64_t q_d, int64_t S, int W, int G,
-                                                      float* out, int64_t o_b, int64_t o_h, int64_t o_r,
-                                                      int64_t o_c, int H) {
+                                                      float inv_g, float* out, int64_t o_b, int64_t o_h,
+                                                      int64_t o_r, int64_t o_c, int H) {
   constexpr int CP = 129;
   __shared__ float s_C[128 * CP];
   __shared__ float s_part[16][128];
@@ -601,11 +603,11 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
     }
   }
 
-  // ---- group mean in the query dtype, then the squares.  The fp32 product
-  // is rounded to fp32 first and then to the dtype, as torch's MeanOps does;
+  // ---- group mean in the query dtype, then the squares: fp32 sum times
+  // torch's mean factor inv_g (formed on the host), rounded to fp32 first and
+  // then to the dtype, as torch's MeanOps does;
   // the empty asm keeps the product in an fp32 register (otherwise the
   // multiply and the conversion fuse into one v_fma_mix, a single rounding)
-  const float inv_g = 1.f / (float)G;
   float sq[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) sq[e] = 0.f;
@@ -757,18 +759,20 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
   float* mpart = (float*)((char*)ws + p.off_mean);
   float* cpart = (float*)((char*)ws + p.off_cov);
   const dim3 gm((unsigned)p.mean_splits, (unsigned)bh), gc((unsigned)p.cov_splits, (unsigned)bh);
+  // mean over the token dim of [B, H, S, 128] (kv_pruning_utils.py:112)
+  const float mfac = rk::mean_factor(bh * 128, bh * k.S * 128);
   if (vec) {
     hipLaunchKernelGGL((mean_kernel<TT, true>), gm, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits, mpart);
     hipLaunchKernelGGL((cov_kernel<TT, true>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
-                       p.mean_splits, cpart);
+                       p.mean_splits, mfac, cpart);
   } else {
     hipLaunchKernelGGL((mean_kernel<TT, false>), gm, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits, mpart);
     hipLaunchKernelGGL((cov_kernel<TT, false>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
-                       p.mean_splits, cpart);
+                       p.mean_splits, mfac, cpart);
   }
   hipLaunchKernelGGL((covfin_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits,
                      mpart,
-                     p.mean_splits, k.S, cov, cov_t->stride[0], cov_t->stride[1], cov_t->stride[2],
+                     p.mean_splits, mfac, cov, cov_t->stride[0], cov_t->stride[1], cov_t->stride[2],
                      cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0, mu_t ? mu_t->stride[1] : 0,
                      mu_t ? mu_t->stride[2] : 0, k.H);
   return hipGetLastError();
@@ -1043,6 +1047,8 @@ extern "C" int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, i
   if (!cov->data || !queries->data || !out->data) return RK_ERR_NULL;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)(B * H));
+  // the group mean over dim 2 of [B, H_kv, G, W, 128] (kv_pruning_utils.py:127-129)
+  const float inv_g = rk::mean_factor(B * H * W * 128, B * H * num_kv_groups * W * 128);
   // 16-byte loads: unit inner stride, rows (and the bases) 16-byte aligned
   const bool cvec = cov->stride[3] == 1 && cov->stride[2] % 4 == 0 && cov->stride[1] % 4 == 0 &&
                     cov->stride[0] % 4 == 0 && ((uintptr_t)cov->data & 15) == 0;
@@ -1051,7 +1057,7 @@ extern "C" int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, i
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, (const float*)cov->data, cov->stride[0], cov->stride[1],
                        cov->stride[2], cov->stride[3], (const uint16_t*)queries->data, queries->stride[0],
-                       queries->stride[1], queries->stride[2], queries->stride[3], S, W, (int)num_kv_groups,
+                       queries->stride[1], queries->stride[2], queries->stride[3], S, W, (int)num_kv_groups, inv_g,
                        (float*)out->data, out->stride[0], out->stride[1], out->stride[2], out->stride[3], (int)H);
   };
   if (queries->dtype == RK_F16) {

@@ -48,3 +48,53 @@ def test_spark_ratio_outside_unit_interval_is_a_value_error():
     k = torch.zeros(1, 1, 4, 128)
     with pytest.raises(ValueError):
         per_token_channel_prune(torch.zeros(1, 1, 2, 128), k, 1.5)
+
+
+@pytest.mark.parametrize("S,prompt,text,want", [
+    (10, 3, 2, ([0, 1, 2], [3, 4, 5, 6, 7], [8, 9])),
+    (10, 0, 0, ([], list(range(10)), [])),
+    (10, 12, 2, (list(range(10)), [], [])),          # prompt clamped to S, nothing left for text
+    (10, 4, 9, ([0, 1, 2, 3], [], [4, 5, 6, 7, 8, 9])),  # text clamped to what the prompt leaves
+    (10, -3, -1, ([], list(range(10)), [])),          # negative lengths count as 0
+    (0, 2, 2, ([], [], [])),
+])
+def test_split_spans_clamping(S, prompt, text, want):
+    """Span split of kv_pruning_utils.py:26-35 on written-out cases."""
+    import torch
+    from rotatek_amd.pruning import _split_spans
+
+    class Pruner:
+        prompt_seqlen, query_seqlen = prompt, text
+
+    x = torch.arange(S).view(1, 1, S, 1)
+    got = tuple(t.flatten().tolist() for t in _split_spans(Pruner, x))
+    assert got == want
+
+
+@pytest.mark.parametrize("ratio,want", [(0.0, 128), (0.75, 32), (0.875, 16), (0.5, 64), (1.0, 0),
+                                        (1.5, 0), (-0.25, 128), (0.999, 1)])
+def test_keep_count(ratio, want):
+    """keep = 128 - clamp(int(128 * ratio), 0, 128) (kv_pruning_utils.py:108)."""
+    from rotatek_amd.pruning import keep_count
+    assert keep_count(128, ratio) == want
+
+
+@pytest.mark.parametrize("value,want", [("gqa", "rotatek_decode_gqa full_channel_decode_gqa"),
+                                        (" Paper ", "rotatek_decode_fused full_channel_decode"),
+                                        ("bogus", "ValueError")])
+def test_kernel_family_from_environment(value, want):
+    """ROTATEK_KERNEL is read once at import; an unknown family raises
+    ValueError (rotatek/kernels/__init__.py:15-24).  Fresh interpreter each."""
+    import os
+    import subprocess
+    import sys
+    code = ("import rotatek_amd.kernels as k\n"
+            "print(k.rotatek_decode.__name__, k.full_channel_decode.__name__)")
+    env = dict(os.environ, ROTATEK_KERNEL=value)
+    r = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
+                       cwd=os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    if want == "ValueError":
+        assert r.returncode != 0 and "ValueError" in r.stderr
+    else:
+        assert r.returncode == 0, r.stderr
+        assert r.stdout.strip() == want
