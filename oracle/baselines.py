@@ -35,14 +35,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle.numerics import round_to
-
-
-def mean_factor(n_out: int, n_in: int) -> np.float32:
-    """torch's mean factor ``float(n_out) / float(n_in)`` in fp32 (inf when
-    ``n_in`` is 0, so the mean of nothing is NaN)."""
-    with np.errstate(divide="ignore", invalid="ignore"):
-        return np.float32(np.float32(n_out) / np.float32(n_in))
+from oracle.numerics import mean_factor, round_to
 
 
 def _mean16(x, axis: int, factor: np.float32, dtype: str) -> np.ndarray:

@@ -51,3 +51,11 @@ def round_to(x, dtype: str) -> np.ndarray:
     if dtype == "float64":
         return np.asarray(x, dtype=np.float64)
     raise ValueError(f"unknown dtype {dtype!r}")
+
+
+def mean_factor(n_out: int, n_in: int) -> np.float32:
+    """torch's GPU mean factor ``float(n_out) / float(n_in)`` in fp32 (ATen
+    MeanOps multiplies the fp32 sum by it; inf when ``n_in`` is 0, so the
+    mean of nothing is NaN)."""
+    with np.errstate(divide="ignore", invalid="ignore"):
+        return np.float32(np.float32(n_out) / np.float32(n_in))

@@ -30,7 +30,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from oracle.numerics import round_to
+from oracle.numerics import mean_factor, round_to
 
 QUERY_WINDOW = 32   # kv_pruning_utils.py:23
 
@@ -49,15 +49,25 @@ def keep_count(head_dim: int, ratio: float) -> int:
     return head_dim - min(head_dim, max(0, int(head_dim * ratio)))
 
 
-def key_covariance(keys_vision, dtype: str):
+def key_covariance(keys_vision, dtype: str, mean=None):
     """(mean_fp32 [B,H,D], cov [B,H,D,D]) as the reference computes them.
 
-    mean = fp32 mean of the Keys; Kc = dtype(K - dtype(mean)); cov =
+    mean = fp32 mean of the Keys as torch's GPU mean forms it, fp32(sum) *
+    fp32(n_out / n_in) (ATen MeanOps); Kc = dtype(K - dtype(mean)); cov =
     dtype(Kc^T Kc) (the einsum output is in the key dtype) then
-    0.5 (cov + cov^T) in fp32.
+    0.5 (cov + cov^T) in fp32.  ``mean`` (fp32 [B,H,D]) replaces the computed
+    mean as the centre: the fp32 sum's rounding depends on its order, which
+    no restatement shares with torch's reduction, and a centre that rounds
+    the other way in the key dtype moves whole rows of the covariance.
     """
     K = np.asarray(keys_vision, np.float64)
-    mean = round_to(K.mean(axis=-2), "float32")
+    B, H, S, D = K.shape
+    if mean is None:
+        s32 = np.asarray(K.sum(axis=-2), np.float32)
+        with np.errstate(invalid="ignore"):
+            mean = (s32 * mean_factor(B * H * D, B * H * S * D)).astype(np.float64)
+    else:
+        mean = np.asarray(mean, np.float32).astype(np.float64)
     Kc = round_to(K - round_to(mean, dtype)[..., None, :], dtype)
     cov = np.einsum("bhsd,bhse->bhde", Kc, Kc)
     cov = round_to(round_to(cov, "float32"), dtype)
@@ -93,7 +103,8 @@ def query_weight(cov, queries, num_kv_groups: int, window: int = QUERY_WINDOW,
             acc = np.zeros(grp.shape[:2] + grp.shape[3:], np.float32)
             for g in range(num_kv_groups):
                 acc = acc + grp[:, :, g]
-            Qr = round_to((acc * np.float32(1.0 / num_kv_groups)).astype(np.float64), dtype)
+            f = mean_factor(B * Hkv * w * D, B * Hkv * num_kv_groups * w * D)
+            Qr = round_to((acc * f).astype(np.float64), dtype)
         else:
             Qr = grp.mean(axis=2)
     qn = np.sqrt((Qr ** 2).sum(axis=-2))                           # [B,Hkv,D]

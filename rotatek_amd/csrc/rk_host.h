@@ -25,9 +25,10 @@ inline int dtype_size(int d) {
 inline bool is_half(int d) { return d == RK_F16 || d == RK_BF16; }
 
 // torch's mean scale factor, float(n_out) / float(n_in), formed in float as
-// ATen's mean kernels form it (MeanOps multiplies the fp32 sum by it).
+// ATen's GPU mean kernels form it (MeanOps multiplies the fp32 sum by it).
+// n_in == 0 gives inf, so the mean of nothing is NaN, as torch's is.
 inline float mean_factor(int64_t n_out, int64_t n_in) {
-  return n_in > 0 ? static_cast<float>(n_out) / static_cast<float>(n_in) : 0.f;
+  return static_cast<float>(n_out) / static_cast<float>(n_in);
 }
 inline bool is_float_param(int d) { return d == RK_F16 || d == RK_BF16 || d == RK_F32; }
 

@@ -127,9 +127,15 @@ __device__ __forceinline__ float strided_sum(const float* p, int n, int64_t stri
 }
 
 // fp32 mean of channel c of head bh: the fp32 sum of the split partials
-// times torch's mean factor (fp32 1/S), as torch's fp32 mean forms it.
+// times torch's mean factor (fp32 1/S), as torch's fp32 mean forms it.  The
+// empty asm keeps the product an fp32 value: a caller that converts it to
+// the key dtype would otherwise get one v_fma_mix, a single rounding of the
+// exact product, where torch rounds to fp32 first (the two differ when the
+// fp32 mean lands on a 16-bit midpoint).
 __device__ __forceinline__ float head_mean(const float* part, int bh, int splits, int c, float mfac) {
-  return strided_sum(part + (int64_t)bh * splits * 128 + c, splits, 128) * mfac;
+  float m = strided_sum(part + (int64_t)bh * splits * 128 + c, splits, 128) * mfac;
+  asm volatile("" : "+v"(m));
+  return m;
 }
 
 // ------------------------------------------------------------------ pass 2

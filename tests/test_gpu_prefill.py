@@ -20,6 +20,15 @@ DT = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
 ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
 
 
+def _storage_ulp(a, b, dtype):
+    """One ulp of the 16-bit storage format at the larger magnitude of a and
+    b (normal range): a value just under a power of two that rounds to it
+    differs by the ulp of the binade above."""
+    m = np.maximum(np.abs(a), np.abs(b))
+    e = np.floor(np.log2(np.maximum(m, 1e-30)))
+    return 2.0 ** e * ULP[dtype]
+
+
 def _np(t):
     return t.detach().cpu().to(torch.float64).numpy()
 
@@ -68,11 +77,14 @@ def test_covariance_matches_oracle(dtype, S):
     Kv = full[:, :, 30:30 + S]                                   # strided span view
     mean, cov = prefill.key_covariance(Kv)
     torch.cuda.synchronize()
-    om, oc = op.key_covariance(_np(Kv), DT[dtype])
+    om, _ = op.key_covariance(_np(Kv), DT[dtype])
     np.testing.assert_allclose(_np(mean), om, rtol=1e-5, atol=1e-6)
+    # the covariance to one storage ulp about the kernel's own centre (the
+    # fp32 mean's last bit depends on the summation order)
+    _, oc = op.key_covariance(_np(Kv), DT[dtype], mean=_np(mean))
     scale = np.abs(oc).max(axis=(-1, -2), keepdims=True)
     err = np.abs(_np(cov) - oc)
-    assert np.all(err <= ULP[dtype] * np.abs(oc) + 1e-6 * scale), err.max()
+    assert np.all(err <= _storage_ulp(oc, _np(cov), dtype) + 1e-6 * scale), err.max()
     c = _np(cov)
     np.testing.assert_array_equal(c, np.swapaxes(c, -1, -2))
 
@@ -276,3 +288,28 @@ def test_query_weight_small_covariance_ridge(cscale):
     dw = np.diagonal(want, axis1=-2, axis2=-1)
     assert np.abs(dg - dw).max() <= 1e-5 * np.abs(dw).max()
     assert np.abs(_np(got) - want).max() <= 1e-5 * np.abs(want).max()
+
+
+def test_covariance_centre_rounds_through_fp32():
+    """Channel 0's fp32 mean, fp32(1.500732421875 * fp32(1/3)), is exactly
+    0.500244140625, a midpoint of the fp16 grid, while the exact product lies
+    just above it.  torch rounds the fp32 mean to fp16 (ties to even: 0.5),
+    so the centre must be 0.5, not 0.50048828125 (one rounding of the exact
+    product, what a fused multiply-and-convert gives)."""
+    from rotatek_amd import prefill
+    _say("covariance centre on an fp16 midpoint")
+    K = np.zeros((1, 1, 3, 128), np.float32)
+    K[0, 0, :, 0] = [1.0, 0.5, 0.000732421875]
+    # fp16 values whose centres are not their means, so channel 0's centre
+    # shows in the cross terms (cov[0][2] is -0.002956390380859375 with the
+    # centre 0.5 and -0.0029582977294921875 with 0.50048828125)
+    K[0, 0, :, 1:5] = [[-0.58447265625, -1.26953125, -0.181396484375, -0.0099945068359375],
+                       [-1.412109375, 0.85302734375, 1.4931640625, 0.316162109375],
+                       [3.427734375, -1.2646484375, 1.041015625, -0.8173828125]]
+    mean, cov = prefill.key_covariance(torch.tensor(K, device="cuda").to(torch.float16))
+    torch.cuda.synchronize()
+    assert _np(mean)[0, 0, 0] == np.float32(0.500244140625)
+    om, oc = op.key_covariance(K.astype(np.float64), "float16")
+    np.testing.assert_array_equal(_np(mean), om)
+    assert _np(cov)[0, 0, 0, 2] == np.float32(-0.002956390380859375)
+    np.testing.assert_array_equal(_np(cov), oc)
