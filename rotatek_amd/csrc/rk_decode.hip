@@ -56,13 +56,13 @@ struct DecodeArgs {
   // visual span sits between them in the span cache); UINT32_MAX = no gap.
   uint32_t vf_gap_at, vf_gap;
   // Fused append (span cache): the token k_new / v_new [B, H_kv, 128] joins
-  // at row pos[b] = len_full[b] (captured by the split pass into ws_pos),
-  // the merge folds it in, writes it to kf_w / vf_w and advances len_full.
+  // at row pos[b] = len_full[b].  Workgroup 0 of each unit folds it into
+  // its partial and the first unit of the KV head writes it to kf_w / vf_w;
+  // the merge launch advances len_full (nothing else reads it there).
   const uint16_t* k_new;
   const uint16_t* v_new;
   uint16_t* kf_w;
   uint16_t* vf_w;
-  int32_t* ws_pos;
   int64_t kn_sb, kn_sh, kn_sd, vn_sb, vn_sh, vn_sd;
   const uint16_t* ks;
   const uint16_t* vs;
@@ -260,32 +260,14 @@ struct FullBuf {
 // One wave per row.  Lane (sl, c8) = (lane >> 4, lane & 15) owns channels
 // 8 c8 .. 8 c8 + 7 and folds partials p = sl, sl + 4, ... (eight partials'
 // loads in flight at a time); the four slices are then combined across
-// lanes.  With a fused append the new token (score q . k_new, value v_new)
-// is folded in last, written to the span buffers once per (b, KV head), and
-// len_full[b] advances.
+// lanes.  With a fused append the new token is already in partial 0 of the
+// unit; the row of query head 0 advances len_full[b] (a full buffer stays).
 template <class TT>
-__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int kv, int hq, int h,
+__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int hq, int h,
                                           int lane) {
   const int sl = lane >> 4, c8 = lane & 15;
   const int64_t base = u * a.np;
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  // fused append: the new token's q, k, v and position are loaded up front,
-  // together with the partials
-  uint16_t qn[8], kn[8], vn[8];
-  int32_t pos = 0;
-  if (a.k_new) {
-    const uint16_t* qr = a.q + b * a.q_sb + (int64_t)hq * a.q_sh;
-    const uint16_t* kr = a.k_new + b * a.kn_sb + (int64_t)kv * a.kn_sh;
-    const uint16_t* vr = a.v_new + b * a.vn_sb + (int64_t)kv * a.vn_sh;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int ch = 8 * c8 + e;
-      qn[e] = qr[ch * a.q_sd];
-      kn[e] = kr[ch * a.kn_sd];
-      vn[e] = vr[ch * a.vn_sd];
-    }
-    pos = a.ws_pos[b];
-  }
   auto fold = [&](const float* mm, const float* ll, const float4* v0, const float4* v1, int k) {
     float mx = M;
     for (int i = 0; i < k; ++i) mx = fmaxf(mx, mm[i]);
@@ -333,35 +315,9 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
     for (int e = 0; e < 8; ++e) A[e] = A[e] * ws + shfl_xor(A[e], off) * wo;
     M = Mx;
   }
-  if (a.k_new) {
-    if (pos < a.S_f) {
-      float d = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(TT::to_f32(qn[e]), TT::to_f32(kn[e]), d);
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) d += shfl_xor(d, off);
-      const float sn = d * a.scale_log2;
-      const float Mx = fmaxf(M, sn);
-      const float ws = fast_exp2(M - Mx), wn = fast_exp2(sn - Mx);
-      L = L * ws + wn;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) A[e] = A[e] * ws + TT::to_f32(vn[e]) * wn;
-      M = Mx;
-      if (hq == kv * a.G) {  // first query head of the group writes the token once
-        if (sl == 1) {
-          uint16_t* dst = a.kf_w + b * a.kf_sb + (int64_t)kv * a.kf_sh + (int64_t)pos * a.kf_ss;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dst[(int64_t)(8 * c8 + e) * a.kf_sd] = kn[e];
-        } else if (sl == 2) {
-          const uint32_t row = (uint32_t)pos + ((uint32_t)pos >= a.vf_gap_at ? a.vf_gap : 0u);
-          uint16_t* dst = a.vf_w + b * a.vf_sb + (int64_t)kv * a.vf_sh + (int64_t)row * a.vf_ss;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dst[(int64_t)(8 * c8 + e) * a.vf_sd] = vn[e];
-        } else if (sl == 3 && c8 == 0 && hq == 0) {
-          a.len_full[b] = pos + 1;
-        }
-      }
-    }
+  if (a.k_new && hq == 0 && lane == 0) {
+    const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
+    if (pos < a.S_f) a.len_full[b] = pos + 1;
   }
   if (sl != 0) return;
   const float den = L + kDenomEps;
@@ -377,7 +333,9 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
   }
 }
 
-template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
+// APPEND: fused append of k_new / v_new (span cache decode step); a
+// separate instantiation so the plain decode carries none of its registers.
+template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const DecodeArgs a) {
   constexpr int DKP = DKB * 32;
@@ -410,8 +368,36 @@ decode_kernel(const DecodeArgs a) {
   const bool is_vis = HAS_VIS && x < a.wg_vis;
   const int xf = HAS_VIS ? x - a.wg_vis : x;
 
-  if (a.k_new && r_in_b == 0 && x == 0 && tid == 0)
-    a.ws_pos[b] = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
+  // Fused append: workgroup 0 of the unit stages the new token in LDS
+  // behind the ring's prime and folds it into wave 0's state at the end.
+  __shared__ float s_new[2][128];  // k_new, v_new of this unit's KV head
+  const bool fold_new = APPEND && x == 0;
+  int64_t pos_new = 0;
+  if (fold_new) pos_new = min(a.S_f, (int64_t)max(a.len_full[b], 0));
+  const bool has_new = fold_new && pos_new < a.S_f;  // a full buffer neither attends nor stores
+  uint16_t new_raw = 0;
+  auto load_new = [&]() {
+    if (has_new) {
+      const int c = tid & 127;
+      new_raw = tid < 128 ? a.k_new[b * a.kn_sb + (int64_t)kv * a.kn_sh + (int64_t)c * a.kn_sd]
+                          : a.v_new[b * a.vn_sb + (int64_t)kv * a.vn_sh + (int64_t)c * a.vn_sd];
+    }
+  };
+  // after the staging barrier: the first unit of the KV head stores the row
+  auto store_new = [&]() {
+    if (has_new) {
+      s_new[tid >> 7][tid & 127] = TT::to_f32(new_raw);
+      if (jblk == 0) {
+        const int64_t c = tid & 127;
+        if (tid < 128) {
+          a.kf_w[b * a.kf_sb + (int64_t)kv * a.kf_sh + pos_new * a.kf_ss + c * a.kf_sd] = new_raw;
+        } else {
+          const uint32_t row = (uint32_t)pos_new + ((uint32_t)pos_new >= a.vf_gap_at ? a.vf_gap : 0u);
+          a.vf_w[b * a.vf_sb + (int64_t)kv * a.vf_sh + (int64_t)row * a.vf_ss + c * a.vf_sd] = new_raw;
+        }
+      }
+    }
+  };
 
   float m = kNegInit, l = 0.f;
   f32x4 acc[8];
@@ -515,6 +501,7 @@ decode_kernel(const DecodeArgs a) {
     Ring<NBUF_V, VisBuf<DKB>> ring(nblk, wave, rot_seed);
     ring.prime(load);
     load_q();
+    load_new();
     if (a.r_vec) {
       // LDS DMA (global_load_lds_dwordx4): wave w copies 1 KB blocks
       // r * 4 + w of R straight into s_r, holding no registers across the
@@ -537,6 +524,7 @@ decode_kernel(const DecodeArgs a) {
 
     const float dmv = (tid < 128 && a.has_bias) ? raw_to_f32(dmraw, a.dm_dtype) : 0.f;
     store_q();
+    store_new();
     if (tid < 128) s_dm[tid] = dmv;
     __syncthreads();
     float rv[kL];
@@ -643,6 +631,7 @@ decode_kernel(const DecodeArgs a) {
     Ring<NBUF_F, FullBuf> ring(nblk, wave, rot_seed);
     ring.prime(load);
     load_q();
+    load_new();
     const uint8_t* mb = a.mask ? a.mask + b * a.mf_sb : nullptr;
     uint32_t mv[kMaskChunk / kThreads];  // one register each: no byte packing between loads
     if (mb && t_end > t_begin) {  // uniform: all mask loads issued together
@@ -659,6 +648,7 @@ decode_kernel(const DecodeArgs a) {
     for (int k = 0; k < kMaskChunk / kThreads; ++k) asm volatile("" : "+v"(mv[k]));
 
     store_q();
+    store_new();
 #pragma unroll
     for (int k = 0; k < kMaskChunk / kThreads; ++k) {
       const int i = tid + k * kThreads;
@@ -690,6 +680,25 @@ decode_kernel(const DecodeArgs a) {
       softmax_pv<TT>(s, B.v, m, l, acc);
     };
     ring.run(load, compute);
+  }
+
+  // ---- fused append: wave 0 attends the new token (score q . k_new, a
+  // full-width token without bias) as one more row of its online softmax
+  if (has_new && wave == 0) {
+    float d = 0.f;
+#pragma unroll
+    for (int c = 0; c < 32; ++c) d = fmaf(s_q[nq][32 * g + c], s_new[0][32 * g + c], d);
+    d += shfl_xor(d, 16);
+    d += shfl_xor(d, 32);
+    const float sn = d * a.scale_log2;
+    const float m_new = fmaxf(m, sn);
+    const float alpha = fast_exp2(m - m_new), w = fast_exp2(sn - m_new);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[j][i] = acc[j][i] * alpha + w * s_new[1][32 * g + 8 * i + j];
+    l = l * alpha + (g == 0 ? w : 0.f);
+    m = m_new;
   }
 
   // ---- merge the four wave states into this workgroup's partial
@@ -746,7 +755,7 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a, int
   const int kv = r_in_b / a.spk;
   const int jblk = r_in_b - kv * a.spk;
   if (h >= min(a.hpu, a.G - jblk * a.hpu)) return;
-  merge_row<TT>(a, u, b, kv, kv * a.G + jblk * a.hpu + h, h, tid & 63);
+  merge_row<TT>(a, u, b, kv * a.G + jblk * a.hpu + h, h, tid & 63);
 }
 
 }  // namespace rk
@@ -773,20 +782,18 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
 
 struct WsLayout {
-  size_t part_m, part_l, part_acc, pos, total;
+  size_t part_m, part_l, part_acc, total;
 };
 
-// partials (m, l, acc) per (unit, workgroup, head), then one int32 append
-// position per batch row (units / units_per_b = B)
-WsLayout ws_layout(const rk_decode_plan& p, int64_t B) {
+// partials (m, l, acc) per (unit, workgroup, head)
+WsLayout ws_layout(const rk_decode_plan& p) {
   const int64_t np = p.wg_vis + p.wg_full;
   const size_t parts = (size_t)p.units * np * p.heads_per_unit;
   WsLayout w;
   w.part_m = 0;
   w.part_l = w.part_m + align256(parts * sizeof(float));
   w.part_acc = w.part_l + align256(parts * sizeof(float));
-  w.pos = w.part_acc + align256(parts * 128 * sizeof(float));
-  w.total = w.pos + align256((size_t)B * sizeof(int32_t));
+  w.total = w.part_acc + align256(parts * 128 * sizeof(float));
   return w;
 }
 
@@ -865,7 +872,7 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   }
   p.grid = p.units * (p.wg_vis + p.wg_full);
   if (p.units > 65535 * 1024 || p.wg_vis + p.wg_full > (1 << 30)) return RK_ERR_SHAPE;
-  p.workspace_bytes = ws_layout(p, B).total;
+  p.workspace_bytes = ws_layout(p).total;
   *plan = p;
   return RK_OK;
 }
@@ -955,8 +962,17 @@ int resolve_cus(int32_t num_cus, int* st) {
 
 template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
 hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS>), grid, dim3(rk::kThreads), 0, s,
-                     a);
+  bool appended = false;
+  if constexpr (HAS_VIS) {  // the span cache's step always carries the visual span
+    if (a.k_new) {
+      hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, true, true>), grid, dim3(rk::kThreads), 0,
+                         s, a);
+      appended = true;
+    }
+  }
+  if (!appended)
+    hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false>), grid, dim3(rk::kThreads), 0,
+                       s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)grid.y * a.hpu;
@@ -1035,7 +1051,7 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   if (!q->data || !out->data || (vis_work && (!R->data || !ks->data || !vs->data)) ||
       (c.S_f > 0 && (!kf->data || !vf->data)))
     return RK_ERR_NULL;
-  const WsLayout w = ws_layout(p, c.B);
+  const WsLayout w = ws_layout(p);
   rk::DecodeArgs a;
   memset(&a, 0, sizeof(a));
   a.q = (const uint16_t*)q->data;
@@ -1095,7 +1111,6 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     a.v_new = (const uint16_t*)v_new->data;
     a.kf_w = (uint16_t*)kf->data;
     a.vf_w = (uint16_t*)vf->data;
-    a.ws_pos = (int32_t*)((char*)ws + w.pos);
     a.kn_sb = k_new->stride[0];
     a.kn_sh = k_new->stride[1];
     a.kn_sd = k_new->stride[3];
