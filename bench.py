@@ -27,6 +27,7 @@ committed summary of those passes (profiles/traffic_<config>.json).
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -461,6 +462,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2")
     ap.add_argument("--family", default="paper", choices=["paper", "gqa"])
+    ap.add_argument("--seqlen", type=int, default=0,
+                    help="override the visual span length (kernel_profile.py's --seqlen)")
+    ap.add_argument("--batch-size", type=int, default=0,
+                    help="override the batch (kernel_profile.py's --batch_size)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -502,6 +507,8 @@ def main():
     from rotatek_amd.kernels.gqa_decode import full_channel_decode_gqa, rotatek_decode_gqa
 
     cfg = synth.CONFIGS[args.config]
+    if args.seqlen > 0 or args.batch_size > 0:
+        cfg = dataclasses.replace(cfg, S_v=args.seqlen or cfg.S_v, B=args.batch_size or cfg.B)
     torch.cuda.set_device(0)
     _log(f"[bench] {torch.cuda.get_device_name(0)}; generating {cfg}")
     inp = synth.make_decode_inputs(cfg, "cuda", seed=0, with_dense=not args.no_dense)

@@ -780,6 +780,10 @@ int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
+// Bytes one resident workgroup slot streams during a workgroup's fixed
+// latency (prologue + epilogue, ~8 us at ~14 GB/s per slot on MI355X).
+constexpr int64_t kSlotLatencyBytes = INT64_C(128) << 10;
+constexpr int64_t kMinWgsPerUnit = 8;
 
 struct WsLayout {
   size_t part_m, part_l, part_acc, total;
@@ -843,19 +847,38 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   // one query head per unit at 512 KB.
   const int64_t max_wg = p.heads_per_unit > 1 ? 8 * g_max_wg_bytes : g_max_wg_bytes;
   int64_t rounds = cdiv(total, slots * max_wg);
+  // ... and enough rounds for kMinWgsPerUnit workgroups per unit: with many
+  // units a single round leaves each unit one or two workgroups of several
+  // MB (measured on MI355X, B=32 with 8 KV heads of 4 query heads: 228 us
+  // at 2-3 workgroups per unit, 216 us at 7)
+  const int64_t by_units = cdiv(kMinWgsPerUnit * p.units, slots);
+  if (rounds < by_units && total / (by_units * slots) >= g_min_wg_bytes) rounds = by_units;
   if (rounds < 1) rounds = 1;
   int64_t budget = p.units > 0 ? rounds * slots / p.units : 1;
   const int64_t by_min = unit_bytes / g_min_wg_bytes;
   if (budget > by_min) budget = by_min;
   if (budget < 1) budget = 1;
+  // Each span gets its byte share of the budget, rounded, at least one
+  // workgroup.  A prompt/text span too small for a workgroup of its own
+  // still gets one; the visual span then keeps its full share (and the grid
+  // overflows the rounds) only if that shortens each visual workgroup by
+  // more than a slot streams during a workgroup's fixed latency, since the
+  // overflow waits that long for the small workgroups' slots.  80
+  // prompt/text tokens beside 16000 visual ones at two slots per unit keep
+  // two visual workgroups (not one); 60 beside 12001 at sixteen slots give
+  // the slot back.
   int64_t w_full = 0, w_vis = 0;
   if (S_f > 0) {
     w_full = (budget * unit_full + unit_bytes / 2) / unit_bytes;
     if (w_full < 1) w_full = 1;
   }
   if (S_v > 0) {
-    w_vis = budget - w_full;
+    w_vis = (budget * unit_vis + unit_bytes / 2) / unit_bytes;
     if (w_vis < 1) w_vis = 1;
+    const int64_t fit = budget - w_full > 1 ? budget - w_full : 1;
+    if (w_vis > fit && p.units * (w_vis + w_full) > rounds * slots &&
+        unit_vis / fit - unit_vis / w_vis < kSlotLatencyBytes)
+      w_vis = fit;
   }
   if (S_v > 0) {
     p.chunk_vis = round_up(cdiv(S_v, w_vis), kWgTokens);

@@ -46,6 +46,10 @@ CONFIGS = {
     "cfg1": DecodeConfig("cfg1", 1, 32, 32, 15360, 640, 32, torch.float16),
     "cfg2": DecodeConfig("cfg2", 32, 32, 32, 14000, 2000, 32, torch.float16),
     "cfg3": DecodeConfig("cfg3", 16, 28, 4, 30720, 2048, 32, torch.bfloat16),
+    # the reference's kernel microbenchmark shape (scripts/paper/kernel/
+    # kernel_profile.py:37-45 and its usage line): H_q 32, H_kv 8, D_keep 32,
+    # 50 prompt + 30 text tokens, bf16, 16000 visual tokens at batch 32
+    "kp": DecodeConfig("kp", 32, 32, 8, 16000, 80, 32, torch.bfloat16),
 }
 
 

@@ -241,10 +241,11 @@ def _sample_oracle(inp, pairs):
     return res
 
 
-@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3"])
+@pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "kp"])
 def test_benchmark_configs_full_size(cfg):
-    """Full BASELINE shapes: sampled (b, kv) groups against the oracle, the
-    rest through properties (paper == gqa family for MHA, finite outputs)."""
+    """Full BASELINE shapes (and the reference kernel harness's shape, kp):
+    sampled (b, kv) groups against the oracle, the rest through properties
+    (paper == gqa family, bit for bit for MHA, finite outputs)."""
     from rotatek_amd import synth
     c = synth.CONFIGS[cfg]
     _say(f"full-size {cfg}")
@@ -260,6 +261,8 @@ def test_benchmark_configs_full_size(cfg):
     for (b, kv), w in want.items():
         got = _np(out[b, 0, kv * G:(kv + 1) * G])
         assert np.abs(got - w).max() <= TOL[c.dtype], (b, kv)
+    out_p = _decode(args, "paper")
     if c.G == 1:
-        out_p = _decode(args, "paper")
         assert torch.equal(out_p, out)
+    else:
+        assert (out_p.float() - out.float()).abs().max().item() <= TOL[c.dtype]
