@@ -82,7 +82,7 @@ struct DecodeArgs {
   int64_t S_v, S_f, chunk_vis, chunk_full;
   // within-head strides (elements); a head's span is < 2^31 elements
   uint32_t kf_ss, kf_sd, vf_ss, vf_sd, ks_ss, ks_sd, vs_ss, vs_sd;
-  int32_t G, Dk, hpu, spk, units_per_b, wg_vis, np;
+  int32_t G, Dk, hpu, spk, units_per_b, wg_vis, np, rot_x;
   int32_t r_dtype, dm_dtype, has_bias, has_mask;
   // prologue layouts: q rows contiguous and 16-byte aligned (one 16-byte load
   // per thread); R a contiguous, 16-byte aligned [128][Dk] 16-bit block
@@ -357,8 +357,11 @@ decode_kernel(const DecodeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
   const int nq = n < HMAX ? n : 0;  // LDS row for this lane's head column
+  // Workgroups go to the 8 XCDs round-robin by linear id u * np + x; rot_x
+  // rotates each unit's chunk numbers by the unit index (see run_decode).
   const int u = blockIdx.y;
-  const int x = blockIdx.x;
+  int x = (int)blockIdx.x + (a.rot_x ? u % a.np : 0);
+  x = x >= a.np ? x - a.np : x;
   const int b = u / a.units_per_b;
   const int r_in_b = u - b * a.units_per_b;
   const int kv = r_in_b / a.spk;
@@ -1151,6 +1154,20 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   a.units_per_b = (int32_t)(p.units / c.B);
   a.wg_vis = p.wg_vis;
   a.np = p.wg_vis + p.wg_full;
+  // XCD balance.  Workgroup u * np + x runs on XCD (u * np + x) mod 8, so
+  // with g = gcd(np, 8) > 1 chunk x of every unit lands on the XCDs
+  // congruent to x mod g.  When the visual chunks do not split evenly over
+  // those classes, some XCDs get the small prompt/text chunks and less of
+  // the visual stream (np = 8: all prompt/text chunks on XCD 7).  Rotating
+  // each unit's chunk numbers by u spreads them.  Measured on MI355X:
+  // B=32 with 8 KV heads of 4 query heads 219.8 -> 208.7 us, config 3
+  // 112.7 -> 110.0 us.  The rotation is not applied where nothing aliases:
+  // there it measured 0.6-2.4 % slower (configs 2 and 4).
+  {
+    int gx = 8;
+    while (a.np % gx != 0) gx >>= 1;
+    a.rot_x = gx > 1 && p.wg_vis % gx != 0 ? 1 : 0;
+  }
   a.scale_log2 = (float)(rk::kLog2e / sqrt(128.0));
   const dim3 grid((unsigned)a.np, (unsigned)p.units);
   const int hmax = p.heads_per_unit > 1 ? 16 : 1;
