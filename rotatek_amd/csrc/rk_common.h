@@ -33,6 +33,12 @@ struct F16 {
   static __device__ __forceinline__ uint16_t from_f32(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);
   }
+  // (lo, hi) rounded to nearest even and packed into one dword
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, h2));
+  }
   static __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -54,6 +60,12 @@ struct BF16 {
   // round to nearest even (v_cvt_pk_bf16_f32 on gfx950)
   static __device__ __forceinline__ uint16_t from_f32(float x) {
     return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  // (lo, hi) rounded to nearest even and packed into one dword
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
   }
   static __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),

@@ -180,22 +180,26 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
     uint4 rows[8];
 #pragma unroll
     for (int r = 0; r < 8; ++r) rows[r] = ldrow<VEC>(base, k, min((uint32_t)(tb + r), last), 8u * n);
-    // centre in fp32, round to the key dtype; rows past the end are zero
-    uint16_t cb[8][8];
+    // Centre in fp32 and round to the key dtype, two tokens of one channel
+    // per conversion, which is already the transposed operand word:
+    // op[i] element r = Kc[token 8g + r][channel 8n + i].  Rows past the end
+    // (clamped loads) are masked to zero after the conversion: a select
+    // around the conversion itself compiled to one branch per element.
+    const int64_t left = t1 - tb;
+    const int nvalid = left >= 8 ? 8 : (left > 0 ? (int)left : 0);
+    uint32_t w[8][4];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      float f[8];
-      unpack8<TT>(rows[r], f);
-      const bool ok = tb + r < t1;
+    for (int rp = 0; rp < 4; ++rp) {
+      float f0[8], f1[8];
+      unpack8<TT>(rows[2 * rp], f0);
+      unpack8<TT>(rows[2 * rp + 1], f1);
+      const uint32_t keep = (2 * rp < nvalid ? 0xffffu : 0u) | (2 * rp + 1 < nvalid ? 0xffff0000u : 0u);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) cb[r][e] = ok ? TT::from_f32(f[e] - cen[e]) : (uint16_t)0;
+      for (int i = 0; i < 8; ++i) w[i][rp] = TT::pack2(f0[i] - cen[i], f1[i] - cen[i]) & keep;
     }
-    // transpose: op[i] element r = Kc[token 8g + r][channel 8n + i]
     uint4 op[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      op[i] = make_uint4(cb[0][i] | ((uint32_t)cb[1][i] << 16), cb[2][i] | ((uint32_t)cb[3][i] << 16),
-                         cb[4][i] | ((uint32_t)cb[5][i] << 16), cb[6][i] | ((uint32_t)cb[7][i] << 16));
+    for (int i = 0; i < 8; ++i) op[i] = make_uint4(w[i][0], w[i][1], w[i][2], w[i][3]);
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) acc[t] = TT::mfma(op[tile_row(t)], op[tile_col(t)], acc[t]);
   }
