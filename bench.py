@@ -461,7 +461,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2")
-    ap.add_argument("--family", default="paper", choices=["paper", "gqa"])
+    ap.add_argument("--family", default="paper", choices=["paper", "gqa"],
+                    help="decode family (default: gqa when G > 1, else paper)")
     ap.add_argument("--seqlen", type=int, default=0,
                     help="override the visual span length (kernel_profile.py's --seqlen)")
     ap.add_argument("--batch-size", type=int, default=0,
@@ -518,6 +519,10 @@ def main():
     copies = 1 if nbytes >= (1 << 30) else min(8, -(-(1 << 30) // nbytes))
     sets = [inp] + [synth.clone_inputs(inp) for _ in range(copies - 1)]
     dsets = [synth.decode_args(x) for x in sets]
+    # default family: gqa when query heads share a KV head (the per-query-head
+    # paper decomposition re-reads K/V G times), paper otherwise (identical)
+    if not args.family_given:
+        args.family = "gqa" if cfg.G > 1 else "paper"
     rot = rotatek_decode_gqa if args.family == "gqa" else rotatek_decode_fused
     dense = full_channel_decode_gqa if args.family == "gqa" else full_channel_decode
     turn = [0, 0]
