@@ -98,3 +98,52 @@ def test_kernel_family_from_environment(value, want):
     else:
         assert r.returncode == 0, r.stderr
         assert r.stdout.strip() == want
+
+
+def _decode_args(**over):
+    """CPU tensors shaped like a valid decode call (B=1, H_q=4, H_kv=2, Dk=8);
+    the guards run before anything touches the device."""
+    import torch
+    a = dict(q_full=torch.zeros(1, 4, 128), R_partial=torch.zeros(1, 2, 128, 8), delta_mu=torch.zeros(1, 2, 128),
+             k_full=torch.zeros(1, 2, 5, 128), v_full=torch.zeros(1, 2, 5, 128),
+             mask_full=torch.ones(1, 5, dtype=torch.uint8), k_sparse=torch.zeros(1, 2, 7, 8),
+             v_sparse=torch.zeros(1, 2, 7, 128), num_kv_groups=2)
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("over", [
+    dict(q_full="rank2"),                 # q_full not [B, H_q, D]       (fused_decode.py:323-324)
+    dict(R_partial="rank3"),              # R_partial not rank 4         (fused_decode.py:325-326)
+    dict(mask_full="bool"),               # mask not uint8               (fused_decode.py:327-328)
+    dict(num_kv_groups=3),                # H_q / G != H_kv              (fused_decode.py:335-338)
+])
+@pytest.mark.parametrize("family", ["paper", "gqa"])
+def test_rotatek_decode_guards_are_value_errors(over, family):
+    import torch
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
+    fn = rotatek_decode_fused if family == "paper" else rotatek_decode_gqa
+    bad = {"rank2": torch.zeros(4, 128), "rank3": torch.zeros(1, 2, 128), "bool": torch.ones(1, 5, dtype=torch.bool)}
+    over = {k: bad.get(v, v) if isinstance(v, str) else v for k, v in over.items()}
+    with pytest.raises(ValueError):
+        fn(**_decode_args(**over))
+
+
+@pytest.mark.parametrize("q_shape,kv_dim", [((4, 128), 128), ((1, 4, 128), 64)])
+def test_full_channel_decode_guards_are_value_errors(q_shape, kv_dim):
+    """q rank != 3 or a K/V head size other than q's (full_channel_flash_decoding.py:173-178)."""
+    import torch
+    from rotatek_amd.kernels.full_channel_flash_decoding import full_channel_decode
+    q = torch.zeros(*q_shape)
+    k = torch.zeros(1, 4, 9, kv_dim)
+    with pytest.raises(ValueError):
+        full_channel_decode(q=q, k=k, v=k, num_kv_groups=1)
+
+
+def test_decode_on_host_tensors_fails_loudly():
+    """Well-formed host tensors are not silently computed on the CPU: the
+    HIP kernels are the only implementation."""
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    with pytest.raises(RuntimeError):
+        rotatek_decode_fused(**_decode_args())
