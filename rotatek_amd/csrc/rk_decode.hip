@@ -83,6 +83,10 @@ struct DecodeArgs {
   // within-head strides (elements); a head's span is < 2^31 elements
   uint32_t kf_ss, kf_sd, vf_ss, vf_sd, ks_ss, ks_sd, vs_ss, vs_sd;
   int32_t G, Dk, hpu, spk, units_per_b, wg_vis, np, rot_x;
+  // xgroup > 1 (one unit per query head, G query heads per KV head): the
+  // units of a KV head that read the same chunk run in consecutive slots of
+  // one XCD (see decode_kernel); units = B * H_q
+  int32_t xgroup, units;
   int32_t r_dtype, dm_dtype, has_bias, has_mask;
   // prologue layouts: q rows contiguous and 16-byte aligned (one 16-byte load
   // per thread); R a contiguous, 16-byte aligned [128][Dk] 16-bit block
@@ -335,7 +339,10 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
 
 // APPEND: fused append of k_new / v_new (span cache decode step); a
 // separate instantiation so the plain decode carries none of its registers.
-template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND>
+// NTL: V rows and compact visual Key rows use non-temporal loads (false for
+// the grouped one-unit-per-query-head mode, whose G units of a KV head read
+// each line through one XCD's L2).
+template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND, bool NTL = true>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const DecodeArgs a) {
   constexpr int DKP = DKB * 32;
@@ -359,9 +366,24 @@ decode_kernel(const DecodeArgs a) {
   const int nq = n < HMAX ? n : 0;  // LDS row for this lane's head column
   // Workgroups go to the 8 XCDs round-robin by linear id u * np + x; rot_x
   // rotates each unit's chunk numbers by the unit index (see run_decode).
-  const int u = blockIdx.y;
+  int u = blockIdx.y;
   int x = (int)blockIdx.x + (a.rot_x ? u % a.np : 0);
   x = x >= a.np ? x - a.np : x;
+  if (a.xgroup > 1) {
+    // Workgroup id i = y * np + x runs on XCD i mod 8 as the (i / 8)-th of
+    // that XCD.  Each XCD takes a contiguous range of the work items
+    // ((b, kv) major, then chunk, then the query head j of the group), so
+    // the G units that read one K/V chunk are neighbours on one XCD and
+    // share its L2 instead of each fetching the chunk from HBM.
+    const int64_t N = (int64_t)a.units * a.np, bid = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
+    const int64_t c = bid & 7, q8 = N >> 3, r8 = N & 7;
+    const int64_t item = c * q8 + min(c, r8) + (bid >> 3);
+    const int64_t grp = item / a.xgroup;  // (b, kv, chunk)
+    const int j = (int)(item - grp * a.xgroup);
+    const int64_t ukv = grp / a.np;
+    x = (int)(grp - ukv * a.np);
+    u = (int)(ukv * a.xgroup + j);
+  }
   const int b = u / a.units_per_b;
   const int r_in_b = u - b * a.units_per_b;
   const int kv = r_in_b / a.spk;
@@ -408,7 +430,9 @@ decode_kernel(const DecodeArgs a) {
   for (int j = 0; j < 8; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   // A-operand token row of this lane inside a block, per score sub-block
   const uint32_t krow0 = 8 * (n >> 2) + (n & 3), krow1 = krow0 + 4;
-  const uint32_t rot_seed = ((uint32_t)u * 0x9E3779B1u) ^ ((uint32_t)x * 0x85EBCA77u);
+  // the units of one KV head visit a chunk's blocks in the same order
+  const uint32_t useed = a.xgroup > 1 ? (uint32_t)(u / a.xgroup) : (uint32_t)u;
+  const uint32_t rot_seed = (useed * 0x9E3779B1u) ^ ((uint32_t)x * 0x85EBCA77u);
 
   // Prologue order: the first NBUF K/V blocks are requested, then the
   // prologue's own loads (q rows; R / delta_mu or the mask bytes), and only
@@ -483,12 +507,12 @@ decode_kernel(const DecodeArgs a) {
       const uint32_t r0 = min(t0 + krow0, t_last) * a.ks_ss, r1 = min(t0 + krow1, t_last) * a.ks_ss;
 #pragma unroll
       for (int kb = 0; kb < DKB; ++kb) {
-        B.k[0][kb] = load_row8<VEC, DKB == 1>(ksb, r0, kch[kb], a.ks_sd, knv[kb]);
-        B.k[1][kb] = load_row8<VEC, DKB == 1>(ksb, r1, kch[kb], a.ks_sd, knv[kb]);
+        B.k[0][kb] = load_row8<VEC, NTL && DKB == 1>(ksb, r0, kch[kb], a.ks_sd, knv[kb]);
+        B.k[1][kb] = load_row8<VEC, NTL && DKB == 1>(ksb, r1, kch[kb], a.ks_sd, knv[kb]);
       }
 #pragma unroll
       for (int r = 0; r < 8; ++r)
-        B.v[r] = load_row8<VEC>(vsb, min(t0 + 8u * g + r, t_last) * a.vs_ss, vch, a.vs_sd, 8);
+        B.v[r] = load_row8<VEC, NTL>(vsb, min(t0 + 8u * g + r, t_last) * a.vs_ss, vch, a.vs_sd, 8);
     };
 
     // q R: thread (c, part) loads R[part*L .. part*L+L-1][c], forms partial
@@ -626,7 +650,7 @@ decode_kernel(const DecodeArgs a) {
       for (int r = 0; r < 8; ++r) {
         uint32_t row = min(t0 + 8u * g + r, t_last);
         row += row >= a.vf_gap_at ? a.vf_gap : 0u;
-        B.v[r] = load_row8<VEC>(vfb, row * a.vf_ss, vch, a.vf_sd, 8);
+        B.v[r] = load_row8<VEC, NTL>(vfb, row * a.vf_ss, vch, a.vf_sd, 8);
       }
     };
 
@@ -988,15 +1012,26 @@ int resolve_cus(int32_t num_cus, int* st) {
 
 template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
 hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
-  bool appended = false;
-  if constexpr (HAS_VIS) {  // the span cache's step always carries the visual span
-    if (a.k_new) {
-      hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, true, true>), grid, dim3(rk::kThreads), 0,
-                         s, a);
-      appended = true;
+  bool launched = false;
+  if constexpr (VEC && HMAX == 1) {  // grouped one-unit-per-query-head mode: temporal loads
+    if (a.xgroup > 1) {
+      if (HAS_VIS && a.k_new)
+        hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, HAS_VIS, false>), grid,
+                           dim3(rk::kThreads), 0, s, a);
+      else
+        hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false>), grid,
+                           dim3(rk::kThreads), 0, s, a);
+      launched = true;
     }
   }
-  if (!appended)
+  if constexpr (HAS_VIS) {  // the span cache's step always carries the visual span
+    if (!launched && a.k_new) {
+      hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, true, true>), grid, dim3(rk::kThreads), 0,
+                         s, a);
+      launched = true;
+    }
+  }
+  if (!launched)
     hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false>), grid, dim3(rk::kThreads), 0,
                        s, a);
   hipError_t e = hipGetLastError();
@@ -1168,6 +1203,9 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     while (a.np % gx != 0) gx >>= 1;
     a.rot_x = gx > 1 && p.wg_vis % gx != 0 ? 1 : 0;
   }
+  a.units = (int32_t)p.units;
+  a.xgroup = policy == RK_POLICY_PAPER && c.G > 1 ? (int32_t)c.G : 0;
+  if (a.xgroup) a.rot_x = 0;
   a.scale_log2 = (float)(rk::kLog2e / sqrt(128.0));
   const dim3 grid((unsigned)a.np, (unsigned)p.units);
   const int hmax = p.heads_per_unit > 1 ? 16 : 1;
