@@ -369,7 +369,7 @@ decode_kernel(const DecodeArgs a) {
   int u = blockIdx.y;
   int x = (int)blockIdx.x + (a.rot_x ? u % a.np : 0);
   x = x >= a.np ? x - a.np : x;
-  if (a.xgroup > 1) {
+  if (!NTL && a.xgroup > 1) {  // compiled into the grouped mode's instantiation only
     // Workgroup id i = y * np + x runs on XCD i mod 8 as the (i / 8)-th of
     // that XCD.  Each XCD takes a contiguous range of the work items
     // ((b, kv) major, then chunk, then the query head j of the group), so
@@ -431,7 +431,7 @@ decode_kernel(const DecodeArgs a) {
   // A-operand token row of this lane inside a block, per score sub-block
   const uint32_t krow0 = 8 * (n >> 2) + (n & 3), krow1 = krow0 + 4;
   // the units of one KV head visit a chunk's blocks in the same order
-  const uint32_t useed = a.xgroup > 1 ? (uint32_t)(u / a.xgroup) : (uint32_t)u;
+  const uint32_t useed = !NTL && a.xgroup > 1 ? (uint32_t)(u / a.xgroup) : (uint32_t)u;
   const uint32_t rot_seed = (useed * 0x9E3779B1u) ^ ((uint32_t)x * 0x85EBCA77u);
 
   // Prologue order: the first NBUF K/V blocks are requested, then the
