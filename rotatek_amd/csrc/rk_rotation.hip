@@ -5,14 +5,19 @@
 // Per iteration, as the reference:
 //   W = C V;  G = W^T W;  G += eps * mean(diag G) * I;  G = L L^T;  V = W L^-T
 // One 256-thread workgroup owns one matrix and keeps everything in LDS
-// (C 128 x 132, V/W 128 x (KP+4), G/L KP x (KP+1), (L^-1)^T 64 x (KP+4):
-// 136 KB at KP = 64).  The three products run on v_mfma_f32_16x16x4_f32:
+// (C 128 x 132, V/W 128 x (KP+4), G KP x (KP+1), L KP x KP, (L^-1)^T
+// KP x (KP+4), 4 KB scratch: 153 KB at KP = 64).  The three products run on v_mfma_f32_16x16x4_f32:
 //   W = C V            8 x KP/16 tiles of 16 x 16 over the four waves
 //   G = W^T W          (KP/16)^2 tiles
-//   Cholesky + L^-1    wave 0 in one pass: lane i holds row i of G, column
-//                      j of L goes through LDS and serves both the row
-//                      updates and step j of the substitution L x = e_c
-//                      that lane c runs for column c of L^-1
+//   Cholesky + L^-1    KP <= 32: one pass in wave 0 (lane i holds row i of
+//                      G; column j of L goes through LDS and serves both
+//                      the row updates and step j of the substitution
+//                      L x = e_c that lane c runs for column c of L^-1).
+//                      KP = 64: 16-column panels, each factored in wave 0
+//                      with its diagonal block of L^-1; the trailing update
+//                      of G and the blocks of L^-1 below the diagonal run
+//                      on the MFMA over all waves (141.7 -> 100.5 us for 32
+//                      matrices at k = 64; no gain at k <= 32)
 //   V = W (L^-1)^T     8 x KP/16 tiles
 // Padding columns of V are zero, so their rows and columns of G are too: a
 // unit diagonal there makes that block the identity, and V keeps them zero.
@@ -33,7 +38,7 @@ typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
 constexpr int kD = 128;
 constexpr int kThreads = 256;
 constexpr int kCPad = kD + 4;  // C row stride: 16-byte reads of rows n = 0..15 cover all 64 banks
-constexpr int kLook = 3;       // Cholesky: column entries passed by readlane ahead of the LDS broadcast
+constexpr int kLook = 3;       // single-pass Cholesky: column entries passed by readlane ahead of the LDS broadcast
 
 // D = A B + D on v_mfma_f32_16x16x4_f32 (A 16x4, B 4x16): lane (g, n) supplies
 // A[n][g] and B[g][n] and holds D[4g + i][n], i = 0..3.
@@ -63,11 +68,19 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
   constexpr int TPW = 8 * NTJ / 4;  // 16 x 16 tiles of W per wave
   constexpr int NG = NTJ * NTJ;     // 16 x 16 tiles of G
   constexpr int TPG = NG >= 4 ? NG / 4 : 1;
+  constexpr int NP16 = KP / 16;     // Cholesky panels
   __shared__ __align__(16) float sC[kD * kCPad];
   __shared__ __align__(16) float sV[kD * SP];
   // G, then L by columns; the tail takes the idle lanes' last column writes
+  // G (the single-pass path rewrites it as L by columns; its tail takes the
+  // idle lanes' last column writes)
   __shared__ __align__(16) float sG[KP * GP > KP * KP + 64 ? KP * GP : KP * KP + 64];
-  __shared__ float sLt[64 * LP];  // rows >= KP: scratch for the idle lanes of wave 0
+  // blocked path: L by columns, sLc[j * KP + m] = L_mj (1 / L_jj on the diagonal)
+  __shared__ __align__(16) float sLc[KP > 32 ? KP * KP : 1];
+  // X = L^-1 transposed, sLt[c * LP + i] = X[i][c]; rows >= KP: scratch for
+  // the single-pass path's idle lanes
+  __shared__ float sLt[64 * LP];
+  __shared__ float sT[KP > 32 ? 4 * 256 : 1];  // blocked path: per-wave 16 x 16 product scratch
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
   const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
@@ -106,6 +119,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
       sV[r * SP + (e - r * KP)] = v[i];
     }
   }
+  for (int e = tid; e < 64 * LP; e += kThreads) sLt[e] = 0.f;  // X's upper blocks are never written
   __syncthreads();
 
   // Wave w owns the 16 x 16 output tiles w, w + 4, w + 8, ... of each
@@ -123,6 +137,8 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     lds_f32* const lV = opaque_lds(sV);
     lds_f32* const lG = opaque_lds(sG);
     lds_f32* const lLt = opaque_lds(sLt);
+    lds_f32* const lLc = opaque_lds(sLc);
+    lds_f32* const lT = opaque_lds(sT);
 
     // ---- W = C V on the MFMA.  In the four MFMA steps of k-group q, lane
     // (g, n) supplies k = 16q + 4g + r, r = 0..3 (any assignment of k to
@@ -190,6 +206,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     }
     __syncthreads();
 
+    if constexpr (KP <= 32) {
     // ---- ridge, Cholesky G = L L^T and L^-1, one pass in wave 0.
     // Lane i holds row i of G.  Step j takes the pivot from lane j, scales
     // column j by r_j = 1/sqrt(pivot) and publishes it to LDS (column j of
@@ -278,6 +295,126 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
       for (int i = 0; i < KP; ++i) px[i] = x[i];
     }
     __syncthreads();
+    } else {
+    // ---- ridge: G += eps * mean(diag G) * I (wave 0); the padding rows
+    // and columns of G are zero (V's padding columns are): a unit diagonal
+    // there makes them the identity
+    if (wave == 0) {
+      const int lr = min(lane, KP - 1);
+      const float dii = lG[lr * GP + lr];
+      float dg = lane < k ? dii : 0.f;
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) dg += shfl_xor(dg, off);
+      const float ridge = eps * (dg / (float)k);
+      if (lane < KP) lG[lane * GP + lane] = lane < k ? dii + ridge : 1.f;
+    }
+    __syncthreads();
+
+    // ---- blocked Cholesky G = L L^T and X = L^-1, 16-column panels.
+    // Panel p: wave 0 factors columns 16p..16p+15 (lane i holds those
+    // entries of row i; the entries of column j that the panel's later
+    // columns need come lane to lane by readlane), writes them to sLc by
+    // columns (r_j = 1 / L_jj on the diagonal) and, in lanes 16p..16p+15,
+    // the diagonal block of X by forward substitution.  All waves then
+    // subtract the panel's product from the trailing lower tiles of G on
+    // the MFMA.  Afterwards X's blocks below the diagonal follow by block
+    // rows: X_qr = -X_qq (sum_{s=r}^{q-1} L_qs X_sr), two 16 x 16 MFMA
+    // products per tile.  X goes to sLt transposed (row c = column c of X,
+    // the layout the solve below reads); its upper blocks stay zero.
+#pragma unroll
+    for (int p = 0; p < NP16; ++p) {
+      const int P0 = 16 * p;
+      if (wave == 0) {
+        const int lr = min(lane, KP - 1);  // lanes >= KP work on a copy of row KP-1 and store nothing
+        const lds_f32* prow = lG + lr * GP + P0;
+        float a[16], xv[16], lc[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          a[c] = prow[c];
+          xv[c] = lane == P0 + c ? 1.f : 0.f;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          const int j = P0 + jj;
+          const float piv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a[jj]), j));
+          const float rj = __builtin_amdgcn_rsqf(piv);
+          const float lij = lane > j ? a[jj] * rj : (lane == j ? rj : 0.f);
+          lc[jj] = lij;
+          xv[jj] *= rj;
+#pragma unroll
+          for (int mm = jj + 1; mm < 16; ++mm) {
+            const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lij), P0 + mm));
+            a[mm] = fmaf(-lij, c, a[mm]);
+            xv[mm] = fmaf(-c, xv[jj], xv[mm]);
+          }
+        }
+        if (lane < KP) {
+#pragma unroll
+          for (int jj = 0; jj < 16; ++jj) lLc[(P0 + jj) * KP + lane] = lc[jj];
+        }
+        if (lane >= P0 && lane < P0 + 16) {
+#pragma unroll
+          for (int mm = 0; mm < 16; ++mm) lLt[lane * LP + P0 + mm] = xv[mm];
+        }
+      }
+      __syncthreads();
+      if (p + 1 < NP16) {
+        // G[16 ti + a][16 tj + b] -= sum_c L[16 ti + a][P0 + c] L[16 tj + b][P0 + c]
+        // over the lower tiles p < tj <= ti < NP16, tile t to wave t mod 4
+        int t = 0;
+#pragma unroll
+        for (int ti = p + 1; ti < NP16; ++ti) {
+#pragma unroll
+          for (int tj = p + 1; tj <= ti; ++tj, ++t) {
+            if (t % 4 == wave) {  // wave-uniform
+              f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int st = 0; st < 4; ++st) {
+                const int cc = P0 + 4 * st + g;
+                acc = mfma4(lLc[cc * KP + 16 * ti + n], lLc[cc * KP + 16 * tj + n], acc);
+              }
+              lds_f32* pg = lG + (16 * ti + 4 * g) * GP + 16 * tj + n;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) pg[i * GP] -= acc[i];
+            }
+          }
+        }
+        __syncthreads();
+      }
+    }
+#pragma unroll
+    for (int q = 1; q < NP16; ++q) {
+      if (wave < q) {  // tile (q, r = wave)
+        const int r = wave;
+        f32x4 tacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < NP16 - 1; ++s) {
+          if (s >= r && s < q) {  // wave-uniform
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+              const int kk = 16 * s + 4 * st + g;
+              tacc = mfma4(lLc[kk * KP + 16 * q + n], lLt[(16 * r + n) * LP + kk], tacc);
+            }
+          }
+        }
+        lds_f32* pt = lT + wave * 256;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pt[(4 * g + i) * 16 + n] = tacc[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        f32x4 xacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int kk = 4 * st + g;
+          xacc = mfma4(lLt[(16 * q + kk) * LP + 16 * q + n], pt[kk * 16 + n], xacc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lLt[(16 * r + n) * LP + 16 * q + 4 * g + i] = -xacc[i];
+      }
+      __syncthreads();
+    }
+    }
 
     // ---- V = W (L^-1)^T on the MFMA: V[r][j] = sum_m W[r][m] (L^-1)^T[m][j],
     // k assigned as in C V, so one 16-byte read of W's row feeds four steps
