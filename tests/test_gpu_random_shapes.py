@@ -1,0 +1,76 @@
+"""Seeded random decode shapes against the CPU oracle.
+
+The grid planner, the per-unit chunk rotation (XCD balance) and the grouped
+one-unit-per-query-head mapping all depend on the shape: (B, H_q, H_kv,
+D_keep, S_v, S_f) decide the workgroups per unit, whether chunk numbers are
+rotated, and which workgroup ids carry which (unit, chunk).  This test draws
+48 shapes with a fixed seed over both families and both 16-bit dtypes,
+including odd and empty spans, G up to 20 and D_keep from 8 to 128, and
+checks every output against the float64 oracle at the north-star bars
+(max-abs 2e-3 fp16, 1e-2 bf16).  Every case prints its parameters first.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import decode as od
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}
+D = 128
+
+
+def _cases(n=48, seed=2024):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 1, 2, 4, 7, 8, 16, 20]))
+        B = int(rng.choice([1, 2, 3, 5]))
+        dk = int(rng.choice([8, 16, 24, 32, 32, 40, 64, 128]))
+        S_v = int(rng.choice([0, 1, 63, 129, 777, 2049, 4097, 9001]))
+        S_f = int(rng.choice([0, 1, 17, 80, 300, 1025]))
+        if S_v + S_f == 0:
+            S_f = 5
+        dtype = torch.float16 if rng.random() < 0.5 else torch.bfloat16
+        family = "paper" if rng.random() < 0.5 else "gqa"
+        mask_p = float(rng.choice([0.0, 0.0, 0.3]))
+        out.append((i, B, hkv * G, hkv, dk, S_v, S_f, dtype, family, mask_p))
+    return out
+
+
+CASES = _cases()
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{c[0]}" for c in CASES])
+def test_random_shape_matches_oracle(case):
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
+    i, B, Hq, Hkv, dk, S_v, S_f, dtype, family, mask_p = case
+    print(f"[case] {case}", flush=True)
+    sys.stdout.flush()
+    g = torch.Generator(device="cuda").manual_seed(1000 + i)
+
+    def rn(*s, scale=1.0):
+        return (torch.randn(*s, generator=g, device="cuda") * scale).to(dtype)
+
+    R = torch.linalg.qr(torch.randn(B, Hkv, D, D, generator=g, device="cuda"))[0][..., :dk].contiguous().to(dtype)
+    V = rn(B, Hkv, S_v + S_f, D)
+    mask = (torch.rand(B, S_f, generator=g, device="cuda") >= mask_p).to(torch.uint8)
+    inp = dict(q_full=rn(B, Hq, D), R_partial=R, delta_mu=rn(B, Hkv, D, scale=0.5), k_full=rn(B, Hkv, S_f, D),
+               v_full=V[:, :, S_v:], mask_full=mask, k_sparse=rn(B, Hkv, S_v, dk, scale=2.0),
+               v_sparse=V[:, :, :S_v], num_kv_groups=Hq // Hkv)
+    fn = rotatek_decode_gqa if family == "gqa" else rotatek_decode_fused
+    out = fn(**inp)[0]
+    torch.cuda.synchronize()
+    a = {k: (v.detach().float().cpu().numpy().astype(np.float64) if torch.is_tensor(v) else v)
+         for k, v in inp.items()}
+    want = od.rotatek_decode(a["q_full"], a["R_partial"], a["delta_mu"], a["k_full"], a["v_full"],
+                             a["mask_full"], a["k_sparse"], a["v_sparse"], a["num_kv_groups"])
+    got = out.float().cpu().numpy().astype(np.float64)
+    assert got.shape == want.shape
+    err = float(np.nanmax(np.abs(got - want))) if got.size else 0.0
+    assert np.isfinite(got).all() and err <= TOL[dtype], (case, err)
