@@ -361,3 +361,31 @@ def test_recover_validation():
     assert lib.rk_channel_selection(r(tm), r(_t((B, H, 128, 0), _lib.RK_F32)), None) == _lib.RK_ERR_KEEP_DIM
     assert lib.rk_channel_selection(r(tm), r(_t((B, H, 64, Dk), _lib.RK_F32)), None) == _lib.RK_ERR_HEAD_DIM
     assert lib.rk_channel_selection(r(sm), r(sel), None) == _lib.RK_ERR_RANK
+
+
+def test_plan_small_span_does_not_starve_the_other():
+    """A prompt/text span too small for a workgroup of its own still gets
+    one, but at two slots per unit it must not leave the visual span a
+    single workgroup (the reference kernel-benchmark shape: B=32, 8 KV heads
+    of 4 query heads, 16000 visual + 80 prompt/text tokens)."""
+    p = _lib.plan_decode(32, 32, 8, 32, 16000, 80, policy=1)
+    assert p["wg_full"] == 1 and p["wg_vis"] >= 2
+
+
+def test_plan_gives_every_unit_several_workgroups():
+    """With many units the planner adds rounds so each unit streams through
+    at least 8 workgroups (while a workgroup keeps >= 64 KB)."""
+    p = _lib.plan_decode(32, 32, 8, 32, 16000, 80, policy=1)
+    assert p["wg_vis"] + p["wg_full"] >= 8
+    # a small problem keeps its workgroups above the minimum size instead
+    q = _lib.plan_decode(1, 4, 4, 32, 300, 50, policy=1)
+    assert q["wg_vis"] + q["wg_full"] <= 4
+
+
+def test_plan_keeps_one_round_when_the_extra_slot_saves_little():
+    """Config 4 layer (B=8, 4 KV heads of 7, 12001 visual + 61 prompt/text,
+    256 CUs): giving the visual span its full share would overflow the
+    single round by 32 workgroups for a 6 % shorter workgroup, so the grid
+    stays within 2 x 256 slots."""
+    p = _lib.plan_decode(8, 28, 4, 32, 12001, 61, policy=1)
+    assert p["grid"] <= 2 * 256
