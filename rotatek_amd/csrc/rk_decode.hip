@@ -769,11 +769,12 @@ decode_kernel(const DecodeArgs a) {
 
 }
 
-// Second launch: one wave per (unit, head) row, four rows per workgroup.
+// Second launch: one wave per (unit, head) row, one row per workgroup, so
+// a small decode's rows spread over as many CUs as there are rows.
 template <class TT>
-__global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a, int64_t rows) {
+__global__ void __launch_bounds__(64) merge_kernel(const DecodeArgs a, int64_t rows) {
   const int tid = threadIdx.x;
-  const int64_t row = (int64_t)blockIdx.x * kWaves + (tid >> 6);
+  const int64_t row = blockIdx.x;
   if (row >= rows) return;
   const int64_t u = row / a.hpu;
   const int h = (int)(row - u * a.hpu);
@@ -1037,8 +1038,7 @@ hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)grid.y * a.hpu;
-  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)((rows + rk::kWaves - 1) / rk::kWaves)),
-                     dim3(rk::kThreads), 0, s, a, rows);
+  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)rows), dim3(64), 0, s, a, rows);
   return hipGetLastError();
 }
 
