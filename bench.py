@@ -467,6 +467,8 @@ def main():
                     help="override the visual span length (kernel_profile.py's --seqlen)")
     ap.add_argument("--batch-size", type=int, default=0,
                     help="override the batch (kernel_profile.py's --batch_size)")
+    ap.add_argument("--merge", default="auto", choices=["auto", "two", "one"],
+                    help="decode merge: by grid size (auto), two launches, or one launch")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -479,6 +481,9 @@ def main():
     args = ap.parse_args()
     args.steps_given = any(a == "--steps" or a.startswith("--steps=") for a in sys.argv[1:])
     args.family_given = any(a == "--family" or a.startswith("--family=") for a in sys.argv[1:])
+    if args.merge != "auto" and not args.pmc_summary:
+        from rotatek_amd import _lib
+        _lib.set_decode_merge({"two": _lib.MERGE_TWO_LAUNCHES, "one": _lib.MERGE_SINGLE_LAUNCH}[args.merge])
     if args.config == "cfg4":
         if args.gpus != 1:
             print("bench.py measures one GPU only", file=sys.stderr)

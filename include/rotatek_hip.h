@@ -115,10 +115,16 @@ int rk_device_cu_count(int device, int* status);
  * ones); k_sparse [B,H_kv,S_v,Dk]; v_sparse [B,H_kv,S_v,D]; out [B,H_q,D]
  * (dtype of q_full).  D must be 128.  q, K, V and out share one dtype
  * (F16 or BF16); R_partial and delta_mu may be F16, BF16 or F32.
- * The workspace (size from rk_rotatek_decode_check, 256-byte aligned, no
- * initialisation needed) holds the split partials; a step is two launches
- * on `stream` (split kernel, merge kernel) and is hipGraph-capturable.
- * Calls that overlap on one workspace race.
+ * The workspace (size from rk_rotatek_decode_check, 256-byte aligned) holds
+ * the split partials and, in its first RK_DECODE_TICKET_BYTES, the
+ * counters of the single-launch merge; pass a new workspace through
+ * rk_decode_workspace_init once before its first use (every call leaves
+ * the counters at zero again).  A step is one launch (small grids: the
+ * last workgroup of each unit merges) or two (split kernel, merge kernel)
+ * on `stream`, and is hipGraph-capturable.  Calls that overlap on one
+ * workspace race.  policy RK_POLICY_PAPER with num_kv_groups > 1 runs the
+ * grouped decomposition (each K/V tile read once per KV head; the result
+ * differs from one unit per query head only in fp32 summation order).
  */
 int rk_rotatek_decode_check(const rk_tensor* q_full, const rk_tensor* R_partial,
                             const rk_tensor* delta_mu, const rk_tensor* k_full,
@@ -200,6 +206,18 @@ int rk_full_channel_decode(const rk_tensor* q, const rk_tensor* k,
                            void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* Bytes at the start of a decode workspace that hold the single-launch
+ * merge's counters; rk_decode_workspace_init zeroes them (a kernel on
+ * `stream`, not a memset, so it may also be recorded in a graph). */
+#define RK_DECODE_TICKET_BYTES (256u * 1024u)
+int rk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+
+/* Merge of the decode entry points: 0 = by grid size (default: one launch
+ * when the grid fits two rounds of resident workgroups), 1 = always two
+ * launches, 2 = one launch whenever the counters fit.  Both merges give
+ * bit-identical results. */
+void rk_set_decode_merge(int32_t mode);
+
 /* Split plan the decode entry points use for a shape (host only), exposed
  * for tests and benchmarks.  Fields are filled on RK_OK. */
 typedef struct rk_decode_plan {
@@ -212,6 +230,7 @@ typedef struct rk_decode_plan {
   int64_t chunk_full;     /* prompt+text tokens per workgroup                */
   int64_t grid;           /* total workgroups launched                       */
   size_t workspace_bytes;
+  int32_t single_launch;  /* 1: the merge runs in the split launch           */
 } rk_decode_plan;
 
 int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,

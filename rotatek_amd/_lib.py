@@ -59,6 +59,7 @@ class RkDecodePlan(ctypes.Structure):
         ("chunk_full", ctypes.c_int64),
         ("grid", ctypes.c_int64),
         ("workspace_bytes", ctypes.c_size_t),
+        ("single_launch", ctypes.c_int32),
     ]
 
 
@@ -86,6 +87,8 @@ _SIGNATURES = {
     "rk_plan_decode": (ctypes.c_int, [ctypes.c_int64] * 6 + [ctypes.c_int32] * 3
                        + [ctypes.POINTER(RkDecodePlan)]),
     "rk_set_decode_tuning": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
+    "rk_set_decode_merge": (None, [ctypes.c_int32]),
+    "rk_decode_workspace_init": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rk_key_covariance_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
     "rk_key_covariance": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rk_rotate_keys": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p]),
@@ -177,18 +180,28 @@ def stream_handle(device: torch.device) -> int:
 
 # ---------------------------------------------------------------- workspace
 _WORKSPACE: dict = {}
+# Buffers a larger request replaced.  A captured HIP graph keeps the address
+# it was recorded with, so a replaced buffer is never handed back to the
+# allocator: graph replays keep writing memory that no other tensor owns.
+_RETIRED: list = []
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Decode workspace (split partials), cached per device and grown on
-    demand, so steady-state calls allocate nothing (it stays valid inside
-    captured HIP graphs once it has been allocated before capture).
-    Concurrent decodes on different streams of one device would share it
-    and must not overlap."""
+    demand, so steady-state calls allocate nothing.  A graph captured with
+    one buffer stays valid after a later call grows the workspace: the old
+    buffer is retired, not freed.  Concurrent decodes on different streams
+    of one device share it and must not overlap."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     buf = _WORKSPACE.get(idx)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=torch.device("cuda", idx))
+        if buf is not None:
+            _RETIRED.append(buf)
+        dev = torch.device("cuda", idx)
+        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        # the single-launch merge's counters start at zero (every call leaves them so)
+        check(load().rk_decode_workspace_init(buf.data_ptr(), buf.numel(), stream_handle(dev)),
+              "decode_workspace_init")
         _WORKSPACE[idx] = buf
     return buf
 
@@ -202,3 +215,13 @@ def plan_decode(B, H_q, H_kv, Dk, S_v, S_f, elem_bytes=2, policy=RK_POLICY_GQA, 
 
 def set_decode_tuning(min_bytes=0, max_bytes=0, wgs_per_cu=0):
     load().rk_set_decode_tuning(int(min_bytes), int(max_bytes), int(wgs_per_cu))
+
+
+MERGE_AUTO, MERGE_TWO_LAUNCHES, MERGE_SINGLE_LAUNCH = 0, 1, 2
+DECODE_TICKET_BYTES = 256 * 1024  # RK_DECODE_TICKET_BYTES
+
+
+def set_decode_merge(mode: int) -> None:
+    """Decode merge: MERGE_AUTO (one launch on grids of at most two rounds),
+    MERGE_TWO_LAUNCHES or MERGE_SINGLE_LAUNCH (bit-identical results)."""
+    load().rk_set_decode_merge(int(mode))

@@ -67,9 +67,14 @@ struct DecodeArgs {
   const uint16_t* ks;
   const uint16_t* vs;
   uint16_t* out;
-  float* part_m;
-  float* part_l;
-  float* part_acc;
+  // split partials: one record of kRecFloats per (unit, workgroup, head),
+  // acc[0..127], then m, l (each record on cache lines of its own)
+  float* part;
+  // single-launch merge: per-unit arrival tickets and, with a fused append,
+  // per-batch-row unit tickets; both zero between calls
+  uint32_t* ticket;
+  uint32_t* bticket;
+  int32_t fused;
   int64_t q_sb, q_sh, q_sd;
   int64_t R_sb, R_sh, R_sd, R_sk;
   int64_t dm_sb, dm_sh, dm_sd;
@@ -99,6 +104,7 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kBlk = 32;
 constexpr int kMaskChunk = 4096;  // max prompt+text tokens per workgroup
+constexpr int kRecFloats = 160;   // partial record: acc[128], m, l; 640 B = five 128-byte lines
 
 // Eight 16-bit elements of one row: channels chan..chan+7 (element index,
 // not yet scaled by the channel stride) at element offset `row_off` from a
@@ -258,72 +264,122 @@ struct FullBuf {
   uint4 v[8];
 };
 
-// Final merge of the np partials of one (unit, head) row:
+// ---- partial records and their merge
 //   out = sum_p acc_p 2^(m_p - M) / (sum_p l_p 2^(m_p - M) + 1e-6),
 //   M = max_p m_p                                  (fused_decode.py:275-296)
-// One wave per row.  Lane (sl, c8) = (lane >> 4, lane & 15) owns channels
-// 8 c8 .. 8 c8 + 7 and folds partials p = sl, sl + 4, ... (eight partials'
-// loads in flight at a time); the four slices are then combined across
-// lanes.  With a fused append the new token is already in partial 0 of the
-// unit; the row of query head 0 advances len_full[b] (a full buffer stays).
-template <class TT>
-__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int hq, int h,
-                                          int lane) {
-  const int sl = lane >> 4, c8 = lane & 15;
-  const int64_t base = u * a.np;
-  float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  auto fold = [&](const float* mm, const float* ll, const float4* v0, const float4* v1, int k) {
+// Record (u, x, h) of a unit's workgroup x and head h sits at
+// part + ((u * np + x) * hpu + h) * kRecFloats.
+
+// Channels 8 c8 .. 8 c8 + 7 of a record's acc, and its (m, l).  COH: relaxed
+// agent-scope atomic loads, which the single-launch merge uses to read
+// records written by workgroups on other XCDs in the same launch (each XCD
+// has its own L2; these loads are coherent across them).
+template <bool COH>
+__device__ __forceinline__ void load_rec(const float* rec, int c8, float (&v)[8], float& m, float& l) {
+  if constexpr (COH) {
+    const uint64_t* p = (const uint64_t*)(rec + 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v[2 * i] = __builtin_bit_cast(float, (uint32_t)w);
+      v[2 * i + 1] = __builtin_bit_cast(float, (uint32_t)(w >> 32));
+    }
+    const uint64_t w = __hip_atomic_load((const uint64_t*)(rec + 128), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    m = __builtin_bit_cast(float, (uint32_t)w);
+    l = __builtin_bit_cast(float, (uint32_t)(w >> 32));
+  } else {
+    const float4 s0 = ((const float4*)(rec + 8 * c8))[0], s1 = ((const float4*)(rec + 8 * c8))[1];
+    const float2 ml = *(const float2*)(rec + 128);
+    v[0] = s0.x; v[1] = s0.y; v[2] = s0.z; v[3] = s0.w;
+    v[4] = s1.x; v[5] = s1.y; v[6] = s1.z; v[7] = s1.w;
+    m = ml.x;
+    l = ml.y;
+  }
+}
+
+// Store of a workgroup's record slice (the lane's eight acc channels; m, l
+// by the c8 == 0 lane).  COH: relaxed agent-scope atomic stores, which
+// write through to memory, so that after the storing thread's wait for
+// their completion any XCD reads them.
+template <bool COH>
+__device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8], float M, float L) {
+  if constexpr (COH) {
+    uint64_t* p = (uint64_t*)(rec + 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __hip_atomic_store(p + i,
+                         (uint64_t)__builtin_bit_cast(uint32_t, A[2 * i]) |
+                             ((uint64_t)__builtin_bit_cast(uint32_t, A[2 * i + 1]) << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (c8 == 0)
+      __hip_atomic_store((uint64_t*)(rec + 128),
+                         (uint64_t)__builtin_bit_cast(uint32_t, M) |
+                             ((uint64_t)__builtin_bit_cast(uint32_t, L) << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    float4* dst = (float4*)(rec + 8 * c8);
+    dst[0] = make_float4(A[0], A[1], A[2], A[3]);
+    dst[1] = make_float4(A[4], A[5], A[6], A[7]);
+    if (c8 == 0) *(float2*)(rec + 128) = make_float2(M, L);
+  }
+}
+
+// Folds the records x = p0, p0 + step, ... < np of one (unit, head) into
+// (M, L, A) for channels 8 c8 .. 8 c8 + 7; `rec0` is the record of x = 0
+// and `rstride` the floats between consecutive x.  Eight records' loads are
+// issued together; entries past np are clamped in-bounds loads with weight
+// zero (a batch's first entry is always valid, so its max is finite).
+template <bool COH>
+__device__ __forceinline__ void fold_records(const float* rec0, int64_t rstride, int np, int p0, int step,
+                                             int c8, float& M, float& L, float (&A)[8]) {
+  for (int p = p0; p < np; p += 8 * step) {
+    float mm[8], ll[8], vv[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int q = p + step * i;
+      const bool ok = q < np;
+      load_rec<COH>(rec0 + (int64_t)(ok ? q : p) * rstride, c8, vv[i], mm[i], ll[i]);
+      if (!ok) {
+        mm[i] = -INFINITY;
+        ll[i] = 0.f;
+      }
+    }
     float mx = M;
-    for (int i = 0; i < k; ++i) mx = fmaxf(mx, mm[i]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, mm[i]);
     const float sc = fast_exp2(M - mx);
     L *= sc;
 #pragma unroll
     for (int e = 0; e < 8; ++e) A[e] *= sc;
-    for (int i = 0; i < k; ++i) {
-      const float w = fast_exp2(mm[i] - mx);
-      L += ll[i] * w;
-      A[0] += v0[i].x * w; A[1] += v0[i].y * w; A[2] += v0[i].z * w; A[3] += v0[i].w * w;
-      A[4] += v1[i].x * w; A[5] += v1[i].y * w; A[6] += v1[i].z * w; A[7] += v1[i].w * w;
-    }
-    M = mx;
-  };
-  // eight of this slice's partials per batch, loads issued together; entries
-  // past np are clamped in-bounds loads with weight zero (the batch's first
-  // entry is always valid, so its max is finite)
-  for (int p = sl; p < a.np; p += 32) {
-    float mm[8], ll[8];
-    float4 v0[8], v1[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int q = p + 4 * i;
-      const bool ok = q < a.np;
-      const int64_t pi = (base + (ok ? q : a.np - 1)) * a.hpu + h;
-      const float4* src = (const float4*)(a.part_acc + pi * 128 + 8 * c8);
-      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f), s0 = src[0], s1 = src[1];
-      mm[i] = ok ? a.part_m[pi] : -INFINITY;
-      ll[i] = ok ? a.part_l[pi] : 0.f;
-      v0[i] = ok ? s0 : z;
-      v1[i] = ok ? s1 : z;
+      const float w = fast_exp2(mm[i] - mx);
+      L += ll[i] * w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) A[e] += vv[i][e] * w;
     }
-    fold(mm, ll, v0, v1, 8);
+    M = mx;
   }
-  // combine the four slices (a slice without partials has M = -inf)
+}
+
+// (M, L, A) += (Mo, Lo, Ao) rescaled to the common max (either side may be
+// empty, M = -inf).
+__device__ __forceinline__ void combine(float& M, float& L, float (&A)[8], float Mo, float Lo,
+                                        const float (&Ao)[8]) {
+  const float Mx = fmaxf(M, Mo);
+  const float ws = M == -INFINITY ? 0.f : fast_exp2(M - Mx);
+  const float wo = Mo == -INFINITY ? 0.f : fast_exp2(Mo - Mx);
+  L = L * ws + Lo * wo;
 #pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-    const float Mo = shfl_xor(M, off), Lo = shfl_xor(L, off);
-    const float Mx = fmaxf(M, Mo);
-    const float ws = M == -INFINITY ? 0.f : fast_exp2(M - Mx);
-    const float wo = Mo == -INFINITY ? 0.f : fast_exp2(Mo - Mx);
-    L = L * ws + Lo * wo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) A[e] = A[e] * ws + shfl_xor(A[e], off) * wo;
-    M = Mx;
-  }
-  if (a.k_new && hq == 0 && lane == 0) {
-    const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
-    if (pos < a.S_f) a.len_full[b] = pos + 1;
-  }
-  if (sl != 0) return;
+  for (int e = 0; e < 8; ++e) A[e] = A[e] * ws + Ao[e] * wo;
+  M = Mx;
+}
+
+// acc / (l + 1e-6) in the output dtype, channels 8 c8 .. 8 c8 + 7 of (b, hq).
+template <class TT>
+__device__ __forceinline__ void write_out(const DecodeArgs& a, int b, int hq, int c8, float L,
+                                          const float (&A)[8]) {
   const float den = L + kDenomEps;
   uint16_t o[8];
 #pragma unroll
@@ -334,6 +390,80 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) dst[e * a.o_sd] = o[e];
+  }
+}
+
+// Second-launch merge of one (unit, head) row by one wave: lane (sl, c8) =
+// (lane >> 4, lane & 15) folds records x = sl, sl + 4, ...; the four slices
+// are then combined across lanes.  With a fused append the new token is
+// already in record 0 of the unit; the row of query head 0 advances
+// len_full[b] (a full buffer stays).
+template <class TT>
+__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int hq, int h,
+                                          int lane) {
+  const int sl = lane >> 4, c8 = lane & 15;
+  float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const float* rec0 = a.part + (u * a.np * a.hpu + h) * kRecFloats;
+  fold_records<false>(rec0, (int64_t)a.hpu * kRecFloats, a.np, sl, 4, c8, M, L, A);
+#pragma unroll
+  for (int off = 16; off <= 32; off <<= 1) {
+    float Ao[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Ao[e] = shfl_xor(A[e], off);
+    combine(M, L, A, shfl_xor(M, off), shfl_xor(L, off), Ao);
+  }
+  if (a.k_new && hq == 0 && lane == 0) {
+    const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
+    if (pos < a.S_f) a.len_full[b] = pos + 1;
+  }
+  if (sl != 0) return;
+  write_out<TT>(a, b, hq, c8, L, A);
+}
+
+// Single-launch merge, run by every workgroup after it has stored its
+// record.  The workgroup waits until its record stores have completed
+// (they write through to memory), then takes a ticket on the unit's
+// counter; the last of the unit's np workgroups resets the counter and
+// merges the unit's records, read with coherent loads, in the order of
+// merge_row (the result is bit-identical to the two-launch merge).  No
+// agent-scope release or acquire fence is needed, so no XCD L2 is written
+// back or invalidated.  With a fused append, the last unit of a batch row
+// to finish advances len_full[b] behind a second ticket: by then every
+// workgroup of the row has read it.  Both counters are left at zero.
+template <class TT, bool APPEND>
+__device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, int h0, int nh, int tid) {
+  __shared__ uint32_t s_ticket;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores have completed
+  __syncthreads();                // ... and so have every thread's
+  if (tid == 0)
+    s_ticket = __hip_atomic_fetch_add(a.ticket + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_ticket != (uint32_t)(a.np - 1)) return;
+  if (tid == 0) __hip_atomic_store(a.ticket + u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int lane = tid & 63, wave = tid >> 6, sl = lane >> 4, c8 = lane & 15;
+  const float* recu = a.part + (int64_t)u * a.np * a.hpu * kRecFloats;
+  for (int h = wave; h < nh; h += kWaves) {
+    float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    fold_records<true>(recu + (int64_t)h * kRecFloats, (int64_t)a.hpu * kRecFloats, a.np, sl, 4, c8, M, L, A);
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+      float Ao[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Ao[e] = shfl_xor(A[e], off);
+      combine(M, L, A, shfl_xor(M, off), shfl_xor(L, off), Ao);
+    }
+    if (sl == 0) write_out<TT>(a, b, h0 + h, c8, L, A);
+  }
+  if constexpr (APPEND) {
+    if (tid == 0) {
+      const uint32_t t = __hip_atomic_fetch_add(a.bticket + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t == (uint32_t)(a.units_per_b - 1)) {
+        __hip_atomic_store(a.bticket + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
+        if (pos < a.S_f) a.len_full[b] = pos + 1;
+      }
+    }
   }
 }
 
@@ -756,17 +886,14 @@ decode_kernel(const DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) A[e] += s_acc[w][h][8 * c8 + e] * wt;
       }
-      const int64_t pi = ((int64_t)u * a.np + x) * a.hpu + h;
-      if (c8 == 0) {
-        a.part_m[pi] = M;
-        a.part_l[pi] = L;
-      }
-      float4* dst = (float4*)(a.part_acc + pi * 128 + 8 * c8);
-      dst[0] = make_float4(A[0], A[1], A[2], A[3]);
-      dst[1] = make_float4(A[4], A[5], A[6], A[7]);
+      float* rec = a.part + (((int64_t)u * a.np + x) * a.hpu + h) * kRecFloats;
+      if (a.fused)
+        store_rec<true>(rec, c8, A, M, L);
+      else
+        store_rec<false>(rec, c8, A, M, L);
     }
   }
-
+  if (a.fused) merge_fused<TT, APPEND>(a, u, b, h0, nh, tid);
 }
 
 // Second launch: one wave per (unit, head) row, one row per workgroup, so
@@ -813,23 +940,64 @@ constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
 constexpr int64_t kSlotLatencyBytes = INT64_C(128) << 10;
 constexpr int64_t kMinWgsPerUnit = 8;
 
+// Merge mode (rk_set_decode_merge): 0 = by grid size, 1 = two launches,
+// 2 = single launch where the ticket region holds the counters.
+int32_t g_merge_mode = 0;
+
 struct WsLayout {
-  size_t part_m, part_l, part_acc, total;
+  size_t ticket, bticket, part, total;
 };
 
-// partials (m, l, acc) per (unit, workgroup, head)
+// The ticket region (fixed size, at offset 0, so that every shape finds its
+// counters at zero whatever earlier calls wrote past it), then one partial
+// record per (unit, workgroup, head).
 WsLayout ws_layout(const rk_decode_plan& p) {
   const int64_t np = p.wg_vis + p.wg_full;
   const size_t parts = (size_t)p.units * np * p.heads_per_unit;
   WsLayout w;
-  w.part_m = 0;
-  w.part_l = w.part_m + align256(parts * sizeof(float));
-  w.part_acc = w.part_l + align256(parts * sizeof(float));
-  w.total = w.part_acc + align256(parts * 128 * sizeof(float));
+  w.ticket = 0;
+  w.bticket = (size_t)p.units * sizeof(uint32_t);
+  w.part = RK_DECODE_TICKET_BYTES;
+  w.total = w.part + align256(parts * rk::kRecFloats * sizeof(float));
   return w;
 }
 
+// Single-launch merge for a plan: the grid fits in `max_rounds` rounds of
+// resident workgroups (two per CU).  On grids of many rounds every
+// workgroup would hold its slot through the wait for its record stores and
+// its ticket, while the second launch costs a few microseconds once.
+constexpr int64_t kFusedMaxRounds = 2;
+bool use_single_launch(const rk_decode_plan& p, int64_t B, int cus) {
+  if (p.units + B > (int64_t)(RK_DECODE_TICKET_BYTES / sizeof(uint32_t))) return false;
+  if (g_merge_mode == 1) return false;
+  if (g_merge_mode == 2) return true;
+  return p.grid <= kFusedMaxRounds * (int64_t)cus * g_wgs_per_cu;
+}
+
 }  // namespace
+
+namespace {
+
+__global__ void __launch_bounds__(256) zero_words_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+}  // namespace
+
+extern "C" int rk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
+  if (!workspace) return RK_ERR_NULL;
+  if ((((uintptr_t)workspace) & 255) != 0) return RK_ERR_WORKSPACE;
+  const size_t n = (workspace_bytes < RK_DECODE_TICKET_BYTES ? workspace_bytes : RK_DECODE_TICKET_BYTES) / 4;
+  if (n == 0) return RK_OK;
+  hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, (hipStream_t)stream, (uint32_t*)workspace,
+                     (int64_t)n);
+  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+extern "C" void rk_set_decode_merge(int32_t mode) {
+  if (mode >= 0 && mode <= 2) g_merge_mode = mode;
+}
 
 extern "C" void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu) {
   if (min_bytes > 0) g_min_wg_bytes = min_bytes;
@@ -924,6 +1092,7 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   p.grid = p.units * (p.wg_vis + p.wg_full);
   if (p.units > 65535 * 1024 || p.wg_vis + p.wg_full > (1 << 30)) return RK_ERR_SHAPE;
   p.workspace_bytes = ws_layout(p).total;
+  p.single_launch = use_single_launch(p, B, num_cus) ? 1 : 0;
   *plan = p;
   return RK_OK;
 }
@@ -1002,6 +1171,19 @@ int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
   return RK_OK;
 }
 
+// The RotateK entry points run the paper family (ROTATEK_KERNEL=paper, one
+// unit per query head, fused_decode.py:370) with the grouped decomposition
+// when query heads share a KV head: the G heads of a group then read each
+// K/V tile once instead of G times (measured on MI355X, B=32 with 8 KV heads
+// of 4 query heads: 429 -> 208 us).  Every head's scores, softmax and P V
+// are computed as in the per-head decomposition, in fp32 with the same
+// hi + lo operand splits, so the two differ only in fp32 summation order.
+// The dense baseline keeps the per-head decomposition (the reference's
+// structure, full_channel_flash_decoding.py:197-203).
+int32_t rotatek_policy(int32_t policy, int64_t G) {
+  return policy == RK_POLICY_PAPER && G > 1 ? RK_POLICY_GQA : policy;
+}
+
 int resolve_cus(int32_t num_cus, int* st) {
   *st = RK_OK;
   if (num_cus > 0) return num_cus;
@@ -1014,14 +1196,13 @@ int resolve_cus(int32_t num_cus, int* st) {
 template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
 hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
   bool launched = false;
-  if constexpr (VEC && HMAX == 1) {  // grouped one-unit-per-query-head mode: temporal loads
+  // grouped one-unit-per-query-head mode (temporal loads): the dense
+  // baseline's paper family at G > 1 only (the RotateK entries run that
+  // family grouped, see rotatek_policy)
+  if constexpr (VEC && HMAX == 1 && !HAS_VIS) {
     if (a.xgroup > 1) {
-      if (HAS_VIS && a.k_new)
-        hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, HAS_VIS, false>), grid,
-                           dim3(rk::kThreads), 0, s, a);
-      else
-        hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false>), grid,
-                           dim3(rk::kThreads), 0, s, a);
+      hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false>), grid,
+                         dim3(rk::kThreads), 0, s, a);
       launched = true;
     }
   }
@@ -1036,7 +1217,7 @@ hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
     hipLaunchKernelGGL((rk::decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false>), grid, dim3(rk::kThreads), 0,
                        s, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || a.fused) return e;
   const int64_t rows = (int64_t)grid.y * a.hpu;
   hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)rows), dim3(64), 0, s, a, rows);
   return hipGetLastError();
@@ -1119,9 +1300,10 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   a.out = (uint16_t*)out->data;
   a.kf = (const uint16_t*)kf->data;
   a.vf = (const uint16_t*)vf->data;
-  a.part_m = (float*)((char*)ws + w.part_m);
-  a.part_l = (float*)((char*)ws + w.part_l);
-  a.part_acc = (float*)((char*)ws + w.part_acc);
+  a.part = (float*)((char*)ws + w.part);
+  a.ticket = (uint32_t*)((char*)ws + w.ticket);
+  a.bticket = (uint32_t*)((char*)ws + w.bticket);
+  a.fused = p.single_launch;
   a.q_sb = q->stride[0];
   a.q_sh = q->stride[1];
   a.q_sd = q->stride[2];
@@ -1230,8 +1412,9 @@ extern "C" int rk_rotatek_decode_check(const rk_tensor* q_full, const rk_tensor*
   if (out && (st = check_out(out, c))) return st;
   const int cus = resolve_cus(num_cus, &st);
   if (st) return st;
+  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
   rk_decode_plan p;
-  st = rk_plan_decode(c.B, c.H_q, c.H_kv, c.Dk, c.S_v, c.S_f, 2, policy, cus, &p);
+  st = rk_plan_decode(c.B, c.H_q, c.H_kv, c.Dk, c.S_v, c.S_f, 2, rotatek_policy(policy, c.G), cus, &p);
   if (st) return st;
   if (workspace_bytes) *workspace_bytes = p.workspace_bytes;
   return RK_OK;
@@ -1251,7 +1434,7 @@ extern "C" int rk_rotatek_decode(const rk_tensor* q_full, const rk_tensor* R_par
   if ((st = check_out(out, c))) return st;
   if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
   return run_decode(c, q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse,
-                    out, policy, workspace, workspace_bytes, stream, true);
+                    out, rotatek_policy(policy, c.G), workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor* R_partial,
@@ -1289,7 +1472,7 @@ extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor
     }
   }
   return run_decode(c, q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse,
-                    out, policy, workspace, workspace_bytes, stream, true, len_full,
+                    out, rotatek_policy(policy, c.G), workspace, workspace_bytes, stream, true, len_full,
                     v_gap > 0 ? v_gap_at : -1, v_gap, k_new, v_new);
 }
 

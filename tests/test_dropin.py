@@ -147,3 +147,20 @@ def test_decode_on_host_tensors_fails_loudly():
     from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
     with pytest.raises(RuntimeError):
         rotatek_decode_fused(**_decode_args())
+
+
+def test_captured_cache_refuses_to_reallocate():
+    """Once a decode graph holds the span buffers, an append past capacity
+    raises instead of moving them (host tensors: no GPU needed)."""
+    import torch
+
+    from rotatek_amd.cache import DynamicCache
+    cache = DynamicCache(reserve_tokens=0)
+    B, H, D = 1, 2, 128
+    cache._spans.append(__import__("rotatek_amd.cache", fromlist=["_Spans"])._Spans(
+        torch.zeros(B, H, 3, D), torch.zeros(B, H, 3, D), torch.zeros(B, dtype=torch.int32), 1, 0, 2, False))
+    cache._captured = True
+    with pytest.raises(RuntimeError, match="reserve"):
+        cache._grow(0, 4)
+    with pytest.raises(RuntimeError, match="reserve"):
+        cache.reserve(1)

@@ -320,3 +320,57 @@ def test_fused_append_with_ragged_lengths():
                         mask_full=mask, k_sparse=p["k_pruned"], v_sparse=vb_want[:, :, s_p:s_p + s_v],
                         num_kv_groups=Hq // Hkv))
     assert np.abs(_np(out)[:, None] - want).max() <= TOL[dtype]
+
+
+def test_graph_survives_workspace_growth_after_capture():
+    """A captured decode graph keeps its workspace: a later, larger decode
+    grows the shared workspace (the old buffer is retired, not freed), a
+    tensor allocated afterwards must not alias it, and the replays still
+    match the oracle."""
+    from rotatek_amd import _lib
+    from rotatek_amd.cache import DynamicCache
+    from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
+    B, Hq, Hkv, Dk, s_p, s_v, s_t, steps = 2, 8, 2, 32, 7, 900, 5, 3
+    dtype = torch.bfloat16
+    _say("graph replay after the workspace grew")
+    p = _prefill(B, Hkv, Dk, s_p, s_v, s_t, dtype, seed=61)
+    cache = DynamicCache(reserve_tokens=steps)
+    cache.store_pruned(p["k_pruned"], p["k_prompt"], p["k_text"], None, p["v"], 0)
+    cache.rotatek_rotations.append(p["R"])
+    cache.rotatek_means.append(p["dm"])
+    ref = _CatCache(p)
+    q = torch.zeros(1, B, Hq, D, dtype=dtype, device="cuda")
+    kn = torch.zeros(1, B, Hkv, 1, D, dtype=dtype, device="cuda")
+    vn = torch.zeros_like(kn)
+    out = torch.empty(1, B, Hq, D, dtype=dtype, device="cuda")
+    graph = cache.capture_decode(q, kn, vn, out, Hq // Hkv)
+    torch.cuda.synchronize()
+    old_ws = _lib._WORKSPACE[torch.cuda.current_device()].data_ptr()
+    # a much larger decode grows the workspace past the captured buffer
+    g = torch.Generator(device="cuda").manual_seed(3)
+    big = dict(q_full=torch.randn(16, 32, D, generator=g, device="cuda").to(dtype),
+               R_partial=torch.randn(16, 8, D, Dk, generator=g, device="cuda").to(dtype),
+               delta_mu=None,
+               k_full=torch.randn(16, 8, 4000, D, generator=g, device="cuda").to(dtype),
+               v_full=torch.randn(16, 8, 4000, D, generator=g, device="cuda").to(dtype),
+               mask_full=torch.ones(16, 4000, dtype=torch.uint8, device="cuda"),
+               k_sparse=torch.randn(16, 8, 30000, Dk, generator=g, device="cuda").to(dtype),
+               v_sparse=torch.randn(16, 8, 30000, D, generator=g, device="cuda").to(dtype),
+               num_kv_groups=4)
+    rotatek_decode_gqa(**big)
+    torch.cuda.synchronize()
+    assert _lib._WORKSPACE[torch.cuda.current_device()].data_ptr() != old_ws
+    del big
+    torch.cuda.empty_cache()
+    filler = torch.full((1 << 22,), 7.0, device="cuda")   # may land where a freed buffer was
+    for step in range(steps):
+        kq, kk, kv = p["rn"](B, Hq, D), p["rn"](B, Hkv, 1, D), p["rn"](B, Hkv, 1, D)
+        q[0].copy_(kq)
+        kn[0].copy_(kk)
+        vn[0].copy_(kv)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref.update(kk, kv)
+        want = _oracle(ref.rotatek_args(kq, p["R"], p["dm"], Hq // Hkv))
+        assert np.abs(_np(out[0])[:, None] - want).max() <= TOL[dtype], step
+    assert bool((filler == 7.0).all())
