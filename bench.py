@@ -469,6 +469,8 @@ def main():
                     help="override the batch (kernel_profile.py's --batch_size)")
     ap.add_argument("--merge", default="auto", choices=["auto", "two", "one"],
                     help="decode merge: by grid size (auto), two launches, or one launch")
+    ap.add_argument("--graph-steps", type=int, default=0,
+                    help="decode steps captured per hipGraph (default: one per input copy)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -542,7 +544,8 @@ def main():
     _log("[bench] warmup done")
     us = _time_wall(step, args.steps)
     us_launch = _time_launches(step, args.steps)
-    us_graph = _time_graph(step, args.steps, args.warmup, copies) if not args.no_graph else None
+    per_graph = copies * max(1, -(-args.graph_steps // copies))
+    us_graph = _time_graph(step, args.steps, args.warmup, per_graph) if not args.no_graph else None
     gbps = nbytes / (us_launch * 1e-6) / 1e9
     _log(f"[bench] rotatek eager {us:.1f} us/step, per-launch {us_launch:.1f} us, graph {us_graph} us, "
          f"{gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS * 100:.1f}% of peak)")
@@ -558,7 +561,7 @@ def main():
             dstep()
         d_us = _time_wall(dstep, args.steps)
         d_launch = _time_launches(dstep, args.steps)
-        d_graph = _time_graph(dstep, args.steps, args.warmup, copies) if not args.no_graph else None
+        d_graph = _time_graph(dstep, args.steps, args.warmup, per_graph) if not args.no_graph else None
         dbytes = synth.decode_bytes(cfg, dense=True)
         extra = {
             "dense_us_per_step": round(d_us, 2),
@@ -608,6 +611,7 @@ def main():
         "achieved_gbps": round(gbps, 1),
         "pct_of_peak_hbm": round(gbps / HBM_PEAK_GBPS * 100, 2),
         "graph_us_per_step": round(us_graph, 2) if us_graph else None,
+        "graph_steps_per_replay": per_graph,
         "input_copies": copies,
         "launch_us": round(us_launch, 2),
         "roofline": {

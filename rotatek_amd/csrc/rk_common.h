@@ -27,6 +27,7 @@ constexpr float kDenomEps = 1e-6f;  // output guard (fused_decode.py:293)
 struct F16 {
   using elem = _Float16;
   using vec8 = f16x8;
+  static constexpr int kBytes = 2;
   static __device__ __forceinline__ float to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
   }
@@ -54,6 +55,7 @@ struct F16 {
 struct BF16 {
   using elem = __bf16;
   using vec8 = bf16x8;
+  static constexpr int kBytes = 2;
   static __device__ __forceinline__ float to_f32(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
   }
@@ -75,6 +77,11 @@ struct BF16 {
     hi = from_f32(x);
     lo = from_f32(x - to_f32(hi));
   }
+};
+
+// fp32 storage (the fp32 decode path: outputs written as they are computed).
+struct F32 {
+  static constexpr int kBytes = 4;
 };
 
 // Scalar load of one element of a runtime dtype (0 f16, 1 bf16, 2 f32).

@@ -381,43 +381,80 @@ template <class TT>
 __device__ __forceinline__ void write_out(const DecodeArgs& a, int b, int hq, int c8, float L,
                                           const float (&A)[8]) {
   const float den = L + kDenomEps;
-  uint16_t o[8];
+  if constexpr (TT::kBytes == 4) {
+    float* dst = (float*)a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 8 * c8 * a.o_sd;
+    if (a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
+      ((float4*)dst)[0] = make_float4(A[0] / den, A[1] / den, A[2] / den, A[3] / den);
+      ((float4*)dst)[1] = make_float4(A[4] / den, A[5] / den, A[6] / den, A[7] / den);
+    } else {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = TT::from_f32(A[e] / den);
-  uint16_t* dst = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 8 * c8 * a.o_sd;
-  if (a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
-    *(uint4*)dst = pack8(o);
+      for (int e = 0; e < 8; ++e) dst[e * a.o_sd] = A[e] / den;
+    }
   } else {
+    uint16_t o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dst[e * a.o_sd] = o[e];
+    for (int e = 0; e < 8; ++e) o[e] = TT::from_f32(A[e] / den);
+    uint16_t* dst = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 8 * c8 * a.o_sd;
+    if (a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
+      *(uint4*)dst = pack8(o);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e * a.o_sd] = o[e];
+    }
   }
 }
 
-// Second-launch merge of one (unit, head) row by one wave: lane (sl, c8) =
-// (lane >> 4, lane & 15) folds records x = sl, sl + 4, ...; the four slices
-// are then combined across lanes.  With a fused append the new token is
-// already in record 0 of the unit; the row of query head 0 advances
-// len_full[b] (a full buffer stays).
-template <class TT>
-__device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b, int hq, int h,
-                                          int lane) {
-  const int sl = lane >> 4, c8 = lane & 15;
+// Merge of one unit's records by one 256-thread workgroup (both merges run
+// this, so their results are bit-identical).  The 16 slices of 16 lanes
+// (s = tid >> 4) are shared out S = 16 / nh (a power of two) per head;
+// slice j of head h folds records x = j, j + S, ... (eight records' loads
+// in flight at a time, so one or two memory round trips cover a unit), and
+// the S slices of a head are combined pairwise, lower slice first: within a
+// wave by lane exchange, across waves through LDS (s_mrg, 16 x kRecFloats
+// floats).  COH: the records were written in this launch (coherent loads).
+template <class TT, bool COH>
+__device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b, int h0, int nh, int tid,
+                                           float* s_mrg) {
+  int S = 16;
+  while (S * nh > 16) S >>= 1;
+  const int s = tid >> 4, c8 = tid & 15, h = s / S, j = s - (s / S) * S;
+  const bool act = h < nh;
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const float* rec0 = a.part + (u * a.np * a.hpu + h) * kRecFloats;
-  fold_records<false>(rec0, (int64_t)a.hpu * kRecFloats, a.np, sl, 4, c8, M, L, A);
-#pragma unroll
-  for (int off = 16; off <= 32; off <<= 1) {
-    float Ao[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) Ao[e] = shfl_xor(A[e], off);
-    combine(M, L, A, shfl_xor(M, off), shfl_xor(L, off), Ao);
+  if (act) {
+    const float* rec0 = a.part + (u * a.np * a.hpu + h) * kRecFloats;
+    fold_records<COH>(rec0, (int64_t)a.hpu * kRecFloats, a.np, j, S, c8, M, L, A);
   }
-  if (a.k_new && hq == 0 && lane == 0) {
-    const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
-    if (pos < a.S_f) a.len_full[b] = pos + 1;
+#pragma unroll
+  for (int d = 1; d <= 2; d <<= 1) {  // lane exchange: slices s ^ 1, s ^ 2 share a wave
+    if (d < S) {
+      float Ao[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Ao[e] = shfl_xor(A[e], 16 * d);
+      const float Mo = shfl_xor(M, 16 * d), Lo = shfl_xor(L, 16 * d);
+      if ((j & d) == 0) combine(M, L, A, Mo, Lo, Ao);
+    }
   }
-  if (sl != 0) return;
-  write_out<TT>(a, b, hq, c8, L, A);
+  for (int d = 4; d < S; d <<= 1) {  // across waves (S = 8, 16: one or two heads)
+    float* mine = s_mrg + s * kRecFloats;
+    if (act && (j & (2 * d - 1)) == d) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mine[8 * c8 + e] = A[e];
+      if (c8 == 0) {
+        mine[128] = M;
+        mine[129] = L;
+      }
+    }
+    __syncthreads();
+    if (act && (j & (2 * d - 1)) == 0) {
+      const float* o = s_mrg + (s + d) * kRecFloats;
+      float Ao[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Ao[e] = o[8 * c8 + e];
+      combine(M, L, A, o[128], o[129], Ao);
+    }
+    __syncthreads();
+  }
+  if (act && j == 0) write_out<TT>(a, b, h0 + h, c8, L, A);
 }
 
 // Single-launch merge, run by every workgroup after it has stored its
@@ -425,13 +462,15 @@ __device__ __forceinline__ void merge_row(const DecodeArgs& a, int64_t u, int b,
 // (they write through to memory), then takes a ticket on the unit's
 // counter; the last of the unit's np workgroups resets the counter and
 // merges the unit's records, read with coherent loads, in the order of
-// merge_row (the result is bit-identical to the two-launch merge).  No
+// the merge kernel (merge_unit; the result is bit-identical to the
+// two-launch merge).  No
 // agent-scope release or acquire fence is needed, so no XCD L2 is written
 // back or invalidated.  With a fused append, the last unit of a batch row
 // to finish advances len_full[b] behind a second ticket: by then every
 // workgroup of the row has read it.  Both counters are left at zero.
 template <class TT, bool APPEND>
-__device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, int h0, int nh, int tid) {
+__device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, int h0, int nh, int tid,
+                                            float* s_mrg) {
   __shared__ uint32_t s_ticket;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores have completed
@@ -441,20 +480,7 @@ __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, i
   __syncthreads();
   if (s_ticket != (uint32_t)(a.np - 1)) return;
   if (tid == 0) __hip_atomic_store(a.ticket + u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const int lane = tid & 63, wave = tid >> 6, sl = lane >> 4, c8 = lane & 15;
-  const float* recu = a.part + (int64_t)u * a.np * a.hpu * kRecFloats;
-  for (int h = wave; h < nh; h += kWaves) {
-    float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    fold_records<true>(recu + (int64_t)h * kRecFloats, (int64_t)a.hpu * kRecFloats, a.np, sl, 4, c8, M, L, A);
-#pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-      float Ao[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Ao[e] = shfl_xor(A[e], off);
-      combine(M, L, A, shfl_xor(M, off), shfl_xor(L, off), Ao);
-    }
-    if (sl == 0) write_out<TT>(a, b, h0 + h, c8, L, A);
-  }
+  merge_unit<TT, true>(a, u, b, h0, nh, tid, s_mrg);
   if constexpr (APPEND) {
     if (tid == 0) {
       const uint32_t t = __hip_atomic_fetch_add(a.bticket + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -893,24 +919,212 @@ decode_kernel(const DecodeArgs a) {
         store_rec<false>(rec, c8, A, M, L);
     }
   }
-  if (a.fused) merge_fused<TT, APPEND>(a, u, b, h0, nh, tid);
+  if (a.fused) merge_fused<TT, APPEND>(a, u, b, h0, nh, tid, HMAX >= 16 ? &s_acc[0][0][0] : (float*)s_rsep);
 }
 
-// Second launch: one wave per (unit, head) row, one row per workgroup, so
-// a small decode's rows spread over as many CUs as there are rows.
+// ---- fp32 decode (q, K, V and out in F32; R_partial and delta_mu F16,
+// BF16 or F32), the dtype of the reference's CPU-scale configuration.  The
+// reference kernels load any float input as fp32 and compute in fp32
+// (fused_decode.py:133,166,174; full_channel_flash_decoding.py:65,84,92);
+// so does this kernel, on the VALU: fp32 has no MFMA path that keeps its
+// precision at this arithmetic intensity.  One unit per query head (hpu 1),
+// the plan's grid and records as the 16-bit kernel, so both merges apply.
+// Each wave walks 64-token blocks of its workgroup's chunk (blocks wave,
+// wave + 4, ...): lane t scores token t0 + t as a dot product over its
+// row, the wave runs the online softmax (log2 domain), and lane j
+// accumulates channels 2j, 2j + 1 of P V over the block's rows, with the
+// block's probabilities broadcast from LDS.
+constexpr int kBlk32 = 64;
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, shfl_xor(v, off));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += shfl_xor(v, off);
+  return v;
+}
+
+// sum_c w[c] * row[c * sd], c < n; w in LDS.  VEC: unit stride, 16-byte
+// aligned row, n a multiple of 4.
+template <bool VEC>
+__device__ __forceinline__ float dot_row32(const float* row, uint32_t sd, const float* w, int n) {
+  float s0 = 0.f, s1 = 0.f;
+  if constexpr (VEC) {
+    for (int c = 0; c < n; c += 8) {
+      const float4 r0 = *(const float4*)(row + c);
+      const float4 w0 = *(const float4*)(w + c);
+      s0 = fmaf(w0.x, r0.x, s0);
+      s0 = fmaf(w0.y, r0.y, s0);
+      s0 = fmaf(w0.z, r0.z, s0);
+      s0 = fmaf(w0.w, r0.w, s0);
+      if (c + 4 < n) {
+        const float4 r1 = *(const float4*)(row + c + 4);
+        const float4 w1 = *(const float4*)(w + c + 4);
+        s1 = fmaf(w1.x, r1.x, s1);
+        s1 = fmaf(w1.y, r1.y, s1);
+        s1 = fmaf(w1.z, r1.z, s1);
+        s1 = fmaf(w1.w, r1.w, s1);
+      }
+    }
+  } else {
+    for (int c = 0; c < n; ++c) s0 = fmaf(w[c], row[(int64_t)c * sd], s0);
+  }
+  return s0 + s1;
+}
+
+template <bool HAS_VIS, bool VEC>
+__global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) float s_q[128];
+  __shared__ __attribute__((aligned(16))) float s_qt[128];
+  __shared__ float s_bias[2];
+  __shared__ float s_p[kWaves][kBlk32];
+  __shared__ float s_m[kWaves], s_l[kWaves];
+  __shared__ float s_acc[kWaves][128];
+  __shared__ float s_mrg[16 * kRecFloats];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int u = blockIdx.y, x = blockIdx.x;
+  const int b = u / a.units_per_b;
+  const int r_in_b = u - b * a.units_per_b;
+  const int kv = r_in_b / a.spk;
+  const int h0 = kv * a.G + (r_in_b - kv * a.spk) * a.hpu;
+  const bool is_vis = HAS_VIS && x < a.wg_vis;
+  const int xf = HAS_VIS ? x - a.wg_vis : x;
+  const float* q = (const float*)a.q;
+
+  if (tid < 128) s_q[tid] = q[b * a.q_sb + (int64_t)h0 * a.q_sh + (int64_t)tid * a.q_sd];
+  __syncthreads();
+
+  float m = kNegInit, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+  // online-softmax step over one block: s = log2-domain score of token
+  // t0 + lane (-inf when invalid), V rows clamped to t_last
+  auto step = [&](float s, const float* vb, uint32_t vss, uint32_t vsd, int64_t t0, int64_t t_last,
+                  uint32_t gap_at, uint32_t gap) {
+    const float m_new = fmaxf(m, wave_max(s));
+    const float alpha = fast_exp2(m - m_new);
+    const float p = fast_exp2(s - m_new);
+    l = l * alpha + wave_sum(p);
+    acc0 *= alpha;
+    acc1 *= alpha;
+    m = m_new;
+    s_p[wave][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll 8
+    for (int j = 0; j < kBlk32; ++j) {
+      uint32_t row = (uint32_t)min(t0 + j, t_last);
+      row += row >= gap_at ? gap : 0u;
+      const float* vr = vb + (int64_t)row * vss;
+      float v0, v1;
+      if constexpr (VEC) {
+        const float2 v = *(const float2*)(vr + 2 * lane);
+        v0 = v.x;
+        v1 = v.y;
+      } else {
+        v0 = vr[(int64_t)(2 * lane) * vsd];
+        v1 = vr[(int64_t)(2 * lane + 1) * vsd];
+      }
+      const float pj = s_p[wave][j];
+      acc0 = fmaf(pj, v0, acc0);
+      acc1 = fmaf(pj, v1, acc1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  if (is_vis) {
+    if (tid < a.Dk) {  // q R_partial, column tid
+      const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)tid * a.R_sk;
+      float sum = 0.f;
+      for (int d = 0; d < 128; ++d) sum = fmaf(s_q[d], load_any(a.R, rb + (int64_t)d * a.R_sd, a.r_dtype), sum);
+      s_qt[tid] = sum;
+    }
+    if (wave < 2) {  // q . delta_mu
+      const int d = tid;
+      const float t = a.has_bias ? s_q[d] * load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)d * a.dm_sd,
+                                                    a.dm_dtype)
+                                 : 0.f;
+      const float w = wave_sum(t);
+      if (lane == 0) s_bias[wave] = w;
+    }
+    __syncthreads();
+    const float bias2 = (s_bias[0] + s_bias[1]) * a.scale_log2;
+    const int64_t t_begin = (int64_t)x * a.chunk_vis;
+    const int64_t t_end = min(a.S_v, t_begin + a.chunk_vis);
+    const float* ksb = (const float*)a.ks + b * a.ks_sb + kv * a.ks_sh;
+    const float* vsb = (const float*)a.vs + b * a.vs_sb + kv * a.vs_sh;
+    for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
+      const int64_t t = t0 + lane;
+      const float d = dot_row32<VEC>(ksb + (int64_t)min(t, t_end - 1) * a.ks_ss, a.ks_sd, s_qt, a.Dk);
+      const float s = t < t_end ? fmaf(d, a.scale_log2, bias2) : -INFINITY;
+      step(s, vsb, a.vs_ss, a.vs_sd, t0, t_end - 1, UINT32_MAX, 0u);
+    }
+  } else {
+    const int64_t t_begin = (int64_t)xf * a.chunk_full;
+    const int64_t t_end = min(a.S_f, t_begin + a.chunk_full);
+    const float* kfb = (const float*)a.kf + b * a.kf_sb + kv * a.kf_sh;
+    const float* vfb = (const float*)a.vf + b * a.vf_sb + kv * a.vf_sh;
+    for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
+      const int64_t t = t0 + lane;
+      const int64_t tc = min(t, t_end - 1);
+      const float d = dot_row32<VEC>(kfb + tc * a.kf_ss, a.kf_sd, s_q, 128);
+      const bool ok = t < t_end && (!a.mask || a.mask[b * a.mf_sb + tc * a.mf_ss] != 0);
+      step(ok ? d * a.scale_log2 : -INFINITY, vfb, a.vf_ss, a.vf_sd, t0, t_end - 1, a.vf_gap_at, a.vf_gap);
+    }
+  }
+
+  // the four wave states -> this workgroup's record
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+  }
+  s_acc[wave][2 * lane] = acc0;
+  s_acc[wave][2 * lane + 1] = acc1;
+  __syncthreads();
+  if (tid < 16) {
+    const int c8 = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w]);
+    float L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = fast_exp2(s_m[w] - M);
+      L += s_l[w] * wt;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) A[e] += s_acc[w][8 * c8 + e] * wt;
+    }
+    float* rec = a.part + ((int64_t)u * a.np + x) * kRecFloats;
+    if (a.fused)
+      store_rec<true>(rec, c8, A, M, L);
+    else
+      store_rec<false>(rec, c8, A, M, L);
+  }
+  if (a.fused) merge_fused<F32, false>(a, u, b, h0, 1, tid, s_mrg);
+}
+
+// Second launch: one workgroup per unit runs merge_unit.  With a fused
+// append the unit holding query head 0 of row b advances len_full[b]; the
+// split launch that read it has completed.
 template <class TT>
-__global__ void __launch_bounds__(64) merge_kernel(const DecodeArgs a, int64_t rows) {
+__global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
+  __shared__ float s_mrg[16 * kRecFloats];
   const int tid = threadIdx.x;
-  const int64_t row = blockIdx.x;
-  if (row >= rows) return;
-  const int64_t u = row / a.hpu;
-  const int h = (int)(row - u * a.hpu);
+  const int64_t u = blockIdx.x;
   const int b = (int)(u / a.units_per_b);
   const int r_in_b = (int)(u - (int64_t)b * a.units_per_b);
   const int kv = r_in_b / a.spk;
   const int jblk = r_in_b - kv * a.spk;
-  if (h >= min(a.hpu, a.G - jblk * a.hpu)) return;
-  merge_row<TT>(a, u, b, kv * a.G + jblk * a.hpu + h, h, tid & 63);
+  const int h0 = kv * a.G + jblk * a.hpu;
+  merge_unit<TT, false>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg);
+  if (a.k_new && r_in_b == 0 && tid == 0) {
+    const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
+    if (pos < a.S_f) a.len_full[b] = pos + 1;
+  }
 }
 
 }  // namespace rk
@@ -1142,7 +1356,7 @@ int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
   c->Dk = R->shape[3];
   c->dtype = q->dtype;
   if (c->H_q / G != c->H_kv || c->H_q % G != 0) return RK_ERR_HEADS;
-  if (!rk::is_half(q->dtype)) return RK_ERR_DTYPE;
+  if (!rk::is_half(q->dtype) && q->dtype != RK_F32) return RK_ERR_DTYPE;
   if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
   if (!rk::is_float_param(R->dtype)) return RK_ERR_DTYPE;
   if (R->shape[0] != c->B || R->shape[2] != 128) return RK_ERR_SHAPE;
@@ -1184,6 +1398,14 @@ int32_t rotatek_policy(int32_t policy, int64_t G) {
   return policy == RK_POLICY_PAPER && G > 1 ? RK_POLICY_GQA : policy;
 }
 
+// The plan of a checked call.  fp32 runs one unit per query head (the
+// VALU kernel has no grouped form) over 4-byte elements.
+int plan_for(const Checked& c, bool has_vis, int32_t policy, int cus, rk_decode_plan* p) {
+  const bool f32 = c.dtype == RK_F32;
+  return rk_plan_decode(c.B, c.H_q, c.H_kv, has_vis ? c.Dk : 0, has_vis ? c.S_v : 0, c.S_f, f32 ? 4 : 2,
+                        f32 ? RK_POLICY_PAPER : policy, cus, p);
+}
+
 int resolve_cus(int32_t num_cus, int* st) {
   *st = RK_OK;
   if (num_cus > 0) return num_cus;
@@ -1218,8 +1440,7 @@ hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
                        s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fused) return e;
-  const int64_t rows = (int64_t)grid.y * a.hpu;
-  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)rows), dim3(64), 0, s, a, rows);
+  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3(grid.y), dim3(rk::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1250,6 +1471,34 @@ hipError_t launch_dk(int dkb, bool vec, int hmax, bool has_vis, const rk::Decode
     case 2: return launch_v<TT, 2>(vec, hmax, has_vis, a, grid, s);
     default: return launch_v<TT, 4>(vec, hmax, has_vis, a, grid, s);
   }
+}
+
+// fp32 rows read as float4 / float2: unit channel stride, every other
+// stride a multiple of 4 elements, 16-byte aligned base.
+bool vec32_ok(const rk_tensor* t) {
+  if (!t || !t->data) return true;
+  if (t->stride[t->ndim - 1] != 1 && t->shape[t->ndim - 1] > 1) return false;
+  for (int i = 0; i < t->ndim - 1; ++i)
+    if (t->shape[i] > 1 && (t->stride[i] % 4) != 0) return false;
+  return (((uintptr_t)t->data) & 15) == 0;
+}
+
+hipError_t launch32(bool has_vis, bool vec, const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
+  if (has_vis) {
+    if (vec)
+      hipLaunchKernelGGL((rk::decode32_kernel<true, true>), grid, dim3(rk::kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((rk::decode32_kernel<true, false>), grid, dim3(rk::kThreads), 0, s, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((rk::decode32_kernel<false, true>), grid, dim3(rk::kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((rk::decode32_kernel<false, false>), grid, dim3(rk::kThreads), 0, s, a);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.fused) return e;
+  hipLaunchKernelGGL((rk::merge_kernel<rk::F32>), dim3(grid.y), dim3(rk::kThreads), 0, s, a);
+  return hipGetLastError();
 }
 
 void set4(const rk_tensor* t, int64_t& s0, int64_t& s1, int64_t& s2, int64_t& s3) {
@@ -1284,8 +1533,7 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   const int cus = resolve_cus(0, &st);
   if (st) return st;
   rk_decode_plan p;
-  st = rk_plan_decode(c.B, c.H_q, c.H_kv, has_vis ? c.Dk : 0, has_vis ? c.S_v : 0, c.S_f, 2,
-                      policy, cus, &p);
+  st = plan_for(c, has_vis, policy, cus, &p);
   if (st) return st;
   if (!ws || (((uintptr_t)ws) & 255) != 0 || ws_bytes < p.workspace_bytes) return RK_ERR_WORKSPACE;
   if (c.B == 0) return RK_OK;
@@ -1386,12 +1634,17 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     a.rot_x = gx > 1 && p.wg_vis % gx != 0 ? 1 : 0;
   }
   a.units = (int32_t)p.units;
-  a.xgroup = policy == RK_POLICY_PAPER && c.G > 1 ? (int32_t)c.G : 0;
-  if (a.xgroup) a.rot_x = 0;
+  a.xgroup = policy == RK_POLICY_PAPER && c.G > 1 && c.dtype != RK_F32 ? (int32_t)c.G : 0;
+  if (a.xgroup || c.dtype == RK_F32) a.rot_x = 0;
+  if (c.dtype == RK_F32) a.spk = (int32_t)c.G;  // one unit per query head
   a.scale_log2 = (float)(rk::kLog2e / sqrt(128.0));
   const dim3 grid((unsigned)a.np, (unsigned)p.units);
   const int hmax = p.heads_per_unit > 1 ? 16 : 1;
   hipStream_t s = (hipStream_t)stream;
+  if (c.dtype == RK_F32) {
+    const bool v32 = vec32_ok(kf) && vec32_ok(vf) && (!has_vis || (vec32_ok(ks) && vec32_ok(vs) && c.Dk % 4 == 0));
+    return launch32(has_vis, v32, a, grid, s) == hipSuccess ? RK_OK : RK_ERR_HIP;
+  }
   hipError_t e = c.dtype == RK_F16 ? launch_dk<rk::F16>(dkb, vec, hmax, has_vis, a, grid, s)
                                    : launch_dk<rk::BF16>(dkb, vec, hmax, has_vis, a, grid, s);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
@@ -1414,7 +1667,7 @@ extern "C" int rk_rotatek_decode_check(const rk_tensor* q_full, const rk_tensor*
   if (st) return st;
   if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
   rk_decode_plan p;
-  st = rk_plan_decode(c.B, c.H_q, c.H_kv, c.Dk, c.S_v, c.S_f, 2, rotatek_policy(policy, c.G), cus, &p);
+  st = plan_for(c, true, rotatek_policy(policy, c.G), cus, &p);
   if (st) return st;
   if (workspace_bytes) *workspace_bytes = p.workspace_bytes;
   return RK_OK;
@@ -1459,6 +1712,7 @@ extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor
                      num_kv_groups, &c);
   if (st) return st;
   if (!out || !len_full) return RK_ERR_NULL;
+  if (c.dtype == RK_F32) return RK_ERR_DTYPE;  // the span cache holds 16-bit Keys and Values
   if ((st = check_out(out, c))) return st;
   if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
   if ((k_new == nullptr) != (v_new == nullptr)) return RK_ERR_NULL;
@@ -1556,7 +1810,7 @@ int check_dense(const rk_tensor* q, const rk_tensor* k, const rk_tensor* v, int6
   if (k->shape[3] != q->shape[2] || v->ndim < 1 || v->shape[v->ndim - 1] != q->shape[2])
     return RK_ERR_SHAPE;
   if (c->H_kv <= 0 || c->H_q / G != c->H_kv || c->H_q % G != 0) return RK_ERR_HEADS;
-  if (!rk::is_half(q->dtype)) return RK_ERR_DTYPE;
+  if (!rk::is_half(q->dtype) && q->dtype != RK_F32) return RK_ERR_DTYPE;
   if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
   if ((st = check_kv4(k, *c, c->S_f, 128, true))) return st;
   if ((st = check_kv4(v, *c, c->S_f, 128, true))) return st;
@@ -1576,7 +1830,7 @@ extern "C" int rk_full_channel_decode_check(const rk_tensor* q, const rk_tensor*
   const int cus = resolve_cus(num_cus, &st);
   if (st) return st;
   rk_decode_plan p;
-  st = rk_plan_decode(c.B, c.H_q, c.H_kv, 0, 0, c.S_f, 2, policy, cus, &p);
+  st = plan_for(c, false, policy, cus, &p);
   if (st) return st;
   if (workspace_bytes) *workspace_bytes = p.workspace_bytes;
   return RK_OK;

@@ -88,13 +88,46 @@ def test_rotatek_check_ok_and_workspace():
     (dict(mask_dtype=_lib.RK_F16), -3),         # mask not uint8
     (dict(G=3), -5),                            # H_q / G != H_kv
     (dict(D=64), -6),                           # head_dim != 128
-    (dict(dtype=_lib.RK_F32), -3),              # fp32 K/V not supported
+    (dict(dtype=_lib.RK_F64), -3),              # fp64 not supported
     (dict(Dk=0), -7),
     (dict(policy=7), -10),
 ])
 def test_rotatek_check_errors(kw, code):
     st, _ = _rot_check(**kw)
     assert st == code, (st, _lib.strerror(st))
+
+
+def test_rotatek_check_fp32():
+    """fp32 q/K/V/out (the reference's kernels accept it) plan one unit per
+    query head; mixing fp32 q with 16-bit K/V is a dtype error."""
+    st, need = _rot_check(dtype=_lib.RK_F32)
+    assert st == 0 and need > 0
+    p = _lib.plan_decode(2, 8, 4, 32, 100, 20, elem_bytes=4, policy=_lib.RK_POLICY_PAPER)
+    assert p["heads_per_unit"] == 1 and p["units"] == 2 * 8
+    lib = _lib.load()
+    B, Hq, Hkv, D = 2, 8, 4, 128
+    q, R = _t((B, Hq, D), _lib.RK_F32), _t((B, Hkv, D, 32), _lib.RK_F32)
+    kf, vf = _t((B, Hkv, 10, D)), _t((B, Hkv, 10, D))
+    ks, vs = _t((B, Hkv, 50, 32)), _t((B, Hkv, 50, D))
+    st = lib.rk_rotatek_decode_check(*[ctypes.byref(x) for x in (q, R)], None,
+                                     *[ctypes.byref(x) for x in (kf, vf)], None,
+                                     *[ctypes.byref(x) for x in (ks, vs)], 2, None, 1, 256, None)
+    assert st == -3
+
+
+def test_varlen_rejects_fp32():
+    """The span cache decode is 16-bit only: fp32 is a dtype error."""
+    lib = _lib.load()
+    B, Hq, Hkv, D = 1, 4, 4, 128
+    f = _lib.RK_F32
+    q, R, o = _t((B, Hq, D), f), _t((B, Hkv, D, 32), f), _t((B, Hq, D), f)
+    kf, vb = _t((B, Hkv, 10, D), f), _t((B, Hkv, 60, D), f)
+    ks, vs = _t((B, Hkv, 50, 32), f), _t((B, Hkv, 50, D), f)
+    lens = (ctypes.c_int32 * 1)()
+    st = lib.rk_rotatek_decode_varlen(ctypes.byref(q), ctypes.byref(R), None, ctypes.byref(kf), ctypes.byref(vb),
+                                      4, 50, None, ctypes.byref(ks), ctypes.byref(vs), 1, None, None,
+                                      ctypes.cast(lens, ctypes.c_void_p), ctypes.byref(o), 1, None, 0, None)
+    assert st == -3
 
 
 def test_rotatek_check_shape_mismatch():

@@ -266,3 +266,89 @@ def test_benchmark_configs_full_size(cfg):
         assert torch.equal(out_p, out)
     else:
         assert (out_p.float() - out.float()).abs().max().item() <= TOL[c.dtype]
+
+
+# ---------------------------------------------------------------- fp32
+# The reference kernels load any float input as fp32 and compute in fp32
+# (fused_decode.py:133,166,174; full_channel_flash_decoding.py:65,84,92);
+# the HIP fp32 path does the same on the VALU.  Bar: max-abs 1e-4 against
+# the float64 oracle on the same fp32 inputs (outputs are O(0.1); a dropped
+# bias or a wrong scale is off by 1e-2 or more).
+TOL32 = 1e-4
+
+FP32_CASES = [
+    # B, Hq, Hkv, Dk, S_v, S_f
+    (1, 32, 32, 32, 2304, 128),     # config 0
+    (2, 8, 2, 32, 1000, 77),        # GQA
+    (1, 4, 4, 40, 300, 0),          # no prompt/text, Dk % 8 != 0
+    (2, 4, 4, 32, 0, 257),          # no visual span
+    (1, 28, 4, 128, 513, 65),
+    (1, 2, 2, 6, 5, 3),             # Dk not a multiple of 4 (element loads)
+]
+
+
+@pytest.mark.parametrize("family", ["paper", "gqa"])
+@pytest.mark.parametrize("case", FP32_CASES)
+def test_fp32_decode_matches_oracle(case, family):
+    B, Hq, Hkv, Dk, S_v, S_f = case
+    _say(f"rotatek fp32 {family} B={B} Hq={Hq} Hkv={Hkv} Dk={Dk} S_v={S_v} S_f={S_f}")
+    inp = _rand_inputs(B, Hq, Hkv, Dk, S_v, S_f, torch.float32, seed=sum(case), mask_p=0.2)
+    out = _decode(inp, family)
+    assert out.dtype == torch.float32 and out.shape == (B, 1, Hq, 128)
+    err = np.abs(_np(out) - _oracle(inp)).max()
+    assert err <= TOL32, err
+
+
+def test_fp32_config0_end_to_end():
+    """BASELINE config 0 (B=1, 32 heads, 2304 visual + 128 text tokens, fp32,
+    seeded orthogonal R_k, top 32 channels by mean |K R_k|): the kept channels
+    and the decode against the oracle."""
+    from rotatek_amd import synth
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    from oracle import prefill as op
+    cfg = synth.CONFIGS["cfg0"]
+    _say("config 0 fp32 end to end")
+    inp = synth.make_decode_inputs(cfg, "cuda", seed=0, with_raw=True)
+    # selection rule: the kept indices are the oracle's top 32 of mean |K R_k|
+    # on every head whose 32nd and 33rd scores are apart by more than the
+    # fp32 scoring error (a closer boundary may go either way)
+    Rk = synth.random_rotations(cfg.B, cfg.H_kv, cfg.D, 2).numpy().astype(np.float32).astype(np.float64)
+    scores = np.abs(_np(inp["k_vis_raw"]) @ Rk).mean(axis=-2)
+    idx_o, _ = op.topk_channels(scores, cfg.keep)
+    top = -np.sort(-scores, axis=-1)
+    clear = (top[..., cfg.keep - 1] - top[..., cfg.keep]) > 1e-4 * top[..., cfg.keep - 1]
+    assert clear.sum() >= cfg.H_kv // 2
+    assert np.array_equal(inp["keep_idx"].cpu().numpy()[clear], idx_o[clear])
+    args = synth.decode_args(inp)
+    out, _, _ = rotatek_decode_fused(**args)
+    torch.cuda.synchronize()
+    want = _oracle(dict(args))
+    err = np.abs(_np(out) - want).max()
+    assert err <= TOL32, err
+
+
+def test_fp32_strided_and_bf16_rotation():
+    _say("rotatek fp32 strided views, bf16 R and delta_mu")
+    inp = _rand_inputs(2, 8, 4, 32, 700, 90, torch.float32, seed=9, view_v=False)
+    inp["R_partial"] = inp["R_partial"].to(torch.bfloat16)
+    inp["delta_mu"] = inp["delta_mu"].to(torch.bfloat16)
+    big = torch.randn(2, 4, 700, 48, device="cuda")
+    big[..., :32] = inp["k_sparse"]
+    inp["k_sparse"] = big[..., :32]            # row stride 48: element loads
+    out = _decode(inp, "gqa")
+    assert np.abs(_np(out) - _oracle(inp)).max() <= TOL32
+
+
+@pytest.mark.parametrize("G", [1, 4])
+def test_fp32_dense_matches_oracle(G):
+    from rotatek_amd.kernels.full_channel_flash_decoding import full_channel_decode
+    _say(f"dense fp32 G={G}")
+    g = torch.Generator(device="cuda").manual_seed(G)
+    q = torch.randn(2, 8, 128, generator=g, device="cuda")
+    k = torch.randn(2, 8 // G, 1500, 128, generator=g, device="cuda")
+    v = torch.randn(2, 8 // G, 1500, 128, generator=g, device="cuda")
+    out = full_channel_decode(q, k, v, num_kv_groups=G)
+    torch.cuda.synchronize()
+    want = od.full_channel_decode(_np(q), _np(k), _np(v), G)
+    assert out.dtype == torch.float32
+    assert np.abs(_np(out) - want).max() <= TOL32
