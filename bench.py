@@ -468,9 +468,10 @@ def main():
     ap.add_argument("--batch-size", type=int, default=0,
                     help="override the batch (kernel_profile.py's --batch_size)")
     ap.add_argument("--merge", default="auto", choices=["auto", "two", "one"],
-                    help="decode merge: by grid size (auto), two launches, or one launch")
-    ap.add_argument("--graph-steps", type=int, default=0,
-                    help="decode steps captured per hipGraph (default: one per input copy)")
+                    help="decode merge: the library default (auto: two launches), two launches, or one launch")
+    ap.add_argument("--graph-steps", type=int, default=8,
+                    help="decode steps captured per hipGraph replay (rounded up to the input copies); "
+                         "a one-step graph is timed as well")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -544,10 +545,17 @@ def main():
     _log("[bench] warmup done")
     us = _time_wall(step, args.steps)
     us_launch = _time_launches(step, args.steps)
+    # Each hipGraph launch costs a gap of several microseconds before its
+    # first kernel (the kernel trace shows ~8 us between one replay's merge
+    # and the next replay's split kernel, none between eager launches), so a
+    # one-step graph pays it every step; several steps per replay amortise it
     per_graph = copies * max(1, -(-args.graph_steps // copies))
     us_graph = _time_graph(step, args.steps, args.warmup, per_graph) if not args.no_graph else None
+    us_graph1 = (_time_graph(step, args.steps, args.warmup, copies) if not args.no_graph and per_graph != copies
+                 else us_graph)
     gbps = nbytes / (us_launch * 1e-6) / 1e9
-    _log(f"[bench] rotatek eager {us:.1f} us/step, per-launch {us_launch:.1f} us, graph {us_graph} us, "
+    _log(f"[bench] rotatek eager {us:.1f} us/step, per-launch {us_launch:.1f} us, graph {us_graph} us "
+         f"({per_graph} steps per replay; one-step replays {us_graph1} us), "
          f"{gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS * 100:.1f}% of peak)")
 
     extra = {}
@@ -612,6 +620,7 @@ def main():
         "pct_of_peak_hbm": round(gbps / HBM_PEAK_GBPS * 100, 2),
         "graph_us_per_step": round(us_graph, 2) if us_graph else None,
         "graph_steps_per_replay": per_graph,
+        "graph_one_step_replay_us": round(us_graph1, 2) if us_graph1 else None,
         "input_copies": copies,
         "launch_us": round(us_launch, 2),
         "roofline": {

@@ -1154,7 +1154,7 @@ constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
 constexpr int64_t kSlotLatencyBytes = INT64_C(128) << 10;
 constexpr int64_t kMinWgsPerUnit = 8;
 
-// Merge mode (rk_set_decode_merge): 0 = by grid size, 1 = two launches,
+// Merge mode (rk_set_decode_merge): 0 (default) and 1 = two launches,
 // 2 = single launch where the ticket region holds the counters.
 int32_t g_merge_mode = 0;
 
@@ -1176,16 +1176,20 @@ WsLayout ws_layout(const rk_decode_plan& p) {
   return w;
 }
 
-// Single-launch merge for a plan: the grid fits in `max_rounds` rounds of
-// resident workgroups (two per CU).  On grids of many rounds every
-// workgroup would hold its slot through the wait for its record stores and
-// its ticket, while the second launch costs a few microseconds once.
-constexpr int64_t kFusedMaxRounds = 2;
+// Single-launch merge only on request (mode 2) and where the counters fit.
+// Measured on MI355X with per-workgroup timestamps, one launch ends no
+// earlier than two: its tail (record stores written through and waited
+// for, ~2 us under load; the ticket, ~0.5 us; the last workgroup's merge,
+// ~3.5 us) is as long as the kernel boundary plus the merge kernel, and the
+// split phase's slowest workgroup finishes 1-2 us later (B=8 with 4 KV heads
+// of 7 query heads, 12001 + 61 tokens: both end at 34 us; over 28 layers in
+// one graph, one launch 938 us against 891 us per step).  On grids of many
+// rounds it is worse still: every workgroup holds its slot through its own
+// wait (B=32, 16k context: 935 against 815 us).
 bool use_single_launch(const rk_decode_plan& p, int64_t B, int cus) {
+  (void)cus;
   if (p.units + B > (int64_t)(RK_DECODE_TICKET_BYTES / sizeof(uint32_t))) return false;
-  if (g_merge_mode == 1) return false;
-  if (g_merge_mode == 2) return true;
-  return p.grid <= kFusedMaxRounds * (int64_t)cus * g_wgs_per_cu;
+  return g_merge_mode == 2;
 }
 
 }  // namespace
