@@ -79,7 +79,9 @@ typedef enum rk_status {
   RK_ERR_WORKSPACE = -9,     /* workspace NULL, misaligned or too small     */
   RK_ERR_ARG = -10,          /* other invalid scalar argument               */
   RK_ERR_HIP = -11,          /* a HIP runtime call failed                   */
-  RK_ERR_NO_DEVICE = -12     /* no HIP device visible                       */
+  RK_ERR_NO_DEVICE = -12,    /* no HIP device visible                       */
+  RK_ERR_SCRATCH = -13       /* problem too large for the allocation-free
+                                entry point's fixed scratch                 */
 } rk_status;
 
 /* Decode launch policy (ROTATEK_KERNEL). */
@@ -141,6 +143,26 @@ int rk_rotatek_decode(const rk_tensor* q_full, const rk_tensor* R_partial,
                       int64_t num_kv_groups, const rk_tensor* out,
                       int32_t policy, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/* Allocation-free variant of rk_rotatek_decode.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, results (bit for bit) and errors as
+ * rk_rotatek_decode, without the workspace: the split partials and the
+ * merge counters live in a fixed device array of RK_NOALLOC_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends
+ * (its address is resolved, and its counters cleared, by the first call
+ * on each device).  A shape whose workspace would exceed it returns
+ * RK_ERR_SCRATCH (rk_rotatek_decode_check reports the bytes needed).
+ * Nothing is allocated by this call.  Calls that overlap on one GPU (other
+ * streams, other threads) share the array and race; serialise them. */
+#define RK_NOALLOC_SCRATCH_BYTES (16u * 1024u * 1024u)
+int rk_rotatek_decode_noalloc(const rk_tensor* q_full, const rk_tensor* R_partial,
+                              const rk_tensor* delta_mu, const rk_tensor* k_full,
+                              const rk_tensor* v_full, const rk_tensor* mask_full,
+                              const rk_tensor* k_sparse, const rk_tensor* v_sparse,
+                              int64_t num_kv_groups, const rk_tensor* out,
+                              int32_t policy, void* stream);
 
 /* Variable-length variant for a preallocated span cache (no reference
  * counterpart: the reference re-concatenates the spans every decode step,

@@ -20,8 +20,9 @@ RK_F16, RK_BF16, RK_F32, RK_F64, RK_U8, RK_I32, RK_I64 = range(7)
 RK_POLICY_PAPER, RK_POLICY_GQA = 0, 1
 # rk_status (include/rotatek_hip.h)
 (RK_OK, RK_ERR_NULL, RK_ERR_RANK, RK_ERR_DTYPE, RK_ERR_SHAPE, RK_ERR_HEADS, RK_ERR_HEAD_DIM, RK_ERR_KEEP_DIM,
- RK_ERR_STRIDE, RK_ERR_WORKSPACE, RK_ERR_ARG, RK_ERR_HIP, RK_ERR_NO_DEVICE) = (0, -1, -2, -3, -4, -5, -6, -7, -8,
-                                                                               -9, -10, -11, -12)
+ RK_ERR_STRIDE, RK_ERR_WORKSPACE, RK_ERR_ARG, RK_ERR_HIP, RK_ERR_NO_DEVICE,
+ RK_ERR_SCRATCH) = (0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10, -11, -12, -13)
+NOALLOC_SCRATCH_BYTES = 16 * 1024 * 1024  # RK_NOALLOC_SCRATCH_BYTES
 
 _DTYPES = {
     torch.float16: RK_F16,
@@ -35,7 +36,7 @@ _DTYPES = {
 }
 
 # status codes whose Python counterpart is ValueError (bad arguments)
-_VALUE_ERRORS = {-2, -3, -4, -5, -6, -7, -8, -10}
+_VALUE_ERRORS = {-2, -3, -4, -5, -6, -7, -8, -10, -13}
 
 
 class RkTensor(ctypes.Structure):
@@ -74,6 +75,8 @@ _SIGNATURES = {
     "rk_rotatek_decode": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int64, _P,
                                          ctypes.c_int32, ctypes.c_void_p, ctypes.c_size_t,
                                          ctypes.c_void_p]),
+    "rk_rotatek_decode_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int64, _P,
+                                                 ctypes.c_int32, ctypes.c_void_p]),
     "rk_rotatek_decode_varlen": (ctypes.c_int, [_P, _P, _P, _P, _P, ctypes.c_int64, ctypes.c_int64, _P, _P, _P,
                                                 ctypes.c_int64, _P, _P, ctypes.c_void_p, _P, ctypes.c_int32,
                                                 ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),

@@ -36,6 +36,7 @@ extern "C" const char* rk_strerror(int status) {
     case RK_ERR_ARG: return "invalid argument";
     case RK_ERR_HIP: return "HIP runtime error";
     case RK_ERR_NO_DEVICE: return "no HIP device available";
+    case RK_ERR_SCRATCH: return "workspace needed exceeds the allocation-free scratch (RK_NOALLOC_SCRATCH_BYTES)";
     default: return "unknown status";
   }
 }

@@ -39,6 +39,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "rk_common.h"
 #include "rotatek_hip.h"
 
@@ -1851,4 +1853,64 @@ extern "C" int rk_full_channel_decode(const rk_tensor* q, const rk_tensor* k, co
   if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
   return run_decode(c, q, nullptr, nullptr, k, v, nullptr, nullptr, nullptr, out, policy, workspace,
                     workspace_bytes, stream, false);
+}
+
+// ---- allocation-free decode (rk_rotatek_decode_noalloc)
+// The workspace of the other entry points, as a file-scope device array:
+// each GPU the library runs on holds its own copy until the process ends.
+// Host code never uses the array's name as a device address (on the host
+// it is only a stand-in): hipGetSymbolAddress gives each device's address,
+// once per device, and that pointer is what the kernels receive.
+static __device__ __align__(256) unsigned char scratch[RK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// This device's `scratch`: on the first call on a device, its address
+// (checked) and a cleared ticket region (a fill kernel on `stream`, ahead
+// of the decode that follows on the same stream).
+int device_scratch(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return RK_ERR_NO_DEVICE;
+  if (dev >= kMaxDevices) return RK_ERR_ARG;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RK_ERR_HIP;
+    const int st = rk_decode_workspace_init(p, RK_DECODE_TICKET_BYTES, stream);
+    if (st) return st;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return RK_OK;
+}
+
+}  // namespace
+
+extern "C" int rk_rotatek_decode_noalloc(const rk_tensor* q_full, const rk_tensor* R_partial,
+                                         const rk_tensor* delta_mu, const rk_tensor* k_full,
+                                         const rk_tensor* v_full, const rk_tensor* mask_full,
+                                         const rk_tensor* k_sparse, const rk_tensor* v_sparse,
+                                         int64_t num_kv_groups, const rk_tensor* out, int32_t policy,
+                                         void* stream) {
+  Checked c;
+  int st = check_rotatek(q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse,
+                         num_kv_groups, &c);
+  if (st) return st;
+  if (!out) return RK_ERR_NULL;
+  if ((st = check_out(out, c))) return st;
+  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
+  const int32_t pol = rotatek_policy(policy, c.G);
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  rk_decode_plan p;
+  if ((st = plan_for(c, true, pol, cus, &p))) return st;
+  if (p.workspace_bytes > RK_NOALLOC_SCRATCH_BYTES) return RK_ERR_SCRATCH;
+  void* ws = nullptr;
+  if ((st = device_scratch((hipStream_t)stream, &ws))) return st;
+  return run_decode(c, q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse, out, pol,
+                    ws, RK_NOALLOC_SCRATCH_BYTES, stream, true);
 }

@@ -1,0 +1,107 @@
+"""GPU check of the allocation-free decode entry point
+(rk_rotatek_decode_noalloc, a fixed device scratch array in place of the
+workspace): through the C ABI it must equal rk_rotatek_decode bit for bit,
+on two calls in a row, the second with a smaller input, under both merges;
+an oversized problem is refused with RK_ERR_SCRATCH before any launch.
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from rotatek_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _inputs(B, Hq, Hkv, Dk, S_v, S_f, dtype, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+
+    def rn(*s, scale=1.0):
+        return (torch.randn(*s, generator=g, device="cuda") * scale).to(dtype)
+
+    R = torch.linalg.qr(torch.randn(B, Hkv, 128, 128, generator=g, device="cuda"))[0][..., :Dk]
+    V = rn(B, Hkv, S_v + S_f, 128)
+    return [rn(B, Hq, 128), R.contiguous().to(dtype), rn(B, Hkv, 128, scale=0.5), rn(B, Hkv, S_f, 128),
+            V[:, :, S_v:], (torch.rand(B, S_f, generator=g, device="cuda") >= 0.2).to(torch.uint8),
+            rn(B, Hkv, S_v, Dk, scale=2.0), V[:, :, :S_v]]
+
+
+def _run(entry, tensors, G, policy):
+    """out via the C ABI: entry 'workspace' (rk_rotatek_decode) or 'noalloc'."""
+    lib = _lib.load()
+    q = tensors[0]
+    out = torch.empty_like(q)
+    d = [_lib.desc(t) for t in tensors]
+    do = _lib.desc(out)
+    stream = _lib.stream_handle(q.device)
+    if entry == "noalloc":
+        st = lib.rk_rotatek_decode_noalloc(*[ctypes.byref(x) for x in d], G, ctypes.byref(do), policy, stream)
+    else:
+        need = ctypes.c_size_t(0)
+        _lib.check(lib.rk_rotatek_decode_check(*[ctypes.byref(x) for x in d], G, ctypes.byref(do), policy, 0,
+                                               ctypes.byref(need)), "check")
+        ws = _lib.workspace(q.device, need.value)
+        st = lib.rk_rotatek_decode(*[ctypes.byref(x) for x in d], G, ctypes.byref(do), policy, ws.data_ptr(),
+                                   ws.numel(), stream)
+    torch.cuda.synchronize()
+    return st, out
+
+
+@pytest.mark.parametrize("merge", [_lib.MERGE_TWO_LAUNCHES, _lib.MERGE_SINGLE_LAUNCH])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_noalloc_matches_workspace_entry(dtype, merge):
+    _lib.set_decode_merge(merge)
+    try:
+        # a larger call, then a smaller one: the second must not see the first's records
+        for i, (B, Hq, Hkv, S_v, S_f) in enumerate([(8, 28, 4, 12001, 61), (2, 8, 8, 900, 33)]):
+            _say(f"noalloc {dtype} merge={merge} call {i}: B={B} Hq={Hq} Hkv={Hkv} S_v={S_v} S_f={S_f}")
+            t = _inputs(B, Hq, Hkv, 32, S_v, S_f, dtype, seed=100 + i)
+            G = Hq // Hkv
+            st_w, want = _run("workspace", t, G, _lib.RK_POLICY_GQA)
+            st_n, got = _run("noalloc", t, G, _lib.RK_POLICY_GQA)
+            assert st_w == 0 and st_n == 0, (st_w, st_n)
+            assert torch.equal(got, want)
+    finally:
+        _lib.set_decode_merge(_lib.MERGE_AUTO)
+
+
+def test_noalloc_fp32_and_paper_family():
+    _say("noalloc fp32, paper family")
+    t = _inputs(1, 8, 8, 32, 700, 50, torch.float32, seed=7)
+    st_w, want = _run("workspace", t, 1, _lib.RK_POLICY_PAPER)
+    st_n, got = _run("noalloc", t, 1, _lib.RK_POLICY_PAPER)
+    assert st_w == 0 and st_n == 0
+    assert torch.equal(got, want)
+
+
+def test_noalloc_rejects_oversized_problem():
+    """A plan whose partials exceed the scratch is refused before any launch."""
+    _say("noalloc oversized plan")
+    B, Hq, Hkv, S_v, S_f = 64, 64, 64, 40000, 100
+    need = _lib.plan_decode(B, Hq, Hkv, 32, S_v, S_f, 2, _lib.RK_POLICY_PAPER,
+                            torch.cuda.get_device_properties(0).multi_processor_count)["workspace_bytes"]
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    # descriptors only (no device memory behind K/V): the size check comes first
+    def t(shape, dt=_lib.RK_BF16):
+        d = _lib.RkTensor()
+        d.data, d.dtype, d.ndim = 0, dt, len(shape)
+        acc = 1
+        for i in reversed(range(len(shape))):
+            d.shape[i], d.stride[i] = shape[i], acc
+            acc *= shape[i]
+        return d
+    ds = [t((B, Hq, 128)), t((B, Hkv, 128, 32)), t((B, Hkv, 128)), t((B, Hkv, S_f, 128)), t((B, Hkv, S_f, 128)),
+          t((B, S_f), _lib.RK_U8), t((B, Hkv, S_v, 32)), t((B, Hkv, S_v, 128))]
+    o = t((B, Hq, 128))
+    st = _lib.load().rk_rotatek_decode_noalloc(*[ctypes.byref(x) for x in ds], 1, ctypes.byref(o),
+                                               _lib.RK_POLICY_PAPER, None)
+    assert st == _lib.RK_ERR_SCRATCH
+    with pytest.raises(ValueError, match="allocation-free"):
+        _lib.check(st, "noalloc")
