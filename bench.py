@@ -341,6 +341,8 @@ def run_prefill(args):
         kv = st["K"][:, :, c.prompt:c.prompt + S_v]
         (mean, cov), t_cov, _ = timed(lambda: prefill.key_covariance(kv))
         covw, t_qw, _ = timed(lambda: prefill.query_weight(cov, st["Q"], c.G))
+        # the weighting folded into the covariance's last launch (what update_rotatek runs)
+        _, t_covw, _ = timed(lambda: prefill.key_covariance(kv, st["Q"], c.G))
         _, _, w_eigh = timed(lambda: prefill.eigen_rotation(covw, on_host=True), graph=False)
         R_full, _, w_eigh_dev = timed(lambda: prefill.eigen_rotation(covw, on_host=False), graph=False)
         _, t_pi, _ = timed(lambda: power_iteration_gpu(covw, keep, num_iters=5, seed=0), graph=False)
@@ -355,7 +357,9 @@ def run_prefill(args):
                "covariance_us": round(t_cov, 2),
                "covariance_gbps_two_passes": round(2 * kbytes / t_cov / 1e3, 1),
                "covariance_mfma_tflops": round(cov_flops / t_cov / 1e6, 2),
-               "query_weight_us": round(t_qw, 2), "eigh_host_us": round(w_eigh, 1),
+               "query_weight_us": round(t_qw, 2),
+               "covariance_weighted_us": round(t_covw, 2),
+               "eigh_host_us": round(w_eigh, 1),
                "eigh_device_us": round(w_eigh_dev, 1),
                "power_iteration_us": round(t_pi, 2),
                "channel_scores_us": round(t_sc, 2), "topk_us": round(t_tk, 2),

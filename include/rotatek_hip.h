@@ -26,6 +26,9 @@
  *   rk_key_covariance      integrations/lmms_eval/models/model_utils/
  *                          kv_pruning_utils.py:112-115 (mean, centering,
  *                          covariance einsum, symmetrisation)
+ *   rk_key_covariance_weighted   kv_pruning_utils.py:112-140 (the above
+ *                          plus the query-aware weighting and ridge)
+ *   rk_query_weight        kv_pruning_utils.py:116-140 (weighting alone)
  *   rk_rotate_keys         kv_pruning_utils.py:152 (K_vis @ R_partial, the
  *                          truncated visual-Key write)
  *   rk_channel_scores      channel scoring of the head-wise top-k selection
@@ -281,6 +284,19 @@ int rk_key_covariance_check(const rk_tensor* keys, const rk_tensor* mean_out,
 int rk_key_covariance(const rk_tensor* keys, const rk_tensor* mean_out,
                       const rk_tensor* cov_out, void* workspace,
                       size_t workspace_bytes, void* stream);
+
+/* Key covariance followed by the query-aware weighting, in the same three
+ * launches as rk_key_covariance (the weighting is folded into the last):
+ * cov_out = the result of rk_key_covariance then rk_query_weight, bit for
+ * bit (kv_pruning_utils.py:112-140).  queries [B,H_kv*G,S_q,128] in the key
+ * dtype, window 1..32 (the last min(window, S_q) rows).  Workspace size
+ * from the _check variant (the same as rk_key_covariance's). */
+int rk_key_covariance_weighted_check(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_groups,
+                                     int32_t window, const rk_tensor* mean_out, const rk_tensor* cov_out,
+                                     int32_t num_cus, size_t* workspace_bytes);
+int rk_key_covariance_weighted(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_groups,
+                               int32_t window, const rk_tensor* mean_out, const rk_tensor* cov_out,
+                               void* workspace, size_t workspace_bytes, void* stream);
 
 /* Truncated visual-Key write (kv_pruning_utils.py:152):
  * out[b,h,s,:] = dtype(K[b,h,s,:] @ R_partial[b,h]), R_partial

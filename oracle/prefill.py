@@ -174,23 +174,32 @@ def topk_channels(scores, k: int):
 
 def update_rotatek(key_states, query_states, prompt_seqlen: int, query_seqlen: int,
                    ratio: float, num_kv_groups: int, dtype: str,
-                   query_aware: bool = True, select: str = "eig", R_full=None):
+                   query_aware: bool = True, select: str = "eig", R_full=None, cov=None, mean=None):
     """ChannelPruner.update_rotatek (kv_pruning_utils.py:92-160), eigh solver.
 
     select="eig": kept channels are the top-``keep`` eigenvectors (the
     reference rule, kept mask = first ``keep`` rotated channels).
     select="score": rotate by the full basis (``R_full`` if given, else all
     eigenvectors, eigenvalue-descending) and keep the top-``keep`` channels by
-    mean |K R|.  Returns a dict of numpy arrays.
+    mean |K R|.  ``cov`` (the weighted covariance) and ``mean`` (fp32) replace
+    the computed ones, so that a test can compare the stages after them on
+    the very same input.  Returns a dict of numpy arrays.
     """
     K = np.asarray(key_states, np.float64)
     B, Hkv, S, D = K.shape
     (p0, p1), (v0, v1), (t0, t1) = split_spans(S, prompt_seqlen, query_seqlen)
     Kv = K[:, :, v0:v1]
     keep = keep_count(D, ratio)
-    mean, cov = key_covariance(Kv, dtype)
-    if query_aware:
-        cov = query_weight(cov, query_states, num_kv_groups, dtype=dtype)
+    if cov is None:
+        mean_c, cov = key_covariance(Kv, dtype)
+        if query_aware:
+            cov = query_weight(cov, query_states, num_kv_groups, dtype=dtype)
+        mean = mean_c if mean is None else mean
+    else:
+        cov = np.asarray(cov, np.float64)
+        if mean is None:
+            mean = key_covariance(Kv, dtype)[0]
+        mean = np.asarray(mean, np.float64)
     if select == "eig":
         Rp, evals = eigh_rotation(cov, keep)
         idx = np.broadcast_to(np.arange(keep), (B, Hkv, keep)).copy()

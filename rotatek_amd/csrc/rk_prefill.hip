@@ -522,44 +522,17 @@ __global__ void __launch_bounds__(128) gather_kernel(const void* R, int r_dtype,
 // transposed read is conflict-free; out may alias cov.  CV / QV: 16-byte
 // row loads of the covariance / the queries (unit inner stride, aligned).
 constexpr int kQHeads = 8;  // query heads whose window rows are loaded together (G <= 8: one batch)
-template <class TT, bool CV, bool QV>
-__global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t c_b, int64_t c_h, int64_t c_r,
-                                                      int64_t c_c, const uint16_t* q, int64_t q_b, int64_t q_h,
-                                                      int64_t q_s, int64_t q_d, int64_t S, int W, int G,
-                                                      float inv_g, float* out, int64_t o_b, int64_t o_h,
-                                                      int64_t o_r, int64_t o_c, int H) {
-  constexpr int CP = 129;
-  __shared__ float s_C[128 * CP];
-  __shared__ float s_part[16][128];
-  __shared__ __align__(16) float s_qn[128];
-  __shared__ float s_wsum[2];
-  __shared__ float s_floor;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int bh = blockIdx.x, b = bh / H, kv = bh - b * H;
-  const float* C = cov + b * c_b + (int64_t)kv * c_h;
 
-  // ---- covariance loads (64 floats per thread)
-  float cv[64];
-  if constexpr (CV) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e4 = tid + 256 * i, r = e4 >> 5, c = (e4 & 31) * 4;
-      const float4 v = *(const float4*)(C + r * c_r + c);
-      cv[4 * i] = v.x, cv[4 * i + 1] = v.y, cv[4 * i + 2] = v.z, cv[4 * i + 3] = v.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const int e = tid + 256 * i;
-      cv[i] = C[(e >> 7) * c_r + (e & 127) * c_c];
-    }
-  }
-
-  // ---- query rows: group sums in fp32, G in order, kQHeads heads' loads at a time
+// Thread (rs = t/16, c8 = t%16) of 256: the fp32 sums over the G query
+// heads of window rows rs and rs + 16 (of the last W rows), channels
+// 8 c8..8 c8+7, G in order, kQHeads heads' loads issued at a time.
+template <class TT, bool QV>
+__device__ __forceinline__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, int64_t q_s,
+                                                  int64_t q_d, int64_t S, int W, int G, int b, int kv, int tid,
+                                                  float (&acc)[2][8]) {
   const int rs = tid >> 4, c8 = tid & 15;
   const int w0 = rs, w1 = rs + 16;
   const uint16_t* qb = q + b * q_b + (int64_t)(kv * G) * q_h + (S - W) * q_s + (int64_t)(8 * c8) * q_d;
-  float acc[2][8];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -596,34 +569,25 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
         }
       }
   }
+}
 
-  // ---- the covariance into LDS
-  if constexpr (CV) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e4 = tid + 256 * i, r = e4 >> 5, c = (e4 & 31) * 4;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) s_C[r * CP + c + u] = cv[4 * i + u];
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const int e = tid + 256 * i;
-      s_C[(e >> 7) * CP + (e & 127)] = cv[i];
-    }
-  }
-
-  // ---- group mean in the query dtype, then the squares: fp32 sum times
-  // torch's mean factor inv_g (formed on the host), rounded to fp32 first and
-  // then to the dtype, as torch's MeanOps does;
-  // the empty asm keeps the product in an fp32 register (otherwise the
-  // multiply and the conversion fuse into one v_fma_mix, a single rounding)
+// From the window group sums: the group mean in the query dtype (fp32 sum
+// times torch's mean factor inv_g, formed on the host, rounded to fp32
+// first and then to the dtype, as torch's MeanOps does; the empty asm keeps
+// the product in an fp32 register, otherwise the multiply and the
+// conversion fuse into one v_fma_mix, a single rounding), the per-channel
+// L2 norms over the window, and the floor at 1e-3 x the lower median (the
+// norm of rank 63, ties by index).  Leaves s_qn[c] = the floored norms.
+template <class TT>
+__device__ __forceinline__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g, int tid,
+                                                    float (*s_part)[128], float* s_qn, float* s_floor) {
+  const int rs = tid >> 4, c8 = tid & 15;
   float sq[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) sq[e] = 0.f;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    if ((j ? w1 : w0) < W) {
+    if ((j ? rs + 16 : rs) < W) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float prod = acc[j][e] * inv_g;
@@ -643,9 +607,9 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
     s_qn[tid] = sqrtf(t);
   }
   __syncthreads();
-  // ---- lower median: the norm of rank 63 (ties by index)
+  float v = 0.f;
   if (tid < 128) {
-    const float v = s_qn[tid];
+    v = s_qn[tid];
     int rank = 0;
 #pragma unroll
     for (int j4 = 0; j4 < 32; ++j4) {
@@ -654,20 +618,92 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
 #pragma unroll
       for (int e = 0; e < 4; ++e) rank += (uu[e] < v) || (uu[e] == v && 4 * j4 + e < tid);
     }
-    if (rank == 63) s_floor = 1e-3f * v;
+    if (rank == 63) *s_floor = 1e-3f * v;
   }
   __syncthreads();
-  // ---- floored norms and mean |diag| of the weighted matrix (waves 0, 1)
+  if (tid < 128) s_qn[tid] = fmaxf(v, *s_floor);
+  __syncthreads();
+}
+
+// 1e-4 max(mean|diag(C o qn qn^T)|, 1e-6) from the diagonal dg_in[c] =
+// C[c][c] (threads 0..127; the sum is a fixed xor tree in each of waves 0
+// and 1, then the two halves), as the weighted covariance's ridge.
+__device__ __forceinline__ float weighted_ridge(float diag, const float* s_qn, int tid, float* s_wsum) {
   if (tid < 128) {
-    const float qd = fmaxf(s_qn[tid], s_floor);
-    float dg = fabsf(s_C[tid * CP + tid] * (qd * qd));
+    const float qd = s_qn[tid];
+    float dg = fabsf(diag * (qd * qd));
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) dg += shfl_xor(dg, off);
-    if (lane == 0) s_wsum[wave] = dg;
-    s_qn[tid] = qd;
+    if ((tid & 63) == 0) s_wsum[tid >> 6] = dg;
   }
   __syncthreads();
-  const float ridge = 1e-4f * fmaxf((s_wsum[0] + s_wsum[1]) * (1.f / 128.f), 1e-6f);
+  return 1e-4f * fmaxf((s_wsum[0] + s_wsum[1]) * (1.f / 128.f), 1e-6f);
+}
+
+// grid (B*H_kv), 256 threads: query-aware weighting of one covariance
+// (kv_pruning_utils.py:116-140).  q_norm[d] = || mean_g q[g, S-W+w, d] ||_2
+// over the last W queries, the group mean (over the G query heads of the KV
+// head) rounded to the query dtype as torch's bf16/fp16 mean is; floored at
+// 1e-3 x the lower median of the 128 norms; then
+//   out = 0.5 (C o (qn qn^T) + (C o (qn qn^T))^T) + 1e-4 max(mean|diag|, 1e-6) I
+// (the clamp binds to the mean).  Every global load (the covariance and the
+// G x W query rows) is issued before the first is used, so the kernel costs
+// one memory latency plus its LDS work.  The covariance goes through LDS
+// (rows padded to 129), so the transposed read is conflict-free; out may
+// alias cov.  CV / QV: 16-byte row loads of the covariance / the queries
+// (unit inner stride, aligned).
+template <class TT, bool CV, bool QV>
+__global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t c_b, int64_t c_h, int64_t c_r,
+                                                      int64_t c_c, const uint16_t* q, int64_t q_b, int64_t q_h,
+                                                      int64_t q_s, int64_t q_d, int64_t S, int W, int G,
+                                                      float inv_g, float* out, int64_t o_b, int64_t o_h,
+                                                      int64_t o_r, int64_t o_c, int H) {
+  constexpr int CP = 129;
+  __shared__ float s_C[128 * CP];
+  __shared__ float s_part[16][128];
+  __shared__ __align__(16) float s_qn[128];
+  __shared__ float s_wsum[2];
+  __shared__ float s_floor;
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.x, b = bh / H, kv = bh - b * H;
+  const float* C = cov + b * c_b + (int64_t)kv * c_h;
+
+  // ---- covariance loads (64 floats per thread)
+  float cv[64];
+  if constexpr (CV) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e4 = tid + 256 * i, r = e4 >> 5, c = (e4 & 31) * 4;
+      const float4 v = *(const float4*)(C + r * c_r + c);
+      cv[4 * i] = v.x, cv[4 * i + 1] = v.y, cv[4 * i + 2] = v.z, cv[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int e = tid + 256 * i;
+      cv[i] = C[(e >> 7) * c_r + (e & 127) * c_c];
+    }
+  }
+  float acc[2][8];
+  window_group_sums<TT, QV>(q, q_b, q_h, q_s, q_d, S, W, G, b, kv, tid, acc);
+
+  // ---- the covariance into LDS
+  if constexpr (CV) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e4 = tid + 256 * i, r = e4 >> 5, c = (e4 & 31) * 4;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) s_C[r * CP + c + u] = cv[4 * i + u];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int e = tid + 256 * i;
+      s_C[(e >> 7) * CP + (e & 127)] = cv[i];
+    }
+  }
+  floored_query_norms<TT>(acc, W, inv_g, tid, s_part, s_qn, &s_floor);
+  const float ridge = weighted_ridge(tid < 128 ? s_C[tid * CP + tid] : 0.f, s_qn, tid, s_wsum);
   // ---- out[r][c] = 0.5 (C[r][c] w + C[c][r] w) + ridge [r == c], w = qn[r] qn[c]
   float* O = out + b * o_b + (int64_t)kv * o_h;
 #pragma unroll 8
@@ -677,6 +713,59 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
     const float a = s_C[r * CP + c] * w, bt = s_C[c * CP + r] * w;
     O[r * o_r + c * o_c] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
   }
+}
+
+// grid (kTiles, B*H), 256 threads: covfin_kernel and the query-aware
+// weighting in one launch, bit-identical to covfin_kernel followed by
+// qweight_kernel.  Each tile workgroup sums its tile's partials (as
+// covfin), the 128 diagonal entries' partials (for the ridge), and the
+// window query rows of its KV head (for the norms), all loads in flight
+// together; it then writes its weighted tile and the mirror:
+//   out[r][c] = 0.5 (a + a) + ridge [r == c],  a = sym[r][c] (qn[r] qn[c]),
+// sym = 0.5 (C[r][c] + C[c][r]) the symmetrised covariance, which is what
+// qweight_kernel reads back from covfin's output.
+template <class TT, bool QV>
+__global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, int splits,
+                                                             const float* mean_part, int mean_splits, float mfac,
+                                                             const uint16_t* q, int64_t q_b, int64_t q_h,
+                                                             int64_t q_s, int64_t q_d, int64_t S, int W, int G,
+                                                             float inv_g, float* cov, int64_t cs_b, int64_t cs_h,
+                                                             int64_t cs_r, int64_t cs_c, float* mu, int64_t ms_b,
+                                                             int64_t ms_h, int64_t ms_c, int H) {
+  __shared__ float s_t[256];
+  __shared__ float s_part[16][128];
+  __shared__ __align__(16) float s_qn[128];
+  __shared__ float s_wsum[2];
+  __shared__ float s_floor;
+  const int tid = threadIdx.x, t = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / H, h = bh - b * H;
+  const float* pb = part + (int64_t)bh * splits * (kTiles * 256);
+  // tile entry tid and (threads < 128) diagonal entry C[tid][tid]: tile
+  // (tid % 8, tid % 8), entry 17 (tid / 8)
+  float sum = strided_sum(pb + t * 256 + tid, splits, kTiles * 256);
+  const int dt = tile_index(tid & 7, tid & 7);
+  float dsum = strided_sum(pb + dt * 256 + 17 * ((tid & 127) >> 3), splits, kTiles * 256);
+  float acc[2][8];
+  window_group_sums<TT, QV>(q, q_b, q_h, q_s, q_d, S, W, G, b, h, tid, acc);
+  asm volatile("" : "+v"(sum));  // fp32, then the key dtype (two roundings)
+  asm volatile("" : "+v"(dsum));
+  s_t[tid] = TT::to_f32(TT::from_f32(sum));
+  const float dx = TT::to_f32(TT::from_f32(dsum));
+  const float diag = 0.5f * (dx + dx);  // the symmetrised diagonal, as covfin writes it
+  floored_query_norms<TT>(acc, W, inv_g, tid, s_part, s_qn, &s_floor);  // (syncs s_t too)
+  const float ridge = weighted_ridge(diag, s_qn, tid, s_wsum);
+  const int i = tile_row(t), j = tile_col(t), m = tid >> 4, n = tid & 15;
+  float* cb = cov + b * cs_b + (int64_t)h * cs_h;
+  const int r = 8 * m + i, c = 8 * n + j;
+  const float rc = s_t[tid];
+  const float cr = i == j ? s_t[n * 16 + m] : rc;
+  const float sym = 0.5f * (rc + cr), symt = 0.5f * (cr + rc);
+  const float w = s_qn[r] * s_qn[c];
+  const float a = sym * w, bt = symt * w;
+  cb[r * cs_r + c * cs_c] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
+  if (i != j) cb[c * cs_r + r * cs_c] = 0.5f * (bt + a);
+  if (t == 0 && tid < 128 && mu)
+    mu[b * ms_b + (int64_t)h * ms_h + tid * ms_c] = head_mean(mean_part, bh, mean_splits, tid, mfac);
 }
 
 }  // namespace prefill
@@ -762,9 +851,19 @@ int check_f32_out(const rk_tensor* t, int ndim, int64_t B, int64_t H, int64_t la
   return RK_OK;
 }
 
+// Query-aware weighting fused into the covariance's last launch.
+struct QwArgs {
+  const rk_tensor* q;
+  int64_t G;
+  int W;
+  float inv_g;
+  bool vec;
+};
+
 template <class TT>
 hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, float* ws, float* cov,
-                      const rk_tensor* cov_t, float* mu, const rk_tensor* mu_t, hipStream_t s) {
+                      const rk_tensor* cov_t, float* mu, const rk_tensor* mu_t, hipStream_t s,
+                      const QwArgs* qw = nullptr) {
   const int64_t bh = B * k.H;
   float* mpart = (float*)((char*)ws + p.off_mean);
   float* cpart = (float*)((char*)ws + p.off_cov);
@@ -779,6 +878,21 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
     hipLaunchKernelGGL((mean_kernel<TT, false>), gm, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits, mpart);
     hipLaunchKernelGGL((cov_kernel<TT, false>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
                        p.mean_splits, mfac, cpart);
+  }
+  if (qw) {
+    const rk_tensor* q = qw->q;
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits, mpart,
+                         p.mean_splits, mfac, (const uint16_t*)q->data, q->stride[0], q->stride[1], q->stride[2],
+                         q->stride[3], q->shape[2], qw->W, (int)qw->G, qw->inv_g, cov, cov_t->stride[0],
+                         cov_t->stride[1], cov_t->stride[2], cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0,
+                         mu_t ? mu_t->stride[1] : 0, mu_t ? mu_t->stride[2] : 0, k.H);
+    };
+    if (qw->vec)
+      go(covfin_qw_kernel<TT, true>);
+    else
+      go(covfin_qw_kernel<TT, false>);
+    return hipGetLastError();
   }
   hipLaunchKernelGGL((covfin_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits,
                      mpart,
@@ -830,6 +944,71 @@ extern "C" int rk_key_covariance(const rk_tensor* keys, const rk_tensor* mean_ou
                                 mean_out ? (float*)mean_out->data : nullptr, mean_out, s)
           : launch_cov<rk::BF16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
                                  mean_out ? (float*)mean_out->data : nullptr, mean_out, s);
+  return e == hipSuccess ? RK_OK : RK_ERR_HIP;
+}
+
+namespace {
+
+// Queries of the fused weighting: [B, H_kv * G, S_q, 128] in the key dtype,
+// window = min(window, S_q) rows (window 1..32).
+int check_queries(const rk_tensor* keys, const rk_tensor* q, int64_t G, int32_t window, QwArgs* qw) {
+  if (!q) return RK_ERR_NULL;
+  int st = rk::check_desc(q, 4);
+  if (st) return st;
+  if (q->dtype != keys->dtype) return RK_ERR_DTYPE;
+  if (q->shape[3] != 128) return RK_ERR_HEAD_DIM;
+  if (G <= 0 || q->shape[0] != keys->shape[0] || q->shape[1] != keys->shape[1] * G) return RK_ERR_HEADS;
+  if (window <= 0 || window > 32) return RK_ERR_ARG;
+  const int64_t S = q->shape[2];
+  qw->q = q;
+  qw->G = G;
+  qw->W = (int)(S < window ? S : window);
+  if (keys->shape[0] * keys->shape[1] > 0 && qw->W == 0) return RK_ERR_SHAPE;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  // the group mean over dim 2 of [B, H_kv, G, W, 128] (kv_pruning_utils.py:127-129)
+  qw->inv_g = rk::mean_factor(B * H * qw->W * 128, B * H * G * qw->W * 128);
+  qw->vec = q->stride[3] == 1 && q->stride[2] % 8 == 0 && q->stride[1] % 8 == 0 && q->stride[0] % 8 == 0 &&
+            ((uintptr_t)q->data & 15) == 0;
+  return RK_OK;
+}
+
+}  // namespace
+
+extern "C" int rk_key_covariance_weighted_check(const rk_tensor* keys, const rk_tensor* queries,
+                                                int64_t num_kv_groups, int32_t window, const rk_tensor* mean_out,
+                                                const rk_tensor* cov_out, int32_t num_cus, size_t* workspace_bytes) {
+  int st = rk_key_covariance_check(keys, mean_out, cov_out, num_cus, workspace_bytes);
+  if (st) return st;
+  QwArgs qw;
+  return check_queries(keys, queries, num_kv_groups, window, &qw);
+}
+
+extern "C" int rk_key_covariance_weighted(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_groups,
+                                          int32_t window, const rk_tensor* mean_out, const rk_tensor* cov_out,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  KeyView k;
+  bool vec;
+  int st = key_view(keys, &k, &vec);
+  if (st) return st;
+  const int64_t B = keys->shape[0], H = keys->shape[1];
+  if (!cov_out) return RK_ERR_NULL;
+  if ((st = check_f32_out(cov_out, 4, B, H, 128, RK_F32))) return st;
+  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, 128, RK_F32))) return st;
+  QwArgs qw;
+  if ((st = check_queries(keys, queries, num_kv_groups, window, &qw))) return st;
+  const int cus = resolve_cus(0, &st);
+  if (st) return st;
+  const CovPlan p = cov_plan(B, H, k.S, cus);
+  if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < p.total) return RK_ERR_WORKSPACE;
+  if (B * H == 0) return RK_OK;
+  if ((k.S > 0 && !k.data) || !cov_out->data || !queries->data) return RK_ERR_NULL;
+  hipStream_t s = (hipStream_t)stream;
+  const hipError_t e =
+      keys->dtype == RK_F16
+          ? launch_cov<rk::F16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
+                                mean_out ? (float*)mean_out->data : nullptr, mean_out, s, &qw)
+          : launch_cov<rk::BF16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
+                                 mean_out ? (float*)mean_out->data : nullptr, mean_out, s, &qw);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 

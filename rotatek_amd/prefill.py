@@ -36,8 +36,14 @@ def _gpu(t: torch.Tensor, name: str) -> None:
         raise RuntimeError(f"{name} must be a GPU tensor: the RotateK prefill kernels run only on the HIP device")
 
 
-def key_covariance(keys_vision: torch.Tensor):
-    """(mean [B,H,D] fp32, cov [B,H,D,D] fp32) of ``keys_vision`` [B,H,S,D]."""
+def key_covariance(keys_vision: torch.Tensor, query_states: torch.Tensor | None = None,
+                   num_key_value_groups: int = 1):
+    """(mean [B,H,D] fp32, cov [B,H,D,D] fp32) of ``keys_vision`` [B,H,S,D].
+
+    With ``query_states`` [B, H*G, S_q, D] the covariance comes back already
+    query-weighted (``query_weight``'s result, bit for bit), the weighting
+    folded into the covariance's last launch (``rk_key_covariance_weighted``).
+    """
     _gpu(keys_vision, "keys_vision")
     B, H, _, D = keys_vision.shape
     lib = _lib.load()
@@ -45,11 +51,23 @@ def key_covariance(keys_vision: torch.Tensor):
     cov = torch.empty(B, H, D, D, device=keys_vision.device, dtype=torch.float32)
     dk, dm, dc = _lib.desc(keys_vision), _lib.desc(mean), _lib.desc(cov)
     need = ctypes.c_size_t(0)
-    _lib.check(lib.rk_key_covariance_check(ctypes.byref(dk), ctypes.byref(dm), ctypes.byref(dc), 0,
-                                           ctypes.byref(need)), "key_covariance")
+    stream = _lib.stream_handle(keys_vision.device)
+    if query_states is None:
+        _lib.check(lib.rk_key_covariance_check(ctypes.byref(dk), ctypes.byref(dm), ctypes.byref(dc), 0,
+                                               ctypes.byref(need)), "key_covariance")
+        ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device=keys_vision.device)
+        _lib.check(lib.rk_key_covariance(ctypes.byref(dk), ctypes.byref(dm), ctypes.byref(dc), ws.data_ptr(),
+                                         ws.numel(), stream), "key_covariance")
+        return mean, cov
+    dq = _lib.desc(query_states)
+    G = int(num_key_value_groups)
+    _lib.check(lib.rk_key_covariance_weighted_check(ctypes.byref(dk), ctypes.byref(dq), G, QUERY_WINDOW,
+                                                    ctypes.byref(dm), ctypes.byref(dc), 0, ctypes.byref(need)),
+               "key_covariance")
     ws = torch.empty(max(need.value, 256), dtype=torch.uint8, device=keys_vision.device)
-    _lib.check(lib.rk_key_covariance(ctypes.byref(dk), ctypes.byref(dm), ctypes.byref(dc), ws.data_ptr(),
-                                     ws.numel(), _lib.stream_handle(keys_vision.device)), "key_covariance")
+    _lib.check(lib.rk_key_covariance_weighted(ctypes.byref(dk), ctypes.byref(dq), G, QUERY_WINDOW,
+                                              ctypes.byref(dm), ctypes.byref(dc), ws.data_ptr(), ws.numel(),
+                                              stream), "key_covariance")
     return mean, cov
 
 
