@@ -206,9 +206,9 @@ def test_update_rotatek_matches_oracle(solver):
     The weighted covariance is checked against the oracle from the Keys
     (1e-5 relative); the stages after it are then compared on that very
     covariance and mean.  eigh: the stored R_partial, column signs aligned,
-    within one bf16 ulp on 99 % of the entries (four everywhere: fp32 eigh
-    against fp64), and the truncated Keys and delta_mu within one ulp of the
-    oracle's from that R_partial.
+    within one bf16 ulp on 99 % of the entries and 2e-3 everywhere (fp32
+    eigh against fp64), and the truncated Keys and delta_mu within one ulp of
+    the oracle's from that R_partial.
     Power iteration (an orthonormal basis of the same subspace, not its
     eigenvectors): the kept projector R R^T within 1e-3 and the Keys mapped
     back, K R R^T, within 1e-2 of their scale."""
@@ -236,12 +236,14 @@ def test_update_rotatek_matches_oracle(solver):
         sign = np.sign(np.einsum("bhdk,bhdk->bhk", R, Rw))[:, :, None, :]
         assert np.all(sign != 0)
         # fp32 eigh (here on the device; the reference's LAPACK call is fp32
-        # too) against the fp64 oracle: eigenvectors agree to ~n eps |C| / gap,
-        # a few 1e-4 on this spectrum, so a few entries round one bf16 ulp
-        # further apart; 99 % must be within one ulp, all within four
+        # too) against the fp64 oracle: unit eigenvectors agree to ~n eps
+        # |C| / gap, up to ~1e-3 on this spectrum, so a few entries round one
+        # or more bf16 ulps apart; 99 % must be within one ulp, all within
+        # 2e-3 (a wrong column, sign or gather is off by O(0.1))
         Ra = R * sign
         ulps = np.abs(Ra - Rw) / _storage_ulp(Ra, Rw, dtype)
-        assert np.mean(ulps <= 1.0) >= 0.99 and ulps.max() <= 4.0, (np.mean(ulps <= 1.0), ulps.max())
+        assert np.mean(ulps <= 1.0) >= 0.99, np.mean(ulps <= 1.0)
+        assert np.abs(Ra - Rw).max() <= 2e-3, np.abs(Ra - Rw).max()
         # the truncated write and delta_mu from the stored R_partial: one ulp
         # (an R entry one ulp off, where fp32 and fp64 eigh round a value
         # near a bf16 midpoint apart, moves small rotated values by more)
