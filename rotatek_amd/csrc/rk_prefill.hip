@@ -74,12 +74,40 @@ __device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
 // grid (splits, B*H): workgroup x sums tokens [x*chunk, (x+1)*chunk) of one
 // head into part[bh][x][128] (fp32).  Thread (row group rg = t/16, channel
 // chunk c8 = t%16) walks rows rg, rg+16, ... four at a time.
-template <class TT, bool VEC>
+// Query-aware weighting inputs (kv_pruning_utils.py:116-140): the window
+// query rows of each KV head's G query heads; qn receives the floored norms
+// per head ([B*H][128] fp32, in the workspace).
+struct QNormArgs {
+  const uint16_t* q;
+  int64_t q_b, q_h, q_s, q_d, S;
+  int W, G;
+  float inv_g;
+  float* qn;
+};
+
+template <class TT, bool QV>
+__device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, int64_t q_s, int64_t q_d,
+                                  int64_t S, int W, int G, int b, int kv, int tid, float (&acc)[2][8]);
+template <class TT>
+__device__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g, int tid, float (*s_part)[128],
+                                    float* s_qn, float* s_floor);
+
+template <class TT, bool VEC, bool QV = false>
 __global__ void __launch_bounds__(kThreads) mean_kernel(KeyView k, int64_t chunk, int splits,
-                                                        float* part) {
+                                                        float* part, QNormArgs qa) {
   __shared__ float s_sum[16][128];
   const int tid = threadIdx.x, rg = tid >> 4, c8 = tid & 15;
   const int x = blockIdx.x, bh = blockIdx.y;
+  if (x == splits) {  // the extra column (weighted covariance only): this head's query norms
+    __shared__ __align__(16) float s_qn[128];
+    __shared__ float s_floor;
+    const int b = bh / k.H, kv = bh - b * k.H;
+    float acc[2][8];
+    window_group_sums<TT, QV>(qa.q, qa.q_b, qa.q_h, qa.q_s, qa.q_d, qa.S, qa.W, qa.G, b, kv, tid, acc);
+    floored_query_norms<TT>(acc, qa.W, qa.inv_g, tid, s_sum, s_qn, &s_floor);
+    if (tid < 128) qa.qn[(int64_t)bh * 128 + tid] = s_qn[tid];
+    return;
+  }
   const uint16_t* base = head_base(k, bh);
   const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -527,9 +555,8 @@ constexpr int kQHeads = 8;  // query heads whose window rows are loaded together
 // heads of window rows rs and rs + 16 (of the last W rows), channels
 // 8 c8..8 c8+7, G in order, kQHeads heads' loads issued at a time.
 template <class TT, bool QV>
-__device__ __forceinline__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, int64_t q_s,
-                                                  int64_t q_d, int64_t S, int W, int G, int b, int kv, int tid,
-                                                  float (&acc)[2][8]) {
+__device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, int64_t q_s, int64_t q_d,
+                                  int64_t S, int W, int G, int b, int kv, int tid, float (&acc)[2][8]) {
   const int rs = tid >> 4, c8 = tid & 15;
   const int w0 = rs, w1 = rs + 16;
   const uint16_t* qb = q + b * q_b + (int64_t)(kv * G) * q_h + (S - W) * q_s + (int64_t)(8 * c8) * q_d;
@@ -579,8 +606,8 @@ __device__ __forceinline__ void window_group_sums(const uint16_t* q, int64_t q_b
 // L2 norms over the window, and the floor at 1e-3 x the lower median (the
 // norm of rank 63, ties by index).  Leaves s_qn[c] = the floored norms.
 template <class TT>
-__device__ __forceinline__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g, int tid,
-                                                    float (*s_part)[128], float* s_qn, float* s_floor) {
+__device__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g, int tid, float (*s_part)[128],
+                                    float* s_qn, float* s_floor) {
   const int rs = tid >> 4, c8 = tid & 15;
   float sq[8];
 #pragma unroll
@@ -717,26 +744,22 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
 
 // grid (kTiles, B*H), 256 threads: covfin_kernel and the query-aware
 // weighting in one launch, bit-identical to covfin_kernel followed by
-// qweight_kernel.  Each tile workgroup sums its tile's partials (as
-// covfin), the 128 diagonal entries' partials (for the ridge), and the
-// window query rows of its KV head (for the norms), all loads in flight
-// together; it then writes its weighted tile and the mirror:
-//   out[r][c] = 0.5 (a + a) + ridge [r == c],  a = sym[r][c] (qn[r] qn[c]),
+// qweight_kernel.  The floored query norms come from the mean launch's
+// extra column (qn [B*H][128]).  Each tile workgroup sums its tile's
+// partials (as covfin) and the 128 diagonal entries' partials (for the
+// ridge), loads in flight together, then writes its weighted tile and the
+// mirror:  out[r][c] = 0.5 (a + a) + ridge [r == c],  a = sym[r][c] (qn[r] qn[c]),
 // sym = 0.5 (C[r][c] + C[c][r]) the symmetrised covariance, which is what
 // qweight_kernel reads back from covfin's output.
-template <class TT, bool QV>
+template <class TT>
 __global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, int splits,
                                                              const float* mean_part, int mean_splits, float mfac,
-                                                             const uint16_t* q, int64_t q_b, int64_t q_h,
-                                                             int64_t q_s, int64_t q_d, int64_t S, int W, int G,
-                                                             float inv_g, float* cov, int64_t cs_b, int64_t cs_h,
-                                                             int64_t cs_r, int64_t cs_c, float* mu, int64_t ms_b,
-                                                             int64_t ms_h, int64_t ms_c, int H) {
+                                                             const float* qn, float* cov, int64_t cs_b,
+                                                             int64_t cs_h, int64_t cs_r, int64_t cs_c, float* mu,
+                                                             int64_t ms_b, int64_t ms_h, int64_t ms_c, int H) {
   __shared__ float s_t[256];
-  __shared__ float s_part[16][128];
   __shared__ __align__(16) float s_qn[128];
   __shared__ float s_wsum[2];
-  __shared__ float s_floor;
   const int tid = threadIdx.x, t = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
   const float* pb = part + (int64_t)bh * splits * (kTiles * 256);
@@ -745,14 +768,14 @@ __global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, 
   float sum = strided_sum(pb + t * 256 + tid, splits, kTiles * 256);
   const int dt = tile_index(tid & 7, tid & 7);
   float dsum = strided_sum(pb + dt * 256 + 17 * ((tid & 127) >> 3), splits, kTiles * 256);
-  float acc[2][8];
-  window_group_sums<TT, QV>(q, q_b, q_h, q_s, q_d, S, W, G, b, h, tid, acc);
+  const float qv = qn[(int64_t)bh * 128 + (tid & 127)];
   asm volatile("" : "+v"(sum));  // fp32, then the key dtype (two roundings)
   asm volatile("" : "+v"(dsum));
   s_t[tid] = TT::to_f32(TT::from_f32(sum));
+  if (tid < 128) s_qn[tid] = qv;
   const float dx = TT::to_f32(TT::from_f32(dsum));
   const float diag = 0.5f * (dx + dx);  // the symmetrised diagonal, as covfin writes it
-  floored_query_norms<TT>(acc, W, inv_g, tid, s_part, s_qn, &s_floor);  // (syncs s_t too)
+  __syncthreads();
   const float ridge = weighted_ridge(diag, s_qn, tid, s_wsum);
   const int i = tile_row(t), j = tile_col(t), m = tid >> 4, n = tid & 15;
   float* cb = cov + b * cs_b + (int64_t)h * cs_h;
@@ -817,7 +840,7 @@ int splits_for(int64_t bh, int64_t S, int cus, int64_t min_tokens) {
 struct CovPlan {
   int mean_splits, cov_splits;
   int64_t mean_chunk, cov_chunk;
-  size_t off_mean, off_cov, total;
+  size_t off_mean, off_cov, off_qn, total;
 };
 
 CovPlan cov_plan(int64_t B, int64_t H, int64_t S, int cus) {
@@ -829,7 +852,8 @@ CovPlan cov_plan(int64_t B, int64_t H, int64_t S, int cus) {
   p.cov_chunk = cdiv(S > 0 ? S : 1, p.cov_splits);
   p.off_mean = 0;
   p.off_cov = align256((size_t)bh * p.mean_splits * 128 * sizeof(float));
-  p.total = p.off_cov + align256((size_t)bh * p.cov_splits * kTiles * 256 * sizeof(float));
+  p.off_qn = p.off_cov + align256((size_t)bh * p.cov_splits * kTiles * 256 * sizeof(float));
+  p.total = p.off_qn + align256((size_t)bh * 128 * sizeof(float));  // floored query norms (weighted only)
   return p;
 }
 
@@ -870,28 +894,42 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
   const dim3 gm((unsigned)p.mean_splits, (unsigned)bh), gc((unsigned)p.cov_splits, (unsigned)bh);
   // mean over the token dim of [B, H, S, 128] (kv_pruning_utils.py:112)
   const float mfac = rk::mean_factor(bh * 128, bh * k.S * 128);
+  // with the weighting, the mean launch has one more column per head that
+  // forms the head's floored query norms
+  QNormArgs qa;
+  memset(&qa, 0, sizeof(qa));
+  float* qn = (float*)((char*)ws + p.off_qn);
+  dim3 gmq = gm;
+  if (qw) {
+    const rk_tensor* q = qw->q;
+    qa = QNormArgs{(const uint16_t*)q->data, q->stride[0], q->stride[1], q->stride[2], q->stride[3], q->shape[2],
+                   qw->W, (int)qw->G, qw->inv_g, qn};
+    gmq.x += 1;
+  }
   if (vec) {
-    hipLaunchKernelGGL((mean_kernel<TT, true>), gm, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits, mpart);
+    if (qw && qw->vec)
+      hipLaunchKernelGGL((mean_kernel<TT, true, true>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits,
+                         mpart, qa);
+    else
+      hipLaunchKernelGGL((mean_kernel<TT, true, false>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits,
+                         mpart, qa);
     hipLaunchKernelGGL((cov_kernel<TT, true>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
                        p.mean_splits, mfac, cpart);
   } else {
-    hipLaunchKernelGGL((mean_kernel<TT, false>), gm, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits, mpart);
+    if (qw && qw->vec)
+      hipLaunchKernelGGL((mean_kernel<TT, false, true>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits,
+                         mpart, qa);
+    else
+      hipLaunchKernelGGL((mean_kernel<TT, false, false>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk,
+                         p.mean_splits, mpart, qa);
     hipLaunchKernelGGL((cov_kernel<TT, false>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
                        p.mean_splits, mfac, cpart);
   }
   if (qw) {
-    const rk_tensor* q = qw->q;
-    auto go = [&](auto kern) {
-      hipLaunchKernelGGL(kern, dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits, mpart,
-                         p.mean_splits, mfac, (const uint16_t*)q->data, q->stride[0], q->stride[1], q->stride[2],
-                         q->stride[3], q->shape[2], qw->W, (int)qw->G, qw->inv_g, cov, cov_t->stride[0],
-                         cov_t->stride[1], cov_t->stride[2], cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0,
-                         mu_t ? mu_t->stride[1] : 0, mu_t ? mu_t->stride[2] : 0, k.H);
-    };
-    if (qw->vec)
-      go(covfin_qw_kernel<TT, true>);
-    else
-      go(covfin_qw_kernel<TT, false>);
+    hipLaunchKernelGGL((covfin_qw_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart,
+                       p.cov_splits, mpart, p.mean_splits, mfac, qn, cov, cov_t->stride[0], cov_t->stride[1],
+                       cov_t->stride[2], cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0,
+                       mu_t ? mu_t->stride[1] : 0, mu_t ? mu_t->stride[2] : 0, k.H);
     return hipGetLastError();
   }
   hipLaunchKernelGGL((covfin_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits,
