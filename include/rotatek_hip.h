@@ -77,7 +77,8 @@ typedef enum rk_status {
   RK_ERR_SHAPE = -4,         /* sizes disagree between tensors              */
   RK_ERR_HEADS = -5,         /* H_q / num_kv_groups != H_kv                 */
   RK_ERR_HEAD_DIM = -6,      /* head_dim other than 128                     */
-  RK_ERR_KEEP_DIM = -7,      /* kept channels outside 1..head_dim           */
+  RK_ERR_KEEP_DIM = -7,      /* kept channels out of range (decode 0..128,
+                                prefill and power iteration 1..128)         */
   RK_ERR_STRIDE = -8,        /* negative or overflowing stride              */
   RK_ERR_WORKSPACE = -9,     /* workspace NULL, misaligned or too small     */
   RK_ERR_ARG = -10,          /* other invalid scalar argument               */
@@ -118,8 +119,11 @@ int rk_device_cu_count(int device, int* status);
  * Shapes: q_full [B,H_q,D]; R_partial [B,H_kv,D,Dk]; delta_mu [B,H_kv,D] or
  * NULL; k_full, v_full [B,H_kv,S_f,D]; mask_full [B,S_f] u8 or NULL (= all
  * ones); k_sparse [B,H_kv,S_v,Dk]; v_sparse [B,H_kv,S_v,D]; out [B,H_q,D]
- * (dtype of q_full).  D must be 128.  q, K, V and out share one dtype
- * (F16 or BF16); R_partial and delta_mu may be F16, BF16 or F32.
+ * (dtype of q_full).  D must be 128, 0 <= Dk <= 128 (Dk = 0: every channel
+ * pruned, visual logits are the bias alone; R_partial and k_sparse may then
+ * have no storage).  q, K, V and out share one dtype (F16, BF16 or F32;
+ * fp32 runs a VALU kernel, one unit per query head); R_partial and
+ * delta_mu may be F16, BF16 or F32.
  * The workspace (size from rk_rotatek_decode_check, 256-byte aligned) holds
  * the split partials and, in its first RK_DECODE_TICKET_BYTES, the
  * counters of the single-launch merge; pass a new workspace through
@@ -205,9 +209,12 @@ int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, int64_t num_
  * (_power_iter_loop; power_iteration_gpu draws v0 with torch.randn from a
  * seeded device generator and calls this).  cov [B,H,128,128], v0 / out
  * [B,H,128,k] F32, 1 <= k <= 64; per iteration V = C V, G = V^T V +
- * eps * mean(diag G) * I, V = V chol(G)^-T.  out may alias v0. */
+ * eps * mean(diag G) * I, V = V chol(G)^-T.  out may alias v0.  info
+ * (device int32 [B*H], optional) receives 1 for a matrix whose Cholesky
+ * met a pivot that is not positive and finite (its output is then not a
+ * basis; the reference's torch.linalg.cholesky raises), else 0. */
 int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, const rk_tensor* out, int32_t num_iters,
-                       float eps, void* stream);
+                       float eps, int32_t* info, void* stream);
 
 /* In-place decode append for the span cache (replaces the per-step
  * torch.cat of cache_utils.py:52-53): k_new/v_new [B,H,1,128] are written

@@ -81,7 +81,8 @@ _SIGNATURES = {
                                                 ctypes.c_int64, _P, _P, ctypes.c_void_p, _P, ctypes.c_int32,
                                                 ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rk_query_weight": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int32, _P, ctypes.c_void_p]),
-    "rk_power_iteration": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p]),
+    "rk_power_iteration": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p,
+                                          ctypes.c_void_p]),
     "rk_append_kv": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_void_p, ctypes.c_void_p]),
     "rk_full_channel_decode_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int64, _P, ctypes.c_int32,
                                                     ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),

@@ -1366,7 +1366,10 @@ int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
   if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
   if (!rk::is_float_param(R->dtype)) return RK_ERR_DTYPE;
   if (R->shape[0] != c->B || R->shape[2] != 128) return RK_ERR_SHAPE;
-  if (c->Dk < 1 || c->Dk > 128) return RK_ERR_KEEP_DIM;
+  // Dk = 0 (channel_ratio >= 1, every channel pruned): visual logits are the
+  // bias q . delta_mu alone, as the reference's kernels give with no kept
+  // channel (its masked BLOCK_DK loads, fused_decode.py:131-148)
+  if (c->Dk < 0 || c->Dk > 128) return RK_ERR_KEEP_DIM;
   if (dm) {
     st = rk::check_desc(dm, 3);
     if (st) return st;
@@ -1544,7 +1547,7 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   if (!ws || (((uintptr_t)ws) & 255) != 0 || ws_bytes < p.workspace_bytes) return RK_ERR_WORKSPACE;
   if (c.B == 0) return RK_OK;
   const bool vis_work = has_vis && c.S_v > 0;
-  if (!q->data || !out->data || (vis_work && (!R->data || !ks->data || !vs->data)) ||
+  if (!q->data || !out->data || (vis_work && ((c.Dk > 0 && (!R->data || !ks->data)) || !vs->data)) ||
       (c.S_f > 0 && (!kf->data || !vf->data)))
     return RK_ERR_NULL;
   const WsLayout w = ws_layout(p);
@@ -1593,12 +1596,21 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
               R->stride[1] % 8 == 0 && R->stride[0] % 8 == 0 && (((uintptr_t)R->data) & 15) == 0;
     a.ks = (const uint16_t*)ks->data;
     a.vs = (const uint16_t*)vs->data;
-    if (!set_head(ks, a.ks_sb, a.ks_sh, a.ks_ss, a.ks_sd) ||
-        !set_head(vs, a.vs_sb, a.vs_sh, a.vs_ss, a.vs_sd))
-      return RK_ERR_STRIDE;
+    if (!set_head(vs, a.vs_sb, a.vs_sh, a.vs_ss, a.vs_sd)) return RK_ERR_STRIDE;
+    if (c.Dk > 0) {
+      if (!set_head(ks, a.ks_sb, a.ks_sh, a.ks_ss, a.ks_sd)) return RK_ERR_STRIDE;
+    } else {
+      // no kept channel: the (unconditional, masked-out) Key loads read the
+      // visual Value rows instead, so no address depends on an empty tensor
+      a.ks = a.vs;
+      a.ks_sb = a.vs_sb;
+      a.ks_sh = a.vs_sh;
+      a.ks_ss = a.vs_ss;
+      a.ks_sd = a.vs_sd;
+    }
     a.S_v = c.S_v;
     a.Dk = (int32_t)c.Dk;
-    vec = vec && rk::vec_ok(ks) && rk::vec_ok(vs) && (c.Dk % 8 == 0);
+    vec = vec && (c.Dk == 0 || rk::vec_ok(ks)) && rk::vec_ok(vs) && (c.Dk % 8 == 0);
     dkb = c.Dk <= 32 ? 1 : c.Dk <= 64 ? 2 : 4;
   }
   a.S_f = c.S_f;
@@ -1648,7 +1660,8 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   const int hmax = p.heads_per_unit > 1 ? 16 : 1;
   hipStream_t s = (hipStream_t)stream;
   if (c.dtype == RK_F32) {
-    const bool v32 = vec32_ok(kf) && vec32_ok(vf) && (!has_vis || (vec32_ok(ks) && vec32_ok(vs) && c.Dk % 4 == 0));
+    const bool v32 = vec32_ok(kf) && vec32_ok(vf) &&
+                     (!has_vis || ((c.Dk == 0 || vec32_ok(ks)) && vec32_ok(vs) && c.Dk % 4 == 0));
     return launch32(has_vis, v32, a, grid, s) == hipSuccess ? RK_OK : RK_ERR_HIP;
   }
   hipError_t e = c.dtype == RK_F16 ? launch_dk<rk::F16>(dkb, vec, hmax, has_vis, a, grid, s)

@@ -57,7 +57,7 @@ template <int KP>
 __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     const float* cov, int64_t c_sb, int64_t c_sh, int64_t c_sr, int64_t c_sc, const float* v0, int64_t v_sb,
     int64_t v_sh, int64_t v_sr, int64_t v_sc, float* out, int64_t o_sb, int64_t o_sh, int64_t o_sr,
-    int64_t o_sc, int H, int k, int iters, float eps) {
+    int64_t o_sc, int H, int k, int iters, float eps, int32_t* info) {
   // V / W and (L^-1)^T row stride, 4 mod 16: reads of rows 4g + r (r fixed)
   // at columns n = 0..15 hit banks 16g + n, and 16-byte reads of rows n at
   // column 4g cover all 64 banks
@@ -127,6 +127,8 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
   // tile ti0 + t * RS and column tile tj0.
   constexpr int RS = 4 / NTJ;
   const int ti0 = wave / NTJ, tj0 = wave - (wave / NTJ) * NTJ;
+  // a pivot that is not positive and finite (wave 0, uniform)
+  bool bad = false;
 
   for (int it = 0; it < iters; ++it) {
     // LDS bases, opaque to the compiler once per iteration: every access
@@ -255,6 +257,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
 #pragma unroll
       for (int j = 0; j < KP; ++j) {
         const float piv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, row[j]), j));
+        bad |= !(piv > 0.f && piv <= 3.402823466e38f);
         const float rj = __builtin_amdgcn_rsqf(piv);
         const float lij = ln > j ? row[j] * rj : (ln == j ? rj : 0.f);
         pl[j * KP] = lij;
@@ -337,6 +340,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
         for (int jj = 0; jj < 16; ++jj) {
           const int j = P0 + jj;
           const float piv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a[jj]), j));
+          bad |= !(piv > 0.f && piv <= 3.402823466e38f);
           const float rj = __builtin_amdgcn_rsqf(piv);
           const float lij = lane > j ? a[jj] * rj : (lane == j ? rj : 0.f);
           lc[jj] = lij;
@@ -453,6 +457,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     __syncthreads();
   }
 
+  if (info && tid == 0) info[bh] = bad ? 1 : 0;  // thread 0 is in wave 0, which ran the pivots
   float* O = out + b * o_sb + (int64_t)h * o_sh;
   for (int e = tid; e < kD * k; e += kThreads) {
     const int r = e / k, c = e - (e / k) * k;
@@ -462,11 +467,11 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
 
 template <int KP>
 hipError_t launch(const rk_tensor* cov, const rk_tensor* v0, const rk_tensor* out, int64_t BH, int H, int k,
-                  int iters, float eps, hipStream_t s) {
+                  int iters, float eps, int32_t* info, hipStream_t s) {
   hipLaunchKernelGGL((power_iter_kernel<KP>), dim3((unsigned)BH), dim3(kThreads), 0, s, (const float*)cov->data,
                      cov->stride[0], cov->stride[1], cov->stride[2], cov->stride[3], (const float*)v0->data,
                      v0->stride[0], v0->stride[1], v0->stride[2], v0->stride[3], (float*)out->data, out->stride[0],
-                     out->stride[1], out->stride[2], out->stride[3], H, k, iters, eps);
+                     out->stride[1], out->stride[2], out->stride[3], H, k, iters, eps, info);
   return hipGetLastError();
 }
 
@@ -474,7 +479,7 @@ hipError_t launch(const rk_tensor* cov, const rk_tensor* v0, const rk_tensor* ou
 }  // namespace rk
 
 extern "C" int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, const rk_tensor* out,
-                                  int32_t num_iters, float eps, void* stream) {
+                                  int32_t num_iters, float eps, int32_t* info, void* stream) {
   using namespace rk::rot;
   if (!cov || !v0 || !out) return RK_ERR_NULL;
   int st;
@@ -492,10 +497,10 @@ extern "C" int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, con
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (k <= 16)
-    e = launch<16>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, s);
+    e = launch<16>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
   else if (k <= 32)
-    e = launch<32>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, s);
+    e = launch<32>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
   else
-    e = launch<64>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, s);
+    e = launch<64>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }

@@ -89,7 +89,8 @@ def test_rotatek_check_ok_and_workspace():
     (dict(G=3), -5),                            # H_q / G != H_kv
     (dict(D=64), -6),                           # head_dim != 128
     (dict(dtype=_lib.RK_F64), -3),              # fp64 not supported
-    (dict(Dk=0), -7),
+    (dict(Dk=129), -7),
+    (dict(Dk=0), 0),                            # every channel pruned: bias-only visual logits
     (dict(policy=7), -10),
 ])
 def test_rotatek_check_errors(kw, code):
@@ -297,16 +298,16 @@ def test_power_iteration_validation():
     lib = _lib.load()
     r = ctypes.byref
     cov, v0, out = _t((2, 4, 128, 128), _lib.RK_F32), _t((2, 4, 128, 16), _lib.RK_F32), _t((2, 4, 128, 16), _lib.RK_F32)
-    assert lib.rk_power_iteration(r(cov), r(v0), r(out), 5, 1e-4, None) == -1        # no device memory
+    assert lib.rk_power_iteration(r(cov), r(v0), r(out), 5, 1e-4, None, None) == -1        # no device memory
     bad = _t((2, 4, 128, 16), _lib.RK_F16)
-    assert lib.rk_power_iteration(r(cov), r(bad), r(out), 5, 1e-4, None) == -3
+    assert lib.rk_power_iteration(r(cov), r(bad), r(out), 5, 1e-4, None, None) == -3
     wide = _t((2, 4, 128, 65), _lib.RK_F32)
-    assert lib.rk_power_iteration(r(cov), r(wide), r(wide), 5, 1e-4, None) == -7     # k > 64
+    assert lib.rk_power_iteration(r(cov), r(wide), r(wide), 5, 1e-4, None, None) == -7     # k > 64
     c64 = _t((2, 4, 64, 64), _lib.RK_F32)
-    assert lib.rk_power_iteration(r(c64), r(v0), r(out), 5, 1e-4, None) == -6
+    assert lib.rk_power_iteration(r(c64), r(v0), r(out), 5, 1e-4, None, None) == -6
     o2 = _t((2, 4, 128, 8), _lib.RK_F32)
-    assert lib.rk_power_iteration(r(cov), r(v0), r(o2), 5, 1e-4, None) == -4
-    assert lib.rk_power_iteration(r(cov), r(v0), r(out), -1, 1e-4, None) == -10
+    assert lib.rk_power_iteration(r(cov), r(v0), r(o2), 5, 1e-4, None, None) == -4
+    assert lib.rk_power_iteration(r(cov), r(v0), r(out), -1, 1e-4, None, None) == -10
 
 
 def test_query_weight_validation():

@@ -352,3 +352,42 @@ def test_fp32_dense_matches_oracle(G):
     want = od.full_channel_decode(_np(q), _np(k), _np(v), G)
     assert out.dtype == torch.float32
     assert np.abs(_np(out) - want).max() <= TOL32
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("family", ["paper", "gqa"])
+def test_zero_kept_channels(dtype, family):
+    """channel_ratio >= 1 keeps no channel: R_partial [B,H,D,0], k_sparse
+    [B,H,S_v,0] (no storage), delta_mu = the Key mean.  Visual logits are the
+    bias q . delta_mu alone, as in the reference's kernels."""
+    _say(f"rotatek Dk=0 {family} {dtype}")
+    inp = _rand_inputs(2, 8, 4, 32, 500, 40, dtype, seed=13)
+    inp["R_partial"] = inp["R_partial"][..., :0]
+    inp["k_sparse"] = torch.empty(2, 4, 500, 0, device="cuda", dtype=dtype)
+    out = _decode(inp, family)
+    want = _oracle(inp)
+    assert np.abs(_np(out) - want).max() <= (TOL32 if dtype == torch.float32 else TOL[dtype])
+
+
+def test_pruner_ratio_one_decodes():
+    """ChannelPruner with channel_ratio 1.0 (keep 0) feeds the decode."""
+    from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
+    from rotatek_amd.pruning import ChannelPruner
+    _say("pruner ratio 1.0 -> decode")
+    g = torch.Generator(device="cuda").manual_seed(2)
+    B, H, G, S = 1, 2, 4, 300
+    K = torch.randn(B, H, S, 128, generator=g, device="cuda").to(torch.bfloat16)
+    Q = torch.randn(B, H * G, S, 128, generator=g, device="cuda").to(torch.bfloat16)
+    V = torch.randn(B, H, S, 128, generator=g, device="cuda").to(torch.bfloat16)
+    pr = ChannelPruner(1.0, 10, 20, solver="power_iter", query_aware=True)
+    kept, kp, kt, mask, v = pr.update_rotatek(K, Q, V, None, G)
+    assert kept.shape[-1] == 0 and pr.current_rotatek_R_partial.shape[-1] == 0
+    q = torch.randn(B, H * G, 128, generator=g, device="cuda").to(torch.bfloat16)
+    kf, vf = torch.cat([kp, kt], -2), torch.cat([V[:, :, :10], V[:, :, -20:]], -2)
+    mask_full = torch.ones(B, 30, dtype=torch.uint8, device="cuda")
+    args = dict(q_full=q, R_partial=pr.current_rotatek_R_partial, delta_mu=pr.current_rotatek_delta_mu,
+                k_full=kf, v_full=vf, mask_full=mask_full, k_sparse=kept, v_sparse=V[:, :, 10:-20],
+                num_kv_groups=G)
+    out, _, _ = rotatek_decode_gqa(**args)
+    torch.cuda.synchronize()
+    assert np.abs(_np(out) - _oracle(args)).max() <= TOL[torch.bfloat16]

@@ -129,3 +129,41 @@ def test_power_iteration_rank_deficient_covariance():
     g_np = got.double().cpu().numpy()
     assert np.isfinite(g_np).all()
     assert np.abs(g_np - want).max() < 2e-3 * max(1.0, np.abs(want).max())
+
+
+@pytest.mark.parametrize("k", [16, 48])
+def test_power_iteration_failed_pivot_raises(k):
+    """A zero covariance with no ridge: every Gram pivot is 0.  The HIP
+    Cholesky records it and the call raises torch.linalg.LinAlgError, as the
+    reference's torch.linalg.cholesky does (rotation.py:49); the same call
+    with the ridge on a sound covariance does not."""
+    from rotatek_amd.rotation import power_iteration_hip
+    _say(f"power iteration failed pivot, k={k}")
+    cov = torch.zeros(1, 2, 128, 128, device="cuda")
+    V0 = torch.randn(1, 2, 128, k, device="cuda")
+    with pytest.raises(torch.linalg.LinAlgError):
+        power_iteration_hip(cov, V0, 2, 0.0)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    X = torch.randn(1, 2, 128, 128, generator=g, device="cuda")
+    good = (X @ X.transpose(-1, -2)).contiguous()
+    out = power_iteration_hip(good, V0, 5, 1e-4)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+
+
+def test_power_iteration_rank_deficient_small_ridge():
+    """Rank 8 covariance, k = 16 and the 1e-6 ridge (query weighting off):
+    either the factorisation holds and the basis matches the oracle, or the
+    call raises; it never returns a non-finite basis."""
+    from rotatek_amd.rotation import power_iteration_hip
+    _say("power iteration rank-8 covariance, k=16, eps 1e-6")
+    g = torch.Generator(device="cuda").manual_seed(8)
+    X = torch.randn(2, 3, 128, 8, generator=g, device="cuda", dtype=torch.float64)
+    cov = (X @ X.transpose(-1, -2) / 8).float().contiguous()
+    V0 = torch.randn(2, 3, 128, 16, generator=g, device="cuda")
+    try:
+        got = power_iteration_hip(cov, V0, 5, 1e-6)
+    except torch.linalg.LinAlgError:
+        return
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
