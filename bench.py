@@ -129,54 +129,109 @@ def _timed(fn, reps, graph=True):
     return out, e0.elapsed_time(e1) * 1e3 / reps, wall
 
 
-def _cpu_baseline(inp, cfg, budget_s=12.0):
-    """CPU oracle (numpy fp32) over whole batch elements of the same inputs,
-    cycling over the batch until ~budget_s of CPU work; returns us per full
-    step (median per-element time x B)."""
+def _host_cores():
+    """CPU cores this process may run on (its affinity mask)."""
+    return len(os.sched_getaffinity(0))
+
+
+def _host_decode_inputs(inp, b0=0, b1=None):
+    """fp32 numpy copies of the decode inputs of batch rows b0..b1."""
     import numpy as np
-    from threadpoolctl import threadpool_info
-
-    from oracle import decode as od
-
-    def host(t, b):
-        return None if t is None else t[b:b + 1].float().cpu().numpy()
 
     names = ("q_full", "R_partial", "delta_mu", "k_full", "v_full", "mask_full", "k_sparse", "v_sparse")
-    nb = min(cfg.B, 4)
-    elems = []
-    for b in range(nb):
-        a = {k: host(inp[k], b) for k in names}
-        elems.append({k: (v.astype(np.float32) if v is not None else v) for k, v in a.items()})
-    times, t_total, i = [], 0.0, 0
-    while t_total < budget_s or len(times) < 3:
-        a = elems[i % nb]
+    out = {}
+    for k in names:
+        t = inp[k]
+        out[k] = None if t is None else np.ascontiguousarray(t[b0:b1].float().cpu().numpy(), dtype=np.float32)
+    return out
+
+
+def _time_oracle_steps(a, G, budget_s):
+    """Median wall time (s) of whole oracle decode steps over ``a``, repeated
+    for about ``budget_s`` seconds (at least three)."""
+    import numpy as np
+
+    from oracle import decode as od
+    times, total = [], 0.0
+    while total < budget_s or len(times) < 3:
         t0 = time.perf_counter()
-        od.rotatek_decode(a["q_full"], a["R_partial"], a["delta_mu"], a["k_full"], a["v_full"],
-                          a["mask_full"], a["k_sparse"], a["v_sparse"], inp["num_kv_groups"],
-                          compute_dtype=np.float32)
+        od.rotatek_decode(a["q_full"], a["R_partial"], a["delta_mu"], a["k_full"], a["v_full"], a["mask_full"],
+                          a["k_sparse"], a["v_sparse"], G, compute_dtype=np.float32)
         dt = time.perf_counter() - t0
         times.append(dt)
-        t_total += dt
-        i += 1
-    per_b = sorted(times)[len(times) // 2]
-    threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+        total += dt
+    return sorted(times)[len(times) // 2], len(times), total
+
+
+def _cpu_baseline(inp, cfg, budget_s=12.0):
+    """The CPU oracle (numpy fp32 restatement of the reference's decode; the
+    reference has no CPU path) on every core of this process's affinity
+    mask: whole decode steps of the same inputs (all B batch rows, every head,
+    full context), repeated for about ``budget_s`` seconds; the median step."""
+    from threadpoolctl import threadpool_limits
+    import torch
+
+    cores = _host_cores()
+    torch.set_num_threads(cores)
+    a = _host_decode_inputs(inp)
+    with threadpool_limits(limits=cores):
+        med, n, total = _time_oracle_steps(a, inp["num_kv_groups"], budget_s)
     return {
-        "value": per_b * cfg.B * 1e6,
+        "value": round(med * 1e6, 1),
         "unit": "us/step",
-        "cores": int(threads),
+        "cores": cores,
         "kind": "port",
-        "sample": f"numpy fp32 oracle (oracle/decode.py) on batch elements 0..{nb - 1} of the same inputs "
-                  f"(all {cfg.H_q} heads, full {cfg.S_v}+{cfg.S_f} context each), {len(times)} runs, "
-                  f"median per-element time x B={cfg.B}; {t_total:.1f} s of CPU work",
+        "sample": f"numpy fp32 oracle (oracle/decode.py) over whole steps of the same inputs ({cfg.name}: all "
+                  f"{cfg.B} batch rows, {cfg.H_q} heads, {cfg.S_v}+{cfg.S_f} context), {n} steps, median; "
+                  f"{total:.1f} s of CPU work on {cores} threads (BLAS pool limited to the affinity mask)",
     }
 
 
+def _cfg0_leg(budget_s=3.0):
+    """BASELINE config 0 (B=1, 32 heads, 2304 + 128 tokens, fp32): the CPU
+    oracle over whole steps on every core of the affinity mask, and the HIP
+    fp32 decode of the same inputs (eager, inputs resident in HBM)."""
+    from threadpoolctl import threadpool_limits
+    import torch
+
+    from rotatek_amd import synth
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    cfg = synth.CONFIGS["cfg0"]
+    inp = synth.make_decode_inputs(cfg, "cuda", seed=0)
+    args = synth.decode_args(inp)
+    for _ in range(5):
+        rotatek_decode_fused(**args)
+    gpu_us = _time_wall(lambda: rotatek_decode_fused(**args), 100)
+    cores = _host_cores()
+    a = _host_decode_inputs(inp)
+    with threadpool_limits(limits=cores):
+        med, n, total = _time_oracle_steps(a, inp["num_kv_groups"], budget_s)
+    return {"cpu_us_per_step": round(med * 1e6, 1), "cpu_cores": cores, "cpu_steps": n,
+            "hip_fp32_us_per_step": round(gpu_us, 2),
+            "workload": "cfg0: B=1, H=32 MHA, D=128, S_v=2304 (keep 32), S_f=128, fp32"}
+
+
+DECODE_SOURCE = os.path.join(ROOT, "rotatek_amd", "csrc", "rk_decode.hip")
+
+
+def _source_sha():
+    import hashlib
+    with open(DECODE_SOURCE, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
 def _traffic(cfg_name):
+    """HBM bytes per decode launch from the committed counter summary, or
+    None when that summary was taken on another decode source than this
+    tree's (it records the sha256 of rk_decode.hip it measured)."""
     path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        d = json.load(f)
+    if d.get("decode_source_sha256") != _source_sha():
+        return None
+    return d.get("hbm_bytes_per_launch")
 
 
 def _pmc_rows(path):
@@ -218,6 +273,15 @@ def pmc_summary(fetch_csv, write_csv, calib_bytes, calib_copies, cfg_name):
     out["decode_kernel_write_bytes"] = wr
     out["algorithmic_bytes_per_step"] = alg
     out["traffic_over_algorithmic"] = round((rd + wr) / alg, 4)
+    # what was measured: the decode source the counters ran (bench.py reports
+    # the traffic only while the tree's source matches) and the commit
+    out["decode_source_sha256"] = _source_sha()
+    try:
+        import subprocess
+        out["commit"] = subprocess.run(["git", "-C", ROOT, "rev-parse", "--short=12", "HEAD"], capture_output=True,
+                                       text=True, check=True).stdout.strip()
+    except Exception:
+        out["commit"] = None
     path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
@@ -594,11 +658,17 @@ def main():
         _log(f"[bench] copy calibration: {args.steps} copies of {n} bytes")
         del src, dst
 
-    cpu = None
+    cpu, cfg0 = None, None
     if not args.no_cpu:
-        _log("[bench] timing the CPU oracle on a bounded sample")
+        del sets, dsets
+        torch.cuda.empty_cache()
+        _log("[bench] timing the CPU oracle over whole steps")
         cpu = _cpu_baseline(inp, cfg)
         _log(f"[bench] cpu baseline {cpu['value']:.0f} us/step on {cpu['cores']} threads")
+        if args.config == "cfg2":
+            cfg0 = _cfg0_leg()
+            _log(f"[bench] config 0: cpu {cfg0['cpu_us_per_step']} us/step on {cfg0['cpu_cores']} threads, "
+                 f"HIP fp32 {cfg0['hip_fp32_us_per_step']} us/step")
 
     line = {
         "metric": METRIC,
@@ -611,7 +681,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp16" if cfg.dtype == torch.float16 else "bf16",
+        "dtype": {torch.float16: "fp16", torch.bfloat16: "bf16", torch.float32: "fp32"}[cfg.dtype],
         "data": "synthetic: seeded N(0,1) q/K/V, x8 outlier Key channels, orthogonal R_k per head, "
                 "top-32 channels by mean |K R_k|",
         "config": {
@@ -636,6 +706,7 @@ def main():
             "traffic": _traffic(cfg.name),
         },
         "cpu_baseline": cpu,
+        "config0": cfg0,
     }
     line.update(extra)
     print(json.dumps(line), flush=True)
