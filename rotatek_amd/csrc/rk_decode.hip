@@ -1039,11 +1039,24 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
   };
 
   if (is_vis) {
-    if (tid < a.Dk) {  // q R_partial, column tid
-      const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)tid * a.R_sk;
+    {  // q R_partial: thread (half, c) sums rows 64 half .. 64 half + 63 of
+       // column c, sixteen loads in flight at a time; the halves meet in LDS
+      const int c = tid & 127, half = tid >> 7;
+      const int cc = min(c, max(a.Dk - 1, 0));
+      const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)cc * a.R_sk;
       float sum = 0.f;
-      for (int d = 0; d < 128; ++d) sum = fmaf(s_q[d], load_any(a.R, rb + (int64_t)d * a.R_sd, a.r_dtype), sum);
-      s_qt[tid] = sum;
+      if (a.Dk > 0) {
+        for (int d0 = 64 * half; d0 < 64 * half + 64; d0 += 16) {
+          float rv[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) rv[i] = load_any(a.R, rb + (int64_t)(d0 + i) * a.R_sd, a.r_dtype);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sum = fmaf(s_q[d0 + i], rv[i], sum);
+        }
+      }
+      s_acc[half][c] = sum;  // s_acc is free until the epilogue
+      __syncthreads();
+      if (tid < 128) s_qt[tid] = tid < a.Dk ? s_acc[0][tid] + s_acc[1][tid] : 0.f;
     }
     if (wave < 2) {  // q . delta_mu
       const int d = tid;

@@ -1,6 +1,7 @@
 // Top-k eigenbasis by truncated subspace iteration with Cholesky-QR
 // orthonormalisation (rotation.py:21-91), for the 128 x 128 Key covariances
-// of every (batch, KV head), k <= 64.
+// of every (batch, KV head), k <= 128 (k <= 64 here; wider bases in
+// power_iter128_kernel below).
 //
 // Per iteration, as the reference:
 //   W = C V;  G = W^T W;  G += eps * mean(diag G) * I;  G = L L^T;  V = W L^-T
@@ -465,6 +466,268 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
   }
 }
 
+// ---- 64 < k <= 128.  C, V/W, G, L and L^-1 do not all fit in LDS at this
+// width, so C is read from global memory (each matrix's 64 KB stays in its
+// XCD's L2 across the iterations) and G, L and X = L^-1 share one array:
+//   strict lower triangle  L (rows below the diagonal)
+//   diagonal               r_j = 1 / L_jj (= X_jj)
+//   strict upper triangle  X^T (X is lower triangular)
+// The Cholesky is blocked by 16-column panels as at k = 64 (wave 0 factors
+// a panel with two rows per lane; all waves apply the trailing update on
+// the MFMA), X's off-diagonal blocks follow by block rows, and V = W X^T
+// reads X^T from the upper triangle (masked to zero below it).
+constexpr int kW = 128;       // padded basis width
+constexpr int kWS = kW + 4;   // V / W row stride
+constexpr int kWG = kW + 1;   // G row stride
+
+// X^T[m][j] from the packed array (zero below the diagonal, where L lives)
+__device__ __forceinline__ float xt_at(const lds_f32* P, int m, int j) {
+  const float v = P[m * kWG + j];
+  return m <= j ? v : 0.f;
+}
+
+__global__ void __launch_bounds__(kThreads) power_iter128_kernel(
+    const float* cov, int64_t c_sb, int64_t c_sh, int64_t c_sr, int64_t c_sc, const float* v0, int64_t v_sb,
+    int64_t v_sh, int64_t v_sr, int64_t v_sc, float* out, int64_t o_sb, int64_t o_sh, int64_t o_sr,
+    int64_t o_sc, int H, int k, int iters, float eps, int32_t* info, int cvec) {
+  __shared__ __align__(16) float sV[kD * kWS];
+  __shared__ __align__(16) float sP[kW * kWG];
+  __shared__ float sT[4 * 256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+  const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
+  const float* C = cov + b * c_sb + (int64_t)h * c_sh;
+  const float* V0 = v0 + b * v_sb + (int64_t)h * v_sh;
+  constexpr int kB = 16;
+  for (int e0 = 0; e0 < kD * kW; e0 += kThreads * kB) {
+    float v[kB];
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const int e = e0 + i * kThreads + tid, r = e >> 7, c = e & 127;
+      v[i] = c < k ? V0[r * v_sr + c * v_sc] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kB; ++i) {
+      const int e = e0 + i * kThreads + tid;
+      sV[(e >> 7) * kWS + (e & 127)] = v[i];
+    }
+  }
+  __syncthreads();
+  bool bad = false;
+  lds_f32* const lV = (lds_f32*)sV;
+  lds_f32* const lP = (lds_f32*)sP;
+  lds_f32* const lT = (lds_f32*)sT + wave * 256;
+  const int tjw = 2 * wave;  // this wave's output column tiles in C V and W X^T: tjw, tjw + 1
+
+  for (int it = 0; it < iters; ++it) {
+    // ---- W = C V: tiles (ti, tjw + t2), ti = 0..7; in k-group q lane (g, n)
+    // supplies k = 16 q + 4 g + r (one 16-byte read of C's row feeds four steps)
+    {
+      f32x4 acc[8][2];
+#pragma unroll
+      for (int ti = 0; ti < 8; ++ti) acc[ti][0] = acc[ti][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < kD / 16; ++q) {
+        float a[8][4];
+#pragma unroll
+        for (int ti = 0; ti < 8; ++ti) {
+          const float* cr = C + (int64_t)(16 * ti + n) * c_sr;
+          if (cvec) {
+            const float4 v = *(const float4*)(cr + 16 * q + 4 * g);
+            a[ti][0] = v.x, a[ti][1] = v.y, a[ti][2] = v.z, a[ti][3] = v.w;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) a[ti][r] = cr[(int64_t)(16 * q + 4 * g + r) * c_sc];
+          }
+        }
+        float bv[2][4];
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) bv[t2][r] = lV[(16 * q + 4 * g + r) * kWS + 16 * (tjw + t2) + n];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int ti = 0; ti < 8; ++ti)
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) acc[ti][t2] = mfma4(a[ti][r], bv[t2][r], acc[ti][t2]);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ti = 0; ti < 8; ++ti)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) lV[(16 * ti + 4 * g + i) * kWS + 16 * (tjw + t2) + n] = acc[ti][t2][i];
+    }
+    __syncthreads();
+
+    // ---- G = W^T W, the 36 lower tiles (ti >= tj), tile t to wave t mod 4
+    {
+      int t = 0;
+      for (int ti = 0; ti < 8; ++ti) {
+        for (int tj = 0; tj <= ti; ++tj, ++t) {
+          if (t % 4 != wave) continue;  // wave-uniform
+          f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+          for (int q = 0; q < kD / 4; ++q)
+            acc = mfma4(lV[(4 * q + g) * kWS + 16 * ti + n], lV[(4 * q + g) * kWS + 16 * tj + n], acc);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) lP[(16 * ti + 4 * g + i) * kWG + 16 * tj + n] = acc[i];
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- ridge: G += eps * mean(diag G) * I over the first k; padding
+    // rows and columns are zero (V's padding columns are): unit diagonal
+    if (wave == 0) {
+      const float d0 = lP[lane * kWG + lane], d1 = lP[(lane + 64) * kWG + lane + 64];
+      float dg = (lane < k ? d0 : 0.f) + (lane + 64 < k ? d1 : 0.f);
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) dg += shfl_xor(dg, off);
+      const float ridge = eps * (dg / (float)k);
+      lP[lane * kWG + lane] = lane < k ? d0 + ridge : 1.f;
+      lP[(lane + 64) * kWG + lane + 64] = lane + 64 < k ? d1 + ridge : 1.f;
+    }
+    __syncthreads();
+
+    // ---- blocked Cholesky and the diagonal blocks of X
+    for (int p = 0; p < kW / 16; ++p) {
+      const int P0 = 16 * p;
+      if (wave == 0) {
+        // lane holds rows lane and lane + 64 (entries of panel columns P0..P0+15)
+        float a0[16], a1[16], lc0[16], lc1[16], xv[16];
+        const bool hi = P0 >= 64;  // the panel's rows sit in the second half
+        const int prow = (hi ? lane + 64 : lane);  // the half whose lanes hold the panel rows
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          a0[c] = lP[lane * kWG + P0 + c];
+          a1[c] = lP[(lane + 64) * kWG + P0 + c];
+          xv[c] = prow == P0 + c ? 1.f : 0.f;
+        }
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          const int j = P0 + jj;
+          const float pv = hi ? a1[jj] : a0[jj];
+          const float piv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), j & 63));
+          bad |= !(piv > 0.f && piv <= 3.402823466e38f);
+          const float rj = __builtin_amdgcn_rsqf(piv);
+          const float l0 = lane > j ? a0[jj] * rj : (lane == j ? rj : 0.f);
+          const float l1 = lane + 64 > j ? a1[jj] * rj : (lane + 64 == j ? rj : 0.f);
+          lc0[jj] = l0;
+          lc1[jj] = l1;
+          xv[jj] *= rj;
+          const float lp = hi ? l1 : l0;  // column j of L in the panel rows' half
+#pragma unroll
+          for (int mm = jj + 1; mm < 16; ++mm) {
+            const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lp), (P0 + mm) & 63));
+            a0[mm] = fmaf(-l0, c, a0[mm]);
+            a1[mm] = fmaf(-l1, c, a1[mm]);
+            xv[mm] = fmaf(-c, xv[jj], xv[mm]);
+          }
+        }
+        // L (lower triangle and diagonal) in place of G
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) {
+          if (lane >= P0 + jj) lP[lane * kWG + P0 + jj] = lc0[jj];
+          if (lane + 64 >= P0 + jj) lP[(lane + 64) * kWG + P0 + jj] = lc1[jj];
+        }
+        // X's diagonal block, transposed into the upper triangle: row prow
+        // of X^T holds column prow of X (lanes whose row is in the panel)
+        if (prow >= P0 && prow < P0 + 16) {
+#pragma unroll
+          for (int mm = 0; mm < 16; ++mm)
+            if (P0 + mm > prow) lP[prow * kWG + P0 + mm] = xv[mm];
+        }
+      }
+      __syncthreads();
+      if (p + 1 < kW / 16) {
+        // G[16 ti + a][16 tj + b] -= sum_c L[16 ti + a][P0 + c] L[16 tj + b][P0 + c], p < tj <= ti
+        int t = 0;
+        for (int ti = p + 1; ti < kW / 16; ++ti) {
+          for (int tj = p + 1; tj <= ti; ++tj, ++t) {
+            if (t % 4 != wave) continue;  // wave-uniform
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+              const int cc = P0 + 4 * st + g;
+              acc = mfma4(lP[(16 * ti + n) * kWG + cc], lP[(16 * tj + n) * kWG + cc], acc);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lP[(16 * ti + 4 * g + i) * kWG + 16 * tj + n] -= acc[i];
+          }
+        }
+        __syncthreads();
+      }
+    }
+
+    // ---- X's blocks below the diagonal by block rows q:
+    // X_qr = -X_qq sum_{s=r}^{q-1} L_qs X_sr, stored transposed in the upper triangle
+    for (int q = 1; q < kW / 16; ++q) {
+      for (int r = wave; r < q; r += 4) {  // wave-uniform
+        f32x4 tacc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int kk0 = 16 * r; kk0 < 16 * q; kk0 += 4) {
+          const int kk = kk0 + g;
+          tacc = mfma4(lP[(16 * q + n) * kWG + kk], xt_at(lP, 16 * r + n, kk), tacc);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lT[(4 * g + i) * 16 + n] = tacc[i];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        f32x4 xacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int kk = 4 * st + g;
+          xacc = mfma4(xt_at(lP, 16 * q + kk, 16 * q + n), lT[kk * 16 + n], xacc);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lP[(16 * r + n) * kWG + 16 * q + 4 * g + i] = -xacc[i];
+      }
+      __syncthreads();
+    }
+
+    // ---- V = W X^T: V[r][j] = sum_{m <= j} W[r][m] X^T[m][j], tiles (ti, tjw + t2)
+    {
+      f32x4 acc[8][2];
+#pragma unroll
+      for (int ti = 0; ti < 8; ++ti) acc[ti][0] = acc[ti][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q <= tjw + 1; ++q) {  // k-blocks of 16 up to the wave's last column tile
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const int m = 16 * q + 4 * st + g;
+          float bv[2];
+#pragma unroll
+          for (int t2 = 0; t2 < 2; ++t2) bv[t2] = xt_at(lP, m, 16 * (tjw + t2) + n);
+#pragma unroll
+          for (int ti = 0; ti < 8; ++ti) {
+            const float av = lV[(16 * ti + n) * kWS + m];
+#pragma unroll
+            for (int t2 = 0; t2 < 2; ++t2) acc[ti][t2] = mfma4(av, bv[t2], acc[ti][t2]);
+          }
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ti = 0; ti < 8; ++ti)
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) lV[(16 * ti + 4 * g + i) * kWS + 16 * (tjw + t2) + n] = acc[ti][t2][i];
+    }
+    __syncthreads();
+  }
+
+  if (info && tid == 0) info[bh] = bad ? 1 : 0;
+  float* O = out + b * o_sb + (int64_t)h * o_sh;
+  for (int e = tid; e < kD * k; e += kThreads) {
+    const int r = e / k, c = e - (e / k) * k;
+    O[r * o_sr + c * o_sc] = sV[r * kWS + c];
+  }
+}
+
 template <int KP>
 hipError_t launch(const rk_tensor* cov, const rk_tensor* v0, const rk_tensor* out, int64_t BH, int H, int k,
                   int iters, float eps, int32_t* info, hipStream_t s) {
@@ -489,7 +752,7 @@ extern "C" int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, con
   const int64_t B = cov->shape[0], H = cov->shape[1], k = v0->shape[3];
   for (const rk_tensor* t : {v0, out})
     if (t->shape[0] != B || t->shape[1] != H || t->shape[2] != kD || t->shape[3] != k) return RK_ERR_SHAPE;
-  if (k < 1 || k > 64) return RK_ERR_KEEP_DIM;
+  if (k < 1 || k > 128) return RK_ERR_KEEP_DIM;
   if (num_iters < 0 || !(eps >= 0.f)) return RK_ERR_ARG;
   if (B * H == 0) return RK_OK;
   if (B * H > (INT64_C(1) << 31) || H > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
@@ -500,7 +763,17 @@ extern "C" int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, con
     e = launch<16>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
   else if (k <= 32)
     e = launch<32>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
-  else
+  else if (k <= 64)
     e = launch<64>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
+  else {
+    const int cvec = cov->stride[3] == 1 && cov->stride[2] % 4 == 0 && cov->stride[1] % 4 == 0 &&
+                     cov->stride[0] % 4 == 0 && (((uintptr_t)cov->data) & 15) == 0;
+    hipLaunchKernelGGL(power_iter128_kernel, dim3((unsigned)(B * H)), dim3(kThreads), 0, s, (const float*)cov->data,
+                       cov->stride[0], cov->stride[1], cov->stride[2], cov->stride[3], (const float*)v0->data,
+                       v0->stride[0], v0->stride[1], v0->stride[2], v0->stride[3], (float*)out->data,
+                       out->stride[0], out->stride[1], out->stride[2], out->stride[3], (int)H, (int)k, num_iters, eps,
+                       info, cvec);
+    e = hipGetLastError();
+  }
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }

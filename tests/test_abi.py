@@ -301,8 +301,10 @@ def test_power_iteration_validation():
     assert lib.rk_power_iteration(r(cov), r(v0), r(out), 5, 1e-4, None, None) == -1        # no device memory
     bad = _t((2, 4, 128, 16), _lib.RK_F16)
     assert lib.rk_power_iteration(r(cov), r(bad), r(out), 5, 1e-4, None, None) == -3
-    wide = _t((2, 4, 128, 65), _lib.RK_F32)
-    assert lib.rk_power_iteration(r(cov), r(wide), r(wide), 5, 1e-4, None, None) == -7     # k > 64
+    wide = _t((2, 4, 128, 129), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(cov), r(wide), r(wide), 5, 1e-4, None, None) == -7     # k > 128
+    w96 = _t((2, 4, 128, 96), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(cov), r(w96), r(w96), 5, 1e-4, None, None) == -1       # 96 is valid
     c64 = _t((2, 4, 64, 64), _lib.RK_F32)
     assert lib.rk_power_iteration(r(c64), r(v0), r(out), 5, 1e-4, None, None) == -6
     o2 = _t((2, 4, 128, 8), _lib.RK_F32)
