@@ -69,7 +69,9 @@ def test_power_iteration_matches_oracle_from_same_start(k, eps):
     VtV = np.swapaxes(g_np, -1, -2) @ g_np
     VtV_want = np.swapaxes(want, -1, -2) @ want
     assert np.abs(VtV - VtV_want).max() < tol
-    if eps == 1e-6:
+    if eps == 1e-6 and k <= 64:
+        # (a full-width basis reaches eigenvalues the ridge dominates, where
+        # the oracle's V^T V departs from I just as much)
         assert np.abs(VtV - np.eye(k)).max() < 1e-2
 
 
