@@ -1015,23 +1015,32 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll 8
-    for (int j = 0; j < kBlk32; ++j) {
-      uint32_t row = (uint32_t)min(t0 + j, t_last);
-      row += row >= gap_at ? gap : 0u;
-      const float* vr = vb + (int64_t)row * vss;
-      float v0, v1;
-      if constexpr (VEC) {
-        const float2 v = *(const float2*)(vr + 2 * lane);
-        v0 = v.x;
-        v1 = v.y;
-      } else {
-        v0 = vr[(int64_t)(2 * lane) * vsd];
-        v1 = vr[(int64_t)(2 * lane + 1) * vsd];
+    // the block's V rows in two batches of 32 loads in flight (one memory
+    // round trip each), then their fused multiply-adds in token order
+    constexpr int kVB = 32;
+#pragma unroll
+    for (int j0 = 0; j0 < kBlk32; j0 += kVB) {
+      float v0[kVB], v1[kVB];
+#pragma unroll
+      for (int jj = 0; jj < kVB; ++jj) {
+        uint32_t row = (uint32_t)min(t0 + j0 + jj, t_last);
+        row += row >= gap_at ? gap : 0u;
+        const float* vr = vb + (int64_t)row * vss;
+        if constexpr (VEC) {
+          const float2 v = *(const float2*)(vr + 2 * lane);
+          v0[jj] = v.x;
+          v1[jj] = v.y;
+        } else {
+          v0[jj] = vr[(int64_t)(2 * lane) * vsd];
+          v1[jj] = vr[(int64_t)(2 * lane + 1) * vsd];
+        }
       }
-      const float pj = s_p[wave][j];
-      acc0 = fmaf(pj, v0, acc0);
-      acc1 = fmaf(pj, v1, acc1);
+#pragma unroll
+      for (int jj = 0; jj < kVB; ++jj) {
+        const float pj = s_p[wave][j0 + jj];
+        acc0 = fmaf(pj, v0[jj], acc0);
+        acc1 = fmaf(pj, v1[jj], acc1);
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -1040,18 +1049,18 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
 
   if (is_vis) {
     {  // q R_partial: thread (half, c) sums rows 64 half .. 64 half + 63 of
-       // column c, sixteen loads in flight at a time; the halves meet in LDS
+       // column c, 32 loads in flight at a time; the halves meet in LDS
       const int c = tid & 127, half = tid >> 7;
       const int cc = min(c, max(a.Dk - 1, 0));
       const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)cc * a.R_sk;
       float sum = 0.f;
       if (a.Dk > 0) {
-        for (int d0 = 64 * half; d0 < 64 * half + 64; d0 += 16) {
-          float rv[16];
+        for (int d0 = 64 * half; d0 < 64 * half + 64; d0 += 32) {
+          float rv[32];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) rv[i] = load_any(a.R, rb + (int64_t)(d0 + i) * a.R_sd, a.r_dtype);
+          for (int i = 0; i < 32; ++i) rv[i] = load_any(a.R, rb + (int64_t)(d0 + i) * a.R_sd, a.r_dtype);
 #pragma unroll
-          for (int i = 0; i < 16; ++i) sum = fmaf(s_q[d0 + i], rv[i], sum);
+          for (int i = 0; i < 32; ++i) sum = fmaf(s_q[d0 + i], rv[i], sum);
         }
       }
       s_acc[half][c] = sum;  // s_acc is free until the epilogue
