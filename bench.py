@@ -540,6 +540,8 @@ def main():
     ap.add_argument("--graph-steps", type=int, default=8,
                     help="decode steps captured per hipGraph replay (rounded up to the input copies); "
                          "a one-step graph is timed as well")
+    ap.add_argument("--chunk-align", type=int, default=0, choices=[0, 32, 64, 128],
+                    help="visual chunk granularity of the decode planner (0: the library default)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -552,6 +554,9 @@ def main():
     args = ap.parse_args()
     args.steps_given = any(a == "--steps" or a.startswith("--steps=") for a in sys.argv[1:])
     args.family_given = any(a == "--family" or a.startswith("--family=") for a in sys.argv[1:])
+    if args.chunk_align and not args.pmc_summary:
+        from rotatek_amd import _lib
+        _lib.set_decode_chunk_align(args.chunk_align)
     if args.merge != "auto" and not args.pmc_summary:
         from rotatek_amd import _lib
         _lib.set_decode_merge({"two": _lib.MERGE_TWO_LAUNCHES, "one": _lib.MERGE_SINGLE_LAUNCH}[args.merge])

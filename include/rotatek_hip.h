@@ -275,6 +275,10 @@ int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
  * wgs_per_cu workgroups per compute unit).  Pass 0 to keep a value. */
 void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu);
 
+/* Granularity of the visual chunks in tokens (32, 64 or 128: whole
+ * 32-token blocks, or one block per wave).  Planner override for sweeps. */
+void rk_set_decode_chunk_align(int32_t tokens);
+
 /* ------------------------------------------------------------------ prefill
  * Keys are the visual span of the layer's Keys, [B, H_kv, S_v, 128] in F16
  * or BF16, any strides (a head must span < 2^31 elements).

@@ -92,6 +92,7 @@ _SIGNATURES = {
                        + [ctypes.POINTER(RkDecodePlan)]),
     "rk_set_decode_tuning": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
     "rk_set_decode_merge": (None, [ctypes.c_int32]),
+    "rk_set_decode_chunk_align": (None, [ctypes.c_int32]),
     "rk_decode_workspace_init": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rk_key_covariance_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
     "rk_key_covariance": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
@@ -223,6 +224,11 @@ def plan_decode(B, H_q, H_kv, Dk, S_v, S_f, elem_bytes=2, policy=RK_POLICY_GQA, 
 
 def set_decode_tuning(min_bytes=0, max_bytes=0, wgs_per_cu=0):
     load().rk_set_decode_tuning(int(min_bytes), int(max_bytes), int(wgs_per_cu))
+
+
+def set_decode_chunk_align(tokens: int) -> None:
+    """Visual chunk granularity of the decode planner (32, 64 or 128 tokens)."""
+    load().rk_set_decode_chunk_align(int(tokens))
 
 
 MERGE_AUTO, MERGE_TWO_LAUNCHES, MERGE_SINGLE_LAUNCH = 0, 1, 2

@@ -1167,6 +1167,9 @@ namespace {
 int64_t g_min_wg_bytes = INT64_C(64) << 10;
 int64_t g_max_wg_bytes = INT64_C(512) << 10;
 int32_t g_wgs_per_cu = 2;
+// Visual chunks are whole multiples of this many tokens (a 32-token block
+// or the 128 tokens of one block per wave).
+int64_t g_chunk_align = 32;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
@@ -1239,6 +1242,10 @@ extern "C" int rk_decode_workspace_init(void* workspace, size_t workspace_bytes,
 
 extern "C" void rk_set_decode_merge(int32_t mode) {
   if (mode >= 0 && mode <= 2) g_merge_mode = mode;
+}
+
+extern "C" void rk_set_decode_chunk_align(int32_t tokens) {
+  if (tokens == rk::kBlk || tokens == 2 * rk::kBlk || tokens == kWgTokens) g_chunk_align = tokens;
 }
 
 extern "C" void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu) {
@@ -1319,7 +1326,7 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
       w_vis = fit;
   }
   if (S_v > 0) {
-    p.chunk_vis = round_up(cdiv(S_v, w_vis), kWgTokens);
+    p.chunk_vis = round_up(cdiv(S_v, w_vis), g_chunk_align);
     p.wg_vis = (int32_t)cdiv(S_v, p.chunk_vis);
   }
   if (S_f > 0) {
