@@ -1169,7 +1169,7 @@ int64_t g_max_wg_bytes = INT64_C(512) << 10;
 int32_t g_wgs_per_cu = 2;
 // Visual chunks are whole multiples of this many tokens (a 32-token block
 // or the 128 tokens of one block per wave).
-int64_t g_chunk_align = 32;
+int64_t g_chunk_align = 128;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
