@@ -241,11 +241,34 @@ def _sample_oracle(inp, pairs):
     return res
 
 
+def _torch_fp32_reference(args, b):
+    """The decode of batch row b as plain torch fp32 ops on the device
+    (softmax over the visual and prompt/text logits, then P V): an
+    independent reference for every (head) of a full-size shape.  [H_q, D]."""
+    G = args["num_kv_groups"]
+    q = args["q_full"][b].float()
+    R = args["R_partial"][b].float().contiguous()
+    Hkv, D = R.shape[0], q.shape[-1]
+    qg = q.view(Hkv, G, D)
+    scale = 1.0 / math.sqrt(D)
+    s_vis = torch.matmul(torch.matmul(qg, R), args["k_sparse"][b].float().transpose(-1, -2).contiguous())
+    if args["delta_mu"] is not None:
+        s_vis = s_vis + (qg * args["delta_mu"][b].float()[:, None, :]).sum(-1, keepdim=True)
+    s_full = torch.matmul(qg, args["k_full"][b].float().transpose(-1, -2).contiguous())
+    s_full = s_full.masked_fill(args["mask_full"][b][None, None, :] == 0, float("-inf"))
+    p = torch.softmax(torch.cat([s_vis * scale, s_full * scale], dim=-1), dim=-1)
+    S_v = s_vis.shape[-1]
+    out = torch.matmul(p[..., :S_v].contiguous(), args["v_sparse"][b].float().contiguous()) + \
+        torch.matmul(p[..., S_v:].contiguous(), args["v_full"][b].float().contiguous())
+    return out.reshape(Hkv * G, D)
+
+
 @pytest.mark.parametrize("cfg", ["cfg1", "cfg2", "cfg3", "kp"])
 def test_benchmark_configs_full_size(cfg):
     """Full BASELINE shapes (and the reference kernel harness's shape, kp):
-    sampled (b, kv) groups against the oracle, the rest through properties
-    (paper == gqa family, bit for bit for MHA, finite outputs)."""
+    every output against a plain torch fp32 reference on the device, that
+    reference and the HIP output on sampled (b, kv) groups against the
+    oracle, and paper == gqa (bit for bit for MHA)."""
     from rotatek_amd import synth
     c = synth.CONFIGS[cfg]
     _say(f"full-size {cfg}")
@@ -258,9 +281,22 @@ def test_benchmark_configs_full_size(cfg):
     pairs |= {(0, 0), (c.B - 1, c.H_kv - 1)}
     want = _sample_oracle(args, sorted(pairs))
     G = c.G
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        refs = {}
+        for b in range(c.B):                     # every batch row, every head
+            ref = _torch_fp32_reference(args, b)
+            refs[b] = ref
+            err = (out[b, 0].float() - ref).abs().max().item()
+            assert err <= TOL[c.dtype], (b, err)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
     for (b, kv), w in want.items():
         got = _np(out[b, 0, kv * G:(kv + 1) * G])
         assert np.abs(got - w).max() <= TOL[c.dtype], (b, kv)
+        # the torch reference itself against the oracle
+        assert np.abs(_np(refs[b][kv * G:(kv + 1) * G]) - w).max() <= 1e-4, (b, kv)
     out_p = _decode(args, "paper")
     if c.G == 1:
         assert torch.equal(out_p, out)
