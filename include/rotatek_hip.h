@@ -208,7 +208,7 @@ int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, int64_t num_
  * Cholesky-QR orthonormalisation, replacing rotation.py:21-91
  * (_power_iter_loop; power_iteration_gpu draws v0 with torch.randn from a
  * seeded device generator and calls this).  cov [B,H,128,128], v0 / out
- * [B,H,128,k] F32, 1 <= k <= 64; per iteration V = C V, G = V^T V +
+ * [B,H,128,k] F32, 1 <= k <= 128; per iteration V = C V, G = V^T V +
  * eps * mean(diag G) * I, V = V chol(G)^-T.  out may alias v0.  info
  * (device int32 [B*H], optional) receives 1 for a matrix whose Cholesky
  * met a pivot that is not positive and finite (its output is then not a
