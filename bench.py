@@ -542,6 +542,9 @@ def main():
                          "a one-step graph is timed as well")
     ap.add_argument("--chunk-align", type=int, default=0, choices=[0, 32, 64, 128],
                     help="visual chunk granularity of the decode planner (0: the library default)")
+    ap.add_argument("--skew", type=int, default=-1, metavar="PERMILLE",
+                    help="share of the first-dispatched visual chunks of a one-round grid, in thousandths "
+                         "of the others' (-1: the library default, 0: equal chunks)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -557,6 +560,9 @@ def main():
     if args.chunk_align and not args.pmc_summary:
         from rotatek_amd import _lib
         _lib.set_decode_chunk_align(args.chunk_align)
+    if args.skew >= 0 and not args.pmc_summary:
+        from rotatek_amd import _lib
+        _lib.set_decode_skew(args.skew)
     if args.merge != "auto" and not args.pmc_summary:
         from rotatek_amd import _lib
         _lib.set_decode_merge({"two": _lib.MERGE_TWO_LAUNCHES, "one": _lib.MERGE_SINGLE_LAUNCH}[args.merge])

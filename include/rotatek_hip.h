@@ -264,6 +264,9 @@ typedef struct rk_decode_plan {
   int64_t grid;           /* total workgroups launched                       */
   size_t workspace_bytes;
   int32_t single_launch;  /* 1: the merge runs in the split launch           */
+  int32_t chunk_major;    /* 1: workgroup ids run chunk-major (x*units + u)  */
+  int32_t n_fast;         /* visual chunks 0 .. n_fast-1 hold chunk_fast     */
+  int64_t chunk_fast;     /* tokens (the others chunk_vis)                   */
 } rk_decode_plan;
 
 int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
@@ -276,8 +279,16 @@ int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
 void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu);
 
 /* Granularity of the visual chunks in tokens (32, 64 or 128: whole
- * 32-token blocks, or one block per wave).  Planner override for sweeps. */
+ * 32-token blocks, or one block per wave; 0 = the default, 32 in a
+ * chunk-major grid, else 128).  Planner override for sweeps. */
 void rk_set_decode_chunk_align(int32_t tokens);
+
+/* One-round grids of short workgroups: 0 = unit-major launch, 1000 =
+ * chunk-major launch with equal chunks, 1001..4000 = chunk-major with the
+ * first-dispatched chunks of <= 128 KB workgroups given this many
+ * thousandths of the others' tokens (default 1300).  Planner override for
+ * sweeps. */
+void rk_set_decode_skew(int32_t permille);
 
 /* ------------------------------------------------------------------ prefill
  * Keys are the visual span of the layer's Keys, [B, H_kv, S_v, 128] in F16

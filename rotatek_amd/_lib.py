@@ -61,6 +61,9 @@ class RkDecodePlan(ctypes.Structure):
         ("grid", ctypes.c_int64),
         ("workspace_bytes", ctypes.c_size_t),
         ("single_launch", ctypes.c_int32),
+        ("chunk_major", ctypes.c_int32),
+        ("n_fast", ctypes.c_int32),
+        ("chunk_fast", ctypes.c_int64),
     ]
 
 
@@ -93,6 +96,7 @@ _SIGNATURES = {
     "rk_set_decode_tuning": (None, [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32]),
     "rk_set_decode_merge": (None, [ctypes.c_int32]),
     "rk_set_decode_chunk_align": (None, [ctypes.c_int32]),
+    "rk_set_decode_skew": (None, [ctypes.c_int32]),
     "rk_decode_workspace_init": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rk_key_covariance_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
     "rk_key_covariance": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
@@ -227,8 +231,17 @@ def set_decode_tuning(min_bytes=0, max_bytes=0, wgs_per_cu=0):
 
 
 def set_decode_chunk_align(tokens: int) -> None:
-    """Visual chunk granularity of the decode planner (32, 64 or 128 tokens)."""
+    """Visual chunk granularity of the decode planner (32, 64 or 128 tokens;
+    0 = the default: 32 in a chunk-major grid, else 128)."""
     load().rk_set_decode_chunk_align(int(tokens))
+
+
+def set_decode_skew(permille: int) -> None:
+    """One-round decode grids of short workgroups: 0 = unit-major launch,
+    1000 = chunk-major with equal chunks, 1001..4000 = chunk-major with the
+    first-dispatched chunks of <= 128 KB workgroups given this many
+    thousandths of the others' tokens (default 1300)."""
+    load().rk_set_decode_skew(int(permille))
 
 
 MERGE_AUTO, MERGE_TWO_LAUNCHES, MERGE_SINGLE_LAUNCH = 0, 1, 2

@@ -90,6 +90,11 @@ struct DecodeArgs {
   // within-head strides (elements); a head's span is < 2^31 elements
   uint32_t kf_ss, kf_sd, vf_ss, vf_sd, ks_ss, ks_sd, vs_ss, vs_sd;
   int32_t G, Dk, hpu, spk, units_per_b, wg_vis, np, rot_x;
+  // cmajor: the grid is (units, np), so workgroup ids run chunk-major
+  // (x * units + u) and visual chunks x < nfast hold chunk_fast tokens (the
+  // others chunk_vis; see rk_plan_decode)
+  int32_t cmajor, nfast;
+  int64_t chunk_fast;
   // xgroup > 1 (one unit per query head, G query heads per KV head): the
   // units of a KV head that read the same chunk run in consecutive slots of
   // one XCD (see decode_kernel); units = B * H_q
@@ -524,8 +529,8 @@ decode_kernel(const DecodeArgs a) {
   const int nq = n < HMAX ? n : 0;  // LDS row for this lane's head column
   // Workgroups go to the 8 XCDs round-robin by linear id u * np + x; rot_x
   // rotates each unit's chunk numbers by the unit index (see run_decode).
-  int u = blockIdx.y;
-  int x = (int)blockIdx.x + (a.rot_x ? u % a.np : 0);
+  int u = a.cmajor ? (int)blockIdx.x : (int)blockIdx.y;
+  int x = a.cmajor ? (int)blockIdx.y : (int)blockIdx.x + (a.rot_x ? u % a.np : 0);
   x = x >= a.np ? x - a.np : x;
   if (!NTL && a.xgroup > 1) {  // compiled into the grouped mode's instantiation only
     // Workgroup id i = y * np + x runs on XCD i mod 8 as the (i / 8)-th of
@@ -643,8 +648,9 @@ decode_kernel(const DecodeArgs a) {
 
   if (is_vis) {
     // ---- visual span: rotated, truncated Keys (Dk channels)
-    const int64_t t_begin = (int64_t)x * a.chunk_vis;
-    const int64_t t_end = min(a.S_v, t_begin + a.chunk_vis);
+    const int64_t t_begin = x < a.nfast ? (int64_t)x * a.chunk_fast
+                                        : (int64_t)a.nfast * a.chunk_fast + (int64_t)(x - a.nfast) * a.chunk_vis;
+    const int64_t t_end = min(a.S_v, t_begin + (x < a.nfast ? a.chunk_fast : a.chunk_vis));
     const uint32_t t_last = (uint32_t)(t_end - 1);
     const uint16_t* ksb = a.ks + b * a.ks_sb + kv * a.ks_sh;
     const uint16_t* vsb = a.vs + b * a.vs_sb + kv * a.vs_sh;
@@ -1168,8 +1174,14 @@ int64_t g_min_wg_bytes = INT64_C(64) << 10;
 int64_t g_max_wg_bytes = INT64_C(512) << 10;
 int32_t g_wgs_per_cu = 2;
 // Visual chunks are whole multiples of this many tokens (a 32-token block
-// or the 128 tokens of one block per wave).
-int64_t g_chunk_align = 128;
+// or the 128 tokens of one block per wave); 0: 32 in a chunk-major grid,
+// else 128.
+int64_t g_chunk_align = 0;
+// One-round grids of short workgroups (see rk_plan_decode): 0 keeps the
+// unit-major launch, 1000 launches chunk-major with equal chunks, more
+// gives the first-dispatched chunks of the smallest workgroups this many
+// thousandths of the others' tokens.
+int32_t g_skew_permille = 1300;
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
@@ -1180,6 +1192,7 @@ constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
 // latency (prologue + epilogue, ~8 us at ~14 GB/s per slot on MI355X).
 constexpr int64_t kSlotLatencyBytes = INT64_C(128) << 10;
 constexpr int64_t kMinWgsPerUnit = 8;
+constexpr int64_t kSkewMaxBytes = INT64_C(128) << 10;
 
 // Merge mode (rk_set_decode_merge): 0 (default) and 1 = two launches,
 // 2 = single launch where the ticket region holds the counters.
@@ -1245,7 +1258,11 @@ extern "C" void rk_set_decode_merge(int32_t mode) {
 }
 
 extern "C" void rk_set_decode_chunk_align(int32_t tokens) {
-  if (tokens == rk::kBlk || tokens == 2 * rk::kBlk || tokens == kWgTokens) g_chunk_align = tokens;
+  if (tokens == 0 || tokens == rk::kBlk || tokens == 2 * rk::kBlk || tokens == kWgTokens) g_chunk_align = tokens;
+}
+
+extern "C" void rk_set_decode_skew(int32_t permille) {
+  if (permille == 0 || (permille >= 1000 && permille <= 4000)) g_skew_permille = permille;
 }
 
 extern "C" void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu) {
@@ -1325,8 +1342,14 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
         unit_vis / fit - unit_vis / w_vis < kSlotLatencyBytes)
       w_vis = fit;
   }
+  // One round of workgroups of at most g_max_wg_bytes (a grid of short
+  // workgroups, whose fixed costs show) launches chunk-major (below) with
+  // 32-token chunks, so that the round's slots fill.
+  const bool short_round = g_skew_permille > 0 && elem_bytes == 2 && S_v > 0 && rounds == 1 &&
+                           unit_bytes <= (w_vis + w_full) * g_max_wg_bytes;
+  const int64_t align = g_chunk_align > 0 ? g_chunk_align : short_round ? rk::kBlk : kWgTokens;
   if (S_v > 0) {
-    p.chunk_vis = round_up(cdiv(S_v, w_vis), g_chunk_align);
+    p.chunk_vis = round_up(cdiv(S_v, w_vis), align);
     p.wg_vis = (int32_t)cdiv(S_v, p.chunk_vis);
   }
   if (S_f > 0) {
@@ -1340,6 +1363,41 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   }
   p.grid = p.units * (p.wg_vis + p.wg_full);
   if (p.units > 65535 * 1024 || p.wg_vis + p.wg_full > (1 << 30)) return RK_ERR_SHAPE;
+  // Chunk-major launch (workgroup id x * units + u) of a short round: with
+  // units a multiple of 8, all chunks of a unit run on one XCD (ids go to
+  // the XCDs round-robin), which then fetches the unit's q, R_partial and
+  // delta_mu once into its L2 instead of every XCD fetching every unit's.
+  // Measured on MI355X over 28 graph-replayed layers of B=8, 4 KV heads of
+  // 7 query heads: 945 -> 894 us per step at 12001 visual tokens, 740 ->
+  // 665 us at 4097 (keep 32); B=1, 32 heads, 16k: 35.2 -> 35.0 us.  Rounds
+  // of larger workgroups keep the unit-major launch (B=16, 32k, G=7: 1.4 MB
+  // workgroups, 111.8 us unit-major, 113.5 us chunk-major).
+  if (short_round && p.grid <= slots && p.grid <= 65535) p.chunk_major = 1;
+  // The CUs take the first num_cus workgroup ids one each, then the rest.
+  // Both workgroups of a CU start together, but the first-dispatched one
+  // streams faster (per-workgroup timestamps on MI355X: 76 against 103 us
+  // at B=16, 32k context, G=7; 17 against 21 us on a B=8, 12001-token
+  // layer).  In a chunk-major grid the first num_cus ids are the chunks
+  // x < n_fast = num_cus / units of every unit.  Where workgroups stream
+  // <= 128 KB (fixed latency dominates), those chunks take chunk_fast
+  // tokens, g_skew_permille / 1000 times the others' (whole 32-token
+  // blocks): B=8, 4097 visual tokens, keep 32, 665 -> 648 us per step; at
+  // 12001 tokens (256 KB workgroups) the skew measured 894 -> 903 us.
+  if (p.chunk_major && g_skew_permille > 1000 && p.wg_vis >= 2 && p.grid > num_cus &&
+      unit_vis <= p.wg_vis * kSkewMaxBytes) {
+    const int64_t nf = num_cus / p.units, ns = p.wg_vis - nf;
+    const int64_t nb = cdiv(S_v, rk::kBlk);
+    if (nf >= 1 && ns >= 1) {
+      const double rho = g_skew_permille / 1000.0;
+      const int64_t bf = (int64_t)(rho * (double)nb / ((double)nf * rho + (double)ns) + 0.5);
+      const int64_t bs = nb - nf * bf > 0 ? cdiv(nb - nf * bf, ns) : 0;
+      if (bs >= 1 && bf > bs && nf * bf + (ns - 1) * bs < nb) {
+        p.n_fast = (int32_t)nf;
+        p.chunk_fast = bf * rk::kBlk;
+        p.chunk_vis = bs * rk::kBlk;
+      }
+    }
+  }
   p.workspace_bytes = ws_layout(p).total;
   p.single_launch = use_single_launch(p, B, num_cus) ? 1 : 0;
   *plan = p;
@@ -1478,7 +1536,7 @@ hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
                        s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fused) return e;
-  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3(grid.y), dim3(rk::kThreads), 0, s, a);
+  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)a.units), dim3(rk::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1535,7 +1593,7 @@ hipError_t launch32(bool has_vis, bool vec, const rk::DecodeArgs& a, dim3 grid, 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fused) return e;
-  hipLaunchKernelGGL((rk::merge_kernel<rk::F32>), dim3(grid.y), dim3(rk::kThreads), 0, s, a);
+  hipLaunchKernelGGL((rk::merge_kernel<rk::F32>), dim3((unsigned)a.units), dim3(rk::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1685,7 +1743,11 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   if (a.xgroup || c.dtype == RK_F32) a.rot_x = 0;
   if (c.dtype == RK_F32) a.spk = (int32_t)c.G;  // one unit per query head
   a.scale_log2 = (float)(rk::kLog2e / sqrt(128.0));
-  const dim3 grid((unsigned)a.np, (unsigned)p.units);
+  a.cmajor = has_vis && c.dtype != RK_F32 && !a.xgroup ? p.chunk_major : 0;
+  a.nfast = a.cmajor ? p.n_fast : 0;
+  a.chunk_fast = p.chunk_fast;
+  if (a.cmajor) a.rot_x = 0;
+  const dim3 grid = a.cmajor ? dim3((unsigned)p.units, (unsigned)a.np) : dim3((unsigned)a.np, (unsigned)p.units);
   const int hmax = p.heads_per_unit > 1 ? 16 : 1;
   hipStream_t s = (hipStream_t)stream;
   if (c.dtype == RK_F32) {

@@ -183,7 +183,8 @@ def test_launch_without_workspace_fails_cleanly():
 @pytest.mark.parametrize("shape", [
     (32, 32, 32, 32, 14000, 2000), (1, 32, 32, 32, 15360, 640), (16, 28, 4, 32, 30720, 2048),
     (8, 28, 4, 16, 12001, 61), (1, 4, 4, 64, 1, 1), (3, 8, 2, 128, 0, 77), (2, 8, 8, 8, 300, 0),
-    (1, 64, 2, 32, 500, 40), (2, 4, 4, 32, 0, 0),
+    (1, 64, 2, 32, 500, 40), (2, 4, 4, 32, 0, 0), (8, 28, 4, 32, 4097, 61), (8, 28, 4, 64, 4097, 60),
+    (3, 12, 4, 32, 2049, 17), (5, 20, 4, 24, 9001, 300), (4, 32, 8, 32, 3001, 100), (2, 16, 16, 32, 2500, 60),
 ])
 @pytest.mark.parametrize("policy", [0, 1])
 def test_plan_covers_every_token(shape, policy):
@@ -194,11 +195,21 @@ def test_plan_covers_every_token(shape, policy):
         assert p["heads_per_unit"] == min(G, 16) and p["units"] == B * Hkv * -(-G // 16)
     else:
         assert p["heads_per_unit"] == 1 and p["units"] == B * Hq
-    for S, wg, ch in ((S_v, p["wg_vis"], p["chunk_vis"]), (S_f, p["wg_full"], p["chunk_full"])):
-        if S > 0:
-            assert ch % 128 == 0 and wg * ch >= S and (wg - 1) * ch < S
+    if S_v > 0:
+        # visual chunks: n_fast of chunk_fast tokens, then chunk_vis each;
+        # whole 32-token blocks in a chunk-major grid, else 128-token ones
+        nf, cf, cv, wg = p["n_fast"], p["chunk_fast"], p["chunk_vis"], p["wg_vis"]
+        align = 32 if p["chunk_major"] else 128
+        assert cv % align == 0 and cf % align == 0 and 0 <= nf < wg
+        assert nf == 0 or (p["chunk_major"] and cf > cv)
+        assert nf * cf + (wg - nf) * cv >= S_v and nf * cf + (wg - nf - 1) * cv < S_v
+    if S_f > 0:
+        wg, ch = p["wg_full"], p["chunk_full"]
+        assert ch % 128 == 0 and wg * ch >= S_f and (wg - 1) * ch < S_f
     assert p["wg_vis"] + p["wg_full"] >= 1
     assert p["grid"] == p["units"] * (p["wg_vis"] + p["wg_full"])
+    if p["chunk_major"]:
+        assert p["grid"] <= 2 * 256
 
 
 # ----------------------------------------------------------------- prefill ABI
@@ -425,3 +436,32 @@ def test_plan_keeps_one_round_when_the_extra_slot_saves_little():
     stays within 2 x 256 slots."""
     p = _lib.plan_decode(8, 28, 4, 32, 12001, 61, policy=1)
     assert p["grid"] <= 2 * 256
+
+
+def test_plan_chunk_major_short_rounds():
+    """One round of short workgroups launches chunk-major with 32-token
+    chunks (config 4 layers, config 1); rounds of long workgroups (config 3)
+    and multi-round grids (config 2, kp) keep the unit-major launch; the
+    first-dispatched chunks are enlarged only where workgroups stream
+    <= 128 KB (config 4 at 4097 visual tokens)."""
+    cfg4l = _lib.plan_decode(8, 28, 4, 32, 12001, 61, policy=1)
+    assert cfg4l["chunk_major"] == 1 and cfg4l["n_fast"] == 0 and cfg4l["grid"] == 512
+    cfg4s = _lib.plan_decode(8, 28, 4, 32, 4097, 61, policy=1)
+    assert cfg4s["chunk_major"] == 1 and cfg4s["n_fast"] == 256 // cfg4s["units"]
+    assert cfg4s["chunk_fast"] > cfg4s["chunk_vis"]
+    assert _lib.plan_decode(1, 32, 32, 32, 15360, 640, policy=0)["chunk_major"] == 1
+    for shape, pol in (((16, 28, 4, 32, 30720, 2048), 1), ((32, 32, 32, 32, 14000, 2000), 0),
+                       ((32, 32, 8, 32, 16000, 80), 1)):
+        p = _lib.plan_decode(*shape, policy=pol)
+        assert p["chunk_major"] == 0 and p["n_fast"] == 0 and p["chunk_vis"] % 128 == 0
+    # fp32 (the VALU kernel) keeps the unit-major launch
+    assert _lib.plan_decode(1, 32, 32, 32, 2304, 128, elem_bytes=4, policy=0)["chunk_major"] == 0
+    try:
+        _lib.set_decode_skew(1000)      # chunk-major, equal chunks
+        p = _lib.plan_decode(8, 28, 4, 32, 4097, 61, policy=1)
+        assert p["chunk_major"] == 1 and p["n_fast"] == 0
+        _lib.set_decode_skew(0)         # unit-major
+        p = _lib.plan_decode(8, 28, 4, 32, 4097, 61, policy=1)
+        assert p["chunk_major"] == 0 and p["chunk_vis"] % 128 == 0
+    finally:
+        _lib.set_decode_skew(1300)

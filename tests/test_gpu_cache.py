@@ -343,9 +343,14 @@ def test_graph_survives_workspace_growth_after_capture():
     kn = torch.zeros(1, B, Hkv, 1, D, dtype=dtype, device="cuda")
     vn = torch.zeros_like(kn)
     out = torch.empty(1, B, Hq, D, dtype=dtype, device="cuda")
+    # start from a workspace sized for this cache alone (earlier tests may
+    # have grown the shared one past the large decode below)
+    idx = torch.cuda.current_device()
+    if idx in _lib._WORKSPACE:
+        _lib._RETIRED.append(_lib._WORKSPACE.pop(idx))
     graph = cache.capture_decode(q, kn, vn, out, Hq // Hkv)
     torch.cuda.synchronize()
-    old_ws = _lib._WORKSPACE[torch.cuda.current_device()].data_ptr()
+    old_ws = _lib._WORKSPACE[idx].data_ptr()
     # a much larger decode grows the workspace past the captured buffer
     g = torch.Generator(device="cuda").manual_seed(3)
     big = dict(q_full=torch.randn(16, 32, D, generator=g, device="cuda").to(dtype),

@@ -7,7 +7,9 @@ rotated, and which workgroup ids carry which (unit, chunk).  This test draws
 48 shapes with a fixed seed over both families and both 16-bit dtypes,
 including odd and empty spans, G up to 20 and D_keep from 8 to 128, and
 checks every output against the float64 oracle at the north-star bars
-(max-abs 2e-3 fp16, 1e-2 bf16).  Every case prints its parameters first.
+(max-abs 2e-3 fp16, 1e-2 bf16), under each planner layout of one-round
+grids (unit-major, chunk-major, chunk-major with enlarged first-dispatched
+chunks).  Every case prints its parameters first.
 """
 import sys
 
@@ -45,12 +47,23 @@ def _cases(n=48, seed=2024):
 CASES = _cases()
 
 
+@pytest.fixture
+def planner(request):
+    from rotatek_amd import _lib
+    _lib.set_decode_skew(request.param)
+    yield request.param
+    _lib.set_decode_skew(1300)
+
+
+# planner layouts of one-round grids: unit-major, chunk-major, the default
+# (chunk-major, first-dispatched chunks enlarged for short workgroups)
+@pytest.mark.parametrize("planner", [0, 1000, 1300], indirect=True, ids=["um", "cm", "default"])
 @pytest.mark.parametrize("case", CASES, ids=[f"c{c[0]}" for c in CASES])
-def test_random_shape_matches_oracle(case):
+def test_random_shape_matches_oracle(case, planner):
     from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
     from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
     i, B, Hq, Hkv, dk, S_v, S_f, dtype, family, mask_p = case
-    print(f"[case] {case}", flush=True)
+    print(f"[case] {case} planner={planner}", flush=True)
     sys.stdout.flush()
     g = torch.Generator(device="cuda").manual_seed(1000 + i)
 
