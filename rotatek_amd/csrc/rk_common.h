@@ -91,6 +91,31 @@ __device__ __forceinline__ float load_any(const void* p, int64_t idx, int dtype)
   return dtype == 0 ? F16::to_f32(b) : BF16::to_f32(b);
 }
 
+// N elements p[idx0 + i * stride] of a launch-uniform dtype: one branch on
+// the dtype, then N loads issued back to back (load_any per element puts
+// each load in its own branch, and each then waits for its data).
+template <int N>
+__device__ __forceinline__ void load_any_n(const void* p, int64_t idx0, int64_t stride, int dtype,
+                                           float (&out)[N]) {
+  if (dtype == 2) {
+    const float* f = (const float*)p;
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = f[idx0 + i * stride];
+  } else {
+    const uint16_t* h = (const uint16_t*)p;
+    uint16_t r[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = h[idx0 + i * stride];
+    if (dtype == 0) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = F16::to_f32(r[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = BF16::to_f32(r[i]);
+    }
+  }
+}
+
 // Split form of load_any for prologues: load_raw issues the load (32 bits
 // for F32, 16 bits otherwise, chosen by a dtype that is uniform across the
 // launch), raw_to_f32 converts later, so the wait for the data can be placed

@@ -723,11 +723,16 @@ decode_kernel(const DecodeArgs a) {
       const uint16_t* rl = (const uint16_t*)s_r;
 #pragma unroll
       for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? raw_to_f32(rl[(part * kL + i) * a.Dk + c], a.r_dtype) : 0.f;
-    } else {  // element-wise fallback (column c, clamped in-bounds)
-      const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)min(c, a.Dk - 1) * a.R_sk;
+    } else {  // element-wise fallback (column c, clamped in-bounds; no load
+              // at all when Dk == 0, where R_partial has no storage)
 #pragma unroll
-      for (int i = 0; i < kL; ++i)
-        rv[i] = c < a.Dk ? load_any(a.R, rb + (int64_t)(part * kL + i) * a.R_sd, a.r_dtype) : 0.f;
+      for (int i = 0; i < kL; ++i) rv[i] = 0.f;
+      if (a.Dk > 0) {
+        const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)min(c, a.Dk - 1) * a.R_sk;
+        load_any_n(a.R, rb + (int64_t)(part * kL) * a.R_sd, a.R_sd, a.r_dtype, rv);
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
+      }
     }
     float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
 #pragma unroll
@@ -1063,8 +1068,7 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
       if (a.Dk > 0) {
         for (int d0 = 64 * half; d0 < 64 * half + 64; d0 += 32) {
           float rv[32];
-#pragma unroll
-          for (int i = 0; i < 32; ++i) rv[i] = load_any(a.R, rb + (int64_t)(d0 + i) * a.R_sd, a.r_dtype);
+          load_any_n(a.R, rb + (int64_t)d0 * a.R_sd, a.R_sd, a.r_dtype, rv);
 #pragma unroll
           for (int i = 0; i < 32; ++i) sum = fmaf(s_q[d0 + i], rv[i], sum);
         }
