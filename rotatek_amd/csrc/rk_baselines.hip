@@ -352,113 +352,233 @@ struct SparkArgs {
   OutView pm;      // [B, H, S, 1]
 };
 
-// grid (splits, B*H).  Each 16-lane row of a wave owns one token (lane n:
-// channels 8n..8n+7, one 16-byte load), so a wave selects four tokens at
-// once and a workgroup sixteen; rows are prefetched two iterations ahead.
-// Selection per row: the keep-th largest 16-bit score key T by a bitwise
-// search over 16-lane counts, then every channel above T and, of those equal
-// to T, the lowest channels up to keep.  MVEC: 8-byte mask stores.
+// Packed 16-bit lanes: two channels per dword, the lower channel in the low
+// half.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+
+// Scores of one lane's 32 channels, two per dword: dtype(dtype(k^2) qn)
+// (spark.py:40-41; every product of two 16-bit values is exact in fp32, so
+// one rounding per operation matches torch's op-by-op result).
+template <class TT>
+struct SparkScore;
+
+template <>
+struct SparkScore<F16> {
+  uint32_t q[16];  // qn of the lane's channels, packed f16 (qn is f16-exact)
+  static constexpr uint32_t kNaNKey = 0x7C01u;
+  __device__ __forceinline__ void init(const float* qn) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) q[i] = F16::pack2(qn[2 * i], qn[2 * i + 1]);
+  }
+  __device__ __forceinline__ uint32_t score(uint32_t kw, int i) const {
+    const h16x2 k = __builtin_bit_cast(h16x2, kw);
+    const h16x2 k2 = k * k;  // rounded to f16, as torch.pow
+    const h16x2 s = k2 * __builtin_bit_cast(h16x2, q[i]);
+    return __builtin_bit_cast(uint32_t, s);
+  }
+  // acc + both halves of w (fp32 accumulate)
+  static __device__ __forceinline__ float add2(uint32_t w, float acc) {
+    const h16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h16x2, w), one, acc, false);
+  }
+};
+
+template <>
+struct SparkScore<BF16> {
+  float q[32];  // qn of the lane's channels (bf16-exact)
+  static constexpr uint32_t kNaNKey = 0x7F81u;
+  __device__ __forceinline__ void init(const float* qn) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) q[j] = qn[j];
+  }
+  __device__ __forceinline__ uint32_t score(uint32_t kw, int i) const {
+    const float k0 = __builtin_bit_cast(float, kw << 16), k1 = __builtin_bit_cast(float, kw & 0xFFFF0000u);
+    const uint32_t sq = BF16::pack2(k0 * k0, k1 * k1);
+    return BF16::pack2(__builtin_bit_cast(float, sq << 16) * q[2 * i],
+                       __builtin_bit_cast(float, sq & 0xFFFF0000u) * q[2 * i + 1]);
+  }
+  static __device__ __forceinline__ float add2(uint32_t w, float acc) {
+    const b16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b16x2, w), one, acc, false);
+  }
+};
+
+// Number of the lane's 32 keys (15-bit, two per dword) >= cand, cand >= 1,
+// given ksum = the sum of the 32 keys.  Each half of cm - key (packed u16,
+// wrapping) is cm - key + 2^16 [key > cm] with cm = cand - 1, so the
+// v_dot2_u32_u16 sum of those halves is 32 cm - ksum + 2^16 #{key >= cand}:
+// two instructions per two keys.
+__device__ __forceinline__ int count_ge(const uint32_t (&key)[16], uint32_t ksum, uint32_t cand) {
+  const unsigned short c = (unsigned short)(cand - 1u);
+  const u16x2 cm = {c, c}, one = {1, 1};
+  uint32_t acc = ksum - 32u * (cand - 1u);  // mod 2^32: ends at 2^16 #{key >= cand}
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc = __builtin_amdgcn_udot2(cm - __builtin_bit_cast(u16x2, key[i]), one, acc, false);
+  return (int)(acc >> 16);
+}
+
+// Sum over the four lanes of this lane's quad (DPP quad permutations).
+__device__ __forceinline__ int qsum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  return v;
+}
+__device__ __forceinline__ float qsumf(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  return v;
+}
+// Exclusive prefix sum over the lanes of the quad below this one.
+__device__ __forceinline__ int qprefix(int v) {
+  const int q = threadIdx.x & 3;
+  int incl = v;
+  int t = __shfl_up(incl, 1, 4);
+  if (q >= 1) incl += t;
+  t = __shfl_up(incl, 2, 4);
+  if (q >= 2) incl += t;
+  return incl - v;
+}
+
+// grid (splits, B*H).  Each lane quad of a wave owns one token (lane q of
+// the quad: channels 32q..32q+31, four 16-byte loads), so a wave selects 16
+// tokens at once and a workgroup 64; the next 64 rows are loaded while the
+// current ones are selected.  Per token: 15-bit order-preserving score keys
+// (NaN highest, every NaN equal), kept two per dword; the keep-th largest
+// key T by a bitwise search whose counts take three packed 16-bit
+// operations per two keys; every channel above T is kept and, of those
+// equal to T, the lowest channels up to keep (a per-channel pass, taken by a
+// wave only where some token's ties straddle the boundary).  The kept values
+// are compacted through LDS in channel order.  MVEC: 8-byte mask stores.
 template <class TT, bool KVEC, bool MVEC, bool CVEC>
 __global__ void __launch_bounds__(kThreads) spark_kernel(const SparkArgs a) {
-  __shared__ __align__(16) uint16_t s_row[kThreads / 64][4][kD];  // per wave: its four compact rows
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
+  constexpr int kRow = kD + 8;  // compact row slot; element kD is the sink of pruned values
+  __shared__ __align__(16) uint16_t s_row[kThreads / 4][kRow];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, qd = lane >> 2, q = lane & 3;
   const int x = blockIdx.x, bh = blockIdx.y, b = bh / a.k.H, h = bh - b * a.k.H;
-  float qv[8];
+  SparkScore<TT> sc;
+  {
+    float qv[32];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) qv[e] = a.qn[(int64_t)bh * kD + 8 * n + e];
+    for (int j = 0; j < 32; ++j) qv[j] = a.qn[(int64_t)bh * kD + 32 * q + j];
+    sc.init(qv);
+  }
   const uint16_t* kb = a.k.data + head_off(a.k.sb, a.k.sh, b, h);
   uint16_t* cb = a.kc.data + head_off(a.kc.sb, a.kc.sh, b, h);
   uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
   uint16_t* pb = a.pm.data + head_off(a.pm.sb, a.pm.sh, b, h);
   const int64_t t0 = (int64_t)x * a.chunk, t1 = min(a.k.S, t0 + a.chunk);
   const int keep = a.keep;
-  auto load = [&](int64_t t) { return ld8<KVEC>(kb, a.k.ss, a.k.sc, min(t, t1 - 1), 8 * n); };
+  uint16_t* row = s_row[threadIdx.x >> 2];
+  auto load = [&](uint4 (&v)[4], int64_t tb) {
+    const int64_t t = min(tb + qd, t1 - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = ld8<KVEC>(kb, a.k.ss, a.k.sc, t, 32 * q + 8 * i);
+  };
 
-  const int64_t first = t0 + 4 * w;  // this wave's first group; groups advance by 16 tokens
-  uint4 b0 = make_uint4(0, 0, 0, 0), b1 = b0;
-  if (first < t1) b0 = load(first + g);
-  if (first + 16 < t1) b1 = load(first + 16 + g);
-  for (int64_t tb = first; tb < t1; tb += 16) {  // wave-uniform loop
-    const uint4 cur = b0;
-    b0 = b1;
-    if (tb + 32 < t1) b1 = load(tb + 32 + g);
-    const int64_t t = tb + g;
-    float ev[8];
-    uint32_t kk[8];
+  uint4 cur[4], nxt[4];
+  int64_t tb = t0 + 16 * w;  // this wave's first token group; groups advance by 64 tokens
+  if (tb < t1) load(cur, tb);
+  for (; tb < t1; tb += 64) {  // wave-uniform loop
+    if (tb + 64 < t1) load(nxt, tb + 64);
+    const int64_t t = tb + qd;
+    uint32_t kw[16], pm[16];  // raw values; then 0xFFFF per pruned channel
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      ev[e] = TT::to_f32((uint16_t)(word(cur, e >> 1) >> ((e & 1) * 16)));
-      kk[e] = order_key<TT>(rnd<TT>(rnd<TT>(ev[e] * ev[e]) * qv[e]));
-    }
-    uint32_t kept = 0u;  // bit e: channel 8n + e kept
+    for (int i = 0; i < 16; ++i) kw[i] = word(cur[i >> 2], i & 3);
     if (keep >= kD) {
-      kept = 0xFFu;
-    } else if (keep > 0) {
-      uint32_t T = 0u;  // largest T with #{key >= T} >= keep in this row
-      for (int bit = 15; bit >= 0; --bit) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pm[i] = 0u;
+    } else if (keep <= 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pm[i] = 0xFFFFFFFFu;
+    } else {
+      uint32_t key[16];
+      const u16x2 nan_key = {(unsigned short)SparkScore<TT>::kNaNKey, (unsigned short)SparkScore<TT>::kNaNKey};
+#pragma unroll
+      for (int i = 0; i < 16; ++i)  // |score| bits (scores are >= 0), every NaN -> one key above inf
+        key[i] = __builtin_bit_cast(
+            uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, sc.score(kw[i], i) & 0x7FFF7FFFu), nan_key));
+      uint32_t ksum = 0u;
+      const u16x2 one = {1, 1};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ksum = __builtin_amdgcn_udot2(__builtin_bit_cast(u16x2, key[i]), one, ksum, false);
+      uint32_t T = 0u;  // largest T with #{key >= T} >= keep in this token
+#pragma unroll
+      for (int bit = 14; bit >= 0; --bit) {
         const uint32_t cand = T | (1u << bit);
-        int c = 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) c += kk[e] >= cand;
-        T = sum16(c) >= keep ? cand : T;
+        T = qsum(count_ge(key, ksum, cand)) >= keep ? cand : T;
       }
-      int gt = 0, eq = 0;
+      const int ge = T == 0u ? 32 : count_ge(key, ksum, T), gt = count_ge(key, ksum, T + 1u);
+      const int need = keep - qsum(gt), eq = qsum(ge - gt);
+      const unsigned short Ts = (unsigned short)T;
+      const u16x2 T2 = {Ts, Ts};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        gt += kk[e] > T;
-        eq += kk[e] == T;
-      }
-      const int need = keep - sum16(gt);
-      int er = scan16(eq);
+      for (int i = 0; i < 16; ++i)  // key < T: the wrapped 15-bit difference is negative
+        pm[i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, __builtin_bit_cast(u16x2, key[i]) - T2) >> 15);
+      if (__any(need != eq)) {  // some token keeps only part of its ties: lowest channels first
+        int run = qprefix(ge - gt);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bool tie = kk[e] == T;
-        kept |= (kk[e] > T || (tie && er < need) ? 1u : 0u) << e;
-        er += tie;
-      }
-    }
-    int pos = scan16(__popc(kept));
-    float p = 0.f;
+        for (int i = 0; i < 16; ++i) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p += ((kept >> e) & 1u) ? 0.f : ev[e];
-    p = fsum16(p);
-    // the row's kept values in channel order, assembled in LDS and written
-    // as 16-byte chunks (lane n: columns 8n..8n+7)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if ((kept >> e) & 1u) {
-        s_row[w][g][pos] = (uint16_t)(word(cur, e >> 1) >> ((e & 1) * 16));
-        ++pos;
+          for (int hh = 0; hh < 2; ++hh) {
+            const uint32_t k = (key[i] >> (16 * hh)) & 0xFFFFu;
+            const bool tie = k == T;
+            if (tie && run >= need) pm[i] |= 0xFFFFu << (16 * hh);
+            run += tie;
+          }
+        }
       }
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (t < t1 && 8 * n < keep) {
-      const uint16_t* src = &s_row[w][g][8 * n];
-      if constexpr (CVEC) {
-        *(uint4*)(cb + t * a.kc.ss + 8 * n) = *(const uint4*)src;
-      } else {
+    // kept values -> LDS in channel order, the rest to the sink slot
+    int kept = 0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (8 * n + e < keep) cb[t * a.kc.ss + (8 * n + e) * a.kc.sc] = src[e];
+    for (int i = 0; i < 16; ++i) kept += (int)((~pm[i]) & 1u) + (int)((~pm[i] >> 16) & 1u);
+    int pos = qprefix(kept);
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      psum = SparkScore<TT>::add2(kw[i] & pm[i], psum);  // the pruned values (kept ones read as +0)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint16_t v = (uint16_t)(kw[i] >> (16 * hh));
+        const bool k = ((pm[i] >> (16 * hh)) & 1u) == 0u;
+        row[k ? pos : kD] = v;
+        pos += k;
       }
     }
+    psum = qsumf(psum);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (t < t1) {
-      if constexpr (MVEC) {
-        uint64_t m = 0ull;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) m |= (uint64_t)((kept >> e) & 1u) << (8 * e);
-        *(uint64_t*)(mb + t * a.mask.ss + 8 * n) = m;
+      if constexpr (CVEC) {
+        for (int c = q; 8 * c < keep; c += 4) *(uint4*)(cb + t * a.kc.ss + 8 * c) = *(const uint4*)(row + 8 * c);
       } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) mb[t * a.mask.ss + (8 * n + e) * a.mask.sc] = (uint8_t)((kept >> e) & 1u);
+        for (int e = q; e < keep; e += 4) cb[t * a.kc.ss + e * a.kc.sc] = row[e];
       }
-      if (n == 0) pb[t * a.pm.ss] = TT::from_f32(pin(p * a.f_pruned));
+      // kept flags as bytes: bytes 0 and 2 of two mask dwords -> channels 4d..4d+3
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const uint32_t m4 = ~__builtin_amdgcn_perm(pm[2 * d + 1], pm[2 * d], 0x06040200u) & 0x01010101u;
+        if constexpr (MVEC) {
+          if ((d & 1) == 0) continue;
+          const uint32_t m0 = ~__builtin_amdgcn_perm(pm[2 * d - 1], pm[2 * d - 2], 0x06040200u) & 0x01010101u;
+          *(uint64_t*)(mb + t * a.mask.ss + 32 * q + 4 * (d - 1)) = (uint64_t)m0 | ((uint64_t)m4 << 32);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            mb[t * a.mask.ss + (32 * q + 4 * d + e) * a.mask.sc] = (uint8_t)((m4 >> (8 * e)) & 1u);
+        }
+      }
+      if (q == 0) pb[t * a.pm.ss] = TT::from_f32(pin(psum * a.f_pruned));
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
   }
 }
 
