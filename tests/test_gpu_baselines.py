@@ -162,6 +162,38 @@ def test_spark_random_and_views(dtype, layout):
     assert np.all(err <= ULP[dtype] * np.maximum(np.abs(want), 1e-30)), err.max()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("prune", [32, 96, 127])
+def test_spark_nonfinite_matches_oracle(dtype, prune):
+    """Keys holding NaN, +-inf and -0 and a query channel of zeros (so
+    inf * 0 scores NaN): NaN scores rank above +inf and equal one another
+    (lowest channel first), +inf above every finite score, -0 with +0; the
+    pruned mean carries NaN / inf as torch's does."""
+    from rotatek_amd.baselines import spark_prune
+    B, H, G, S, W = 2, 2, 2, 333, 16
+    _say(f"spark non-finite {dtype} prune={prune}")
+    K = _grid((B, H, S, D), dtype, 21).float()
+    g = torch.Generator().manual_seed(22)
+    for val in (float("nan"), float("inf"), float("-inf"), -0.0):
+        tok = torch.randint(0, S, (40,), generator=g)
+        ch = torch.randint(0, D, (40,), generator=g)
+        K[0, :, tok, ch] = val
+        K[1, 1, tok[:10], ch[:10]] = val
+    K[1, 0, 7, :40] = float("nan")          # a token with more NaN scores than some keeps
+    K[1, 0, 9, ::2] = float("inf")
+    K = K.to(dtype)
+    Q = _grid((B, H * G, W, D), dtype, 23).float()
+    Q[0, :G, :, 5] = 0.0                    # head 0 of batch 0: q_norm 0 on channel 5
+    Q = Q.to(dtype)
+    Kc, mask, pm = spark_prune(K, Q, G, prune)
+    torch.cuda.synchronize()
+    qg = ob.group_queries(_np(Q), G, DT[dtype])
+    Kc_o, mask_o, pm_o, _ = ob.per_token_channel_prune(qg, _np(K), prune, DT[dtype])
+    _assert_same(mask.cpu().numpy(), mask_o, "keep_mask")
+    _assert_same(_np(Kc), Kc_o, "K_compact")
+    _assert_same(_np(pm), pm_o, "pruned_mean")
+
+
 # --------------------------------------------------- torch's GPU semantics
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_think_and_spark_equal_torch_gpu_op_chain(dtype):
