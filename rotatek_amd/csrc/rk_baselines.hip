@@ -16,11 +16,11 @@
 // queries from kv_pruning_utils.py:76-79): one channel subset per token.
 //   spark_qnorm_kernel   q_g = dtype(mean over the G query heads of a KV
 //                        head), q_norm = dtype(||q_g||_2 over the window)
-//   spark_kernel         16 lanes per token: score = dtype(dtype(k^2) qn);
+//   spark_kernel         4 lanes per token: score = dtype(dtype(k^2) qn);
 //                        keep the Dk largest (bitwise search for the
-//                        threshold score, lowest channels among the ties);
-//                        writes K_compact, the per-token mask and
-//                        dtype(mean of the pruned values)
+//                        threshold score over packed 15-bit keys, lowest
+//                        channels among the ties); writes K_compact, the
+//                        per-token mask and dtype(mean of the pruned values)
 // Recovery (llama_visionzip.py:216-233):
 //   recover_kernel       64-row tiles of [prompt | visual | text]: the
 //                        visual rows get the kept channels from K_compact
