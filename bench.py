@@ -537,7 +537,7 @@ def main():
                     help="override the batch (kernel_profile.py's --batch_size)")
     ap.add_argument("--merge", default="auto", choices=["auto", "two", "one"],
                     help="decode merge: the library default (auto: two launches), two launches, or one launch")
-    ap.add_argument("--graph-steps", type=int, default=8,
+    ap.add_argument("--graph-steps", type=int, default=32,
                     help="decode steps captured per hipGraph replay (rounded up to the input copies); "
                          "a one-step graph is timed as well")
     ap.add_argument("--chunk-align", type=int, default=0, choices=[0, 32, 64, 128],
