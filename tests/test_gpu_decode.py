@@ -304,6 +304,62 @@ def test_benchmark_configs_full_size(cfg):
         assert (out_p.float() - out.float()).abs().max().item() <= TOL[c.dtype]
 
 
+LONG_CASES = [
+    # dtype, family, B, Hq, Hkv, S_v, S_f
+    (torch.bfloat16, "gqa", 1, 8, 2, 4_000_003, 100_001),
+    (torch.float16, "paper", 1, 4, 4, 1_000_003, 30_001),
+]
+
+
+@pytest.mark.parametrize("case", LONG_CASES, ids=["bf16-gqa-4M", "f16-mha-1M"])
+def test_long_context(case):
+    """Millions of tokens per head (a V head spans 0.5 G elements, the
+    kernels' offsets are 32-bit within a head).  Needle tokens at the first
+    and last rows of both spans carry large logits for one query head of
+    each group, so that head's output is a mix of those four V rows and an
+    offset error at the far end of a span shows at O(1); every output is
+    checked against the plain torch fp32 reference on the device (relative
+    to its magnitude, since the other heads average millions of rows)."""
+    dtype, family, B, Hq, Hkv, S_v, S_f = case
+    G, Dk = Hq // Hkv, 32
+    _say(f"long context {dtype} {family} B={B} Hq={Hq} Hkv={Hkv} S_v={S_v} S_f={S_f}")
+    g = torch.Generator(device="cuda").manual_seed(11)
+
+    def rn(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g, device="cuda") * scale).to(dtype)
+
+    q = rn(B, Hq, 128)
+    R = torch.linalg.qr(torch.randn(B, Hkv, 128, 128, generator=g, device="cuda"))[0][..., :Dk].contiguous()
+    ks = rn(B, Hkv, S_v, Dk, scale=0.5)
+    V = rn(B, Hkv, S_v + S_f, 128)
+    kf = rn(B, Hkv, S_f, 128, scale=0.5)
+    qh = q.float().view(B, Hkv, G, 128)[:, :, 0]                  # the first query head of each group
+    qt = torch.einsum("bhd,bhdk->bhk", qh, R)
+    # needle logits of 20 (e^20 outweighs millions of O(1)-logit tokens)
+    for t in (0, S_v - 1):
+        ks[:, :, t] = (qt * (20.0 / qt.norm(dim=-1, keepdim=True) ** 2 * 128 ** 0.5)).to(dtype)
+    for t in (0, S_f - 1):
+        kf[:, :, t] = (qh * (20.0 / qh.norm(dim=-1, keepdim=True) ** 2 * 128 ** 0.5)).to(dtype)
+    args = dict(q_full=q, R_partial=R.to(dtype), delta_mu=rn(B, Hkv, 128, scale=0.1), k_full=kf,
+                v_full=V[:, :, S_v:], mask_full=torch.ones(B, S_f, dtype=torch.uint8, device="cuda"),
+                k_sparse=ks, v_sparse=V[:, :, :S_v], num_kv_groups=G)
+    out = _decode(args, family)
+    assert torch.isfinite(out.float()).all()
+    tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        for b in range(B):
+            ref = _torch_fp32_reference(args, b)
+            got = out[b, 0].float()
+            scale = ref.abs().amax(dim=-1, keepdim=True)
+            err = ((got - ref).abs() / scale).max().item()
+            assert err <= 2e-2, (b, err)
+            # the needle heads: a mix of the four needle rows, O(1)
+            assert scale.view(Hkv, G)[:, 0].min().item() > 0.3, scale.view(Hkv, G)[:, 0]
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = tf32
+
+
 # ---------------------------------------------------------------- fp32
 # The reference kernels load any float input as fp32 and compute in fp32
 # (fused_decode.py:133,166,174; full_channel_flash_decoding.py:65,84,92);
