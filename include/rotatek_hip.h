@@ -55,7 +55,10 @@
 extern "C" {
 #endif
 
-#define RK_ABI_VERSION 1
+/* 2: rk_power_iteration takes eps and a per-matrix info flag; the decode
+ * plan carries the chunk-major layout fields; rk_rotatek_decode_noalloc,
+ * rk_key_covariance_weighted and the merge / workspace entry points. */
+#define RK_ABI_VERSION 2
 
 /* Element types. */
 typedef enum rk_dtype {

@@ -126,6 +126,7 @@ _SIGNATURES = {
 
 _lib = None
 _lock = threading.Lock()
+ABI_VERSION = 2  # RK_ABI_VERSION of include/rotatek_hip.h
 
 
 class HipLibraryMissing(RuntimeError):
@@ -144,6 +145,11 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
                     f"{path} is not built; run `python -m rotatek_amd.build` "
                     "(there is no CPU fallback for the RotateK kernels)")
             lib = ctypes.CDLL(path)
+            lib.rk_abi_version.restype = ctypes.c_int
+            if lib.rk_abi_version() != ABI_VERSION:
+                raise HipLibraryMissing(
+                    f"{path} has ABI version {lib.rk_abi_version()}, this package needs {ABI_VERSION}; "
+                    "rebuild with `python -m rotatek_amd.build`")
             for name, (res, args) in _SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.restype = res

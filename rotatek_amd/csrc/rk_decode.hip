@@ -527,8 +527,9 @@ decode_kernel(const DecodeArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
   const int nq = n < HMAX ? n : 0;  // LDS row for this lane's head column
-  // Workgroups go to the 8 XCDs round-robin by linear id u * np + x; rot_x
-  // rotates each unit's chunk numbers by the unit index (see run_decode).
+  // Workgroups go to the 8 XCDs round-robin by linear id: u * np + x, or
+  // x * units + u in a chunk-major grid (rk_plan_decode); rot_x rotates
+  // each unit's chunk numbers by the unit index (see run_decode).
   int u = a.cmajor ? (int)blockIdx.x : (int)blockIdx.y;
   int x = a.cmajor ? (int)blockIdx.y : (int)blockIdx.x + (a.rot_x ? u % a.np : 0);
   x = x >= a.np ? x - a.np : x;
