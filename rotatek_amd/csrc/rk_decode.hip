@@ -334,16 +334,16 @@ __device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8
 
 // Folds the records x = p0, p0 + step, ... < np of one (unit, head) into
 // (M, L, A) for channels 8 c8 .. 8 c8 + 7; `rec0` is the record of x = 0
-// and `rstride` the floats between consecutive x.  Eight records' loads are
+// and `rstride` the floats between consecutive x.  NB records' loads are
 // issued together; entries past np are clamped in-bounds loads with weight
 // zero (a batch's first entry is always valid, so its max is finite).
-template <bool COH>
+template <bool COH, int NB = 8>
 __device__ __forceinline__ void fold_records(const float* rec0, int64_t rstride, int np, int p0, int step,
                                              int c8, float& M, float& L, float (&A)[8]) {
-  for (int p = p0; p < np; p += 8 * step) {
-    float mm[8], ll[8], vv[8][8];
+  for (int p = p0; p < np; p += NB * step) {
+    float mm[NB], ll[NB], vv[NB][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const int q = p + step * i;
       const bool ok = q < np;
       load_rec<COH>(rec0 + (int64_t)(ok ? q : p) * rstride, c8, vv[i], mm[i], ll[i]);
@@ -354,13 +354,13 @@ __device__ __forceinline__ void fold_records(const float* rec0, int64_t rstride,
     }
     float mx = M;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, mm[i]);
+    for (int i = 0; i < NB; ++i) mx = fmaxf(mx, mm[i]);
     const float sc = fast_exp2(M - mx);
     L *= sc;
 #pragma unroll
     for (int e = 0; e < 8; ++e) A[e] *= sc;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < NB; ++i) {
       const float w = fast_exp2(mm[i] - mx);
       L += ll[i] * w;
 #pragma unroll
@@ -464,6 +464,17 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b
   if (act && j == 0) write_out<TT>(a, b, h0 + h, c8, L, A);
 }
 
+// Merge of one unit of one query head (hpu == 1) by the 16 lanes of one
+// slice: the records x = 0 .. np - 1 in order, eight loads in flight, no
+// cross-slice combine.  Both merges run this for such units (bit-identical
+// results); the merge kernel gives each slice of a workgroup its own unit.
+template <class TT, bool COH>
+__device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int b, int hq, int c8) {
+  float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  fold_records<COH>(a.part + u * a.np * kRecFloats, kRecFloats, a.np, 0, 1, c8, M, L, A);
+  write_out<TT>(a, b, hq, c8, L, A);
+}
+
 // Single-launch merge, run by every workgroup after it has stored its
 // record.  The workgroup waits until its record stores have completed
 // (they write through to memory), then takes a ticket on the unit's
@@ -487,7 +498,11 @@ __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, i
   __syncthreads();
   if (s_ticket != (uint32_t)(a.np - 1)) return;
   if (tid == 0) __hip_atomic_store(a.ticket + u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  merge_unit<TT, true>(a, u, b, h0, nh, tid, s_mrg);
+  if (a.hpu == 1) {
+    if (tid < 16) merge_slice<TT, true>(a, u, b, h0, tid);
+  } else {
+    merge_unit<TT, true>(a, u, b, h0, nh, tid, s_mrg);
+  }
   if constexpr (APPEND) {
     if (tid == 0) {
       const uint32_t t = __hip_atomic_fetch_add(a.bticket + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1142,21 +1157,27 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
   if (a.fused) merge_fused<F32, false>(a, u, b, h0, 1, tid, s_mrg);
 }
 
-// Second launch: one workgroup per unit runs merge_unit.  With a fused
-// append the unit holding query head 0 of row b advances len_full[b]; the
-// split launch that read it has completed.
+// Second launch: one workgroup per unit runs merge_unit, or with one query
+// head per unit (hpu == 1) one workgroup per 16 units, a slice each
+// (merge_slice).  With a fused append the unit holding query head 0 of row
+// b advances len_full[b]; the split launch that read it has completed.
 template <class TT>
 __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
   __shared__ float s_mrg[16 * kRecFloats];
   const int tid = threadIdx.x;
-  const int64_t u = blockIdx.x;
+  const bool sliced = a.hpu == 1;
+  const int64_t u = sliced ? (int64_t)blockIdx.x * 16 + (tid >> 4) : (int64_t)blockIdx.x;
+  if (u >= a.units) return;  // sliced: the last workgroup's spare slices
   const int b = (int)(u / a.units_per_b);
   const int r_in_b = (int)(u - (int64_t)b * a.units_per_b);
   const int kv = r_in_b / a.spk;
   const int jblk = r_in_b - kv * a.spk;
   const int h0 = kv * a.G + jblk * a.hpu;
-  merge_unit<TT, false>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg);
-  if (a.k_new && r_in_b == 0 && tid == 0) {
+  if (sliced)
+    merge_slice<TT, false>(a, u, b, h0, tid & 15);
+  else
+    merge_unit<TT, false>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg);
+  if (a.k_new && r_in_b == 0 && (tid & (sliced ? 15 : 255)) == 0) {
     const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
     if (pos < a.S_f) a.len_full[b] = pos + 1;
   }
@@ -1516,6 +1537,12 @@ int resolve_cus(int32_t num_cus, int* st) {
   return cus;
 }
 
+// Workgroups of the merge kernel: one per unit, or one per 16 units of one
+// query head each (merge_kernel's sliced form).
+unsigned merge_grid(const rk::DecodeArgs& a) {
+  return (unsigned)(a.hpu == 1 ? (a.units + 15) / 16 : a.units);
+}
+
 template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
 hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
   bool launched = false;
@@ -1541,7 +1568,7 @@ hipError_t launch_one(const rk::DecodeArgs& a, dim3 grid, hipStream_t s) {
                        s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fused) return e;
-  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3((unsigned)a.units), dim3(rk::kThreads), 0, s, a);
+  hipLaunchKernelGGL((rk::merge_kernel<TT>), dim3(merge_grid(a)), dim3(rk::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1598,7 +1625,7 @@ hipError_t launch32(bool has_vis, bool vec, const rk::DecodeArgs& a, dim3 grid, 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fused) return e;
-  hipLaunchKernelGGL((rk::merge_kernel<rk::F32>), dim3((unsigned)a.units), dim3(rk::kThreads), 0, s, a);
+  hipLaunchKernelGGL((rk::merge_kernel<rk::F32>), dim3(merge_grid(a)), dim3(rk::kThreads), 0, s, a);
   return hipGetLastError();
 }
 
