@@ -209,15 +209,19 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Decode workspace (split partials), cached per device and grown on
     demand, so steady-state calls allocate nothing.  A graph captured with
     one buffer stays valid after a later call grows the workspace: the old
-    buffer is retired, not freed.  Concurrent decodes on different streams
-    of one device share it and must not overlap."""
+    buffer is retired, not freed; growth is by at least half the current
+    size, so a run of growing shapes retires few buffers.  Concurrent
+    decodes on different streams of one device share it and must not
+    overlap."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     buf = _WORKSPACE.get(idx)
     if buf is None or buf.numel() < nbytes:
+        size = max(nbytes, 256)
         if buf is not None:
             _RETIRED.append(buf)
+            size = max(size, buf.numel() * 3 // 2)
         dev = torch.device("cuda", idx)
-        buf = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=dev)
+        buf = torch.empty(size, dtype=torch.uint8, device=dev)
         # the single-launch merge's counters start at zero (every call leaves them so)
         check(load().rk_decode_workspace_init(buf.data_ptr(), buf.numel(), stream_handle(dev)),
               "decode_workspace_init")
