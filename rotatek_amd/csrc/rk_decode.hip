@@ -976,26 +976,28 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// sum_c w[c] * row[c * sd], c < n; w in LDS.  VEC: unit stride, 16-byte
-// aligned row, n a multiple of 4.
-template <bool VEC>
+// sum_c w[c] * row[c * sd], c < n <= KMAX; w in LDS.  VEC: unit stride,
+// 16-byte aligned row, n a multiple of 4: all KMAX / 4 16-byte loads are
+// issued before any is used (those past n re-read the row's last four
+// floats, in bounds, and are not used), so the row costs one memory round
+// trip; float4 i accumulates into s0 (i even) or s1 (i odd).
+template <bool VEC, int KMAX>
 __device__ __forceinline__ float dot_row32(const float* row, uint32_t sd, const float* w, int n) {
   float s0 = 0.f, s1 = 0.f;
   if constexpr (VEC) {
-    for (int c = 0; c < n; c += 8) {
-      const float4 r0 = *(const float4*)(row + c);
-      const float4 w0 = *(const float4*)(w + c);
-      s0 = fmaf(w0.x, r0.x, s0);
-      s0 = fmaf(w0.y, r0.y, s0);
-      s0 = fmaf(w0.z, r0.z, s0);
-      s0 = fmaf(w0.w, r0.w, s0);
-      if (c + 4 < n) {
-        const float4 r1 = *(const float4*)(row + c + 4);
-        const float4 w1 = *(const float4*)(w + c + 4);
-        s1 = fmaf(w1.x, r1.x, s1);
-        s1 = fmaf(w1.y, r1.y, s1);
-        s1 = fmaf(w1.z, r1.z, s1);
-        s1 = fmaf(w1.w, r1.w, s1);
+    if (n <= 0) return 0.f;
+    float4 r[KMAX / 4];
+#pragma unroll
+    for (int i = 0; i < KMAX / 4; ++i) r[i] = *(const float4*)(row + min(4 * i, n - 4));
+#pragma unroll
+    for (int i = 0; i < KMAX / 4; ++i) {
+      if (4 * i < n) {
+        const float4 w4 = *(const float4*)(w + 4 * i);
+        float& acc = (i & 1) ? s1 : s0;
+        acc = fmaf(w4.x, r[i].x, acc);
+        acc = fmaf(w4.y, r[i].y, acc);
+        acc = fmaf(w4.z, r[i].z, acc);
+        acc = fmaf(w4.w, r[i].w, acc);
       }
     }
   } else {
@@ -1076,18 +1078,16 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
 
   if (is_vis) {
     {  // q R_partial: thread (half, c) sums rows 64 half .. 64 half + 63 of
-       // column c, 32 loads in flight at a time; the halves meet in LDS
+       // column c, all 64 loads in flight; the halves meet in LDS
       const int c = tid & 127, half = tid >> 7;
       const int cc = min(c, max(a.Dk - 1, 0));
       const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)cc * a.R_sk;
       float sum = 0.f;
       if (a.Dk > 0) {
-        for (int d0 = 64 * half; d0 < 64 * half + 64; d0 += 32) {
-          float rv[32];
-          load_any_n(a.R, rb + (int64_t)d0 * a.R_sd, a.R_sd, a.r_dtype, rv);
+        float rv[64];
+        load_any_n(a.R, rb + (int64_t)(64 * half) * a.R_sd, a.R_sd, a.r_dtype, rv);
 #pragma unroll
-          for (int i = 0; i < 32; ++i) sum = fmaf(s_q[d0 + i], rv[i], sum);
-        }
+        for (int i = 0; i < 64; ++i) sum = fmaf(s_q[64 * half + i], rv[i], sum);
       }
       s_acc[half][c] = sum;  // s_acc is free until the epilogue
       __syncthreads();
@@ -1109,7 +1109,10 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     const float* vsb = (const float*)a.vs + b * a.vs_sb + kv * a.vs_sh;
     for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
       const int64_t t = t0 + lane;
-      const float d = dot_row32<VEC>(ksb + (int64_t)min(t, t_end - 1) * a.ks_ss, a.ks_sd, s_qt, a.Dk);
+      const float* kr = ksb + (int64_t)min(t, t_end - 1) * a.ks_ss;
+      const float d = a.Dk <= 32   ? dot_row32<VEC, 32>(kr, a.ks_sd, s_qt, a.Dk)
+                      : a.Dk <= 64 ? dot_row32<VEC, 64>(kr, a.ks_sd, s_qt, a.Dk)
+                                   : dot_row32<VEC, 128>(kr, a.ks_sd, s_qt, a.Dk);
       const float s = t < t_end ? fmaf(d, a.scale_log2, bias2) : -INFINITY;
       step(s, vsb, a.vs_ss, a.vs_sd, t0, t_end - 1, UINT32_MAX, 0u);
     }
@@ -1121,7 +1124,7 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
       const int64_t t = t0 + lane;
       const int64_t tc = min(t, t_end - 1);
-      const float d = dot_row32<VEC>(kfb + tc * a.kf_ss, a.kf_sd, s_q, 128);
+      const float d = dot_row32<VEC, 128>(kfb + tc * a.kf_ss, a.kf_sd, s_q, 128);
       const bool ok = t < t_end && (!a.mask || a.mask[b * a.mf_sb + tc * a.mf_ss] != 0);
       step(ok ? d * a.scale_log2 : -INFINITY, vfb, a.vf_ss, a.vf_sd, t0, t_end - 1, a.vf_gap_at, a.vf_gap);
     }
