@@ -536,7 +536,8 @@ def main():
     ap.add_argument("--batch-size", type=int, default=0,
                     help="override the batch (kernel_profile.py's --batch_size)")
     ap.add_argument("--merge", default="auto", choices=["auto", "two", "one"],
-                    help="decode merge: the library default (auto: two launches), two launches, or one launch")
+                    help="decode merge: the library default (auto: one launch for a single round of "
+                         "one-query-head units, else two), two launches, or one launch")
     ap.add_argument("--graph-steps", type=int, default=32,
                     help="decode steps captured per hipGraph replay (rounded up to the input copies); "
                          "a one-step graph is timed as well")

@@ -132,7 +132,7 @@ int rk_device_cu_count(int device, int* status);
  * counters of the single-launch merge; pass a new workspace through
  * rk_decode_workspace_init once before its first use (every call leaves
  * the counters at zero again).  A step is two launches on `stream` (split
- * kernel, merge kernel; one with rk_set_decode_merge(2)) and is
+ * kernel, merge kernel), or one (see rk_set_decode_merge), and is
  * hipGraph-capturable.  Calls that overlap on one
  * workspace race.  policy RK_POLICY_PAPER with num_kv_groups > 1 runs the
  * grouped decomposition (each K/V tile read once per KV head; the result
@@ -247,11 +247,12 @@ int rk_full_channel_decode(const rk_tensor* q, const rk_tensor* k,
 #define RK_DECODE_TICKET_BYTES (256u * 1024u)
 int rk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
 
-/* Merge of the decode entry points: 0 (default) or 1 = two launches (split
- * kernel, then one merge workgroup per unit), 2 = one launch (the last
- * split workgroup of each unit merges, behind a counter in the workspace's
- * ticket region), whenever the counters fit.  Both give bit-identical
- * results; on MI355X one launch measured no faster, so it is opt-in. */
+/* Merge of the decode entry points: 1 = two launches (split kernel, then a
+ * merge kernel), 2 = one launch (the last split workgroup of each unit
+ * merges, behind a counter in the workspace's ticket region) whenever the
+ * counters fit, 0 (default) = one launch for a single round of workgroups
+ * with one query head per unit, else two (what measured faster on
+ * MI355X).  Both give bit-identical results. */
 void rk_set_decode_merge(int32_t mode);
 
 /* Split plan the decode entry points use for a shape (host only), exposed

@@ -259,6 +259,7 @@ DECODE_TICKET_BYTES = 256 * 1024  # RK_DECODE_TICKET_BYTES
 
 
 def set_decode_merge(mode: int) -> None:
-    """Decode merge: MERGE_AUTO (the default, two launches),
-    MERGE_TWO_LAUNCHES or MERGE_SINGLE_LAUNCH (bit-identical results)."""
+    """Decode merge: MERGE_AUTO (the default: one launch for a single round
+    of one-query-head units, else two), MERGE_TWO_LAUNCHES or
+    MERGE_SINGLE_LAUNCH (bit-identical results)."""
     load().rk_set_decode_merge(int(mode))

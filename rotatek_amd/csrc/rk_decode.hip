@@ -1223,7 +1223,8 @@ constexpr int64_t kSlotLatencyBytes = INT64_C(128) << 10;
 constexpr int64_t kMinWgsPerUnit = 8;
 constexpr int64_t kSkewMaxBytes = INT64_C(128) << 10;
 
-// Merge mode (rk_set_decode_merge): 0 (default) and 1 = two launches,
+// Merge mode (rk_set_decode_merge): 0 (default) = per shape (below),
+// 1 = two launches,
 // 2 = single launch where the ticket region holds the counters.
 int32_t g_merge_mode = 0;
 
@@ -1245,20 +1246,25 @@ WsLayout ws_layout(const rk_decode_plan& p) {
   return w;
 }
 
-// Single-launch merge only on request (mode 2) and where the counters fit.
-// Measured on MI355X with per-workgroup timestamps, one launch ends no
+// Single-launch merge where the counters fit: on request (mode 2), or by
+// default for one round of units of one query head each, where the unit's
+// last workgroup merges with one 16-lane slice (merge_slice).  Measured on
+// MI355X (eager / graph us per step, two launches -> one): B=1, 32 heads,
+// 16k context 35.9 / 35.3 -> 33.8 / 33.4; the same at 2.4k tokens in fp32
+// 32.4-33.2 / 26.9 -> 29.3-30.1 / 25.8.  Elsewhere one launch ends no
 // earlier than two: its tail (record stores written through and waited
-// for, ~2 us under load; the ticket, ~0.5 us; the last workgroup's merge,
+// for, ~2 us under load; the ticket, ~0.5 us; a multi-head unit's merge,
 // ~3.5 us) is as long as the kernel boundary plus the merge kernel, and the
 // split phase's slowest workgroup finishes 1-2 us later (B=8 with 4 KV heads
 // of 7 query heads, 12001 + 61 tokens: both end at 34 us; over 28 layers in
 // one graph, one launch 938 us against 891 us per step).  On grids of many
 // rounds it is worse still: every workgroup holds its slot through its own
-// wait (B=32, 16k context: 935 against 815 us).
+// wait (B=32, 16k context: 935 against 815 us; B=4, 32 heads, 4.6k tokens,
+// two rounds: 44.2 -> 44.8 us).
 bool use_single_launch(const rk_decode_plan& p, int64_t B, int cus) {
-  (void)cus;
   if (p.units + B > (int64_t)(RK_DECODE_TICKET_BYTES / sizeof(uint32_t))) return false;
-  return g_merge_mode == 2;
+  if (g_merge_mode != 0) return g_merge_mode == 2;
+  return p.heads_per_unit == 1 && p.grid <= (int64_t)cus * g_wgs_per_cu;
 }
 
 }  // namespace

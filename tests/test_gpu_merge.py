@@ -141,13 +141,15 @@ def test_dense_baseline_single_launch():
     assert _counters_zero(q.device)
 
 
+@pytest.mark.parametrize("G", [7, 1])
 @pytest.mark.parametrize("mode", ["eager", "graph"])
-def test_fused_append_length_advance(mode):
+def test_fused_append_length_advance(mode, G):
     """decode_step (fused append) under both merges over 6 steps: the same
-    outputs, lengths and appended rows, eager or replayed from a graph."""
-    _say(f"merge fused append {mode}")
+    outputs, lengths and appended rows, eager or replayed from a graph; G = 1
+    merges one query head per unit by a slice."""
+    _say(f"merge fused append {mode} G={G}")
     from rotatek_amd.cache import DynamicCache
-    B, Hkv, G, S_p, S_v, S_t, Dk = 3, 4, 7, 5, 2000, 9, 32
+    B, Hkv, S_p, S_v, S_t, Dk = 3, 4, 5, 2000, 9, 32
     dt = torch.bfloat16
     results = []
     for merge in (_lib.MERGE_TWO_LAUNCHES, _lib.MERGE_SINGLE_LAUNCH):
