@@ -2,12 +2,16 @@
 //
 // One launch computes a whole decode step (fused_decode.py:303-420,
 // gqa_decode.py:280-321, and the dense baseline of
-// full_channel_flash_decoding.py:162-229 when the visual span is empty):
+// full_channel_flash_decoding.py:162-229 when the visual span is empty),
+// over a grid of work units x workgroups per unit:
 //
-//   grid.y  = work units: (b, kv head, block of <= 16 query heads) under the
-//             GQA policy, (b, query head) under the paper policy;
-//   grid.x  = the unit's workgroups: wg_vis chunks of the rotated visual span
-//             followed by wg_full chunks of the full-width prompt+text span.
+//   work units = (b, kv head, block of <= 16 query heads) under the GQA
+//                policy, (b, query head) under the paper policy;
+//   workgroups = wg_vis chunks of the rotated visual span followed by
+//                wg_full chunks of the full-width prompt+text span;
+//
+// unit-major (grid (np, units)), or chunk-major (grid (units, np)) for one
+// round of short workgroups (rk_plan_decode).
 //
 // A workgroup is 4 independent waves that walk interleaved 32-token blocks
 // of its chunk.  Each wave keeps a ring of NBUF blocks of K/V in registers:
@@ -28,13 +32,15 @@
 //     by an in-register 8x8 transpose of eight 16-byte row loads.
 // Prompt/text validity (chunk range and mask_full) is staged once per
 // workgroup as bytes in LDS.  The four wave states are merged through LDS
-// into one partial (m, l, acc) per workgroup, and a second, small launch
-// merges each unit's partials into acc / (l + 1e-6) in the output dtype.
-// The kernel boundary is the only cross-workgroup synchronisation: a
-// last-workgroup ticket would need an agent-scope release/acquire per
-// workgroup, which on gfx950 writes back and invalidates the whole XCD L2
-// and measured 2.5x slower at B=32, 16k context.  No counters, no atomics,
-// nothing to re-arm, so the pair of launches is graph-capturable as is.
+// into one partial record (m, l, acc) per workgroup and head; the unit's
+// records are merged into acc / (l + 1e-6) in the output dtype either by a
+// second, small launch (merge_kernel) or, for one round of one-head units,
+// by the unit's last workgroup behind a counter (merge_fused).  There the
+// records are written through to memory and read with coherent loads and
+// the counters are device-scope atomics, with no agent-scope
+// release/acquire (which on gfx950 writes back and invalidates the whole
+// XCD L2, 2.5x slower at B=32, 16k context); every call leaves the
+// counters at zero, so either form is graph-capturable as is.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
