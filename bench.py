@@ -214,16 +214,30 @@ def _cfg0_leg(budget_s=3.0):
 DECODE_SOURCE = os.path.join(ROOT, "rotatek_amd", "csrc", "rk_decode.hip")
 
 
-def _source_sha():
+def _code_text(src: str) -> str:
+    """The source with // and /* */ comments removed and whitespace runs
+    collapsed: what the compiler sees, so that edits of comments alone keep
+    a measurement valid (the decode source has no string literal holding a
+    comment marker)."""
+    import re
+    src = re.sub(r"/\*.*?\*/", " ", src, flags=re.S)
+    src = re.sub(r"//[^\n]*", " ", src)
+    return " ".join(src.split())
+
+
+def _source_sha(text: str | None = None):
+    """sha256 prefix of the decode source's code (comments stripped)."""
     import hashlib
-    with open(DECODE_SOURCE, "rb") as f:
-        return hashlib.sha256(f.read()).hexdigest()[:16]
+    if text is None:
+        with open(DECODE_SOURCE) as f:
+            text = f.read()
+    return hashlib.sha256(_code_text(text).encode()).hexdigest()[:16]
 
 
 def _traffic(cfg_name):
     """HBM bytes per decode launch from the committed counter summary, or
-    None when that summary was taken on another decode source than this
-    tree's (it records the sha256 of rk_decode.hip it measured)."""
+    None when that summary was taken on other decode code than this tree's
+    (it records the sha256 of rk_decode.hip's code, comments stripped)."""
     path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
     if not os.path.exists(path):
         return None
