@@ -560,6 +560,9 @@ def main():
     ap.add_argument("--skew", type=int, default=-1, metavar="PERMILLE",
                     help="share of the first-dispatched visual chunks of a one-round grid, in thousandths "
                          "of the others' (-1: the library default, 0: equal chunks)")
+    ap.add_argument("--wgs-per-cu", type=int, default=0, metavar="N",
+                    help="decode workgroups planned per CU (0: the library default, two or one for a "
+                         "single round of small workgroups)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-dense", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -578,6 +581,9 @@ def main():
     if args.skew >= 0 and not args.pmc_summary:
         from rotatek_amd import _lib
         _lib.set_decode_skew(args.skew)
+    if args.wgs_per_cu > 0 and not args.pmc_summary:
+        from rotatek_amd import _lib
+        _lib.set_decode_tuning(0, 0, args.wgs_per_cu)
     if args.merge != "auto" and not args.pmc_summary:
         from rotatek_amd import _lib
         _lib.set_decode_merge({"two": _lib.MERGE_TWO_LAUNCHES, "one": _lib.MERGE_SINGLE_LAUNCH}[args.merge])

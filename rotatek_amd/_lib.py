@@ -237,6 +237,9 @@ def plan_decode(B, H_q, H_kv, Dk, S_v, S_f, elem_bytes=2, policy=RK_POLICY_GQA, 
 
 
 def set_decode_tuning(min_bytes=0, max_bytes=0, wgs_per_cu=0):
+    """Planner overrides for sweeps: workgroup byte bounds and workgroups per
+    CU (0 keeps a value; ``wgs_per_cu < 0`` restores the default, two per CU
+    or one for a single round of small chunk-major workgroups)."""
     load().rk_set_decode_tuning(int(min_bytes), int(max_bytes), int(wgs_per_cu))
 
 

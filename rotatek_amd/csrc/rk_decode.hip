@@ -1207,7 +1207,11 @@ namespace {
 // get at least ~2 workgroups per CU.
 int64_t g_min_wg_bytes = INT64_C(64) << 10;
 int64_t g_max_wg_bytes = INT64_C(512) << 10;
-int32_t g_wgs_per_cu = 2;
+// Workgroups planned per CU: 0 (default) plans two (the kernel's register
+// budget holds two per CU), or one for a single round of small workgroups
+// (rk_plan_decode); n > 0 plans n.
+int32_t g_wgs_per_cu = 0;
+int64_t resident_wgs() { return g_wgs_per_cu > 0 ? g_wgs_per_cu : 2; }
 // Visual chunks are whole multiples of this many tokens (a 32-token block
 // or the 128 tokens of one block per wave); 0: 32 in a chunk-major grid,
 // else 128.
@@ -1228,6 +1232,9 @@ constexpr int64_t kWgTokens = rk::kWaves * rk::kBlk;  // 128
 constexpr int64_t kSlotLatencyBytes = INT64_C(128) << 10;
 constexpr int64_t kMinWgsPerUnit = 8;
 constexpr int64_t kSkewMaxBytes = INT64_C(128) << 10;
+// Two-slot visual workgroups of at most this many bytes in a one-round
+// chunk-major grid are planned one per CU instead (rk_plan_decode).
+constexpr int64_t kOneSlotMaxBytes = INT64_C(128) << 10;
 
 // Merge mode (rk_set_decode_merge): 0 (default) = per shape (below),
 // 1 = two launches,
@@ -1270,7 +1277,7 @@ WsLayout ws_layout(const rk_decode_plan& p) {
 bool use_single_launch(const rk_decode_plan& p, int64_t B, int cus) {
   if (p.units + B > (int64_t)(RK_DECODE_TICKET_BYTES / sizeof(uint32_t))) return false;
   if (g_merge_mode != 0) return g_merge_mode == 2;
-  return p.heads_per_unit == 1 && p.grid <= (int64_t)cus * g_wgs_per_cu;
+  return p.heads_per_unit == 1 && p.grid <= (int64_t)cus * resident_wgs();
 }
 
 }  // namespace
@@ -1310,29 +1317,16 @@ extern "C" void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32
   if (min_bytes > 0) g_min_wg_bytes = min_bytes;
   if (max_bytes > 0) g_max_wg_bytes = max_bytes;
   if (wgs_per_cu > 0) g_wgs_per_cu = wgs_per_cu;
+  if (wgs_per_cu < 0) g_wgs_per_cu = 0;
   if (g_max_wg_bytes < g_min_wg_bytes) g_max_wg_bytes = g_min_wg_bytes;
 }
 
-extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, int64_t S_v,
-                              int64_t S_f, int32_t elem_bytes, int32_t policy, int32_t num_cus,
-                              rk_decode_plan* plan) {
-  if (!plan) return RK_ERR_NULL;
-  if (B < 0 || H_q <= 0 || H_kv <= 0 || S_v < 0 || S_f < 0 || elem_bytes <= 0 || num_cus <= 0)
-    return RK_ERR_ARG;
-  if (H_q % H_kv != 0) return RK_ERR_HEADS;
-  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
-  const int64_t G = H_q / H_kv;
-  rk_decode_plan p;
-  memset(&p, 0, sizeof(p));
-  if (policy == RK_POLICY_GQA) {
-    p.heads_per_unit = (int32_t)(G < 16 ? G : 16);
-    p.head_blocks = (int32_t)cdiv(G, 16);
-    p.units = B * H_kv * p.head_blocks;
-  } else {
-    p.heads_per_unit = 1;
-    p.head_blocks = 1;
-    p.units = B * H_q;
-  }
+namespace {
+
+// The chunking of a plan whose unit fields are set, for rounds of `slots`
+// resident workgroups on `num_cus` CUs.
+int split_plan(rk_decode_plan& p, int64_t Dk, int64_t S_v, int64_t S_f, int32_t elem_bytes, int64_t slots,
+               int32_t num_cus) {
   // Workgroups run in rounds of `slots` resident workgroups (two per CU at
   // the kernel's register budget).  A partial last round costs as much as a
   // full one, so the grid is sized to whole rounds: the fewest rounds that
@@ -1343,7 +1337,6 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   const int64_t unit_full = S_f * 256 * elem_bytes;
   const int64_t unit_bytes = unit_vis + unit_full;
   const int64_t total = p.units * unit_bytes;
-  const int64_t slots = (int64_t)num_cus * g_wgs_per_cu;
   // A unit with several query heads pays more per workgroup (q R for every
   // head, one merge row each), so it takes larger chunks: measured on MI355X,
   // a GQA group of 7 runs best in a single round of up to 4 MB workgroups,
@@ -1438,6 +1431,52 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
         p.chunk_vis = bs * rk::kBlk;
       }
     }
+  }
+  return RK_OK;
+}
+
+}  // namespace
+
+extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, int64_t S_v,
+                              int64_t S_f, int32_t elem_bytes, int32_t policy, int32_t num_cus,
+                              rk_decode_plan* plan) {
+  if (!plan) return RK_ERR_NULL;
+  if (B < 0 || H_q <= 0 || H_kv <= 0 || S_v < 0 || S_f < 0 || elem_bytes <= 0 || num_cus <= 0)
+    return RK_ERR_ARG;
+  if (H_q % H_kv != 0) return RK_ERR_HEADS;
+  if (policy != RK_POLICY_PAPER && policy != RK_POLICY_GQA) return RK_ERR_ARG;
+  const int64_t G = H_q / H_kv;
+  rk_decode_plan p;
+  memset(&p, 0, sizeof(p));
+  if (policy == RK_POLICY_GQA) {
+    p.heads_per_unit = (int32_t)(G < 16 ? G : 16);
+    p.head_blocks = (int32_t)cdiv(G, 16);
+    p.units = B * H_kv * p.head_blocks;
+  } else {
+    p.heads_per_unit = 1;
+    p.head_blocks = 1;
+    p.units = B * H_q;
+  }
+  const rk_decode_plan units_only = p;
+  int st = split_plan(p, Dk, S_v, S_f, elem_bytes, (int64_t)num_cus * resident_wgs(), num_cus);
+  if (st) return st;
+  // A single round of small workgroups (two-slot visual chunks of <= 128 KB)
+  // runs faster as one workgroup per CU of twice the tokens, where that is
+  // still one chunk-major round: the fixed costs of a workgroup (prologue,
+  // the merge of its waves, its record) are paid once per CU, the unit's
+  // merge folds half the records, and no CU holds a later-dispatched,
+  // slower-streaming second workgroup.  Graph-replayed layers on MI355X (us,
+  // two slots -> one): B=8, 4 KV heads of 7 query heads, keep 32, 2049 /
+  // 4097 / 6001 visual tokens 17.2 -> 16.3, 19.7 -> 18.8, 22.1 -> 21.3;
+  // B=1, 32 heads, 4000 + 640 tokens 20.1 -> 18.2.  At 143-160 KB the two
+  // slots are 1-2 % faster (8001 tokens: 23.8 against 24.1), and where one
+  // slot per CU needs a second round they are faster still (B=16, 2049
+  // tokens: 21.2 against 22.5).
+  if (g_wgs_per_cu == 0 && p.chunk_major && S_v * (Dk + 128) * elem_bytes <= p.wg_vis * kOneSlotMaxBytes) {
+    rk_decode_plan one = units_only;
+    if (split_plan(one, Dk, S_v, S_f, elem_bytes, num_cus, num_cus) == RK_OK && one.chunk_major &&
+        one.grid <= num_cus)
+      p = one;
   }
   p.workspace_bytes = ws_layout(p).total;
   p.single_launch = use_single_launch(p, B, num_cus) ? 1 : 0;

@@ -441,14 +441,18 @@ def test_plan_keeps_one_round_when_the_extra_slot_saves_little():
 def test_plan_chunk_major_short_rounds():
     """One round of short workgroups launches chunk-major with 32-token
     chunks (config 4 layers, config 1); rounds of long workgroups (config 3)
-    and multi-round grids (config 2, kp) keep the unit-major launch; the
-    first-dispatched chunks are enlarged only where workgroups stream
-    <= 128 KB (config 4 at 4097 visual tokens)."""
+    and multi-round grids (config 2, kp) keep the unit-major launch; at two
+    workgroups per CU the first-dispatched chunks are enlarged only where
+    workgroups stream <= 128 KB (config 4 at 4097 visual tokens)."""
     cfg4l = _lib.plan_decode(8, 28, 4, 32, 12001, 61, policy=1)
     assert cfg4l["chunk_major"] == 1 and cfg4l["n_fast"] == 0 and cfg4l["grid"] == 512
-    cfg4s = _lib.plan_decode(8, 28, 4, 32, 4097, 61, policy=1)
-    assert cfg4s["chunk_major"] == 1 and cfg4s["n_fast"] == 256 // cfg4s["units"]
-    assert cfg4s["chunk_fast"] > cfg4s["chunk_vis"]
+    try:
+        _lib.set_decode_tuning(0, 0, 2)
+        cfg4s = _lib.plan_decode(8, 28, 4, 32, 4097, 61, policy=1)
+        assert cfg4s["chunk_major"] == 1 and cfg4s["n_fast"] == 256 // cfg4s["units"]
+        assert cfg4s["chunk_fast"] > cfg4s["chunk_vis"]
+    finally:
+        _lib.set_decode_tuning(0, 0, -1)
     assert _lib.plan_decode(1, 32, 32, 32, 15360, 640, policy=0)["chunk_major"] == 1
     for shape, pol in (((16, 28, 4, 32, 30720, 2048), 1), ((32, 32, 32, 32, 14000, 2000), 0),
                        ((32, 32, 8, 32, 16000, 80), 1)):
@@ -465,3 +469,30 @@ def test_plan_chunk_major_short_rounds():
         assert p["chunk_major"] == 0 and p["chunk_vis"] % 128 == 0
     finally:
         _lib.set_decode_skew(1300)
+
+
+def test_plan_one_workgroup_per_cu_for_small_short_rounds():
+    """Where a one-round chunk-major grid at two workgroups per CU would give
+    each visual workgroup <= 128 KB, the planner takes one workgroup per CU
+    of twice the tokens if that is still one chunk-major round (config 4 at
+    4097 visual tokens, every keep; one query head per unit at 4000 tokens),
+    and keeps two per CU otherwise: larger chunks (config 4 at 12001, config
+    1) or a one-slot plan of two rounds (B=16 at 2049 tokens, which keeps the
+    enlarged first-dispatched chunks).  A fixed count restores the two-slot
+    plan."""
+    for keep in (16, 32, 64):
+        p = _lib.plan_decode(8, 28, 4, keep, 4097, 61, policy=1)
+        assert p["chunk_major"] == 1 and p["n_fast"] == 0 and p["grid"] == 256, (keep, p)
+    p = _lib.plan_decode(1, 32, 32, 32, 4000, 640, policy=0)
+    assert p["chunk_major"] == 1 and p["grid"] == 256 and p["single_launch"] == 1
+    for shape, pol in (((8, 28, 4, 32, 12001, 61), 1), ((1, 32, 32, 32, 15360, 640), 0)):
+        assert _lib.plan_decode(*shape, policy=pol)["grid"] == 512
+    p = _lib.plan_decode(16, 28, 4, 32, 2049, 61, policy=1)
+    assert p["grid"] > 256 and p["chunk_major"] == 1 and p["n_fast"] == 256 // p["units"]
+    try:
+        _lib.set_decode_tuning(0, 0, 2)
+        assert _lib.plan_decode(8, 28, 4, 32, 4097, 61, policy=1)["grid"] == 512
+    finally:
+        _lib.set_decode_tuning(0, 0, -1)
+    assert _lib.plan_decode(8, 28, 4, 32, 4097, 61, policy=1)["grid"] == 256
+

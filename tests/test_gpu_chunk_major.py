@@ -1,14 +1,16 @@
 """GPU checks of the decode planner's launch layouts for one round of short
 workgroups: chunk-major workgroup ids (all chunks of a unit on one XCD),
-32-token visual chunks, and the enlarged first-dispatched chunks where
-workgroups stream <= 128 KB.
+32-token visual chunks, the enlarged first-dispatched chunks where
+workgroups stream <= 128 KB at two workgroups per CU, and one workgroup per
+CU where that is still one round.
 
-Each shape runs under the three planner settings (unit-major, chunk-major
-with equal chunks, the default) and every output is checked against the
-float64 oracle (on sampled (b, kv) groups at full size) at the north-star
-bars; the layouts differ only in where chunk boundaries fall, so the three
-outputs also agree with each other within those bars.  The plan fields
-are asserted, so each case provably runs the layout it names.
+Each shape runs under four planner settings (unit-major; chunk-major with
+equal chunks and with enlarged first chunks, both at two workgroups per CU;
+the default) and every output is checked against the float64 oracle (on
+sampled (b, kv) groups at full size) at the north-star bars; the layouts
+differ only in where chunk boundaries fall, so the outputs also agree with
+each other within those bars.  The plan fields are asserted, so each case
+provably runs the layout it names.
 """
 import sys
 
@@ -22,7 +24,14 @@ from rotatek_amd import _lib
 pytestmark = pytest.mark.gpu
 
 TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}
-MODES = {"unit_major": 0, "chunk_major": 1000, "default": 1300}
+# (skew permille, workgroups per CU; -1 = the default choice)
+MODES = {"unit_major": (0, -1), "chunk_major": (1000, 2), "skewed": (1300, 2), "default": (1300, -1)}
+
+
+def _set_mode(name):
+    skew, wgs = MODES[name]
+    _lib.set_decode_skew(skew)
+    _lib.set_decode_tuning(0, 0, wgs)
 
 
 def _say(msg):
@@ -37,7 +46,7 @@ def _np(t):
 @pytest.fixture(autouse=True)
 def _restore_planner():
     yield
-    _lib.set_decode_skew(MODES["default"])
+    _set_mode("default")
 
 
 def _inputs(B, Hq, Hkv, Dk, S_v, S_f, dtype, seed):
@@ -68,13 +77,14 @@ def _oracle_groups(inp, groups):
 
 
 CASES = [
-    # B, Hq, Hkv, Dk, S_v, S_f, dtype, family, expected (chunk_major, skewed) under the default
-    (8, 28, 4, 32, 4097, 61, torch.bfloat16, "gqa", (1, True)),     # config 4 layer, 4097 tokens
-    (8, 28, 4, 64, 12001, 61, torch.bfloat16, "gqa", (1, False)),   # config 4 layer, 12001 tokens
-    (1, 32, 32, 32, 15360, 640, torch.float16, "paper", (1, False)),  # config 1
-    (3, 12, 4, 32, 2049, 17, torch.float16, "gqa", (1, False)),     # 12 units, 132 workgroups
-    (2, 8, 8, 16, 3001, 129, torch.bfloat16, "paper", (1, False)),  # 208 workgroups: one per CU
-    (2, 16, 16, 32, 2500, 60, torch.float16, "paper", (1, True)),   # 416 workgroups of <= 128 KB
+    # B, Hq, Hkv, Dk, S_v, S_f, dtype, family, expected (chunk_major, skewed at two per CU,
+    # one workgroup per CU by default)
+    (8, 28, 4, 32, 4097, 61, torch.bfloat16, "gqa", (1, True, True)),     # config 4 layer, 4097 tokens
+    (8, 28, 4, 64, 12001, 61, torch.bfloat16, "gqa", (1, False, False)),  # config 4 layer, 12001 tokens
+    (1, 32, 32, 32, 15360, 640, torch.float16, "paper", (1, False, False)),  # config 1
+    (3, 12, 4, 32, 2049, 17, torch.float16, "gqa", (1, False, False)),    # 12 units, 132 workgroups
+    (2, 8, 8, 16, 3001, 129, torch.bfloat16, "paper", (1, False, False)),  # 208 workgroups: one per CU
+    (2, 16, 16, 32, 2500, 60, torch.float16, "paper", (1, True, True)),   # 416 workgroups of <= 128 KB
 ]
 
 
@@ -82,16 +92,17 @@ CASES = [
 def test_layouts_match_oracle(case):
     from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
     from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
-    B, Hq, Hkv, Dk, S_v, S_f, dtype, family, (cm, skewed) = case
+    B, Hq, Hkv, Dk, S_v, S_f, dtype, family, (cm, skewed, one_slot) = case
     fn = rotatek_decode_gqa if family == "gqa" else rotatek_decode_fused
     pol = _lib.RK_POLICY_GQA if Hq != Hkv else _lib.RK_POLICY_PAPER
     inp = _inputs(B, Hq, Hkv, Dk, S_v, S_f, dtype, seed=S_v + Dk)
     groups = sorted({(0, 0), (B - 1, Hkv - 1), (B // 2, Hkv // 2)})
     want = _oracle_groups(inp, groups)
     outs = {}
-    for name, k in MODES.items():
-        _lib.set_decode_skew(k)
-        p = _lib.plan_decode(B, Hq, Hkv, Dk, S_v, S_f, 2, pol)
+    plans = {}
+    for name in MODES:
+        _set_mode(name)
+        p = plans[name] = _lib.plan_decode(B, Hq, Hkv, Dk, S_v, S_f, 2, pol)
         _say(f"{name}: B={B} Hq={Hq} Hkv={Hkv} Dk={Dk} S_v={S_v} S_f={S_f} {dtype} {family} plan "
              f"grid={p['grid']} chunk_major={p['chunk_major']} n_fast={p['n_fast']} "
              f"chunk_fast={p['chunk_fast']} chunk_vis={p['chunk_vis']}")
@@ -99,8 +110,12 @@ def test_layouts_match_oracle(case):
             assert p["chunk_major"] == 0
         elif name == "chunk_major":
             assert p["chunk_major"] == cm and p["n_fast"] == 0
-        else:
+        elif name == "skewed":
             assert p["chunk_major"] == cm and (p["n_fast"] > 0) == skewed
+        elif one_slot:
+            assert p["chunk_major"] == 1 and p["n_fast"] == 0 and p["grid"] <= 256 < plans["skewed"]["grid"]
+        else:
+            assert p == plans["skewed"]
         outs[name] = fn(**inp)[0][:, 0]  # [B, H_q, D]
         torch.cuda.synchronize()
         got = _np(outs[name])
@@ -109,21 +124,28 @@ def test_layouts_match_oracle(case):
         for (b, kv), w in want.items():
             err = np.abs(got[b, kv * G:(kv + 1) * G] - w).max()
             assert err <= TOL[dtype], (name, b, kv, err)
-    for name in ("chunk_major", "default"):
+    for name in ("chunk_major", "skewed", "default"):
         assert (outs[name].float() - outs["unit_major"].float()).abs().max().item() <= TOL[dtype]
 
 
+@pytest.mark.parametrize("layout", ["skewed", "default"])
 @pytest.mark.parametrize("mode", ["eager", "graph"])
-def test_fused_append_chunk_major(mode):
-    """The span cache's decode step (fused append) on a skewed chunk-major
-    grid: every step against the oracle on the grown spans, eager and
+def test_fused_append_chunk_major(mode, layout):
+    """The span cache's decode step (fused append) on a chunk-major grid,
+    skewed at two workgroups per CU and one workgroup per CU (the default
+    here): every step against the oracle on the grown spans, eager and
     replayed from one graph."""
     from rotatek_amd.cache import DynamicCache
     B, Hkv, G, S_p, S_v, S_t, Dk, steps = 8, 4, 7, 30, 4097, 30, 32, 4
     dt = torch.bfloat16
+    _set_mode(layout)
     p = _lib.plan_decode(B, Hkv * G, Hkv, Dk, S_v, S_p + S_t + steps, 2, _lib.RK_POLICY_GQA)
-    _say(f"fused append chunk-major {mode}: plan chunk_major={p['chunk_major']} n_fast={p['n_fast']}")
-    assert p["chunk_major"] == 1 and p["n_fast"] > 0
+    _say(f"fused append chunk-major {mode} {layout}: plan grid={p['grid']} chunk_major={p['chunk_major']} "
+         f"n_fast={p['n_fast']}")
+    if layout == "skewed":
+        assert p["chunk_major"] == 1 and p["n_fast"] > 0
+    else:
+        assert p["chunk_major"] == 1 and p["n_fast"] == 0 and p["grid"] == 256
     g = torch.Generator(device="cuda").manual_seed(5)
 
     def rn(*s):

@@ -192,7 +192,7 @@ def test_split_granularity_does_not_change_results_beyond_rounding():
             out = _decode(inp, "paper")
             assert np.abs(_np(out) - want).max() <= 2e-3
     finally:
-        _lib.set_decode_tuning(64 << 10, 512 << 10, 2)
+        _lib.set_decode_tuning(64 << 10, 512 << 10, -1)
 
 
 def test_graph_capture_replays_match_eager():

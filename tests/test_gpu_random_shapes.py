@@ -9,7 +9,9 @@ including odd and empty spans, G up to 20 and D_keep from 8 to 128, and
 checks every output against the float64 oracle at the north-star bars
 (max-abs 2e-3 fp16, 1e-2 bf16), under each planner layout of one-round
 grids (unit-major, chunk-major, chunk-major with enlarged first-dispatched
-chunks).  Every case prints its parameters first.
+chunks at two workgroups per CU, the default, which takes one workgroup per
+CU for a round of small workgroups).  Every case prints its parameters
+first.
 """
 import sys
 
@@ -50,14 +52,19 @@ CASES = _cases()
 @pytest.fixture
 def planner(request):
     from rotatek_amd import _lib
-    _lib.set_decode_skew(request.param)
+    skew, wgs = request.param
+    _lib.set_decode_skew(skew)
+    _lib.set_decode_tuning(0, 0, wgs)
     yield request.param
     _lib.set_decode_skew(1300)
+    _lib.set_decode_tuning(0, 0, -1)
 
 
-# planner layouts of one-round grids: unit-major, chunk-major, the default
-# (chunk-major, first-dispatched chunks enlarged for short workgroups)
-@pytest.mark.parametrize("planner", [0, 1000, 1300], indirect=True, ids=["um", "cm", "default"])
+# planner layouts of one-round grids, (skew permille, workgroups per CU):
+# unit-major, chunk-major, chunk-major with the first-dispatched chunks
+# enlarged for short workgroups (two per CU), the default (-1)
+@pytest.mark.parametrize("planner", [(0, -1), (1000, 2), (1300, 2), (1300, -1)], indirect=True,
+                         ids=["um", "cm", "skew", "default"])
 @pytest.mark.parametrize("case", CASES, ids=[f"c{c[0]}" for c in CASES])
 def test_random_shape_matches_oracle(case, planner):
     from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
