@@ -50,6 +50,21 @@ struct F16 {
     hi = __builtin_bit_cast(uint16_t, h);
     lo = __builtin_bit_cast(uint16_t, (_Float16)(x - (float)h));
   }
+  // split() of eight values packed as two MFMA operands (element r in half
+  // r of the words): one value per conversion, which measured faster in the
+  // decode kernel than the packed two-value conversion
+  static __device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
+    uint32_t h[8], l[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      uint16_t a, b;
+      split(x[r], a, b);
+      h[r] = a;
+      l[r] = b;
+    }
+    hi = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+    lo = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+  }
 };
 
 struct BF16 {
@@ -69,6 +84,9 @@ struct BF16 {
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){lo, hi}, b2));
   }
+  // the two halves of a packed dword as fp32
+  static __device__ __forceinline__ float lo_f32(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+  static __device__ __forceinline__ float hi_f32(uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
   static __device__ __forceinline__ f32x4 mfma(uint4 a, uint4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -76,6 +94,18 @@ struct BF16 {
   static __device__ __forceinline__ void split(float x, uint16_t& hi, uint16_t& lo) {
     hi = from_f32(x);
     lo = from_f32(x - to_f32(hi));
+  }
+  // split() of eight values packed as two MFMA operands: two values per
+  // packed conversion (v_cvt_pk_bf16_f32), the same roundings
+  static __device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      h[w] = pack2(x[2 * w], x[2 * w + 1]);
+      l[w] = pack2(x[2 * w] - lo_f32(h[w]), x[2 * w + 1] - hi_f32(h[w]));
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
   }
 };
 

@@ -152,6 +152,25 @@ __device__ __forceinline__ uint4 load_row8(const uint16_t* base, uint32_t row_of
   }
 }
 
+// load_row8 with the row given as a byte offset `row_b` (a multiple of 2):
+// VEC, one 16-byte load at row_b + 2 chan; otherwise element loads of
+// channels chan.. at stride sd from element row_b / 2.
+template <bool VEC, bool NT = true>
+__device__ __forceinline__ uint4 load_row8b(const uint16_t* base, uint32_t row_b, uint32_t chan, uint32_t sd,
+                                            int nvalid) {
+  if constexpr (VEC) {
+    const uint32_t boff = row_b + 2u * chan;
+    if constexpr (NT) {
+      const u32x4 v = __builtin_nontemporal_load((const u32x4*)((const char*)base + boff));
+      return make_uint4(v.x, v.y, v.z, v.w);
+    } else {
+      return *(const uint4*)((const char*)base + boff);
+    }
+  } else {
+    return load_row8<false, NT>(base, row_b >> 1, chan, sd, nvalid);
+  }
+}
+
 __device__ __forceinline__ uint4 zero_if(bool keep, uint4 v) {
   return keep ? v : make_uint4(0, 0, 0, 0);
 }
@@ -187,10 +206,8 @@ __device__ __forceinline__ void softmax_pv(const float (&s)[8], const uint4 (&vr
   }
   l = l * alpha + ps;
   // P^T operand: tokens 8g..8g+7 of head n, hi + lo parts
-  uint16_t hi[8], lo[8];
-#pragma unroll
-  for (int r = 0; r < 8; ++r) TT::split(p[r], hi[r], lo[r]);
-  const uint4 ph = pack8(hi), pl = pack8(lo);
+  uint4 ph, pl;
+  TT::split8(p, ph, pl);
   // V^T operand for channel slot j: element r = V[8g + r][8n + j]
   uint4 av[8];
 #pragma unroll
@@ -235,7 +252,7 @@ struct Ring {
 
   __device__ __forceinline__ Ring(int64_t nblk, int wave_, uint32_t seed) : wave(wave_) {
     nw = wave_ < nblk ? (nblk - 1 - wave_) / kWaves + 1 : 0;
-    rot = nw > 0 ? (int64_t)(seed % (uint32_t)nw) : 0;
+    rot = (int64_t)__umulhi(seed, (uint32_t)nw);  // floor(seed * nw / 2^32) < nw
   }
   __device__ __forceinline__ int64_t blk_of(int64_t j) const {
     int64_t r = j + rot;
@@ -546,7 +563,10 @@ decode_kernel(const DecodeArgs a) {
   __shared__ uint4 s_rsep[HMAX >= 16 ? 1 : kRawChunks];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+  // wave index in a scalar register: the ring's block bookkeeping (block
+  // numbers, token offsets, bounds) then runs on the scalar unit, not as
+  // per-lane 64-bit arithmetic
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = lane >> 4, n = lane & 15;
   const int nq = n < HMAX ? n : 0;  // LDS row for this lane's head column
   // Workgroups go to the 8 XCDs round-robin by linear id: u * np + x, or
   // x * units + u in a chunk-major grid (rk_plan_decode); rot_x rotates
@@ -688,17 +708,31 @@ decode_kernel(const DecodeArgs a) {
     }
     const uint32_t vch = 8u * n;
     const int64_t nblk = (t_end - t_begin + kBlk - 1) / kBlk;
+    // Row addresses are byte offsets from the head base: a per-lane part (the
+    // lane's row inside the block, and with 16-byte loads its channel slot)
+    // plus the block's first token times the token stride (a scalar), clamped
+    // to the chunk's last row, so a row costs two vector adds/mins and no
+    // multiply.  Every sum stays below 2^32: the host bounds a head's span
+    // plus 32 rows below 2^31 elements (set_head).
+    constexpr bool kFoldK = VEC && DKB == 1;
+    const uint32_t kss2 = 2u * a.ks_ss, vss2 = 2u * a.vs_ss;
+    const uint32_t kfold = kFoldK ? 2u * kch[0] : 0u, vfold = VEC ? 2u * vch : 0u;
+    const uint32_t kro0 = krow0 * kss2 + kfold, kro1 = krow1 * kss2 + kfold, klast = t_last * kss2 + kfold;
+    const uint32_t vro = 8u * g * vss2 + vfold, vlast = t_last * vss2 + vfold;
     auto load = [&](VisBuf<DKB>& B, int64_t blk) {
-      const uint32_t t0 = (uint32_t)(t_begin + blk * kBlk);
-      const uint32_t r0 = min(t0 + krow0, t_last) * a.ks_ss, r1 = min(t0 + krow1, t_last) * a.ks_ss;
+      // blocks past the chunk start at (and clamp to) its last row
+      const uint32_t t0 = min((uint32_t)(t_begin + blk * kBlk), t_last);
+      const uint32_t kb0 = t0 * kss2, vb0 = t0 * vss2;
+      const uint32_t r0 = min(kro0 + kb0, klast), r1 = min(kro1 + kb0, klast);
 #pragma unroll
       for (int kb = 0; kb < DKB; ++kb) {
-        B.k[0][kb] = load_row8<VEC, NTL && DKB == 1>(ksb, r0, kch[kb], a.ks_sd, knv[kb]);
-        B.k[1][kb] = load_row8<VEC, NTL && DKB == 1>(ksb, r1, kch[kb], a.ks_sd, knv[kb]);
+        const uint32_t ch = kFoldK ? 0u : kch[kb];
+        B.k[0][kb] = load_row8b<VEC, NTL && DKB == 1>(ksb, r0, ch, a.ks_sd, knv[kb]);
+        B.k[1][kb] = load_row8b<VEC, NTL && DKB == 1>(ksb, r1, ch, a.ks_sd, knv[kb]);
       }
 #pragma unroll
       for (int r = 0; r < 8; ++r)
-        B.v[r] = load_row8<VEC, NTL>(vsb, min(t0 + 8u * g + r, t_last) * a.vs_ss, vch, a.vs_sd, 8);
+        B.v[r] = load_row8b<VEC, NTL>(vsb, min(vro + vb0 + (uint32_t)r * vss2, vlast), VEC ? 0u : vch, a.vs_sd, 8);
     };
 
     // q R: thread (c, part) loads R[part*L .. part*L+L-1][c], forms partial
@@ -801,7 +835,8 @@ decode_kernel(const DecodeArgs a) {
     }
     const float bias2 = (n < HMAX ? s_bias[nq] : 0.f) * a.scale_log2;
     auto compute = [&](VisBuf<DKB>& B, int64_t blk) {
-      const int64_t t0 = t_begin + blk * kBlk;
+      // rows 8g + 4sb + i of the block at or past `lim` lie beyond the chunk
+      const int lim = (int)min(t_end - (t_begin + blk * kBlk), (int64_t)kBlk);
       float s[8];
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb) {
@@ -811,10 +846,8 @@ decode_kernel(const DecodeArgs a) {
 #pragma unroll
         for (int kb = 0; kb < DKB; ++kb) cc = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), ql[kb], cc);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t t = t0 + 8 * g + 4 * sb + i;
-          s[4 * sb + i] = (t < t_end) ? fmaf(cc[i], a.scale_log2, bias2) : -INFINITY;
-        }
+        for (int i = 0; i < 4; ++i)
+          s[4 * sb + i] = (8 * g + 4 * sb + i < lim) ? fmaf(cc[i], a.scale_log2, bias2) : -INFINITY;
       }
       softmax_pv<TT>(s, B.v, m, l, acc);
     };
@@ -1691,13 +1724,16 @@ void set4(const rk_tensor* t, int64_t& s0, int64_t& s1, int64_t& s2, int64_t& s3
 }
 
 // Head strides (b, h) as int64; token/channel strides as uint32 with the
-// whole within-head span below 2^31 elements (kernel offsets are 32-bit).
+// whole within-head span, plus 32 rows, below 2^31 elements (kernel offsets
+// are 32-bit byte offsets) and the token stride below 2^26.
 bool set_head(const rk_tensor* t, int64_t& sb, int64_t& sh, uint32_t& ss, uint32_t& sd) {
   sb = t->stride[0];
   sh = t->stride[1];
-  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1) * t->stride[2] : 0) +
+  // (32 rows of slack: the visual ring adds a block's row offsets to its
+  // first row before clamping to the chunk's last row)
+  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1 + 32) * t->stride[2] : 0) +
                        (t->shape[3] > 0 ? (t->shape[3] - 1) * t->stride[3] : 0) + 8;
-  if (span >= (INT64_C(1) << 31) || t->stride[2] >= (INT64_C(1) << 31) ||
+  if (span >= (INT64_C(1) << 31) || t->stride[2] >= (INT64_C(1) << 26) ||
       t->stride[3] >= (INT64_C(1) << 31))
     return false;
   ss = (uint32_t)t->stride[2];
