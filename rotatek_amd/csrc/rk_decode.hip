@@ -776,9 +776,23 @@ decode_kernel(const DecodeArgs a) {
     __syncthreads();
     float rv[kL];
     if (a.r_vec) {
-      const uint16_t* rl = (const uint16_t*)s_r;
+      // the thread's kL reads of column c issued back to back, then one
+      // branch on R's (launch-uniform) 16-bit dtype; lanes past Dk read the
+      // last column and are zeroed after (a per-element dtype and column
+      // test put each read in its own branch, each waiting for its data)
+      const uint16_t* rl = (const uint16_t*)s_r + min(c, max(a.Dk - 1, 0)) + part * kL * a.Dk;
+      uint16_t raw[kL];
 #pragma unroll
-      for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? raw_to_f32(rl[(part * kL + i) * a.Dk + c], a.r_dtype) : 0.f;
+      for (int i = 0; i < kL; ++i) raw[i] = rl[i * a.Dk];
+      if (a.r_dtype == RK_F16) {
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rv[i] = F16::to_f32(raw[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rv[i] = BF16::to_f32(raw[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
     } else {  // element-wise fallback (column c, clamped in-bounds; no load
               // at all when Dk == 0, where R_partial has no storage)
 #pragma unroll
@@ -791,13 +805,21 @@ decode_kernel(const DecodeArgs a) {
       }
     }
     float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
+    // two heads per (uniform) branch, so their q reads share one LDS round
+    // trip; rows of absent heads hold zeros and are never read back
+    constexpr int kHS = HMAX >= 2 ? 2 : 1;
 #pragma unroll
-    for (int h = 0; h < HMAX; ++h) {
-      if (h < nh) {  // uniform; rows of absent heads are never read
-        float acc_h = 0.f;
+    for (int h = 0; h < HMAX; h += kHS) {
+      if (h < nh) {
+        float acc_h[kHS];
 #pragma unroll
-        for (int i = 0; i < kL; ++i) acc_h += s_q[h][part * kL + i] * rv[i];
-        s_part[(part * HMAX + h) * DKP + c] = acc_h;
+        for (int j = 0; j < kHS; ++j) {
+          acc_h[j] = 0.f;
+#pragma unroll
+          for (int i = 0; i < kL; ++i) acc_h[j] += s_q[h + j][part * kL + i] * rv[i];
+        }
+#pragma unroll
+        for (int j = 0; j < kHS; ++j) s_part[(part * HMAX + h + j) * DKP + c] = acc_h[j];
       }
     }
     __syncthreads();
