@@ -28,6 +28,7 @@ struct F16 {
   using elem = _Float16;
   using vec8 = f16x8;
   static constexpr int kBytes = 2;
+  static constexpr int32_t kRk = 0;  // its rk_dtype code (RK_F16)
   static __device__ __forceinline__ float to_f32(uint16_t b) {
     return (float)__builtin_bit_cast(_Float16, b);
   }
@@ -71,6 +72,7 @@ struct BF16 {
   using elem = __bf16;
   using vec8 = bf16x8;
   static constexpr int kBytes = 2;
+  static constexpr int32_t kRk = 1;  // its rk_dtype code (RK_BF16)
   static __device__ __forceinline__ float to_f32(uint16_t b) {
     return __builtin_bit_cast(float, (uint32_t)b << 16);
   }

@@ -549,8 +549,8 @@ decode_kernel(const DecodeArgs a) {
   constexpr int DKP = DKB * 32;
   constexpr int NBUF_V = DKB == 1 ? 3 : 2;
   constexpr int NBUF_F = 2;
-  __shared__ float s_q[HMAX][128];
-  __shared__ float s_qt[HMAX][DKP];
+  __shared__ __attribute__((aligned(16))) float s_q[HMAX][128];
+  __shared__ __attribute__((aligned(16))) float s_qt[HMAX][DKP];
   __shared__ float s_bias[HMAX];
   __shared__ float s_dm[128];
   __shared__ float s_m[kWaves][HMAX];
@@ -774,65 +774,9 @@ decode_kernel(const DecodeArgs a) {
     store_new();
     if (tid < 128) s_dm[tid] = dmv;
     __syncthreads();
-    float rv[kL];
-    if (a.r_vec) {
-      // the thread's kL reads of column c issued back to back, then one
-      // branch on R's (launch-uniform) 16-bit dtype; lanes past Dk read the
-      // last column and are zeroed after (a per-element dtype and column
-      // test put each read in its own branch, each waiting for its data)
-      const uint16_t* rl = (const uint16_t*)s_r + min(c, max(a.Dk - 1, 0)) + part * kL * a.Dk;
-      uint16_t raw[kL];
-#pragma unroll
-      for (int i = 0; i < kL; ++i) raw[i] = rl[i * a.Dk];
-      if (a.r_dtype == RK_F16) {
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = F16::to_f32(raw[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = BF16::to_f32(raw[i]);
-      }
-#pragma unroll
-      for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
-    } else {  // element-wise fallback (column c, clamped in-bounds; no load
-              // at all when Dk == 0, where R_partial has no storage)
-#pragma unroll
-      for (int i = 0; i < kL; ++i) rv[i] = 0.f;
-      if (a.Dk > 0) {
-        const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)min(c, a.Dk - 1) * a.R_sk;
-        load_any_n(a.R, rb + (int64_t)(part * kL) * a.R_sd, a.R_sd, a.r_dtype, rv);
-#pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
-      }
-    }
-    float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
-    // two heads per (uniform) branch, so their q reads share one LDS round
-    // trip; rows of absent heads hold zeros and are never read back
-    constexpr int kHS = HMAX >= 2 ? 2 : 1;
-#pragma unroll
-    for (int h = 0; h < HMAX; h += kHS) {
-      if (h < nh) {
-        float acc_h[kHS];
-#pragma unroll
-        for (int j = 0; j < kHS; ++j) {
-          acc_h[j] = 0.f;
-#pragma unroll
-          for (int i = 0; i < kL; ++i) acc_h[j] += s_q[h + j][part * kL + i] * rv[i];
-        }
-#pragma unroll
-        for (int j = 0; j < kHS; ++j) s_part[(part * HMAX + h + j) * DKP + c] = acc_h[j];
-      }
-    }
-    __syncthreads();
-    for (int i = tid; i < HMAX * DKP; i += kThreads) {
-      const int h = i / DKP, cc = i % DKP;
-      float sum = 0.f;
-      if (h < nh) {
-#pragma unroll
-        for (int pp = 0; pp < kParts; ++pp) sum += s_part[(pp * HMAX + h) * DKP + cc];
-      }
-      s_qt[h][cc] = sum;
-    }
-    {  // q . delta_mu: 16 lanes per head, eight channels each
+    // q . delta_mu: 16 lanes per head, eight channels each (needs only s_q
+    // and s_dm, complete at the barrier above)
+    auto q_dot_dm = [&]() {
       const int hb = tid >> 4, j = tid & 15, hs = min(hb, HMAX - 1);
       float bsum = 0.f;
 #pragma unroll
@@ -840,8 +784,105 @@ decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) bsum += shfl_xor(bsum, off);
       if (hb < HMAX && j == 0) s_bias[hb] = bsum;
+    };
+    if (DKB >= 2 && a.r_vec && a.r_dtype == TT::kRk) {
+      // q R on the MFMA: wave w forms the 16-column tiles w, w + 4, .. of
+      // q R (16 head rows x DKP columns) over the four 32-channel steps.
+      // A = q (16-bit values, exact), B = R columns read from LDS (columns
+      // past Dk zero); the products are exact and summed in fp32.  Taken
+      // for 33-64 kept channels (config 4 at keep 64: 664 -> 618 us per
+      // step at 4097 visual tokens, 1035 -> 990 at 12001); with one block of
+      // 32 (only waves 0 and 1 busy) it measured 2-3 % slower at 12001
+      // tokens, so those keep the FMA form below.
+      const uint16_t* rl = (const uint16_t*)s_r;
+      const int dk1 = max(a.Dk - 1, 0);
+      const bool hrow = n < HMAX;  // HMAX = 1: the other A rows are zero
+      for (int t = wave; t < DKP / 16; t += kWaves) {  // uniform
+        const int col = 16 * t + n;
+        const uint16_t* rc = rl + min(col, dk1);
+        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const int k0 = 32 * kk + 8 * g;
+          uint16_t rb[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rb[e] = rc[(k0 + e) * a.Dk];
+          const float4 f0 = *(const float4*)&s_q[nq][k0], f1 = *(const float4*)&s_q[nq][k0 + 4];
+          const uint4 av = hrow ? make_uint4(TT::pack2(f0.x, f0.y), TT::pack2(f0.z, f0.w), TT::pack2(f1.x, f1.y),
+                                             TT::pack2(f1.z, f1.w))
+                                : make_uint4(0u, 0u, 0u, 0u);
+          const uint4 bv = col < a.Dk ? pack8(rb) : make_uint4(0u, 0u, 0u, 0u);
+          d = TT::mfma(av, bv, d);
+        }
+        // lane (g, n) holds rows 4g .. 4g + 3 of column 16t + n
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (4 * g + i < HMAX) s_qt[4 * g + i][col] = d[i];
+      }
+      q_dot_dm();
+      __syncthreads();
+    } else {  // q R by FMAs: partial sums over 8 (..2) channel slices, then summed
+      float rv[kL];
+      if (a.r_vec) {
+        // the thread's kL reads of column c issued back to back, then one
+        // branch on R's (launch-uniform) 16-bit dtype; lanes past Dk read the
+        // last column and are zeroed after (a per-element dtype and column
+        // test put each read in its own branch, each waiting for its data)
+        const uint16_t* rl = (const uint16_t*)s_r + min(c, max(a.Dk - 1, 0)) + part * kL * a.Dk;
+        uint16_t raw[kL];
+#pragma unroll
+        for (int i = 0; i < kL; ++i) raw[i] = rl[i * a.Dk];
+        if (a.r_dtype == RK_F16) {
+#pragma unroll
+          for (int i = 0; i < kL; ++i) rv[i] = F16::to_f32(raw[i]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < kL; ++i) rv[i] = BF16::to_f32(raw[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
+      } else {  // element-wise fallback (column c, clamped in-bounds; no load
+                // at all when Dk == 0, where R_partial has no storage)
+#pragma unroll
+        for (int i = 0; i < kL; ++i) rv[i] = 0.f;
+        if (a.Dk > 0) {
+          const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)min(c, a.Dk - 1) * a.R_sk;
+          load_any_n(a.R, rb + (int64_t)(part * kL) * a.R_sd, a.R_sd, a.r_dtype, rv);
+#pragma unroll
+          for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
+        }
+      }
+      float* s_part = &s_acc[0][0][0];  // [kParts][HMAX][DKP], free until the epilogue
+      // two heads per (uniform) branch, so their q reads share one LDS round
+      // trip; rows of absent heads hold zeros and are never read back
+      constexpr int kHS = HMAX >= 2 ? 2 : 1;
+#pragma unroll
+      for (int h = 0; h < HMAX; h += kHS) {
+        if (h < nh) {
+          float acc_h[kHS];
+#pragma unroll
+          for (int j = 0; j < kHS; ++j) {
+            acc_h[j] = 0.f;
+#pragma unroll
+            for (int i = 0; i < kL; ++i) acc_h[j] += s_q[h + j][part * kL + i] * rv[i];
+          }
+#pragma unroll
+          for (int j = 0; j < kHS; ++j) s_part[(part * HMAX + h + j) * DKP + c] = acc_h[j];
+        }
+      }
+      __syncthreads();
+      for (int i = tid; i < HMAX * DKP; i += kThreads) {
+        const int h = i / DKP, cc = i % DKP;
+        float sum = 0.f;
+        if (h < nh) {
+#pragma unroll
+          for (int pp = 0; pp < kParts; ++pp) sum += s_part[(pp * HMAX + h) * DKP + cc];
+        }
+        s_qt[h][cc] = sum;
+      }
+      q_dot_dm();
+      __syncthreads();
     }
-    __syncthreads();
 
     uint4 qh[DKB], ql[DKB];
 #pragma unroll
