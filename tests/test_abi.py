@@ -485,6 +485,11 @@ def test_plan_one_workgroup_per_cu_for_small_short_rounds():
         assert p["chunk_major"] == 1 and p["n_fast"] == 0 and p["grid"] == 256, (keep, p)
     p = _lib.plan_decode(1, 32, 32, 32, 4000, 640, policy=0)
     assert p["chunk_major"] == 1 and p["grid"] == 256 and p["single_launch"] == 1
+    # units of one query head take one workgroup per CU up to 192 KB two-slot
+    # chunks (8000 tokens: 177 KB), not at 209 KB (keep 64, 8000 tokens)
+    assert _lib.plan_decode(1, 32, 32, 32, 8000, 640, policy=0)["grid"] == 256
+    assert _lib.plan_decode(1, 32, 32, 64, 8000, 640, policy=0)["grid"] == 512
+    assert _lib.plan_decode(8, 28, 4, 32, 8001, 61, policy=1)["grid"] == 512   # GQA, 159 KB
     for shape, pol in (((8, 28, 4, 32, 12001, 61), 1), ((1, 32, 32, 32, 15360, 640), 0)):
         assert _lib.plan_decode(*shape, policy=pol)["grid"] == 512
     p = _lib.plan_decode(16, 28, 4, 32, 2049, 61, policy=1)

@@ -85,6 +85,7 @@ CASES = [
     (3, 12, 4, 32, 2049, 17, torch.float16, "gqa", (1, False, False)),    # 12 units, 132 workgroups
     (2, 8, 8, 16, 3001, 129, torch.bfloat16, "paper", (1, False, False)),  # 208 workgroups: one per CU
     (2, 16, 16, 32, 2500, 60, torch.float16, "paper", (1, True, True)),   # 416 workgroups of <= 128 KB
+    (1, 32, 32, 32, 8000, 640, torch.float16, "paper", (1, False, True)),  # one-head units, 177 KB: one per CU
 ]
 
 
