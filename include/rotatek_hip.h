@@ -282,7 +282,8 @@ int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
  * wgs_per_cu workgroups per compute unit).  Pass 0 to keep a value;
  * wgs_per_cu < 0 restores the default: two workgroups per CU, one for a
  * single chunk-major round whose two-slot visual chunks would stream
- * <= 128 KB each (192 KB for units of one query head). */
+ * <= 128 KB each (192 KB for units of one query head), and one for fp32
+ * wherever that is still a single round. */
 void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu);
 
 /* Granularity of the visual chunks in tokens (32, 64 or 128: whole

@@ -1582,6 +1582,19 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
         one.grid <= num_cus)
       p = one;
   }
+  // fp32 (the VALU kernel, unit-major): one workgroup per CU whenever that
+  // is still one round, at any workgroup size up to the cap.  With two
+  // slots a grid of a little over num_cus leaves some CUs two workgroups,
+  // which finish last.  Graph-replayed decodes on MI355X (us, two slots ->
+  // one), B=1, 32 heads, 128 prompt/text tokens: 1024 / 2304 / 4608 / 6000
+  // visual tokens 20.9 -> 14.7, 25.9 -> 19.2, 35.2 -> 26.4, 38.6 -> 32.0;
+  // 4 KV heads of 7 query heads at 4096 tokens 28.5 -> 20.4.  Where one
+  // slot per CU needs a second round (B=1 at 8192 tokens, B=2 or 4), the
+  // two-slot plan is as fast or faster and is kept.
+  if (g_wgs_per_cu == 0 && elem_bytes == 4 && p.grid > num_cus) {
+    rk_decode_plan one = units_only;
+    if (split_plan(one, Dk, S_v, S_f, elem_bytes, num_cus, num_cus) == RK_OK && one.grid <= num_cus) p = one;
+  }
   p.workspace_bytes = ws_layout(p).total;
   p.single_launch = use_single_launch(p, B, num_cus) ? 1 : 0;
   *plan = p;

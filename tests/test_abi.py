@@ -490,6 +490,12 @@ def test_plan_one_workgroup_per_cu_for_small_short_rounds():
     assert _lib.plan_decode(1, 32, 32, 32, 8000, 640, policy=0)["grid"] == 256
     assert _lib.plan_decode(1, 32, 32, 64, 8000, 640, policy=0)["grid"] == 512
     assert _lib.plan_decode(8, 28, 4, 32, 8001, 61, policy=1)["grid"] == 512   # GQA, 159 KB
+    # fp32 (the VALU kernel): one workgroup per CU wherever that is still one
+    # round (config 0: 320 -> 224 workgroups), else the two-slot plan
+    for S_v, want in ((2304, 224), (1024, 160), (6000, 256), (8192, 448)):
+        p = _lib.plan_decode(1, 32, 32, 32, S_v, 128, elem_bytes=4, policy=0)
+        assert p["grid"] == want and p["chunk_major"] == 0, (S_v, p)
+    assert _lib.plan_decode(2, 32, 32, 32, 1152, 128, elem_bytes=4, policy=0)["grid"] == 384
     for shape, pol in (((8, 28, 4, 32, 12001, 61), 1), ((1, 32, 32, 32, 15360, 640), 0)):
         assert _lib.plan_decode(*shape, policy=pol)["grid"] == 512
     p = _lib.plan_decode(16, 28, 4, 32, 2049, 61, policy=1)
