@@ -212,6 +212,66 @@ def test_plan_covers_every_token(shape, policy):
         assert p["grid"] <= 2 * 256
 
 
+def _check_plan(p, B, Hq, Hkv, Dk, S_v, S_f, policy, elem_bytes, cus):
+    """Invariants of any decode plan: units, exact token coverage by the
+    chunks, the grid, one round for chunk-major grids, and one workgroup per
+    CU for the one-slot plans."""
+    G = Hq // Hkv
+    if policy == 1:  # (the fp32 entry points plan policy 0 themselves)
+        assert p["heads_per_unit"] == min(G, 16) and p["units"] == B * Hkv * -(-G // 16)
+    else:
+        assert p["heads_per_unit"] == 1 and p["units"] == B * Hq
+    if S_v > 0:
+        nf, cf, cv, wg = p["n_fast"], p["chunk_fast"], p["chunk_vis"], p["wg_vis"]
+        assert cv > 0 and cv % 32 == 0 and 0 <= nf < wg and (nf == 0 or (p["chunk_major"] and cf > cv))
+        assert nf * cf + (wg - nf) * cv >= S_v and nf * cf + (wg - nf - 1) * cv < S_v
+    else:
+        assert p["wg_vis"] == 0
+    if S_f > 0:
+        assert p["chunk_full"] % 128 == 0 and p["wg_full"] * p["chunk_full"] >= S_f
+        assert (p["wg_full"] - 1) * p["chunk_full"] < S_f
+    assert p["wg_vis"] + p["wg_full"] >= 1
+    assert p["grid"] == p["units"] * (p["wg_vis"] + p["wg_full"])
+    if p["chunk_major"]:
+        assert elem_bytes == 2 and S_v > 0 and p["grid"] <= 2 * cus
+    assert p["workspace_bytes"] >= p["grid"] * p["heads_per_unit"] * 640
+
+
+def test_plan_invariants_on_random_shapes():
+    """The planner's rules (rounds, span shares, chunk-major short rounds,
+    enlarged first chunks, one workgroup per CU for small rounds and for
+    fp32) on 600 seeded random shapes, both policies, both element sizes,
+    two CU counts and every planner setting, checked for the plan
+    invariants; the default plan never exceeds the two-slot plan's grid."""
+    import random
+    rng = random.Random(2024)
+    try:
+        for _ in range(600):
+            Hkv = rng.choice([1, 2, 4, 8, 32])
+            G = rng.choice([1, 1, 2, 4, 7, 8, 16, 20])
+            B = rng.choice([1, 2, 3, 8, 16, 32])
+            Dk = rng.choice([0, 8, 16, 32, 48, 64, 128])
+            S_v = rng.choice([0, 1, 31, 200, 1025, 2304, 4097, 8000, 12001, 30720])
+            S_f = rng.choice([0, 1, 60, 128, 640, 2000])
+            if S_v + S_f == 0:
+                S_f = 5
+            policy, eb, cus = rng.choice([0, 1]), rng.choice([2, 2, 4]), rng.choice([256, 304])
+            skew = rng.choice([0, 1000, 1300])
+            _lib.set_decode_skew(skew)
+            _lib.set_decode_tuning(0, 0, 2)
+            two = _lib.plan_decode(B, Hkv * G, Hkv, Dk, S_v, S_f, eb, policy, cus)
+            _check_plan(two, B, Hkv * G, Hkv, Dk, S_v, S_f, policy, eb, cus)
+            _lib.set_decode_tuning(0, 0, -1)
+            dflt = _lib.plan_decode(B, Hkv * G, Hkv, Dk, S_v, S_f, eb, policy, cus)
+            _check_plan(dflt, B, Hkv * G, Hkv, Dk, S_v, S_f, policy, eb, cus)
+            assert dflt["grid"] <= two["grid"]
+            if dflt != two:  # a one-per-CU plan: one workgroup per CU, one round
+                assert dflt["grid"] <= cus and dflt["n_fast"] == 0
+    finally:
+        _lib.set_decode_skew(1300)
+        _lib.set_decode_tuning(0, 0, -1)
+
+
 # ----------------------------------------------------------------- prefill ABI
 def _cov_check(shape=(2, 4, 300, 128), dtype=_lib.RK_BF16, cov_shape=None, mean_shape=None):
     lib = _lib.load()
