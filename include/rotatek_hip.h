@@ -278,8 +278,11 @@ int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk,
                    int32_t policy, int32_t num_cus, rk_decode_plan* plan);
 
 /* Tuning knobs of the split planner (bytes of K/V streamed per workgroup
- * are clamped to [min_bytes, max_bytes] and the planner aims for
- * wgs_per_cu workgroups per compute unit).  Pass 0 to keep a value;
+ * are clamped to [min_bytes, max_bytes], a max below the min reading as
+ * the min, and the planner aims for wgs_per_cu workgroups per compute
+ * unit).  These and the knobs below are process-wide and atomic; each
+ * plan reads them once, so a decode planned while another thread changes
+ * them uses either the old or the new values.  Pass 0 to keep a value;
  * wgs_per_cu < 0 restores the default: two workgroups per CU, one for a
  * single chunk-major round whose two-slot visual chunks would stream
  * <= 128 KB each (192 KB for units of one query head), and one for fp32

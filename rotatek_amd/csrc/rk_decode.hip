@@ -45,6 +45,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "rk_common.h"
@@ -1297,26 +1298,28 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
 
 namespace {
 
+// Planner knobs (rk_set_decode_*): process-wide, atomic, and read once per
+// plan (Knobs), so a plan never mixes values of a concurrent change.
+//
 // Bytes of K/V a workgroup streams: total / (2 * CUs), clamped to
 // [64 KB, 512 KB].  Measured on MI355X: 512 KB chunks are within 2-5% of the
 // best split at B=32/16k (MHA), B=16/32k (GQA) and B=1/16k; small problems
 // get at least ~2 workgroups per CU.
-int64_t g_min_wg_bytes = INT64_C(64) << 10;
-int64_t g_max_wg_bytes = INT64_C(512) << 10;
+std::atomic<int64_t> g_min_wg_bytes{INT64_C(64) << 10};
+std::atomic<int64_t> g_max_wg_bytes{INT64_C(512) << 10};
 // Workgroups planned per CU: 0 (default) plans two (the kernel's register
 // budget holds two per CU), or one for a single round of small workgroups
 // (rk_plan_decode); n > 0 plans n.
-int32_t g_wgs_per_cu = 0;
-int64_t resident_wgs() { return g_wgs_per_cu > 0 ? g_wgs_per_cu : 2; }
+std::atomic<int32_t> g_wgs_per_cu{0};
 // Visual chunks are whole multiples of this many tokens (a 32-token block
 // or the 128 tokens of one block per wave); 0: 32 in a chunk-major grid,
 // else 128.
-int64_t g_chunk_align = 0;
+std::atomic<int64_t> g_chunk_align{0};
 // One-round grids of short workgroups (see rk_plan_decode): 0 keeps the
 // unit-major launch, 1000 launches chunk-major with equal chunks, more
 // gives the first-dispatched chunks of the smallest workgroups this many
 // thousandths of the others' tokens.
-int32_t g_skew_permille = 1300;
+std::atomic<int32_t> g_skew_permille{1300};
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 int64_t round_up(int64_t a, int64_t b) { return cdiv(a, b) * b; }
@@ -1338,7 +1341,28 @@ constexpr int64_t kOneSlotMaxBytesOneHead = INT64_C(192) << 10;
 // Merge mode (rk_set_decode_merge): 0 (default) = per shape (below),
 // 1 = two launches,
 // 2 = single launch where the ticket region holds the counters.
-int32_t g_merge_mode = 0;
+std::atomic<int32_t> g_merge_mode{0};
+
+// One plan's snapshot of the knobs above (a byte cap below the floor reads
+// as the floor).
+struct Knobs {
+  int64_t min_wg, max_wg, chunk_align;
+  int32_t wgs_per_cu, skew_permille, merge_mode;
+  int64_t resident() const { return wgs_per_cu > 0 ? wgs_per_cu : 2; }
+};
+
+Knobs knobs() {
+  constexpr auto r = std::memory_order_relaxed;
+  Knobs k;
+  k.min_wg = g_min_wg_bytes.load(r);
+  k.max_wg = g_max_wg_bytes.load(r);
+  k.chunk_align = g_chunk_align.load(r);
+  k.wgs_per_cu = g_wgs_per_cu.load(r);
+  k.skew_permille = g_skew_permille.load(r);
+  k.merge_mode = g_merge_mode.load(r);
+  if (k.max_wg < k.min_wg) k.max_wg = k.min_wg;
+  return k;
+}
 
 struct WsLayout {
   size_t ticket, bticket, part, total;
@@ -1373,10 +1397,10 @@ WsLayout ws_layout(const rk_decode_plan& p) {
 // rounds it is worse still: every workgroup holds its slot through its own
 // wait (B=32, 16k context: 935 against 815 us; B=4, 32 heads, 4.6k tokens,
 // two rounds: 44.2 -> 44.8 us).
-bool use_single_launch(const rk_decode_plan& p, int64_t B, int cus) {
+bool use_single_launch(const rk_decode_plan& p, int64_t B, int cus, const Knobs& k) {
   if (p.units + B > (int64_t)(RK_DECODE_TICKET_BYTES / sizeof(uint32_t))) return false;
-  if (g_merge_mode != 0) return g_merge_mode == 2;
-  return p.heads_per_unit == 1 && p.grid <= (int64_t)cus * resident_wgs();
+  if (k.merge_mode != 0) return k.merge_mode == 2;
+  return p.heads_per_unit == 1 && p.grid <= (int64_t)cus * k.resident();
 }
 
 }  // namespace
@@ -1401,23 +1425,25 @@ extern "C" int rk_decode_workspace_init(void* workspace, size_t workspace_bytes,
 }
 
 extern "C" void rk_set_decode_merge(int32_t mode) {
-  if (mode >= 0 && mode <= 2) g_merge_mode = mode;
+  if (mode >= 0 && mode <= 2) g_merge_mode.store(mode, std::memory_order_relaxed);
 }
 
 extern "C" void rk_set_decode_chunk_align(int32_t tokens) {
-  if (tokens == 0 || tokens == rk::kBlk || tokens == 2 * rk::kBlk || tokens == kWgTokens) g_chunk_align = tokens;
+  if (tokens == 0 || tokens == rk::kBlk || tokens == 2 * rk::kBlk || tokens == kWgTokens)
+    g_chunk_align.store(tokens, std::memory_order_relaxed);
 }
 
 extern "C" void rk_set_decode_skew(int32_t permille) {
-  if (permille == 0 || (permille >= 1000 && permille <= 4000)) g_skew_permille = permille;
+  if (permille == 0 || (permille >= 1000 && permille <= 4000))
+    g_skew_permille.store(permille, std::memory_order_relaxed);
 }
 
 extern "C" void rk_set_decode_tuning(int64_t min_bytes, int64_t max_bytes, int32_t wgs_per_cu) {
-  if (min_bytes > 0) g_min_wg_bytes = min_bytes;
-  if (max_bytes > 0) g_max_wg_bytes = max_bytes;
-  if (wgs_per_cu > 0) g_wgs_per_cu = wgs_per_cu;
-  if (wgs_per_cu < 0) g_wgs_per_cu = 0;
-  if (g_max_wg_bytes < g_min_wg_bytes) g_max_wg_bytes = g_min_wg_bytes;
+  constexpr auto r = std::memory_order_relaxed;
+  if (min_bytes > 0) g_min_wg_bytes.store(min_bytes, r);
+  if (max_bytes > 0) g_max_wg_bytes.store(max_bytes, r);
+  if (wgs_per_cu > 0) g_wgs_per_cu.store(wgs_per_cu, r);
+  if (wgs_per_cu < 0) g_wgs_per_cu.store(0, r);
 }
 
 namespace {
@@ -1425,12 +1451,12 @@ namespace {
 // The chunking of a plan whose unit fields are set, for rounds of `slots`
 // resident workgroups on `num_cus` CUs.
 int split_plan(rk_decode_plan& p, int64_t Dk, int64_t S_v, int64_t S_f, int32_t elem_bytes, int64_t slots,
-               int32_t num_cus) {
+               int32_t num_cus, const Knobs& k) {
   // Workgroups run in rounds of `slots` resident workgroups (two per CU at
   // the kernel's register budget).  A partial last round costs as much as a
   // full one, so the grid is sized to whole rounds: the fewest rounds that
-  // keep a workgroup at <= g_max_wg_bytes, then as many workgroups per unit
-  // as those rounds hold (but none below g_min_wg_bytes), split between the
+  // keep a workgroup at <= the byte cap, then as many workgroups per unit
+  // as those rounds hold (but none below the byte floor), split between the
   // visual and prompt/text spans in proportion to their bytes.
   const int64_t unit_vis = S_v * (Dk + 128) * elem_bytes;
   const int64_t unit_full = S_f * 256 * elem_bytes;
@@ -1440,17 +1466,17 @@ int split_plan(rk_decode_plan& p, int64_t Dk, int64_t S_v, int64_t S_f, int32_t 
   // head, one merge row each), so it takes larger chunks: measured on MI355X,
   // a GQA group of 7 runs best in a single round of up to 4 MB workgroups,
   // one query head per unit at 512 KB.
-  const int64_t max_wg = p.heads_per_unit > 1 ? 8 * g_max_wg_bytes : g_max_wg_bytes;
+  const int64_t max_wg = p.heads_per_unit > 1 ? 8 * k.max_wg : k.max_wg;
   int64_t rounds = cdiv(total, slots * max_wg);
   // ... and enough rounds for kMinWgsPerUnit workgroups per unit: with many
   // units a single round leaves each unit one or two workgroups of several
   // MB (measured on MI355X, B=32 with 8 KV heads of 4 query heads: 228 us
   // at 2-3 workgroups per unit, 216 us at 7)
   const int64_t by_units = cdiv(kMinWgsPerUnit * p.units, slots);
-  if (rounds < by_units && total / (by_units * slots) >= g_min_wg_bytes) rounds = by_units;
+  if (rounds < by_units && total / (by_units * slots) >= k.min_wg) rounds = by_units;
   if (rounds < 1) rounds = 1;
   int64_t budget = p.units > 0 ? rounds * slots / p.units : 1;
-  const int64_t by_min = unit_bytes / g_min_wg_bytes;
+  const int64_t by_min = unit_bytes / k.min_wg;
   if (budget > by_min) budget = by_min;
   if (budget < 1) budget = 1;
   // Each span gets its byte share of the budget, rounded, at least one
@@ -1475,12 +1501,12 @@ int split_plan(rk_decode_plan& p, int64_t Dk, int64_t S_v, int64_t S_f, int32_t 
         unit_vis / fit - unit_vis / w_vis < kSlotLatencyBytes)
       w_vis = fit;
   }
-  // One round of workgroups of at most g_max_wg_bytes (a grid of short
+  // One round of workgroups of at most the byte cap (a grid of short
   // workgroups, whose fixed costs show) launches chunk-major (below) with
   // 32-token chunks, so that the round's slots fill.
-  const bool short_round = g_skew_permille > 0 && elem_bytes == 2 && S_v > 0 && rounds == 1 &&
-                           unit_bytes <= (w_vis + w_full) * g_max_wg_bytes;
-  const int64_t align = g_chunk_align > 0 ? g_chunk_align : short_round ? rk::kBlk : kWgTokens;
+  const bool short_round = k.skew_permille > 0 && elem_bytes == 2 && S_v > 0 && rounds == 1 &&
+                           unit_bytes <= (w_vis + w_full) * k.max_wg;
+  const int64_t align = k.chunk_align > 0 ? k.chunk_align : short_round ? rk::kBlk : kWgTokens;
   if (S_v > 0) {
     p.chunk_vis = round_up(cdiv(S_v, w_vis), align);
     p.wg_vis = (int32_t)cdiv(S_v, p.chunk_vis);
@@ -1513,15 +1539,15 @@ int split_plan(rk_decode_plan& p, int64_t Dk, int64_t S_v, int64_t S_f, int32_t 
   // layer).  In a chunk-major grid the first num_cus ids are the chunks
   // x < n_fast = num_cus / units of every unit.  Where workgroups stream
   // <= 128 KB (fixed latency dominates), those chunks take chunk_fast
-  // tokens, g_skew_permille / 1000 times the others' (whole 32-token
+  // tokens, skew_permille / 1000 times the others' (whole 32-token
   // blocks): B=8, 4097 visual tokens, keep 32, 665 -> 648 us per step; at
   // 12001 tokens (256 KB workgroups) the skew measured 894 -> 903 us.
-  if (p.chunk_major && g_skew_permille > 1000 && p.wg_vis >= 2 && p.grid > num_cus &&
+  if (p.chunk_major && k.skew_permille > 1000 && p.wg_vis >= 2 && p.grid > num_cus &&
       unit_vis <= p.wg_vis * kSkewMaxBytes) {
     const int64_t nf = num_cus / p.units, ns = p.wg_vis - nf;
     const int64_t nb = cdiv(S_v, rk::kBlk);
     if (nf >= 1 && ns >= 1) {
-      const double rho = g_skew_permille / 1000.0;
+      const double rho = k.skew_permille / 1000.0;
       const int64_t bf = (int64_t)(rho * (double)nb / ((double)nf * rho + (double)ns) + 0.5);
       const int64_t bs = nb - nf * bf > 0 ? cdiv(nb - nf * bf, ns) : 0;
       if (bs >= 1 && bf > bs && nf * bf + (ns - 1) * bs < nb) {
@@ -1557,7 +1583,8 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
     p.units = B * H_q;
   }
   const rk_decode_plan units_only = p;
-  int st = split_plan(p, Dk, S_v, S_f, elem_bytes, (int64_t)num_cus * resident_wgs(), num_cus);
+  const Knobs k = knobs();
+  int st = split_plan(p, Dk, S_v, S_f, elem_bytes, (int64_t)num_cus * k.resident(), num_cus, k);
   if (st) return st;
   // A single round of small workgroups (two-slot visual chunks of <= 128 KB)
   // runs faster as one workgroup per CU of twice the tokens, where that is
@@ -1576,9 +1603,9 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   // 27.5 us) but lose at 209 KB with 64 (24.7 against 25.2), so their bound
   // is 192 KB.
   const int64_t one_slot_max = p.heads_per_unit == 1 ? kOneSlotMaxBytesOneHead : kOneSlotMaxBytes;
-  if (g_wgs_per_cu == 0 && p.chunk_major && S_v * (Dk + 128) * elem_bytes <= p.wg_vis * one_slot_max) {
+  if (k.wgs_per_cu == 0 && p.chunk_major && S_v * (Dk + 128) * elem_bytes <= p.wg_vis * one_slot_max) {
     rk_decode_plan one = units_only;
-    if (split_plan(one, Dk, S_v, S_f, elem_bytes, num_cus, num_cus) == RK_OK && one.chunk_major &&
+    if (split_plan(one, Dk, S_v, S_f, elem_bytes, num_cus, num_cus, k) == RK_OK && one.chunk_major &&
         one.grid <= num_cus)
       p = one;
   }
@@ -1591,12 +1618,12 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   // 4 KV heads of 7 query heads at 4096 tokens 28.5 -> 20.4.  Where one
   // slot per CU needs a second round (B=1 at 8192 tokens, B=2 or 4), the
   // two-slot plan is as fast or faster and is kept.
-  if (g_wgs_per_cu == 0 && elem_bytes == 4 && p.grid > num_cus) {
+  if (k.wgs_per_cu == 0 && elem_bytes == 4 && p.grid > num_cus) {
     rk_decode_plan one = units_only;
-    if (split_plan(one, Dk, S_v, S_f, elem_bytes, num_cus, num_cus) == RK_OK && one.grid <= num_cus) p = one;
+    if (split_plan(one, Dk, S_v, S_f, elem_bytes, num_cus, num_cus, k) == RK_OK && one.grid <= num_cus) p = one;
   }
   p.workspace_bytes = ws_layout(p).total;
-  p.single_launch = use_single_launch(p, B, num_cus) ? 1 : 0;
+  p.single_launch = use_single_launch(p, B, num_cus, k) ? 1 : 0;
   *plan = p;
   return RK_OK;
 }

@@ -272,6 +272,56 @@ def test_plan_invariants_on_random_shapes():
         _lib.set_decode_tuning(0, 0, -1)
 
 
+def test_planner_knobs_read_once_per_plan():
+    """The planner knobs are process-wide atomics that each plan reads once:
+    a byte cap set below the floor plans as the floor, and threads that flip
+    the knobs while others plan (ctypes drops the GIL around each call) only
+    ever get plans that satisfy the plan invariants."""
+    import random
+    import threading
+    shape = (8, 28, 4, 32, 12001, 61, 2, 1, 256)
+    try:
+        _lib.set_decode_tuning(1 << 20, 1 << 20, 0)
+        want = _lib.plan_decode(*shape)
+        _lib.set_decode_tuning(1 << 20, 4096, 0)
+        assert _lib.plan_decode(*shape) == want
+        _lib.set_decode_tuning(64 << 10, 512 << 10, -1)
+
+        stop, errors = threading.Event(), []
+
+        def flip():
+            i = 0
+            while not stop.is_set():
+                _lib.set_decode_tuning((64 << 10) << (i % 2), (512 << 10) << (i % 3), 2 if i % 2 else -1)
+                _lib.set_decode_skew((1000, 1300, 0)[i % 3])
+                i += 1
+
+        def plan(seed):
+            rng = random.Random(seed)
+            try:
+                for _ in range(1500):
+                    Hkv, G = rng.choice([1, 4, 8]), rng.choice([1, 7])
+                    B, Dk = rng.choice([1, 8, 32]), rng.choice([16, 32, 64])
+                    S_v, S_f = rng.choice([0, 200, 4097, 12001]), rng.choice([1, 61, 2000])
+                    pol, eb = rng.choice([0, 1]), rng.choice([2, 4])
+                    p = _lib.plan_decode(B, Hkv * G, Hkv, Dk, S_v, S_f, eb, pol, 256)
+                    _check_plan(p, B, Hkv * G, Hkv, Dk, S_v, S_f, pol, eb, 256)
+            except AssertionError as e:  # reported from the main thread
+                errors.append(e)
+
+        threads = [threading.Thread(target=flip)] + [threading.Thread(target=plan, args=(s,)) for s in range(3)]
+        for t in threads:
+            t.start()
+        for t in threads[1:]:
+            t.join()
+        stop.set()
+        threads[0].join()
+        assert not errors, errors[0]
+    finally:
+        _lib.set_decode_skew(1300)
+        _lib.set_decode_tuning(64 << 10, 512 << 10, -1)
+
+
 # ----------------------------------------------------------------- prefill ABI
 def _cov_check(shape=(2, 4, 300, 128), dtype=_lib.RK_BF16, cov_shape=None, mean_shape=None):
     lib = _lib.load()
