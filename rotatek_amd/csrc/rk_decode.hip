@@ -558,9 +558,11 @@ decode_kernel(const DecodeArgs a) {
   __shared__ float s_l[kWaves][HMAX];
   __shared__ float s_acc[kWaves][HMAX][128];
   __shared__ __attribute__((aligned(16))) uint8_t s_valid[kMaskChunk];
-  // raw R [128][Dk] (Dk <= 64, 16 KB): the upper half of s_acc when that is
-  // large enough (its lower half holds the q R partial sums), else its own
-  constexpr int kRawChunks = 1024;
+  // raw R [128][Dk] (16 KB for Dk <= 64, 32 KB up to 128): in s_acc when
+  // that is large enough (its upper half, the lower one holding the q R
+  // partial sums; all of it for 65-128 channels, whose q R runs on the MFMA
+  // with no partial sums), else its own
+  constexpr int kRawChunks = DKB == 4 ? 2048 : 1024;
   __shared__ uint4 s_rsep[HMAX >= 16 ? 1 : kRawChunks];
 
   const int tid = threadIdx.x;
@@ -743,7 +745,7 @@ decode_kernel(const DecodeArgs a) {
     // The first K/V blocks, then the prologue's own loads (q; R straight
     // into LDS in the fast layout; delta_mu) are issued back to back, so one
     // memory latency covers them all.
-    uint4* s_r = HMAX >= 16 ? (uint4*)&s_acc[0][0][0] + kRawChunks : s_rsep;
+    uint4* s_r = HMAX >= 16 ? (uint4*)&s_acc[0][0][0] + (DKB == 4 ? 0 : kRawChunks) : s_rsep;
     constexpr int kRPer = kRawChunks / kThreads;
     const int nchunks = 16 * a.Dk;  // [128][Dk] 16-bit elements in 16-byte chunks
     Ring<NBUF_V, VisBuf<DKB>> ring(nblk, wave, rot_seed);
@@ -824,7 +826,7 @@ decode_kernel(const DecodeArgs a) {
       __syncthreads();
     } else {  // q R by FMAs: partial sums over 8 (..2) channel slices, then summed
       float rv[kL];
-      if (a.r_vec) {
+      if (DKB < 4 && a.r_vec) {  // (65-128 channels stage R only for the MFMA form)
         // the thread's kL reads of column c issued back to back, then one
         // branch on R's (launch-uniform) 16-bit dtype; lanes past Dk read the
         // last column and are zeroed after (a per-element dtype and column
@@ -1912,7 +1914,11 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
       a.dm_sd = dm->stride[2];
       a.has_bias = 1;
     }
-    a.r_vec = rk::is_half(R->dtype) && c.Dk <= 64 && R->stride[3] == 1 && R->stride[2] == c.Dk &&
+    // R staged into LDS (16-byte DMA): up to 64 channels in either 16-bit
+    // type; 65-128 only in the compute type (their q R is an MFMA product
+    // read straight from the staged rows, and R fills the kernel's s_acc)
+    a.r_vec = rk::is_half(R->dtype) && (c.Dk <= 64 || (c.Dk <= 128 && R->dtype == c.dtype)) &&
+              R->stride[3] == 1 && R->stride[2] == c.Dk &&
               R->stride[1] % 8 == 0 && R->stride[0] % 8 == 0 && (((uintptr_t)R->data) & 15) == 0;
     a.ks = (const uint16_t*)ks->data;
     a.vs = (const uint16_t*)vs->data;

@@ -77,6 +77,9 @@ CASES = [
     (2, 4, 4, 16, 333, 31),
     (2, 4, 4, 64, 1025, 0),         # no prompt/text
     (2, 4, 2, 128, 640, 7),
+    (2, 8, 8, 96, 700, 40),         # 65-128 kept channels: R staged whole in LDS
+    (1, 28, 4, 100, 900, 33),       # ... G = 7, Dk not a multiple of 8
+    (2, 4, 4, 72, 500, 9),          # ... just past 64
     (1, 4, 4, 40, 250, 17),         # Dk not a power of two
     (1, 4, 4, 8, 129, 1),
     (2, 4, 4, 32, 0, 300),          # no visual span
@@ -96,6 +99,20 @@ def test_rotatek_decode_matches_oracle(case, family, dtype):
     want = _oracle(inp)
     err = np.abs(_np(out) - want).max()
     assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("Dk", [48, 96])
+@pytest.mark.parametrize("family", ["paper", "gqa"])
+def test_rotation_in_the_other_16bit_type(Dk, family):
+    """R_partial in bf16 under fp16 q/K/V (and the reverse): up to 64 kept
+    channels R is staged as is, past 64 only in the compute type, so the
+    element-wise R path runs there."""
+    for dt, rdt in ((torch.float16, torch.bfloat16), (torch.bfloat16, torch.float16)):
+        _say(f"rotatek {family} q {dt} R {rdt} Dk={Dk}")
+        inp = _rand_inputs(2, 8, 4, Dk, 600, 50, dt, seed=Dk + 1)
+        inp["R_partial"] = inp["R_partial"].to(rdt)
+        out = _decode(inp, family)
+        assert np.abs(_np(out) - _oracle(inp)).max() <= TOL[dt]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
