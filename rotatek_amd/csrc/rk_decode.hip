@@ -111,6 +111,7 @@ struct DecodeArgs {
   // per thread); R a contiguous, 16-byte aligned [128][Dk] 16-bit block
   // with Dk <= 64 (staged through LDS with 16-byte loads)
   int32_t q_vec, r_vec;
+  int32_t qr_mfma;  // q R on the MFMA also for rows of <= 32 kept channels
   float scale_log2;
 };
 
@@ -788,7 +789,7 @@ decode_kernel(const DecodeArgs a) {
       for (int off = 1; off < 16; off <<= 1) bsum += shfl_xor(bsum, off);
       if (hb < HMAX && j == 0) s_bias[hb] = bsum;
     };
-    if (DKB >= 2 && a.r_vec && a.r_dtype == TT::kRk) {
+    if ((DKB >= 2 || a.qr_mfma) && a.r_vec && a.r_dtype == TT::kRk) {
       // q R on the MFMA: wave w forms the 16-column tiles w, w + 4, .. of
       // q R (16 head rows x DKP columns) over the four 32-channel steps.
       // A = q (16-bit values, exact), B = R columns read from LDS (columns
@@ -1988,6 +1989,14 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   if (a.cmajor) a.rot_x = 0;
   const dim3 grid = a.cmajor ? dim3((unsigned)p.units, (unsigned)a.np) : dim3((unsigned)a.np, (unsigned)p.units);
   const int hmax = p.heads_per_unit > 1 ? 16 : 1;
+  // Rows of <= 32 kept channels form q R on the MFMA too where each CU runs
+  // one workgroup (the one-per-CU plans): nothing streams during that
+  // workgroup's prologue, so the shorter MFMA prologue pays.  In two-slot
+  // rounds the CU's other workgroup hides the FMA prologue and the MFMA
+  // form measured slower.  Graph-replayed config 4 steps on MI355X (28
+  // layers, us): 4097 visual tokens keep 32 / 16 576.5 -> 558.9 / 545.8 ->
+  // 535.2; at 12001 tokens (two slots) 864.1 -> 875.9 with the MFMA form.
+  a.qr_mfma = dkb == 1 && a.cmajor && p.grid <= cus ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
   if (c.dtype == RK_F32) {
     const bool v32 = vec32_ok(kf) && vec32_ok(vf) &&
