@@ -549,7 +549,12 @@ template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND, bool
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const DecodeArgs a) {
   constexpr int DKP = DKB * 32;
-  constexpr int NBUF_V = DKB == 1 ? 3 : 2;
+  // visual blocks in flight per wave: three for multi-head units of <= 32
+  // kept channels, else two (one-head units: measured faster on MI355X, eager
+  // / graph us, config 1 34.1 / 33.2 -> 32.5 / 31.9, B=1 at 4000 tokens
+  // 17.2 -> 16.2 graph, config 2 814.7 -> 811.4; multi-head units of 7 at
+  // 12001 tokens 864 -> 888 us per config 4 step with two)
+  constexpr int NBUF_V = DKB == 1 && HMAX > 1 ? 3 : 2;
   constexpr int NBUF_F = 2;
   __shared__ __attribute__((aligned(16))) float s_q[HMAX][128];
   __shared__ __attribute__((aligned(16))) float s_qt[HMAX][DKP];
