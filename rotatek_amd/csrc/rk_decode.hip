@@ -109,7 +109,8 @@ struct DecodeArgs {
   int32_t r_dtype, dm_dtype, has_bias, has_mask;
   // prologue layouts: q rows contiguous and 16-byte aligned (one 16-byte load
   // per thread); R a contiguous, 16-byte aligned [128][Dk] 16-bit block
-  // with Dk <= 64 (staged through LDS with 16-byte loads)
+  // with Dk <= 64, or up to 128 in the compute type (staged through LDS
+  // with 16-byte loads)
   int32_t q_vec, r_vec;
   int32_t qr_mfma;  // q R on the MFMA also for rows of <= 32 kept channels
   float scale_log2;
@@ -799,10 +800,11 @@ decode_kernel(const DecodeArgs a) {
       // q R (16 head rows x DKP columns) over the four 32-channel steps.
       // A = q (16-bit values, exact), B = R columns read from LDS (columns
       // past Dk zero); the products are exact and summed in fp32.  Taken
-      // for 33-64 kept channels (config 4 at keep 64: 664 -> 618 us per
+      // for 33-128 kept channels (config 4 at keep 64: 664 -> 618 us per
       // step at 4097 visual tokens, 1035 -> 990 at 12001); with one block of
       // 32 (only waves 0 and 1 busy) it measured 2-3 % slower at 12001
-      // tokens, so those keep the FMA form below.
+      // tokens, so those keep the FMA form below except in one-per-CU
+      // plans (qr_mfma, set by the host).
       const uint16_t* rl = (const uint16_t*)s_r;
       const int dk1 = max(a.Dk - 1, 0);
       const bool hrow = n < HMAX;  // HMAX = 1: the other A rows are zero
