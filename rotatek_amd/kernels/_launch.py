@@ -28,15 +28,21 @@ def rotatek_decode(q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_spa
                                 v_sparse)]
     out = torch.empty((bsz, heads, head_dim), dtype=q_full.dtype, device=q_full.device)
     do = _lib.desc(out)
-    need = ctypes.c_size_t(0)
-    _lib.check(lib.rk_rotatek_decode_check(*[_lib.ref(x) for x in d], int(num_kv_groups),
-                                           ctypes.byref(do), policy, 0, ctypes.byref(need)),
-               "rotatek_decode")
-    ws = _lib.workspace(q_full.device, need.value)
-    _lib.check(lib.rk_rotatek_decode(*[_lib.ref(x) for x in d], int(num_kv_groups), ctypes.byref(do),
-                                     policy, ws.data_ptr(), ws.numel(),
-                                     _lib.stream_handle(q_full.device)),
-               "rotatek_decode")
+    refs = [_lib.ref(x) for x in d]
+
+    def launch(ws):
+        return lib.rk_rotatek_decode(*refs, int(num_kv_groups), ctypes.byref(do), policy, ws.data_ptr(),
+                                     ws.numel(), _lib.stream_handle(q_full.device))
+
+    # the cached workspace first (the entry validates everything and checks
+    # its size before it launches); sized by the query only when it is short
+    st = launch(_lib.workspace(q_full.device, 0))
+    if st == _lib.RK_ERR_WORKSPACE:
+        need = ctypes.c_size_t(0)
+        _lib.check(lib.rk_rotatek_decode_check(*refs, int(num_kv_groups), ctypes.byref(do), policy, 0,
+                                               ctypes.byref(need)), "rotatek_decode")
+        st = launch(_lib.workspace(q_full.device, need.value))
+    _lib.check(st, "rotatek_decode")
     return out
 
 
@@ -47,16 +53,19 @@ def full_channel_decode(q, k, v, num_kv_groups: int, policy: int) -> torch.Tenso
     dq, dk, dv = _lib.desc(q), _lib.desc(k), _lib.desc(v)
     out = torch.empty((bsz, heads, head_dim), dtype=q.dtype, device=q.device)
     do = _lib.desc(out)
-    need = ctypes.c_size_t(0)
-    _lib.check(lib.rk_full_channel_decode_check(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv),
-                                                int(num_kv_groups), ctypes.byref(do), policy, 0,
-                                                ctypes.byref(need)),
-               "full_channel_decode")
-    ws = _lib.workspace(q.device, need.value)
-    _lib.check(lib.rk_full_channel_decode(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv),
-                                          int(num_kv_groups), ctypes.byref(do), policy, ws.data_ptr(),
-                                          ws.numel(), _lib.stream_handle(q.device)),
-               "full_channel_decode")
+    refs = (ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv))
+
+    def launch(ws):
+        return lib.rk_full_channel_decode(*refs, int(num_kv_groups), ctypes.byref(do), policy, ws.data_ptr(),
+                                          ws.numel(), _lib.stream_handle(q.device))
+
+    st = launch(_lib.workspace(q.device, 0))
+    if st == _lib.RK_ERR_WORKSPACE:
+        need = ctypes.c_size_t(0)
+        _lib.check(lib.rk_full_channel_decode_check(*refs, int(num_kv_groups), ctypes.byref(do), policy, 0,
+                                                    ctypes.byref(need)), "full_channel_decode")
+        st = launch(_lib.workspace(q.device, need.value))
+    _lib.check(st, "full_channel_decode")
     return out
 
 
@@ -83,16 +92,22 @@ def rotatek_decode_varlen(q_full, R_partial, delta_mu, k_full, v_buf, v_gap_at: 
     if out is None:
         out = torch.empty(q_full.shape, dtype=q_full.dtype, device=q_full.device)
     do = _lib.desc(out)
-    need = varlen_workspace_bytes(q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse, v_sparse,
-                                  num_kv_groups, policy)
-    ws = _lib.workspace(q_full.device, need)
     dkn, dvn = _lib.desc(k_new), _lib.desc(v_new)
-    _lib.check(lib.rk_rotatek_decode_varlen(*[_lib.ref(x) for x in d[:5]], int(v_gap_at), int(v_gap),
-                                            *[_lib.ref(x) for x in d[5:]], int(num_kv_groups),
-                                            _lib.ref(dkn), _lib.ref(dvn), len_full.data_ptr(),
-                                            ctypes.byref(do), policy, ws.data_ptr(),
-                                            ws.numel(), _lib.stream_handle(q_full.device)),
-               "rotatek_decode_varlen")
+    head, tail = [_lib.ref(x) for x in d[:5]], [_lib.ref(x) for x in d[5:]]
+
+    def launch(ws):
+        return lib.rk_rotatek_decode_varlen(*head, int(v_gap_at), int(v_gap), *tail, int(num_kv_groups),
+                                            _lib.ref(dkn), _lib.ref(dvn), len_full.data_ptr(), ctypes.byref(do),
+                                            policy, ws.data_ptr(), ws.numel(), _lib.stream_handle(q_full.device))
+
+    # the cached workspace first (a captured step finds it pre-sized); sized
+    # by the query only when it is short
+    st = launch(_lib.workspace(q_full.device, 0))
+    if st == _lib.RK_ERR_WORKSPACE:
+        need = varlen_workspace_bytes(q_full, R_partial, delta_mu, k_full, v_buf, mask_full, k_sparse,
+                                      v_sparse, num_kv_groups, policy)
+        st = launch(_lib.workspace(q_full.device, need))
+    _lib.check(st, "rotatek_decode_varlen")
     return out
 
 

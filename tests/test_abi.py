@@ -42,6 +42,42 @@ def test_abi_version_and_strerror():
     assert _lib.strerror(-999) == "unknown status"
 
 
+def test_descriptor_matches_the_header_layout():
+    """desc() packs rk_tensor in one step: its bytes equal a field-by-field
+    fill (data, dtype code, ndim, then shape and element strides, zeros past
+    ndim) for every rank, dtype, view and empty tensor; a NULL data pointer
+    for empty tensors; rank > 4 and unknown dtypes raise ValueError."""
+    import torch
+
+    assert ctypes.sizeof(_lib.RkTensor) == 80
+    n = 0
+    for dt in (torch.float16, torch.bfloat16, torch.float32, torch.float64, torch.uint8, torch.int32,
+               torch.int64):
+        for shape in [(), (5,), (3, 4), (2, 3, 4), (2, 3, 4, 5), (0, 4), (2, 0, 3, 1)]:
+            t = torch.zeros(shape, dtype=dt)
+            views = [t]
+            if t.dim() > 1:
+                views.append(t.transpose(0, -1))
+            if t.dim() > 0 and t.shape[-1] > 1:
+                views.append(t[..., ::2])
+            for v in views:
+                want = _lib.RkTensor()
+                want.data = v.data_ptr() if v.numel() > 0 else 0
+                want.dtype = _lib._DTYPES[dt]
+                want.ndim = v.dim()
+                for i in range(v.dim()):
+                    want.shape[i] = v.shape[i]
+                    want.stride[i] = v.stride(i)
+                assert bytes(_lib.desc(v)) == bytes(want), (dt, shape, v.stride())
+                n += 1
+    assert n > 100
+    assert _lib.desc(None) is None
+    with pytest.raises(ValueError):
+        _lib.desc(torch.zeros(1, 1, 1, 1, 1))
+    with pytest.raises(ValueError):
+        _lib.desc(torch.zeros(2, dtype=torch.complex64))
+
+
 def _t(shape, dtype=_lib.RK_F16, strides=None):
     d = _lib.RkTensor()
     d.data = 0
