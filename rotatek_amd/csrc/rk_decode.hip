@@ -1481,7 +1481,9 @@ int split_plan(rk_decode_plan& p, int64_t Dk, int64_t S_v, int64_t S_f, int32_t 
   // ... and enough rounds for kMinWgsPerUnit workgroups per unit: with many
   // units a single round leaves each unit one or two workgroups of several
   // MB (measured on MI355X, B=32 with 8 KV heads of 4 query heads: 228 us
-  // at 2-3 workgroups per unit, 216 us at 7)
+  // at 2-3 workgroups per unit, 216 us at 7; a floor of 12 or 16 instead of
+  // 8 measured slower: that shape 210 -> 218-220 us, config 3 110 -> 114,
+  // config 2 811 -> 817)
   const int64_t by_units = cdiv(kMinWgsPerUnit * p.units, slots);
   if (rounds < by_units && total / (by_units * slots) >= k.min_wg) rounds = by_units;
   if (rounds < 1) rounds = 1;
