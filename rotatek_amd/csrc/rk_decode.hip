@@ -1347,6 +1347,7 @@ constexpr int64_t kSkewMaxBytes = INT64_C(128) << 10;
 // then folds half the records) gain up to larger workgroups.
 constexpr int64_t kOneSlotMaxBytes = INT64_C(128) << 10;
 constexpr int64_t kOneSlotMaxBytesOneHead = INT64_C(192) << 10;
+constexpr int64_t kOneSlotMaxBytesOneHeadNarrow = INT64_C(256) << 10;  // <= 32 kept channels
 
 // Merge mode (rk_set_decode_merge): 0 (default) = per shape (below),
 // 1 = two launches,
@@ -1610,11 +1611,14 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   // slots are 1-2 % faster (8001 tokens: 23.8 against 24.1), and where one
   // slot per CU needs a second round they are faster still (B=16, 2049
   // tokens: 21.2 against 22.5).  Units of one query head gain up to
-  // ~240 KB at 32 kept channels (B=1, 32 heads, 640 prompt/text tokens,
-  // 6000 / 8000 / 11000 visual tokens: 22.2 -> 20.4, 23.9 -> 22.8, 28.4 ->
-  // 27.5 us) but lose at 209 KB with 64 (24.7 against 25.2), so their bound
-  // is 192 KB.
-  const int64_t one_slot_max = p.heads_per_unit == 1 ? kOneSlotMaxBytesOneHead : kOneSlotMaxBytes;
+  // 256 KB at <= 32 kept channels (B=1, 32 heads, 640 prompt/text tokens,
+  // 6000 / 8000 visual tokens: 22.2 -> 20.4, 23.9 -> 22.8 us; with the
+  // one-per-CU MFMA q R, 10000 / 11000 / 12000: 26.6 -> 24.9, 27.2 ->
+  // 26.4, 28.2 -> 27.7 us; 13000, 277 KB, loses: 29.5 against 31.6) but
+  // lose at 209 KB with 64 (24.7 against 25.2), so theirs is 192 KB.
+  const int64_t one_slot_max = p.heads_per_unit > 1 ? kOneSlotMaxBytes
+                               : Dk <= 32            ? kOneSlotMaxBytesOneHeadNarrow
+                                                     : kOneSlotMaxBytesOneHead;
   if (k.wgs_per_cu == 0 && p.chunk_major && S_v * (Dk + 128) * elem_bytes <= p.wg_vis * one_slot_max) {
     rk_decode_plan one = units_only;
     if (split_plan(one, Dk, S_v, S_f, elem_bytes, num_cus, num_cus, k) == RK_OK && one.chunk_major &&

@@ -631,9 +631,12 @@ def test_plan_one_workgroup_per_cu_for_small_short_rounds():
         assert p["chunk_major"] == 1 and p["n_fast"] == 0 and p["grid"] == 256, (keep, p)
     p = _lib.plan_decode(1, 32, 32, 32, 4000, 640, policy=0)
     assert p["chunk_major"] == 1 and p["grid"] == 256 and p["single_launch"] == 1
-    # units of one query head take one workgroup per CU up to 192 KB two-slot
-    # chunks (8000 tokens: 177 KB), not at 209 KB (keep 64, 8000 tokens)
+    # units of one query head take one workgroup per CU up to 256 KB two-slot
+    # chunks at <= 32 kept channels (8000 / 12000 tokens: 177 / 256 KB, not
+    # 13000: 277 KB), up to 192 KB with more (keep 64, 8000 tokens: 209 KB)
     assert _lib.plan_decode(1, 32, 32, 32, 8000, 640, policy=0)["grid"] == 256
+    assert _lib.plan_decode(1, 32, 32, 32, 12000, 640, policy=0)["grid"] == 256
+    assert _lib.plan_decode(1, 32, 32, 32, 13000, 640, policy=0)["grid"] == 512
     assert _lib.plan_decode(1, 32, 32, 64, 8000, 640, policy=0)["grid"] == 512
     assert _lib.plan_decode(8, 28, 4, 32, 8001, 61, policy=1)["grid"] == 512   # GQA, 159 KB
     # fp32 (the VALU kernel): one workgroup per CU wherever that is still one

@@ -86,6 +86,7 @@ CASES = [
     (2, 8, 8, 16, 3001, 129, torch.bfloat16, "paper", (1, False, False)),  # 208 workgroups: one per CU
     (2, 16, 16, 32, 2500, 60, torch.float16, "paper", (1, True, True)),   # 416 workgroups of <= 128 KB
     (1, 32, 32, 32, 8000, 640, torch.float16, "paper", (1, False, True)),  # one-head units, 177 KB: one per CU
+    (1, 32, 32, 32, 12000, 640, torch.bfloat16, "paper", (1, False, True)),  # ... 256 KB at <= 32 channels
 ]
 
 
