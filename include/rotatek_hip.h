@@ -129,12 +129,15 @@ int rk_device_cu_count(int device, int* status);
  * delta_mu may be F16, BF16 or F32.
  * The workspace (size from rk_rotatek_decode_check, 256-byte aligned) holds
  * the split partials and, in its first RK_DECODE_TICKET_BYTES, the
- * counters of the single-launch merge; pass a new workspace through
- * rk_decode_workspace_init once before its first use (every call leaves
- * the counters at zero again).  A step is two launches on `stream` (split
- * kernel, merge kernel), or one (see rk_set_decode_merge), and is
- * hipGraph-capturable.  Calls that overlap on one
- * workspace race.  policy RK_POLICY_PAPER with num_kv_groups > 1 runs the
+ * counters of the single-launch merge.  Every call leaves the counters at
+ * zero.  A workspace the library has not seen (by its address) gets them
+ * zeroed by a fill kernel on `stream` ahead of its first single-launch
+ * decode; rk_decode_workspace_init does the same explicitly, and
+ * rk_decode_workspace_release forgets an address (call it before the
+ * memory is freed or reused for anything else).  A step is two launches
+ * on `stream` (split kernel, merge kernel), or one (see
+ * rk_set_decode_merge), and is hipGraph-capturable.  Calls that overlap
+ * on one workspace race.  policy RK_POLICY_PAPER with num_kv_groups > 1 runs the
  * grouped decomposition (each K/V tile read once per KV head; the result
  * differs from one unit per query head only in fp32 summation order).
  */
@@ -243,16 +246,22 @@ int rk_full_channel_decode(const rk_tensor* q, const rk_tensor* k,
 
 /* Bytes at the start of a decode workspace that hold the single-launch
  * merge's counters; rk_decode_workspace_init zeroes them (a kernel on
- * `stream`, not a memset, so it may also be recorded in a graph). */
+ * `stream`, not a memset, so it may also be recorded in a graph) and marks
+ * the workspace as initialised.  No counterpart in the reference (its
+ * Triton launches need no counters).  rk_decode_workspace_release drops
+ * that mark, so the next decode on the address initialises it again. */
 #define RK_DECODE_TICKET_BYTES (256u * 1024u)
 int rk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream);
+void rk_decode_workspace_release(void* workspace);
 
 /* Merge of the decode entry points: 1 = two launches (split kernel, then a
  * merge kernel), 2 = one launch (the last split workgroup of each unit
  * merges, behind a counter in the workspace's ticket region) whenever the
  * counters fit, 0 (default) = one launch for a single round of workgroups
  * with one query head per unit, else two (what measured faster on
- * MI355X).  Both give bit-identical results. */
+ * MI355X).  Both give bit-identical results.  The one-launch merge relies
+ * on the cross-XCD store/load coherence of gfx942 / gfx950; on any other
+ * device every mode runs two launches. */
 void rk_set_decode_merge(int32_t mode);
 
 /* Split plan the decode entry points use for a shape (host only), exposed

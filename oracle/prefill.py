@@ -84,7 +84,8 @@ def query_weight(cov, queries, num_kv_groups: int, window: int = QUERY_WINDOW,
     fp32 norm, as torch's ``mean`` on a bf16 tensor is), weights cov by outer(||q||, ||q||) with a floor of
     1e-3 * median (lower middle element for an even count, as torch.median),
     symmetrises and adds ridge = 1e-4 * max(mean|diag|, 1e-6) * I (the clamp
-    applies to the mean, kv_pruning_utils.py:137-139).
+    applies to the mean, kv_pruning_utils.py:137-139).  A NaN norm makes the
+    median, hence every weight of the head, NaN (torch.median semantics).
     """
     cov = np.asarray(cov, np.float64)
     Q = np.asarray(queries, np.float64)
@@ -109,6 +110,9 @@ def query_weight(cov, queries, num_kv_groups: int, window: int = QUERY_WINDOW,
             Qr = grp.mean(axis=2)
     qn = np.sqrt((Qr ** 2).sum(axis=-2))                           # [B,Hkv,D]
     med = np.sort(qn, axis=-1)[..., (D - 1) // 2]                  # lower median
+    # torch.median of a row holding a NaN is NaN (torch.nanmedian is the
+    # NaN-skipping one), and the clamp against a NaN floor is NaN
+    med = np.where(np.isnan(qn).any(axis=-1), np.nan, med)
     qn = np.maximum(qn, 1e-3 * med[..., None])
     cov = cov * (qn[..., :, None] * qn[..., None, :])
     cov = 0.5 * (cov + np.swapaxes(cov, -1, -2))

@@ -99,6 +99,7 @@ _SIGNATURES = {
     "rk_set_decode_chunk_align": (None, [ctypes.c_int32]),
     "rk_set_decode_skew": (None, [ctypes.c_int32]),
     "rk_decode_workspace_init": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
+    "rk_decode_workspace_release": (None, [ctypes.c_void_p]),
     "rk_key_covariance_check": (ctypes.c_int, [_P, _P, _P, ctypes.c_int32, ctypes.POINTER(ctypes.c_size_t)]),
     "rk_key_covariance": (ctypes.c_int, [_P, _P, _P, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]),
     "rk_key_covariance_weighted_check": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int32, _P, _P,

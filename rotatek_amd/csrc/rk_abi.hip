@@ -1,6 +1,7 @@
 // rk_abi.hip -- library-wide C ABI entry points: status strings, ABI
 // version and the per-device compute-unit cache used by the split planner.
 #include <hip/hip_runtime.h>
+#include <string.h>
 
 #include "rk_host.h"
 #include "rotatek_hip.h"
@@ -17,6 +18,18 @@ int current_device_cus(int* device_out) {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
   if (dev < 64) cache[dev] = cus;
   return cus;
+}
+
+bool device_has_coherent_tickets() {
+  static int cache[64] = {0};  // 0 unknown, 1 yes, 2 no
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return false;
+  if (dev < 64 && cache[dev] != 0) return cache[dev] == 1;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return false;
+  const bool ok = strncmp(prop.gcnArchName, "gfx942", 6) == 0 || strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  if (dev < 64) cache[dev] = ok ? 1 : 2;
+  return ok;
 }
 
 }  // namespace rk

@@ -9,6 +9,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <unordered_set>
 
 #include "rk_common.h"
 #include "rk_decode.h"
@@ -132,6 +133,26 @@ __global__ void __launch_bounds__(256) zero_words_kernel(uint32_t* p, int64_t n)
     p[i] = 0u;
 }
 
+// Workspaces whose ticket region has been zeroed (rk_decode_workspace_init,
+// or a decode entry's first single-launch use of a workspace it had not
+// seen).  Every call leaves the counters at zero, so a registered
+// workspace stays ready; rk_decode_workspace_release forgets one.
+std::mutex g_ws_mu;
+std::unordered_set<uintptr_t> g_ws_ready;
+
+void mark_ready(void* ws, bool ready) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  if (ready)
+    g_ws_ready.insert((uintptr_t)ws);
+  else
+    g_ws_ready.erase((uintptr_t)ws);
+}
+
+bool is_ready(void* ws) {
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  return g_ws_ready.count((uintptr_t)ws) != 0;
+}
+
 }  // namespace
 
 extern "C" int rk_decode_workspace_init(void* workspace, size_t workspace_bytes, void* stream) {
@@ -141,7 +162,18 @@ extern "C" int rk_decode_workspace_init(void* workspace, size_t workspace_bytes,
   if (n == 0) return RK_OK;
   hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, (hipStream_t)stream, (uint32_t*)workspace,
                      (int64_t)n);
-  return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
+  if (hipGetLastError() != hipSuccess) return RK_ERR_HIP;
+  // under stream capture the fill only runs when the graph is replayed (and
+  // then before every replay's decode), so the address is not marked: the
+  // next eager call initialises it again
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) return RK_ERR_HIP;
+  if (n * 4 == RK_DECODE_TICKET_BYTES && cs == hipStreamCaptureStatusNone) mark_ready(workspace, true);
+  return RK_OK;
+}
+
+extern "C" void rk_decode_workspace_release(void* workspace) {
+  if (workspace) mark_ready(workspace, false);
 }
 
 extern "C" void rk_set_decode_merge(int32_t mode) {
@@ -360,6 +392,17 @@ struct Checked {
   int dtype;
 };
 
+// A [B, H, S, D] K/V descriptor the kernels can address: the whole
+// within-head span, plus 32 rows, below 2^31 elements (kernel offsets are
+// 32-bit byte offsets; the visual ring adds a block's row offsets to its
+// first row before clamping to the chunk's last row) and the token stride
+// below 2^26.
+bool head_span_ok(const rk_tensor* t) {
+  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1 + 32) * t->stride[2] : 0) +
+                       (t->shape[3] > 0 ? (t->shape[3] - 1) * t->stride[3] : 0) + 8;
+  return span < (INT64_C(1) << 31) && t->stride[2] < (INT64_C(1) << 26) && t->stride[3] < (INT64_C(1) << 31);
+}
+
 int check_out(const rk_tensor* out, const Checked& c) {
   int st = rk::check_desc(out, 3);
   if (st) return st;
@@ -422,6 +465,8 @@ int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
   if ((st = check_kv4(vf, *c, c->S_f, 128, true))) return st;
   if ((st = check_kv4(ks, *c, c->S_v, c->Dk, true))) return st;
   if ((st = check_kv4(vs, *c, c->S_v, 128, true))) return st;
+  if (!head_span_ok(kf) || !head_span_ok(vf) || !head_span_ok(vs) || (c->Dk > 0 && !head_span_ok(ks)))
+    return RK_ERR_STRIDE;
   if (mask) {
     st = rk::check_desc(mask, 2);
     if (st) return st;
@@ -477,19 +522,12 @@ void set4(const rk_tensor* t, int64_t& s0, int64_t& s1, int64_t& s2, int64_t& s3
   s3 = t->stride[3];
 }
 
-// Head strides (b, h) as int64; token/channel strides as uint32 with the
-// whole within-head span, plus 32 rows, below 2^31 elements (kernel offsets
-// are 32-bit byte offsets) and the token stride below 2^26.
+// Head strides (b, h) as int64; token/channel strides as uint32 (bounds
+// checked by head_span_ok during validation).
 bool set_head(const rk_tensor* t, int64_t& sb, int64_t& sh, uint32_t& ss, uint32_t& sd) {
+  if (!head_span_ok(t)) return false;
   sb = t->stride[0];
   sh = t->stride[1];
-  // (32 rows of slack: the visual ring adds a block's row offsets to its
-  // first row before clamping to the chunk's last row)
-  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1 + 32) * t->stride[2] : 0) +
-                       (t->shape[3] > 0 ? (t->shape[3] - 1) * t->stride[3] : 0) + 8;
-  if (span >= (INT64_C(1) << 31) || t->stride[2] >= (INT64_C(1) << 26) ||
-      t->stride[3] >= (INT64_C(1) << 31))
-    return false;
   ss = (uint32_t)t->stride[2];
   sd = (uint32_t)t->stride[3];
   return true;
@@ -523,7 +561,8 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   a.part = (float*)((char*)ws + w.part);
   a.ticket = (uint32_t*)((char*)ws + w.ticket);
   a.bticket = (uint32_t*)((char*)ws + w.bticket);
-  a.fused = p.single_launch;
+  // the single-launch merge's ordering holds on gfx942 / gfx950 only
+  a.fused = p.single_launch && rk::device_has_coherent_tickets() ? 1 : 0;
   a.q_sb = q->stride[0];
   a.q_sh = q->stride[1];
   a.q_sd = q->stride[2];
@@ -638,6 +677,13 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   // 535.2; at 12001 tokens (two slots) 864.1 -> 875.9 with the MFMA form.
   a.qr_mfma = dkb == 1 && a.cmajor && p.grid <= cus ? 1 : 0;
   hipStream_t s = (hipStream_t)stream;
+  // a workspace this library has not initialised gets zeroed counters first
+  // (a fill kernel on the same stream; under graph capture it is recorded
+  // with the decode)
+  if (a.fused && !is_ready(ws)) {
+    const int st0 = rk_decode_workspace_init(ws, RK_DECODE_TICKET_BYTES, stream);
+    if (st0) return st0;
+  }
   if (c.dtype == RK_F32) {
     const bool v32 = vec32_ok(kf) && vec32_ok(vf) &&
                      (!has_vis || ((c.Dk == 0 || vec32_ok(ks)) && vec32_ok(vs) && c.Dk % 4 == 0));
@@ -703,6 +749,7 @@ extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor
   const int64_t S_f = k_full->shape[2];
   if (v_gap < 0 || v_gap_at < 0 || v_gap_at > S_f || v_gap >= (INT64_C(1) << 31)) return RK_ERR_ARG;
   if (v_buf->shape[2] != S_f + v_gap) return RK_ERR_SHAPE;
+  if (!head_span_ok(v_buf)) return RK_ERR_STRIDE;
   rk_tensor v_logical = *v_buf;  // prompt/text rows only, for the shape checks
   v_logical.shape[2] = S_f;
   Checked c;
@@ -812,6 +859,7 @@ int check_dense(const rk_tensor* q, const rk_tensor* k, const rk_tensor* v, int6
   if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
   if ((st = check_kv4(k, *c, c->S_f, 128, true))) return st;
   if ((st = check_kv4(v, *c, c->S_f, 128, true))) return st;
+  if (!head_span_ok(k) || !head_span_ok(v)) return RK_ERR_STRIDE;
   return RK_OK;
 }
 
@@ -861,10 +909,10 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];
 
-// This device's `scratch`: on the first call on a device, its address
-// (checked) and a cleared ticket region (a fill kernel on `stream`, ahead
-// of the decode that follows on the same stream).
-int device_scratch(hipStream_t stream, void** ptr) {
+// This device's `scratch`: its address, taken (and checked) on the first
+// call on the device and kept per device.  Its ticket region is zeroed like
+// any workspace the library has not initialised (run_decode).
+int device_scratch(void** ptr) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return RK_ERR_NO_DEVICE;
   if (dev >= kMaxDevices) return RK_ERR_ARG;
@@ -872,8 +920,6 @@ int device_scratch(hipStream_t stream, void** ptr) {
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return RK_ERR_HIP;
-    const int st = rk_decode_workspace_init(p, RK_DECODE_TICKET_BYTES, stream);
-    if (st) return st;
     g_scratch_ptr[dev] = p;
   }
   *ptr = g_scratch_ptr[dev];
@@ -902,7 +948,7 @@ extern "C" int rk_rotatek_decode_noalloc(const rk_tensor* q_full, const rk_tenso
   if ((st = plan_for(c, true, pol, cus, &p))) return st;
   if (p.workspace_bytes > RK_NOALLOC_SCRATCH_BYTES) return RK_ERR_SCRATCH;
   void* ws = nullptr;
-  if ((st = device_scratch((hipStream_t)stream, &ws))) return st;
+  if ((st = device_scratch(&ws))) return st;
   return run_decode(c, q_full, R_partial, delta_mu, k_full, v_full, mask_full, k_sparse, v_sparse, out, pol,
                     ws, RK_NOALLOC_SCRATCH_BYTES, stream, true);
 }

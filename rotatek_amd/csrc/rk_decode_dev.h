@@ -435,26 +435,48 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int 
 // Single-launch merge, run by every workgroup after it has stored its
 // record.  The workgroup waits until its record stores have completed
 // (they write through to memory), then takes a ticket on the unit's
-// counter; the last of the unit's np workgroups resets the counter and
-// merges the unit's records, read with coherent loads, in the order of
-// the merge kernel (merge_unit; the result is bit-identical to the
-// two-launch merge).  No
-// agent-scope release or acquire fence is needed, so no XCD L2 is written
-// back or invalidated.  With a fused append, the last unit of a batch row
-// to finish advances len_full[b] behind a second ticket: by then every
-// workgroup of the row has read it.  Both counters are left at zero.
+// counter; the last of the unit's np workgroups merges the unit's records,
+// read with coherent loads, in the order of the merge kernel (merge_unit;
+// the result is bit-identical to the two-launch merge).  No agent-scope
+// release or acquire fence is needed, so no XCD L2 is written back or
+// invalidated.  With a fused append, the last unit of a batch row to finish
+// advances len_full[b] behind a second ticket: by then every workgroup of
+// the row has read it.
+//
+// Tickets are atomic increments that wrap to zero at n - 1 (the hardware's
+// inc: old >= n - 1 ? 0 : old + 1), so the last arrival's increment is also
+// the reset and every call leaves both counters at zero with no second
+// store.  A counter holding anything else (a workspace that was never
+// initialised) would misplace the merge, which is why the host initialises
+// every workspace it has not seen before its first use.
+//
+// What this relies on, on gfx942 / gfx950 (the only targets that compile
+// it; the host never selects it elsewhere):
+//   * relaxed agent-scope atomic stores compile to global stores with the
+//     sc1 bit, which write through the XCD's L2 to the memory-side
+//     coherence point, and relaxed agent-scope atomic loads to sc1 loads,
+//     which read from that point, not from a possibly stale L2 line;
+//   * vmcnt counts stores on these targets (there is no separate store
+//     counter), so s_waitcnt vmcnt(0) returns only once the thread's
+//     write-through stores are acknowledged; the workgroup barrier then
+//     orders every thread's completed stores before the ticket;
+//   * agent-scope atomics on the ticket are performed at the coherence
+//     point, so the workgroup that sees n - 1 is the last of the unit, and
+//     its record loads, issued after the ticket returns (a dependency
+//     through LDS and a barrier), see every other record;
+//   * the signal fence keeps the compiler from moving the record stores
+//     past the wait.
 template <class TT, bool APPEND>
 __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, int h0, int nh, int tid,
                                             float* s_mrg) {
+#if defined(__gfx942__) || defined(__gfx950__) || !defined(__HIP_DEVICE_COMPILE__)
   __shared__ uint32_t s_ticket;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores have completed
   __syncthreads();                // ... and so have every thread's
-  if (tid == 0)
-    s_ticket = __hip_atomic_fetch_add(a.ticket + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) s_ticket = __builtin_amdgcn_atomic_inc32(a.ticket + u, (uint32_t)(a.np - 1), __ATOMIC_RELAXED, "agent");
   __syncthreads();
   if (s_ticket != (uint32_t)(a.np - 1)) return;
-  if (tid == 0) __hip_atomic_store(a.ticket + u, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (a.hpu == 1) {
     if (tid < 16) merge_slice<TT, true>(a, u, b, h0, tid);
   } else {
@@ -462,14 +484,14 @@ __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, i
   }
   if constexpr (APPEND) {
     if (tid == 0) {
-      const uint32_t t = __hip_atomic_fetch_add(a.bticket + b, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (t == (uint32_t)(a.units_per_b - 1)) {
-        __hip_atomic_store(a.bticket + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t last = (uint32_t)(a.units_per_b - 1);
+      if (__builtin_amdgcn_atomic_inc32(a.bticket + b, last, __ATOMIC_RELAXED, "agent") == last) {
         const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
         if (pos < a.S_f) a.len_full[b] = pos + 1;
       }
     }
   }
+#endif
 }
 
 // APPEND: fused append of k_new / v_new (span cache decode step); a

@@ -70,4 +70,9 @@ inline bool vec_ok(const rk_tensor* t) {
 // CU count of the current HIP device (cached per device); 0 on failure.
 int current_device_cus(int* device_out);
 
+// Whether the current device is gfx942 or gfx950, whose write-through
+// agent-scope stores and coherent agent-scope loads the single-launch
+// decode merge relies on (cached per device; false on failure).
+bool device_has_coherent_tickets();
+
 }  // namespace rk

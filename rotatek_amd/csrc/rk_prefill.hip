@@ -645,10 +645,18 @@ __device__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g
 #pragma unroll
       for (int e = 0; e < 4; ++e) rank += (uu[e] < v) || (uu[e] == v && 4 * j4 + e < tid);
     }
-    if (rank == 63) *s_floor = 1e-3f * v;
+    if (rank == 63) *s_floor = 1e-3f * v;  // exactly one thread when no norm is NaN
   }
   __syncthreads();
-  if (tid < 128) s_qn[tid] = fmaxf(v, *s_floor);
+  // torch.median of a row holding a NaN is NaN, and so is the clamp against
+  // it: every weight of the head becomes NaN (written after the ranks, which
+  // a NaN leaves without a thread of rank 63)
+  if (tid < 128 && isnan(v)) *s_floor = __builtin_nanf("");
+  __syncthreads();
+  if (tid < 128) {
+    const float fl = *s_floor;
+    s_qn[tid] = isnan(fl) ? fl : fmaxf(v, fl);
+  }
   __syncthreads();
 }
 

@@ -134,6 +134,54 @@ def test_rotatek_check_errors(kw, code):
     assert st == code, (st, _lib.strerror(st))
 
 
+@pytest.mark.parametrize("which,ss", [
+    ("v_sparse", ((1 << 31) - 8 - 127) // (63 + 32) + 1),  # span fits 2^31, span + 32 rows does not
+    ("k_sparse", 1 << 26),                                   # token stride at the bound
+    ("k_full", 1 << 26),
+    ("v_full", ((1 << 31) - 8 - 127) // (15 + 32) + 1),
+])
+def test_rotatek_check_refuses_strides_beyond_32bit_offsets(which, ss):
+    """A K/V descriptor whose within-head span plus 32 rows reaches 2^31
+    elements, or whose token stride reaches 2^26, is refused with
+    RK_ERR_STRIDE by the host-side check (the kernels form 32-bit byte
+    offsets of rows up to 31 past a block's first row before clamping
+    them), so the launching entry, which runs the same validation first,
+    never launches such a call."""
+    B, Hq, Hkv, D, Dk, S_v, S_f = 1, 4, 4, 128, 32, 64, 16
+    names = ("q_full", "R_partial", "delta_mu", "k_full", "v_full", "mask_full", "k_sparse", "v_sparse")
+    shapes = dict(q_full=(B, Hq, D), R_partial=(B, Hkv, D, Dk), delta_mu=(B, Hkv, D), k_full=(B, Hkv, S_f, D),
+                  v_full=(B, Hkv, S_f, D), mask_full=(B, S_f), k_sparse=(B, Hkv, S_v, Dk),
+                  v_sparse=(B, Hkv, S_v, D))
+    d = {k: _t(shapes[k], _lib.RK_U8 if k == "mask_full" else _lib.RK_F16) for k in names}
+    t = d[which]
+    t.stride[2] = ss
+    t.stride[1] = ss * t.shape[2]
+    t.stride[0] = t.stride[1] * t.shape[1]
+    o = _t((B, Hq, D))
+    need = ctypes.c_size_t(0)
+    st = _lib.load().rk_rotatek_decode_check(*[ctypes.byref(d[k]) for k in names], 1, ctypes.byref(o), 0, 256,
+                                             ctypes.byref(need))
+    assert st == _lib.RK_ERR_STRIDE, _lib.strerror(st)
+    # one element of stride less (v_sparse: the largest span that fits) is accepted
+    if which == "v_sparse":
+        t.stride[2] = ss - 1
+        t.stride[1] = t.stride[2] * t.shape[2]
+        t.stride[0] = t.stride[1] * t.shape[1]
+        st = _lib.load().rk_rotatek_decode_check(*[ctypes.byref(d[k]) for k in names], 1, ctypes.byref(o), 0,
+                                                 256, ctypes.byref(need))
+        assert st == 0, _lib.strerror(st)
+
+
+def test_dense_check_refuses_strides_beyond_32bit_offsets():
+    q, o = _t((1, 4, 128)), _t((1, 4, 128))
+    k = _t((1, 4, 16, 128), strides=(4 * 16 << 26, 16 << 26, 1 << 26, 1))
+    v = _t((1, 4, 16, 128))
+    need = ctypes.c_size_t(0)
+    st = _lib.load().rk_full_channel_decode_check(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), 1,
+                                                  ctypes.byref(o), 0, 256, ctypes.byref(need))
+    assert st == _lib.RK_ERR_STRIDE, _lib.strerror(st)
+
+
 def test_rotatek_check_fp32():
     """fp32 q/K/V/out (the reference's kernels accept it) plan one unit per
     query head; mixing fp32 q with 16-bit K/V is a dtype error."""

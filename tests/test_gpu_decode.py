@@ -198,37 +198,6 @@ def test_repeated_calls_are_bitwise_stable():
         assert torch.equal(_decode(inp, "gqa"), a)
 
 
-@pytest.mark.parametrize("which,ss", [
-    ("v_sparse", ((1 << 31) - 8 - 127) // (63 + 32) + 1),  # span fits 2^31, span + 32 rows does not
-    ("k_sparse", 1 << 26),                                   # token stride at the bound
-])
-def test_visual_strides_beyond_32bit_offsets_are_refused(which, ss):
-    """A visual Key or Value descriptor whose within-head span plus 32 rows
-    reaches 2^31 elements, or whose token stride reaches 2^26, is refused
-    with RK_ERR_STRIDE before any launch: the visual ring forms 32-bit byte
-    offsets of rows up to 31 past a block's first row before clamping them.
-    The enlarged strides exist only in the descriptor and are never
-    dereferenced (the call returns at validation)."""
-    import ctypes
-
-    from rotatek_amd import _lib
-    _say(f"stride bound {which} ss={ss}")
-    inp = _rand_inputs(1, 4, 4, 32, 64, 16, torch.float16, seed=4)
-    names = ("q_full", "R_partial", "delta_mu", "k_full", "v_full", "mask_full", "k_sparse", "v_sparse")
-    d = [_lib.desc(inp[k]) for k in names]
-    d[names.index(which)].stride[2] = ss
-    out = torch.empty(1, 4, 128, dtype=torch.float16, device="cuda")
-    do = _lib.desc(out)
-    lib = _lib.load()
-    need = ctypes.c_size_t(0)
-    assert lib.rk_rotatek_decode_check(*[_lib.ref(x) for x in d], 1, ctypes.byref(do), 0, 0,
-                                       ctypes.byref(need)) == 0
-    ws = _lib.workspace(out.device, need.value)
-    st = lib.rk_rotatek_decode(*[_lib.ref(x) for x in d], 1, ctypes.byref(do), 0, ws.data_ptr(), ws.numel(),
-                               _lib.stream_handle(out.device))
-    assert st == _lib.RK_ERR_STRIDE, _lib.strerror(st)
-
-
 def test_split_granularity_does_not_change_results_beyond_rounding():
     from rotatek_amd import _lib
     _say("split granularity sweep")

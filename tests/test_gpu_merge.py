@@ -193,3 +193,43 @@ def test_fused_append_length_advance(mode, G):
     rows = S_p + S_t + 6
     assert torch.equal(k1[:, :, :rows], k2[:, :, :rows])
     assert torch.equal(v1[:, :, :rows + S_v], v2[:, :, :rows + S_v])
+
+
+def _abi_decode(inp, ws, policy=_lib.RK_POLICY_GQA):
+    """rk_rotatek_decode through the C ABI on a caller-owned workspace."""
+    import ctypes
+    names = ("q_full", "R_partial", "delta_mu", "k_full", "v_full", "mask_full", "k_sparse", "v_sparse")
+    d = [_lib.desc(inp[k]) for k in names]
+    out = torch.empty_like(inp["q_full"])
+    do = _lib.desc(out)
+    st = _lib.load().rk_rotatek_decode(*[ctypes.byref(x) for x in d], inp["num_kv_groups"], ctypes.byref(do),
+                                       policy, ws.data_ptr(), ws.numel(), _lib.stream_handle(out.device))
+    torch.cuda.synchronize()
+    assert st == 0, _lib.strerror(st)
+    return out
+
+
+@pytest.mark.parametrize("case", [(1, 32, 32, 32, 15360, 640), (8, 28, 4, 32, 12001, 61)])
+def test_uninitialised_workspace_with_garbage_counters(case):
+    """A caller-owned workspace that was never passed to
+    rk_decode_workspace_init, its counter region full of garbage: the first
+    single-launch decode on it already equals the two-launch merge (the
+    library zeroes the counters of an address it has not seen), so does the
+    next one, and the counters are zero after each.  After
+    rk_decode_workspace_release the address is treated as new again."""
+    B, Hq, Hkv, Dk, S_v, S_f = case
+    _say(f"garbage counters B={B} Hq={Hq} Hkv={Hkv}")
+    inp = _inputs(B, Hq, Hkv, Dk, S_v, S_f, torch.bfloat16, seed=sum(case) + 1)
+    want = _decode(inp, "gqa", _lib.MERGE_TWO_LAUNCHES)
+    need = _lib.plan_decode(B, Hq, Hkv, Dk, S_v, S_f, 2, _lib.RK_POLICY_GQA,
+                            torch.cuda.get_device_properties(0).multi_processor_count)["workspace_bytes"]
+    ws = torch.full((need + 4096,), 0x5A, dtype=torch.uint8, device="cuda")
+    _lib.set_decode_merge(_lib.MERGE_SINGLE_LAUNCH)
+    for round_ in range(2):
+        for call in range(2):
+            got = _abi_decode(inp, ws)
+            assert torch.equal(got, want), (round_, call)
+            assert int(torch.count_nonzero(ws[:_lib.DECODE_TICKET_BYTES]).item()) == 0
+        _lib.load().rk_decode_workspace_release(ws.data_ptr())
+        ws.fill_(0x5A)
+        torch.cuda.synchronize()

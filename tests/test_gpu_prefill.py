@@ -377,3 +377,42 @@ def test_weighted_covariance_equals_two_stage(dtype, G, S, strided):
     if S <= 1200:
         ref = op.query_weight(_np(c0), _np(Q), G, dtype=DT[dtype])
         assert np.abs(_np(got) - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_nan_query_norm_poisons_the_weighted_covariance(fused):
+    """One NaN among the window queries of a KV head: torch.median of its
+    norms is NaN, so is the floor and every weight of that head (the oracle
+    restates it); the other heads are unaffected and match the oracle.  A
+    floor read before any thread wrote it would give finite garbage here."""
+    from rotatek_amd import prefill
+    _say(f"NaN query norm, fused={fused}")
+    B, H, G, S = 1, 2, 4, 300
+    K = _lowrank_keys(B, H, S, torch.bfloat16, seed=21)
+    Q = torch.randn(B, H * G, 40, 128, device="cuda").to(torch.bfloat16)
+    Q[0, 1, -3, 17] = float("nan")  # query head 1 belongs to KV head 0
+    m0, c0 = prefill.key_covariance(K)
+    got = prefill.key_covariance(K, Q, G)[1] if fused else prefill.query_weight(c0, Q, G)
+    torch.cuda.synchronize()
+    g = _np(got)
+    assert np.all(np.isnan(g[0, 0]))
+    ref = op.query_weight(_np(c0), _np(Q), G, dtype="bfloat16")
+    assert np.all(np.isnan(ref[0, 0]))
+    assert np.all(np.isfinite(g[0, 1]))
+    assert np.abs(g[0, 1] - ref[0, 1]).max() <= 1e-5 * np.abs(ref[0, 1]).max()
+
+
+def test_nan_query_raises_in_power_iteration_pruner():
+    """With the weighted covariance NaN, the subspace iteration's Cholesky
+    meets a non-finite pivot and update_rotatek raises LinAlgError, as the
+    reference's torch.linalg.cholesky does (rotation.py:49)."""
+    from rotatek_amd.pruning import ChannelPruner
+    _say("NaN query -> LinAlgError (power_iter)")
+    B, H, G, S = 1, 2, 2, 200
+    K = _lowrank_keys(B, H, S + 40, torch.bfloat16, seed=22)
+    Q = torch.randn(B, H * G, S + 40, 128, device="cuda").to(torch.bfloat16)
+    Q[0, 0, -1, 5] = float("nan")
+    pr = ChannelPruner(0.75, 20, 20, solver="power_iter", query_aware=True)
+    with pytest.raises(torch.linalg.LinAlgError):
+        pr.update_rotatek(K, Q, None, None, G)
+        torch.cuda.synchronize()

@@ -112,6 +112,22 @@ def test_query_weight_ridge_clamps_the_mean(scale, ridge):
     np.testing.assert_allclose(np.diag(got[0, 0]), np.full(D, scale + ridge), rtol=1e-12)
 
 
+def test_query_weight_nan_norm_poisons_the_head():
+    """torch.median of a row with a NaN is NaN (torch.nanmedian is the one
+    that skips NaNs), so q_floor is NaN and the clamp against it makes every
+    weight of that head NaN; other heads are untouched.  A median that
+    skipped the NaN (numpy's sort puts it last) would leave the other
+    channels finite."""
+    D = 6
+    q = np.ones((1, 2, 3, D))
+    q[0, 0, 1, 2] = np.nan
+    cov = np.broadcast_to(np.eye(D), (1, 2, D, D)).copy()
+    got = op.query_weight(cov, q, num_kv_groups=1)
+    assert np.all(np.isnan(got[0, 0]))
+    assert np.all(np.isfinite(got[0, 1]))
+    np.testing.assert_allclose(np.diag(got[0, 1]), 3.0 + 1e-4 * 3.0, rtol=1e-12)
+
+
 def test_query_weight_window_and_group_mean():
     rng = np.random.default_rng(4)
     B, Hkv, G, S, D = 1, 2, 3, 40, 6

@@ -105,3 +105,71 @@ def test_noalloc_rejects_oversized_problem():
     assert st == _lib.RK_ERR_SCRATCH
     with pytest.raises(ValueError, match="allocation-free"):
         _lib.check(st, "noalloc")
+
+
+def _graph_replays_match(tensors, G, n_replays=4):
+    """Capture one allocation-free decode in a CUDA graph and replay it
+    n_replays times, with eager decodes of other inputs and synchronisations
+    between the replays; every replay must equal rk_rotatek_decode bit for
+    bit.  Returns the number of replays checked."""
+    q = tensors[0]
+    out = torch.empty_like(q)
+    d = [_lib.desc(t) for t in tensors]
+    do = _lib.desc(out)
+    lib = _lib.load()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        st = lib.rk_rotatek_decode_noalloc(*[ctypes.byref(x) for x in d], G, ctypes.byref(do),
+                                           _lib.RK_POLICY_GQA, _lib.stream_handle(q.device))
+    assert st == 0, _lib.strerror(st)
+    st_w, want = _run("workspace", tensors, G, _lib.RK_POLICY_GQA)
+    assert st_w == 0
+    other = _inputs(1, 4, 4, 32, 300, 20, tensors[0].dtype, seed=999)
+    for i in range(n_replays):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {i}"
+        _run("noalloc", other, 1, _lib.RK_POLICY_GQA)  # eager work between replays, same scratch
+    return n_replays
+
+
+@pytest.mark.parametrize("merge", [_lib.MERGE_TWO_LAUNCHES, _lib.MERGE_SINGLE_LAUNCH])
+def test_noalloc_captured_after_an_eager_call(merge):
+    _lib.set_decode_merge(merge)
+    try:
+        _say(f"noalloc captured after eager, merge={merge}")
+        t = _inputs(2, 16, 4, 32, 3000, 45, torch.bfloat16, seed=31)
+        _run("noalloc", t, 4, _lib.RK_POLICY_GQA)
+        assert _graph_replays_match(t, 4) == 4
+    finally:
+        _lib.set_decode_merge(_lib.MERGE_AUTO)
+
+
+_FIRST_CALL_SCRIPT = r"""
+import ctypes, sys, torch
+sys.path.insert(0, sys.argv[1])
+import tests.test_zz_no_alloc as m
+from rotatek_amd import _lib
+_lib.set_decode_merge(int(sys.argv[2]))
+t = m._inputs(2, 16, 4, 32, 3000, 45, torch.bfloat16, seed=32)
+print("replays", m._graph_replays_match(t, 4), flush=True)
+"""
+
+
+@pytest.mark.parametrize("merge", [_lib.MERGE_TWO_LAUNCHES, _lib.MERGE_SINGLE_LAUNCH])
+def test_noalloc_captured_as_the_first_call_on_the_device(merge):
+    """In a fresh process the first allocation-free decode on the device is
+    the one being captured: the scratch address is taken then, and with the
+    single-launch merge the counters' fill kernel is recorded into the graph
+    ahead of the decode."""
+    import os
+    import subprocess
+    _say(f"noalloc captured as the first call (subprocess), merge={merge}")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_SCRIPT, root, str(merge)], capture_output=True,
+                         text=True, timeout=300)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-4000:]
+    assert "replays 4" in res.stdout
