@@ -220,7 +220,7 @@ def test_uninitialised_workspace_with_garbage_counters(case):
     B, Hq, Hkv, Dk, S_v, S_f = case
     _say(f"garbage counters B={B} Hq={Hq} Hkv={Hkv}")
     inp = _inputs(B, Hq, Hkv, Dk, S_v, S_f, torch.bfloat16, seed=sum(case) + 1)
-    want = _decode(inp, "gqa", _lib.MERGE_TWO_LAUNCHES)
+    want = _decode(inp, "gqa", _lib.MERGE_TWO_LAUNCHES)[:, 0]
     need = _lib.plan_decode(B, Hq, Hkv, Dk, S_v, S_f, 2, _lib.RK_POLICY_GQA,
                             torch.cuda.get_device_properties(0).multi_processor_count)["workspace_bytes"]
     ws = torch.full((need + 4096,), 0x5A, dtype=torch.uint8, device="cuda")
