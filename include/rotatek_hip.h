@@ -79,7 +79,7 @@ typedef enum rk_status {
   RK_ERR_DTYPE = -3,         /* unsupported or mismatched element type      */
   RK_ERR_SHAPE = -4,         /* sizes disagree between tensors              */
   RK_ERR_HEADS = -5,         /* H_q / num_kv_groups != H_kv                 */
-  RK_ERR_HEAD_DIM = -6,      /* head_dim other than 128                     */
+  RK_ERR_HEAD_DIM = -6,      /* head_dim outside 1..128                     */
   RK_ERR_KEEP_DIM = -7,      /* kept channels out of range (decode 0..128,
                                 prefill and power iteration 1..128)         */
   RK_ERR_STRIDE = -8,        /* negative or overflowing stride              */
@@ -122,7 +122,7 @@ int rk_device_cu_count(int device, int* status);
  * Shapes: q_full [B,H_q,D]; R_partial [B,H_kv,D,Dk]; delta_mu [B,H_kv,D] or
  * NULL; k_full, v_full [B,H_kv,S_f,D]; mask_full [B,S_f] u8 or NULL (= all
  * ones); k_sparse [B,H_kv,S_v,Dk]; v_sparse [B,H_kv,S_v,D]; out [B,H_q,D]
- * (dtype of q_full).  D must be 128, 0 <= Dk <= 128 (Dk = 0: every channel
+ * (dtype of q_full).  1 <= D <= 128, 0 <= Dk <= 128 (Dk = 0: every channel
  * pruned, visual logits are the bias alone; R_partial and k_sparse may then
  * have no storage).  q, K, V and out share one dtype (F16, BF16 or F32;
  * fp32 runs a VALU kernel, one unit per query head); R_partial and

@@ -42,7 +42,7 @@ extern "C" const char* rk_strerror(int status) {
     case RK_ERR_DTYPE: return "unsupported or mismatched dtype";
     case RK_ERR_SHAPE: return "tensor shapes disagree";
     case RK_ERR_HEADS: return "H_q / num_kv_groups does not equal H_kv";
-    case RK_ERR_HEAD_DIM: return "head_dim must be 128";
+    case RK_ERR_HEAD_DIM: return "head_dim must be 1..128";
     case RK_ERR_KEEP_DIM: return "kept channels out of range (decode 0..head_dim, prefill 1..head_dim)";
     case RK_ERR_STRIDE: return "negative or overflowing stride";
     case RK_ERR_WORKSPACE: return "workspace is NULL, misaligned (256 B) or too small";

@@ -148,6 +148,36 @@ __device__ __forceinline__ void load_any_n(const void* p, int64_t idx0, int64_t 
   }
 }
 
+// Rows row0 .. row0 + N - 1 of one column (element base + row * stride) of a
+// launch-uniform dtype, as load_any_n; rows at or past nrows are zero (their
+// loads read row nrows - 1, in bounds).
+template <int N>
+__device__ __forceinline__ void load_any_rows(const void* p, int64_t base, int64_t stride, int dtype, int row0,
+                                              int nrows, float (&out)[N]) {
+  int64_t idx[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) idx[i] = base + (int64_t)min(row0 + i, nrows - 1) * stride;
+  if (dtype == 2) {
+    const float* f = (const float*)p;
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = f[idx[i]];
+  } else {
+    const uint16_t* h = (const uint16_t*)p;
+    uint16_t r[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) r[i] = h[idx[i]];
+    if (dtype == 0) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = F16::to_f32(r[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) out[i] = BF16::to_f32(r[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = row0 + i < nrows ? out[i] : 0.f;
+}
+
 // Split form of load_any for prologues: load_raw issues the load (32 bits
 // for F32, 16 bits otherwise, chosen by a dtype that is uniform across the
 // launch), raw_to_f32 converts later, so the wait for the data can be placed

@@ -70,7 +70,11 @@ struct DecodeArgs {
   // with 16-byte loads)
   int32_t q_vec, r_vec;
   int32_t qr_mfma;  // q R on the MFMA also for rows of <= 32 kept channels
-  float scale_log2;
+  // head_dim (1..128): channels >= D of q, K, V, R_partial's rows and
+  // delta_mu do not exist; the kernels treat them as zeros (the reference's
+  // masked BLOCK_D loads) and write only the first D output channels
+  int32_t D;
+  float scale_log2;  // log2(e) / sqrt(D)
 };
 
 constexpr int kThreads = 256;
@@ -87,6 +91,11 @@ hipError_t decode_launch_f16(int dkb, bool vec, int hmax, bool has_vis, const De
                              hipStream_t s);
 hipError_t decode_launch_bf16(int dkb, bool vec, int hmax, bool has_vis, const DecodeArgs& a, dim3 grid,
                               hipStream_t s);
+// The same with 16-byte row loads for head_dim < 128 (a multiple of 8): the
+// instantiations that mask the channels past D (rk_decode_{f16,bf16}_hd.hip).
+// The element-wise kernels (vec false) take any head_dim in the ones above.
+hipError_t decode_launch_f16_hd(int dkb, int hmax, bool has_vis, const DecodeArgs& a, dim3 grid, hipStream_t s);
+hipError_t decode_launch_bf16_hd(int dkb, int hmax, bool has_vis, const DecodeArgs& a, dim3 grid, hipStream_t s);
 // The same for fp32 q / K / V (the VALU kernel, one query head per unit).
 hipError_t decode_launch_f32(bool has_vis, bool vec, const DecodeArgs& a, dim3 grid, hipStream_t s);
 

@@ -388,7 +388,7 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
 namespace {
 
 struct Checked {
-  int64_t B, H_q, H_kv, G, Dk, S_v, S_f;
+  int64_t B, H_q, H_kv, G, D, Dk, S_v, S_f;
   int dtype;
 };
 
@@ -407,7 +407,7 @@ int check_out(const rk_tensor* out, const Checked& c) {
   int st = rk::check_desc(out, 3);
   if (st) return st;
   if (out->dtype != c.dtype) return RK_ERR_DTYPE;
-  if (out->shape[0] != c.B || out->shape[1] != c.H_q || out->shape[2] != 128) return RK_ERR_SHAPE;
+  if (out->shape[0] != c.B || out->shape[1] != c.H_q || out->shape[2] != c.D) return RK_ERR_SHAPE;
   return RK_OK;
 }
 
@@ -438,13 +438,16 @@ int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
   c->H_q = q->shape[1];
   c->H_kv = R->shape[1];
   c->G = G;
+  c->D = q->shape[2];
   c->Dk = R->shape[3];
   c->dtype = q->dtype;
   if (c->H_q / G != c->H_kv || c->H_q % G != 0) return RK_ERR_HEADS;
   if (!rk::is_half(q->dtype) && q->dtype != RK_F32) return RK_ERR_DTYPE;
-  if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
+  // any head size up to 128 (the reference pads D to a power-of-two block
+  // with a channel mask, fused_decode.py:128, 341-342)
+  if (c->D < 1 || c->D > 128) return RK_ERR_HEAD_DIM;
   if (!rk::is_float_param(R->dtype)) return RK_ERR_DTYPE;
-  if (R->shape[0] != c->B || R->shape[2] != 128) return RK_ERR_SHAPE;
+  if (R->shape[0] != c->B || R->shape[2] != c->D) return RK_ERR_SHAPE;
   // Dk = 0 (channel_ratio >= 1, every channel pruned): visual logits are the
   // bias q . delta_mu alone, as the reference's kernels give with no kept
   // channel (its masked BLOCK_DK loads, fused_decode.py:131-148)
@@ -453,7 +456,7 @@ int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
     st = rk::check_desc(dm, 3);
     if (st) return st;
     if (!rk::is_float_param(dm->dtype)) return RK_ERR_DTYPE;
-    if (dm->shape[0] != c->B || dm->shape[1] != c->H_kv || dm->shape[2] != 128) return RK_ERR_SHAPE;
+    if (dm->shape[0] != c->B || dm->shape[1] != c->H_kv || dm->shape[2] != c->D) return RK_ERR_SHAPE;
   }
   st = rk::check_desc(kf, 4);
   if (st) return st;
@@ -461,10 +464,10 @@ int check_rotatek(const rk_tensor* q, const rk_tensor* R, const rk_tensor* dm,
   st = rk::check_desc(ks, 4);
   if (st) return st;
   c->S_v = ks->shape[2];
-  if ((st = check_kv4(kf, *c, c->S_f, 128, true))) return st;
-  if ((st = check_kv4(vf, *c, c->S_f, 128, true))) return st;
+  if ((st = check_kv4(kf, *c, c->S_f, c->D, true))) return st;
+  if ((st = check_kv4(vf, *c, c->S_f, c->D, true))) return st;
   if ((st = check_kv4(ks, *c, c->S_v, c->Dk, true))) return st;
-  if ((st = check_kv4(vs, *c, c->S_v, 128, true))) return st;
+  if ((st = check_kv4(vs, *c, c->S_v, c->D, true))) return st;
   if (!head_span_ok(kf) || !head_span_ok(vf) || !head_span_ok(vs) || (c->Dk > 0 && !head_span_ok(ks)))
     return RK_ERR_STRIDE;
   if (mask) {
@@ -578,9 +581,11 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     a.mf_ss = mask->stride[1];
     a.has_mask = 1;
   }
-  bool vec = rk::vec_ok(kf) && rk::vec_ok(vf);
+  // 16-byte row loads also need whole 8-channel slots (head_dim % 8 == 0)
+  bool vec = rk::vec_ok(kf) && rk::vec_ok(vf) && c.D % 8 == 0;
+  a.D = (int32_t)c.D;
   a.q_vec = q->stride[2] == 1 && q->stride[1] % 8 == 0 && q->stride[0] % 8 == 0 &&
-            (((uintptr_t)q->data) & 15) == 0;
+            (((uintptr_t)q->data) & 15) == 0 && c.D % 8 == 0;
   int dkb = 1;
   if (has_vis) {
     a.R = R->data;
@@ -597,8 +602,9 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     // R staged into LDS (16-byte DMA): up to 64 channels in either 16-bit
     // type; 65-128 only in the compute type (their q R is an MFMA product
     // read straight from the staged rows, and R fills the kernel's s_acc)
+    // (a head's [D][Dk] block is copied as whole 16-byte chunks)
     a.r_vec = rk::is_half(R->dtype) && (c.Dk <= 64 || (c.Dk <= 128 && R->dtype == c.dtype)) &&
-              R->stride[3] == 1 && R->stride[2] == c.Dk &&
+              R->stride[3] == 1 && R->stride[2] == c.Dk && (c.D * c.Dk) % 8 == 0 &&
               R->stride[1] % 8 == 0 && R->stride[0] % 8 == 0 && (((uintptr_t)R->data) & 15) == 0;
     a.ks = (const uint16_t*)ks->data;
     a.vs = (const uint16_t*)vs->data;
@@ -661,7 +667,7 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   a.xgroup = policy == RK_POLICY_PAPER && c.G > 1 && c.dtype != RK_F32 ? (int32_t)c.G : 0;
   if (a.xgroup || c.dtype == RK_F32) a.rot_x = 0;
   if (c.dtype == RK_F32) a.spk = (int32_t)c.G;  // one unit per query head
-  a.scale_log2 = (float)(rk::kLog2e / sqrt(128.0));
+  a.scale_log2 = (float)(rk::kLog2e / sqrt((double)c.D));  // 1 / sqrt(D) (fused_decode.py:340)
   a.cmajor = has_vis && c.dtype != RK_F32 && !a.xgroup ? p.chunk_major : 0;
   a.nfast = a.cmajor ? p.n_fast : 0;
   a.chunk_fast = p.chunk_fast;
@@ -685,12 +691,17 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
     if (st0) return st0;
   }
   if (c.dtype == RK_F32) {
-    const bool v32 = vec32_ok(kf) && vec32_ok(vf) &&
+    const bool v32 = vec32_ok(kf) && vec32_ok(vf) && c.D % 4 == 0 &&
                      (!has_vis || ((c.Dk == 0 || vec32_ok(ks)) && vec32_ok(vs) && c.Dk % 4 == 0));
     return rk::decode_launch_f32(has_vis, v32, a, grid, s) == hipSuccess ? RK_OK : RK_ERR_HIP;
   }
-  hipError_t e = c.dtype == RK_F16 ? rk::decode_launch_f16(dkb, vec, hmax, has_vis, a, grid, s)
-                                   : rk::decode_launch_bf16(dkb, vec, hmax, has_vis, a, grid, s);
+  hipError_t e;
+  if (vec && c.D < 128)  // 16-byte loads with the channels past D masked
+    e = c.dtype == RK_F16 ? rk::decode_launch_f16_hd(dkb, hmax, has_vis, a, grid, s)
+                          : rk::decode_launch_bf16_hd(dkb, hmax, has_vis, a, grid, s);
+  else
+    e = c.dtype == RK_F16 ? rk::decode_launch_f16(dkb, vec, hmax, has_vis, a, grid, s)
+                          : rk::decode_launch_bf16(dkb, vec, hmax, has_vis, a, grid, s);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 
@@ -765,7 +776,7 @@ extern "C" int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor
     for (const rk_tensor* t : {k_new, v_new}) {
       if ((st = rk::check_desc(t, 4))) return st;
       if (t->dtype != c.dtype) return RK_ERR_DTYPE;
-      if (t->shape[0] != c.B || t->shape[1] != c.H_kv || t->shape[2] != 1 || t->shape[3] != 128)
+      if (t->shape[0] != c.B || t->shape[1] != c.H_kv || t->shape[2] != 1 || t->shape[3] != c.D)
         return RK_ERR_SHAPE;
       if (c.B > 0 && !t->data) return RK_ERR_NULL;
     }
@@ -848,6 +859,7 @@ int check_dense(const rk_tensor* q, const rk_tensor* k, const rk_tensor* v, int6
   c->H_q = q->shape[1];
   c->H_kv = k->shape[1];
   c->G = G;
+  c->D = q->shape[2];
   c->Dk = 0;
   c->S_v = 0;
   c->S_f = k->shape[2];
@@ -856,9 +868,11 @@ int check_dense(const rk_tensor* q, const rk_tensor* k, const rk_tensor* v, int6
     return RK_ERR_SHAPE;
   if (c->H_kv <= 0 || c->H_q / G != c->H_kv || c->H_q % G != 0) return RK_ERR_HEADS;
   if (!rk::is_half(q->dtype) && q->dtype != RK_F32) return RK_ERR_DTYPE;
-  if (q->shape[2] != 128) return RK_ERR_HEAD_DIM;
-  if ((st = check_kv4(k, *c, c->S_f, 128, true))) return st;
-  if ((st = check_kv4(v, *c, c->S_f, 128, true))) return st;
+  // any head size up to 128 (full_channel_flash_decoding.py:175-185 pads to
+  // a power-of-two block with a mask)
+  if (c->D < 1 || c->D > 128) return RK_ERR_HEAD_DIM;
+  if ((st = check_kv4(k, *c, c->S_f, c->D, true))) return st;
+  if ((st = check_kv4(v, *c, c->S_f, c->D, true))) return st;
   if (!head_span_ok(k) || !head_span_ok(v)) return RK_ERR_STRIDE;
   return RK_OK;
 }

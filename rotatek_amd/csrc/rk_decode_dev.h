@@ -341,29 +341,35 @@ __device__ __forceinline__ void combine(float& M, float& L, float (&A)[8], float
 }
 
 // acc / (l + 1e-6) in the output dtype, channels 8 c8 .. 8 c8 + 7 of (b, hq).
+// Only the first D channels exist (a slice of eight past D writes nothing,
+// one straddling D writes its first D - 8 c8 elements).
 template <class TT>
 __device__ __forceinline__ void write_out(const DecodeArgs& a, int b, int hq, int c8, float L,
                                           const float (&A)[8]) {
+  const int nv = min(a.D - 8 * c8, 8);
+  if (nv <= 0) return;
   const float den = L + kDenomEps;
   if constexpr (TT::kBytes == 4) {
     float* dst = (float*)a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 8 * c8 * a.o_sd;
-    if (a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
+    if (nv == 8 && a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
       ((float4*)dst)[0] = make_float4(A[0] / den, A[1] / den, A[2] / den, A[3] / den);
       ((float4*)dst)[1] = make_float4(A[4] / den, A[5] / den, A[6] / den, A[7] / den);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[e * a.o_sd] = A[e] / den;
+      for (int e = 0; e < 8; ++e)
+        if (e < nv) dst[e * a.o_sd] = A[e] / den;
     }
   } else {
     uint16_t o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = TT::from_f32(A[e] / den);
     uint16_t* dst = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 8 * c8 * a.o_sd;
-    if (a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
+    if (nv == 8 && a.o_sd == 1 && (((uintptr_t)dst) & 15) == 0) {
       *(uint4*)dst = pack8(o);
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dst[e * a.o_sd] = o[e];
+      for (int e = 0; e < 8; ++e)
+        if (e < nv) dst[e * a.o_sd] = o[e];
     }
   }
 }
@@ -499,9 +505,18 @@ __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, i
 // NTL: V rows and compact visual Key rows use non-temporal loads (false for
 // the grouped one-unit-per-query-head mode, whose G units of a KV head read
 // each line through one XCD's L2).
-template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND, bool NTL = true>
+// DPART (16-byte loads only): head_dim a.D < 128, a multiple of 8.  The
+// lanes of channels past D load an in-bounds duplicate of channels D-8..D-1
+// (V: only output channels past D see it, and those are not written; full
+// K: zeroed before the score product), and q, R_partial's rows and
+// delta_mu past D are zeros.  The element-wise kernels (VEC false) take any
+// D: their loads past D are not issued and read as zeros.  With VEC and
+// not DPART, D is 128 and none of this is compiled.
+template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND, bool NTL = true, bool DPART = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const DecodeArgs a) {
+  static_assert(!DPART || VEC, "the element-wise kernels mask head_dim at run time");
+  constexpr bool kMaskD = DPART || !VEC;  // channels past a.D possible
   constexpr int DKP = DKB * 32;
   // visual blocks in flight per wave: three for multi-head units of <= 32
   // kept channels, else two (one-head units: measured faster on MI355X, eager
@@ -569,9 +584,11 @@ decode_kernel(const DecodeArgs a) {
   if (fold_new) pos_new = min(a.S_f, (int64_t)max(a.len_full[b], 0));
   const bool has_new = fold_new && pos_new < a.S_f;  // a full buffer neither attends nor stores
   uint16_t new_raw = 0;
+  // channel tid & 127 of k_new (tid < 128) or v_new; past head_dim: zero, not stored
+  const bool new_ch = !kMaskD || (tid & 127) < a.D;
   auto load_new = [&]() {
     if (has_new) {
-      const int c = tid & 127;
+      const int c = kMaskD ? min(tid & 127, a.D - 1) : tid & 127;
       new_raw = tid < 128 ? a.k_new[b * a.kn_sb + (int64_t)kv * a.kn_sh + (int64_t)c * a.kn_sd]
                           : a.v_new[b * a.vn_sb + (int64_t)kv * a.vn_sh + (int64_t)c * a.vn_sd];
     }
@@ -579,8 +596,8 @@ decode_kernel(const DecodeArgs a) {
   // after the staging barrier: the first unit of the KV head stores the row
   auto store_new = [&]() {
     if (has_new) {
-      s_new[tid >> 7][tid & 127] = TT::to_f32(new_raw);
-      if (jblk == 0) {
+      s_new[tid >> 7][tid & 127] = new_ch ? TT::to_f32(new_raw) : 0.f;
+      if (jblk == 0 && new_ch) {
         const int64_t c = tid & 127;
         if (tid < 128) {
           a.kf_w[b * a.kf_sb + (int64_t)kv * a.kf_sh + pos_new * a.kf_ss + c * a.kf_sd] = new_raw;
@@ -615,10 +632,14 @@ decode_kernel(const DecodeArgs a) {
   uint4 q16 = make_uint4(0u, 0u, 0u, 0u);
   // load_q issues the fast-layout load before the first K/V blocks; the
   // element-wise fallback loads inside store_q, after them.
+  // (fast layout with head_dim < 128: D is a multiple of 8, and the lanes of
+  // channels past D re-read the row's last eight and are zeroed in store_q)
+  const bool q_ch = !kMaskD || 8 * (tid & 15) < a.D;
   auto load_q = [&]() {
     if (a.q_vec) {
       const int h = min(tid >> 4, nh - 1);
-      q16 = *(const uint4*)(a.q + b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + 8 * (tid & 15));
+      const int c0 = kMaskD ? min(8 * (tid & 15), a.D - 8) : 8 * (tid & 15);
+      q16 = *(const uint4*)(a.q + b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + c0);
     }
   };
   auto store_q = [&]() {
@@ -626,7 +647,7 @@ decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int k = 0; k < kQPer; ++k) {
         const int i = tid + k * kThreads;
-        const int h = min(i >> 7, nh - 1), d = i & 127;
+        const int h = min(i >> 7, nh - 1), d = kMaskD ? min(i & 127, a.D - 1) : i & 127;
         qraw[k] = a.q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + d * a.q_sd];
       }
     }
@@ -636,7 +657,7 @@ decode_kernel(const DecodeArgs a) {
         float f[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          f[e] = h < nh ? TT::to_f32((uint16_t)(word(q16, e >> 1) >> ((e & 1) * 16))) : 0.f;
+          f[e] = h < nh && q_ch ? TT::to_f32((uint16_t)(word(q16, e >> 1) >> ((e & 1) * 16))) : 0.f;
         float4* dst = (float4*)&s_q[h][8 * (tid & 15)];
         dst[0] = make_float4(f[0], f[1], f[2], f[3]);
         dst[1] = make_float4(f[4], f[5], f[6], f[7]);
@@ -645,7 +666,7 @@ decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int k = 0; k < kQPer; ++k) {
         const int i = tid + k * kThreads;
-        qv[k] = (i < HMAX * 128 && (i >> 7) < nh) ? TT::to_f32(qraw[k]) : 0.f;
+        qv[k] = (i < HMAX * 128 && (i >> 7) < nh && (!kMaskD || (i & 127) < a.D)) ? TT::to_f32(qraw[k]) : 0.f;
         if (i < HMAX * 128) s_q[i >> 7][i & 127] = qv[k];
       }
     }
@@ -669,7 +690,11 @@ decode_kernel(const DecodeArgs a) {
       kch[kb] = kval[kb] ? (uint32_t)c0 : 0u;
       knv[kb] = kval[kb] ? min(a.Dk - c0, 8) : 0;
     }
-    const uint32_t vch = 8u * n;
+    // V channel slot of this lane: past head_dim, the row's last eight (with
+    // 16-byte loads; they feed only output channels that are not written),
+    // or no load at all (element-wise)
+    const uint32_t vch = DPART ? (uint32_t)min(8 * n, a.D - 8) : 8u * n;
+    const int vnv = kMaskD ? max(min(a.D - 8 * n, 8), 0) : 8;
     const int64_t nblk = (t_end - t_begin + kBlk - 1) / kBlk;
     // Row addresses are byte offsets from the head base: a per-lane part (the
     // lane's row inside the block, and with 16-byte loads its channel slot)
@@ -695,7 +720,7 @@ decode_kernel(const DecodeArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < 8; ++r)
-        B.v[r] = load_row8b<VEC, NTL>(vsb, min(vro + vb0 + (uint32_t)r * vss2, vlast), VEC ? 0u : vch, a.vs_sd, 8);
+        B.v[r] = load_row8b<VEC, NTL>(vsb, min(vro + vb0 + (uint32_t)r * vss2, vlast), VEC ? 0u : vch, a.vs_sd, vnv);
     };
 
     // q R: thread (c, part) loads R[part*L .. part*L+L-1][c], forms partial
@@ -707,7 +732,7 @@ decode_kernel(const DecodeArgs a) {
     // memory latency covers them all.
     uint4* s_r = HMAX >= 16 ? (uint4*)&s_acc[0][0][0] + (DKB == 4 ? 0 : kRawChunks) : s_rsep;
     constexpr int kRPer = kRawChunks / kThreads;
-    const int nchunks = 16 * a.Dk;  // [128][Dk] 16-bit elements in 16-byte chunks
+    const int nchunks = kMaskD ? (a.D * a.Dk) >> 3 : 16 * a.Dk;  // [D][Dk] 16-bit elements in 16-byte chunks
     Ring<NBUF_V, VisBuf<DKB>> ring(nblk, wave, rot_seed);
     ring.prime(load);
     load_q();
@@ -728,11 +753,11 @@ decode_kernel(const DecodeArgs a) {
     }
     uint32_t dmraw = 0u;
     if (a.has_bias) {
-      const int64_t di = b * a.dm_sb + kv * a.dm_sh + (int64_t)(tid & 127) * a.dm_sd;
+      const int64_t di = b * a.dm_sb + kv * a.dm_sh + (int64_t)(kMaskD ? min(tid & 127, a.D - 1) : tid & 127) * a.dm_sd;
       dmraw = a.dm_dtype == 2 ? ((const uint32_t*)a.dm)[di] : (uint32_t)((const uint16_t*)a.dm)[di];
     }
 
-    const float dmv = (tid < 128 && a.has_bias) ? raw_to_f32(dmraw, a.dm_dtype) : 0.f;
+    const float dmv = (tid < 128 && a.has_bias && (!kMaskD || tid < a.D)) ? raw_to_f32(dmraw, a.dm_dtype) : 0.f;
     store_q();
     store_new();
     if (tid < 128) s_dm[tid] = dmv;
@@ -770,7 +795,7 @@ decode_kernel(const DecodeArgs a) {
           const int k0 = 32 * kk + 8 * g;
           uint16_t rb[8];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) rb[e] = rc[(k0 + e) * a.Dk];
+          for (int e = 0; e < 8; ++e) rb[e] = !kMaskD || k0 + e < a.D ? rc[(k0 + e) * a.Dk] : (uint16_t)0;
           const float4 f0 = *(const float4*)&s_q[nq][k0], f1 = *(const float4*)&s_q[nq][k0 + 4];
           const uint4 av = hrow ? make_uint4(TT::pack2(f0.x, f0.y), TT::pack2(f0.z, f0.w), TT::pack2(f1.x, f1.y),
                                              TT::pack2(f1.z, f1.w))
@@ -804,14 +829,14 @@ decode_kernel(const DecodeArgs a) {
           for (int i = 0; i < kL; ++i) rv[i] = BF16::to_f32(raw[i]);
         }
 #pragma unroll
-        for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
+        for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk && (!kMaskD || part * kL + i < a.D) ? rv[i] : 0.f;
       } else {  // element-wise fallback (column c, clamped in-bounds; no load
                 // at all when Dk == 0, where R_partial has no storage)
 #pragma unroll
         for (int i = 0; i < kL; ++i) rv[i] = 0.f;
         if (a.Dk > 0) {
           const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)min(c, a.Dk - 1) * a.R_sk;
-          load_any_n(a.R, rb + (int64_t)(part * kL) * a.R_sd, a.R_sd, a.r_dtype, rv);
+          load_any_rows(a.R, rb, a.R_sd, a.r_dtype, part * kL, kMaskD ? a.D : 128, rv);
 #pragma unroll
           for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
         }
@@ -887,21 +912,35 @@ decode_kernel(const DecodeArgs a) {
     const uint32_t t_last = (uint32_t)max(t_begin, t_end - 1);
     const uint16_t* kfb = a.kf + b * a.kf_sb + kv * a.kf_sh;
     const uint16_t* vfb = a.vf + b * a.vf_sb + kv * a.vf_sh;
-    const uint32_t vch = 8u * n;
+    // channel slots past head_dim: V as in the visual path; K loads an
+    // in-bounds duplicate that is zeroed before the score (16-byte loads),
+    // or nothing (element-wise)
+    const uint32_t vch = DPART ? (uint32_t)min(8 * n, a.D - 8) : 8u * n;
+    const int vnv = kMaskD ? max(min(a.D - 8 * n, 8), 0) : 8;
+    uint32_t fch[4];
+    int fnv[4];
+    bool fval[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int c0 = kb * 32 + 8 * g;
+      fch[kb] = DPART ? (uint32_t)min(c0, a.D - 8) : (uint32_t)c0;
+      fnv[kb] = kMaskD ? max(min(a.D - c0, 8), 0) : 8;
+      fval[kb] = c0 < a.D;
+    }
     const int64_t nblk = (t_end - t_begin + kBlk - 1) / kBlk;
     auto load = [&](FullBuf& B, int64_t blk) {
       const uint32_t t0 = (uint32_t)(t_begin + blk * kBlk);
       const uint32_t r0 = min(t0 + krow0, t_last) * a.kf_ss, r1 = min(t0 + krow1, t_last) * a.kf_ss;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        B.k[0][kb] = load_row8<VEC, false>(kfb, r0, (uint32_t)(kb * 32 + 8 * g), a.kf_sd, 8);
-        B.k[1][kb] = load_row8<VEC, false>(kfb, r1, (uint32_t)(kb * 32 + 8 * g), a.kf_sd, 8);
+        B.k[0][kb] = load_row8<VEC, false>(kfb, r0, fch[kb], a.kf_sd, fnv[kb]);
+        B.k[1][kb] = load_row8<VEC, false>(kfb, r1, fch[kb], a.kf_sd, fnv[kb]);
       }
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         uint32_t row = min(t0 + 8u * g + r, t_last);
         row += row >= a.vf_gap_at ? a.vf_gap : 0u;
-        B.v[r] = load_row8<VEC, NTL>(vfb, row * a.vf_ss, vch, a.vf_sd, 8);
+        B.v[r] = load_row8<VEC, NTL>(vfb, row * a.vf_ss, vch, a.vf_sd, vnv);
       }
     };
 
@@ -949,7 +988,7 @@ decode_kernel(const DecodeArgs a) {
       for (int sb = 0; sb < 2; ++sb) {
         f32x4 cc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) cc = TT::mfma(B.k[sb][kb], qf[kb], cc);
+        for (int kb = 0; kb < 4; ++kb) cc = TT::mfma(DPART ? zero_if(fval[kb], B.k[sb][kb]) : B.k[sb][kb], qf[kb], cc);
         const uint32_t w = sb ? vb.y : vb.x;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -1091,8 +1130,13 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
   const int xf = HAS_VIS ? x - a.wg_vis : x;
   const float* q = (const float*)a.q;
 
-  if (tid < 128) s_q[tid] = q[b * a.q_sb + (int64_t)h0 * a.q_sh + (int64_t)tid * a.q_sd];
+  // channels past head_dim D are zeros (q, R_partial's rows, delta_mu);
+  // V lanes past D read an in-bounds duplicate (16-byte rows: the row's last
+  // two channels; else no load) that feeds only output channels not written
+  if (tid < 128) s_q[tid] = tid < a.D ? q[b * a.q_sb + (int64_t)h0 * a.q_sh + (int64_t)tid * a.q_sd] : 0.f;
   __syncthreads();
+  const int vc = min(2 * lane, a.D - 2);  // (VEC: D is a multiple of 4)
+  const bool v0ok = 2 * lane < a.D, v1ok = 2 * lane + 1 < a.D;
 
   float m = kNegInit, l = 0.f, acc0 = 0.f, acc1 = 0.f;
   // online-softmax step over one block: s = log2-domain score of token
@@ -1122,12 +1166,12 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
         row += row >= gap_at ? gap : 0u;
         const float* vr = vb + (int64_t)row * vss;
         if constexpr (VEC) {
-          const float2 v = *(const float2*)(vr + 2 * lane);
+          const float2 v = *(const float2*)(vr + vc);
           v0[jj] = v.x;
           v1[jj] = v.y;
         } else {
-          v0[jj] = vr[(int64_t)(2 * lane) * vsd];
-          v1[jj] = vr[(int64_t)(2 * lane + 1) * vsd];
+          v0[jj] = v0ok ? vr[(int64_t)(2 * lane) * vsd] : 0.f;
+          v1[jj] = v1ok ? vr[(int64_t)(2 * lane + 1) * vsd] : 0.f;
         }
       }
 #pragma unroll
@@ -1151,7 +1195,7 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
       float sum = 0.f;
       if (a.Dk > 0) {
         float rv[64];
-        load_any_n(a.R, rb + (int64_t)(64 * half) * a.R_sd, a.R_sd, a.r_dtype, rv);
+        load_any_rows(a.R, rb, a.R_sd, a.r_dtype, 64 * half, a.D, rv);
 #pragma unroll
         for (int i = 0; i < 64; ++i) sum = fmaf(s_q[64 * half + i], rv[i], sum);
       }
@@ -1161,9 +1205,9 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     }
     if (wave < 2) {  // q . delta_mu
       const int d = tid;
-      const float t = a.has_bias ? s_q[d] * load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)d * a.dm_sd,
-                                                    a.dm_dtype)
-                                 : 0.f;
+      const float t = a.has_bias && d < a.D
+                          ? s_q[d] * load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)d * a.dm_sd, a.dm_dtype)
+                          : 0.f;
       const float w = wave_sum(t);
       if (lane == 0) s_bias[wave] = w;
     }
@@ -1190,7 +1234,7 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
       const int64_t t = t0 + lane;
       const int64_t tc = min(t, t_end - 1);
-      const float d = dot_row32<VEC, 128>(kfb + tc * a.kf_ss, a.kf_sd, s_q, 128);
+      const float d = dot_row32<VEC, 128>(kfb + tc * a.kf_ss, a.kf_sd, s_q, a.D);
       const bool ok = t < t_end && (!a.mask || a.mask[b * a.mf_sb + tc * a.mf_ss] != 0);
       step(ok ? d * a.scale_log2 : -INFINITY, vfb, a.vf_ss, a.vf_sd, t0, t_end - 1, a.vf_gap_at, a.vf_gap);
     }
@@ -1254,7 +1298,7 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
 
 // ---- host-side launch templates (instantiated per dtype by the launch units)
 
-template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS>
+template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool DPART>
 hipError_t launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   bool launched = false;
   // grouped one-unit-per-query-head mode (temporal loads): the dense
@@ -1262,20 +1306,20 @@ hipError_t launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   // family grouped, see rotatek_policy)
   if constexpr (VEC && HMAX == 1 && !HAS_VIS) {
     if (a.xgroup > 1) {
-      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false>), grid,
+      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false, DPART>), grid,
                          dim3(kThreads), 0, s, a);
       launched = true;
     }
   }
   if constexpr (HAS_VIS) {  // the span cache's step always carries the visual span
     if (!launched && a.k_new) {
-      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, true, true>), grid, dim3(kThreads), 0,
+      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, true, true, true, DPART>), grid, dim3(kThreads), 0,
                          s, a);
       launched = true;
     }
   }
   if (!launched)
-    hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false>), grid, dim3(kThreads), 0,
+    hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, true, DPART>), grid, dim3(kThreads), 0,
                        s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fused) return e;
@@ -1283,32 +1327,34 @@ hipError_t launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <class TT, int DKB, bool VEC, int HMAX>
+template <class TT, int DKB, bool VEC, int HMAX, bool DPART>
 hipError_t launch_vis(bool has_vis, const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  return has_vis ? launch_one<TT, DKB, VEC, HMAX, true>(a, grid, s)
-                 : launch_one<TT, 1, VEC, HMAX, false>(a, grid, s);
+  return has_vis ? launch_one<TT, DKB, VEC, HMAX, true, DPART>(a, grid, s)
+                 : launch_one<TT, 1, VEC, HMAX, false, DPART>(a, grid, s);
 }
 
-template <class TT, int DKB, bool VEC>
+template <class TT, int DKB, bool VEC, bool DPART>
 hipError_t launch_h(int hmax, bool has_vis, const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  return hmax > 1 ? launch_vis<TT, DKB, VEC, 16>(has_vis, a, grid, s)
-                  : launch_vis<TT, DKB, VEC, 1>(has_vis, a, grid, s);
+  return hmax > 1 ? launch_vis<TT, DKB, VEC, 16, DPART>(has_vis, a, grid, s)
+                  : launch_vis<TT, DKB, VEC, 1, DPART>(has_vis, a, grid, s);
 }
 
-template <class TT, int DKB>
+// DPART: 16-byte loads at head_dim < 128 (vec must be true)
+template <class TT, int DKB, bool DPART>
 hipError_t launch_v(bool vec, int hmax, bool has_vis, const DecodeArgs& a, dim3 grid,
                     hipStream_t s) {
-  return vec ? launch_h<TT, DKB, true>(hmax, has_vis, a, grid, s)
-             : launch_h<TT, DKB, false>(hmax, has_vis, a, grid, s);
+  if constexpr (DPART) return launch_h<TT, DKB, true, true>(hmax, has_vis, a, grid, s);
+  return vec ? launch_h<TT, DKB, true, false>(hmax, has_vis, a, grid, s)
+             : launch_h<TT, DKB, false, false>(hmax, has_vis, a, grid, s);
 }
 
-template <class TT>
+template <class TT, bool DPART = false>
 hipError_t launch_dk(int dkb, bool vec, int hmax, bool has_vis, const DecodeArgs& a, dim3 grid,
                      hipStream_t s) {
   switch (dkb) {
-    case 1: return launch_v<TT, 1>(vec, hmax, has_vis, a, grid, s);
-    case 2: return launch_v<TT, 2>(vec, hmax, has_vis, a, grid, s);
-    default: return launch_v<TT, 4>(vec, hmax, has_vis, a, grid, s);
+    case 1: return launch_v<TT, 1, DPART>(vec, hmax, has_vis, a, grid, s);
+    case 2: return launch_v<TT, 2, DPART>(vec, hmax, has_vis, a, grid, s);
+    default: return launch_v<TT, 4, DPART>(vec, hmax, has_vis, a, grid, s);
   }
 }
 

@@ -123,7 +123,11 @@ def test_rotatek_check_ok_and_workspace():
     (dict(R_shape=(2, 4, 128)), -2),            # R rank != 4
     (dict(mask_dtype=_lib.RK_F16), -3),         # mask not uint8
     (dict(G=3), -5),                            # H_q / G != H_kv
-    (dict(D=64), -6),                           # head_dim != 128
+    (dict(D=64), 0),                            # any head_dim 1..128
+    (dict(D=80), 0),
+    (dict(D=1), 0),
+    (dict(D=129), -6),                          # head_dim past 128
+    (dict(D=0), -6),
     (dict(dtype=_lib.RK_F64), -3),              # fp64 not supported
     (dict(Dk=129), -7),
     (dict(Dk=0), 0),                            # every channel pruned: bias-only visual logits
