@@ -111,9 +111,18 @@ struct BF16 {
   }
 };
 
-// fp32 storage (the fp32 decode path: outputs written as they are computed).
+// fp32 storage (the fp32 decode path: outputs written as they are computed;
+// the fp32 prefill path: "rounding to the key dtype" is the identity).
 struct F32 {
   static constexpr int kBytes = 4;
+  static constexpr int32_t kRk = 2;  // its rk_dtype code (RK_F32)
+  static __device__ __forceinline__ float to_f32(uint32_t b) { return __builtin_bit_cast(float, b); }
+  static __device__ __forceinline__ uint32_t from_f32(float x) { return __builtin_bit_cast(uint32_t, x); }
+  // v_mfma_f32_16x16x4_f32: lane (g, n) supplies A[n][g] and B[g][n] and
+  // receives D[4g + i][n], i = 0..3 (fp32 products, fp32 accumulation)
+  static __device__ __forceinline__ f32x4 mfma(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
 };
 
 // Scalar load of one element of a runtime dtype (0 f16, 1 bf16, 2 f32).

@@ -1,6 +1,7 @@
 // rk_prefill.hip -- RotateK prefill producer kernels for MI355X (gfx950).
 //
-// Per (batch, KV head) of the visual Keys K [S, 128] (any strides):
+// Per (batch, KV head) of the visual Keys K [S, D] (D <= 128, any strides;
+// F16, BF16 or F32; channels past D are treated as absent):
 //
 //   covariance   (kv_pruning_utils.py:112-115)
 //     mean_kernel   split-S fp32 partial sums of K               (pass 1)
@@ -24,7 +25,13 @@
 // rows 8g..8g+7 (tokens) x channels 8n..8n+7 of a 32-token block and
 // transposes them in registers; slot i of that transpose is the MFMA
 // operand for the channel set {8m + i : m = 0..15}, so tile (i, j) of the
-// accumulator holds C[8m + i][8m' + j].
+// accumulator holds C[8m + i][8m' + j].  fp32 Keys keep that layout on
+// v_mfma_f32_16x16x4_f32, one token row of the lane per MFMA step.
+//
+// head_dim D < 128: with 16-byte rows (D a multiple of 8) a lane whose
+// channel slot lies past D re-reads the row's last slot (in bounds) and its
+// values are masked to zero before they meet a valid operand; element-wise
+// loads read only channels < D.  Outputs hold D channels.
 #include <math.h>
 #include <string.h>
 
@@ -39,28 +46,60 @@ constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 
 struct KeyView {
-  const uint16_t* data;
+  const uint16_t* data;  // element pointer (fp32 Keys: reinterpreted)
   int64_t sb, sh;      // batch / head strides (elements)
   uint32_t ss, sd;     // token / channel strides; a head spans < 2^31 elements
   int64_t S;           // tokens
   int32_t H;
+  int32_t D;           // head_dim, 1..128
 };
 
 __device__ __forceinline__ const uint16_t* head_base(const KeyView& k, int bh) {
   const int b = bh / k.H, h = bh - b * k.H;
   return k.data + b * k.sb + (int64_t)h * k.sh;
 }
+template <class TT>
+__device__ __forceinline__ const void* head_base_t(const KeyView& k, int bh) {
+  const int b = bh / k.H, h = bh - b * k.H;
+  return (const char*)k.data + (b * k.sb + (int64_t)h * k.sh) * TT::kBytes;
+}
 
-// Eight channels c0..c0+7 of row `t` (clamped by the caller).
+// The channel slot [c0, c0 + 8) a lane loads: with 16-byte rows a slot past
+// D re-reads the last one (D is then a multiple of 8); element-wise loads
+// take c0 as is and read nv = clamp(D - c0, 0, 8) channels.
 template <bool VEC>
-__device__ __forceinline__ uint4 ldrow(const uint16_t* base, const KeyView& k, uint32_t t, uint32_t c0) {
+__device__ __forceinline__ uint32_t slot_c0(int c0, int D) {
+  return VEC ? (uint32_t)min(c0, D - 8) : (uint32_t)c0;
+}
+__device__ __forceinline__ int slot_nv(int c0, int D) { return max(min(D - c0, 8), 0); }
+
+// Eight 16-bit channels c0..c0+7 of row `t` (clamped by the caller); the
+// element-wise form reads the first nv and zeroes the rest.
+template <bool VEC>
+__device__ __forceinline__ uint4 ldrow(const uint16_t* base, const KeyView& k, uint32_t t, uint32_t c0, int nv = 8) {
   if constexpr (VEC) {
     return *(const uint4*)((const char*)base + (t * k.ss + c0) * 2u);
   } else {
     uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w[e >> 1] |= (uint32_t)base[t * k.ss + (c0 + e) * k.sd] << ((e & 1) * 16);
+    for (int e = 0; e < 8; ++e)
+      if (e < nv) w[e >> 1] |= (uint32_t)base[t * k.ss + (c0 + e) * k.sd] << ((e & 1) * 16);
     return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Eight fp32 channels c0..c0+7 of row `t`, as ldrow (VEC: two 16-byte loads).
+template <bool VEC>
+__device__ __forceinline__ void ldrow32(const float* base, const KeyView& k, uint32_t t, uint32_t c0, int nv,
+                                        float (&f)[8]) {
+  if constexpr (VEC) {
+    const float4 a = *(const float4*)((const char*)base + (t * k.ss + c0) * 4u);
+    const float4 b = *(const float4*)((const char*)base + (t * k.ss + c0 + 4) * 4u);
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = e < nv ? base[t * k.ss + (c0 + e) * k.sd] : 0.f;
   }
 }
 
@@ -78,19 +117,19 @@ __device__ __forceinline__ void unpack8(const uint4& v, float (&f)[8]) {
 // query rows of each KV head's G query heads; qn receives the floored norms
 // per head ([B*H][128] fp32, in the workspace).
 struct QNormArgs {
-  const uint16_t* q;
+  const uint16_t* q;  // element pointer (fp32 queries: reinterpreted)
   int64_t q_b, q_h, q_s, q_d, S;
-  int W, G;
+  int W, G, D;
   float inv_g;
   float* qn;
 };
 
 template <class TT, bool QV>
 __device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, int64_t q_s, int64_t q_d,
-                                  int64_t S, int W, int G, int b, int kv, int tid, float (&acc)[2][8]);
+                                  int64_t S, int W, int G, int D, int b, int kv, int tid, float (&acc)[2][8]);
 template <class TT>
-__device__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g, int tid, float (*s_part)[128],
-                                    float* s_qn, float* s_floor);
+__device__ void floored_query_norms(const float (&acc)[2][8], int W, int D, float inv_g, int tid,
+                                    float (*s_part)[128], float* s_qn, float* s_floor);
 
 template <class TT, bool VEC, bool QV = false>
 __global__ void __launch_bounds__(kThreads) mean_kernel(KeyView k, int64_t chunk, int splits,
@@ -103,31 +142,48 @@ __global__ void __launch_bounds__(kThreads) mean_kernel(KeyView k, int64_t chunk
     __shared__ float s_floor;
     const int b = bh / k.H, kv = bh - b * k.H;
     float acc[2][8];
-    window_group_sums<TT, QV>(qa.q, qa.q_b, qa.q_h, qa.q_s, qa.q_d, qa.S, qa.W, qa.G, b, kv, tid, acc);
-    floored_query_norms<TT>(acc, qa.W, qa.inv_g, tid, s_sum, s_qn, &s_floor);
+    window_group_sums<TT, QV>(qa.q, qa.q_b, qa.q_h, qa.q_s, qa.q_d, qa.S, qa.W, qa.G, qa.D, b, kv, tid, acc);
+    floored_query_norms<TT>(acc, qa.W, qa.D, qa.inv_g, tid, s_sum, s_qn, &s_floor);
     if (tid < 128) qa.qn[(int64_t)bh * 128 + tid] = s_qn[tid];
     return;
   }
-  const uint16_t* base = head_base(k, bh);
   const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
-  for (int64_t t = t0 + rg; t < t1; t += 64) {
-    uint4 v[4];
+  const uint32_t cl = slot_c0<VEC>(8 * c8, k.D);
+  const int nv = slot_nv(8 * c8, k.D);
+  if constexpr (TT::kBytes == 2) {
+    const uint16_t* base = head_base(k, bh);
+    for (int64_t t = t0 + rg; t < t1; t += 64) {
+      uint4 v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = ldrow<VEC>(base, k, min((uint32_t)(t + 16 * i), last), 8u * c8);
+      for (int i = 0; i < 4; ++i) v[i] = ldrow<VEC>(base, k, min((uint32_t)(t + 16 * i), last), cl, nv);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (t + 16 * i < t1) {
-        float f[8];
-        unpack8<TT>(v[i], f);
+      for (int i = 0; i < 4; ++i) {
+        if (t + 16 * i < t1) {
+          float f[8];
+          unpack8<TT>(v[i], f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += f[e];
+          for (int e = 0; e < 8; ++e) acc[e] += f[e];
+        }
       }
     }
-  }
+  } else {
+    const float* base = (const float*)head_base_t<TT>(k, bh);
+    for (int64_t t = t0 + rg; t < t1; t += 64) {
+      float f[4][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) s_sum[rg][8 * c8 + e] = acc[e];
+      for (int i = 0; i < 4; ++i) ldrow32<VEC>(base, k, min((uint32_t)(t + 16 * i), last), cl, nv, f[i]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (t + 16 * i < t1)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[e] += f[i][e];
+    }
+  }
+  // a slot past D (16-byte rows) summed a duplicate: those channels are zero
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s_sum[rg][8 * c8 + e] = 8 * c8 < k.D ? acc[e] : 0.f;
   __syncthreads();
   if (tid < 128) {
     float s = 0.f;
@@ -187,15 +243,20 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
   __shared__ float s_red[kTiles * 256];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
   const int x = blockIdx.x, bh = blockIdx.y;
-  const uint16_t* base = head_base(k, bh);
   if (tid < 128) {
-    // centre = mean rounded to the key dtype (kv_pruning_utils.py:113)
-    s_c[tid] = TT::to_f32(TT::from_f32(head_mean(mean_part, bh, mean_splits, tid, mfac)));
+    // centre = mean rounded to the key dtype (kv_pruning_utils.py:113);
+    // channels past D have none
+    s_c[tid] = tid < k.D ? TT::to_f32(TT::from_f32(head_mean(mean_part, bh, mean_splits, tid, mfac))) : 0.f;
   }
   __syncthreads();
   float cen[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) cen[e] = s_c[8 * n + e];
+  // channel slot 8n..8n+7 of this lane: past D its (duplicate) values are
+  // masked to zero together with the rows past the chunk
+  const uint32_t cl = slot_c0<VEC>(8 * n, k.D);
+  const int nv = slot_nv(8 * n, k.D);
+  const bool ch_ok = 8 * n < k.D;
 
   f32x4 acc[kTiles];
 #pragma unroll
@@ -203,33 +264,62 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
   const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
   const int64_t nblk = (t1 - t0 + 31) / 32;
   const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
-  for (int64_t blk = wave; blk < nblk; blk += kWaves) {
-    const int64_t tb = t0 + blk * 32 + 8 * g;
-    uint4 rows[8];
+  if constexpr (TT::kBytes == 2) {
+    const uint16_t* base = head_base(k, bh);
+    for (int64_t blk = wave; blk < nblk; blk += kWaves) {
+      const int64_t tb = t0 + blk * 32 + 8 * g;
+      uint4 rows[8];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) rows[r] = ldrow<VEC>(base, k, min((uint32_t)(tb + r), last), 8u * n);
-    // Centre in fp32 and round to the key dtype, two tokens of one channel
-    // per conversion, which is already the transposed operand word:
-    // op[i] element r = Kc[token 8g + r][channel 8n + i].  Rows past the end
-    // (clamped loads) are masked to zero after the conversion: a select
-    // around the conversion itself compiled to one branch per element.
-    const int64_t left = t1 - tb;
-    const int nvalid = left >= 8 ? 8 : (left > 0 ? (int)left : 0);
-    uint32_t w[8][4];
+      for (int r = 0; r < 8; ++r) rows[r] = ldrow<VEC>(base, k, min((uint32_t)(tb + r), last), cl, nv);
+      // Centre in fp32 and round to the key dtype, two tokens of one channel
+      // per conversion, which is already the transposed operand word:
+      // op[i] element r = Kc[token 8g + r][channel 8n + i].  Rows past the end
+      // (clamped loads) and channel slots past D are masked to zero after the
+      // conversion: a select around the conversion itself compiled to one
+      // branch per element.
+      const int64_t left = t1 - tb;
+      const int nvalid = !ch_ok ? 0 : left >= 8 ? 8 : (left > 0 ? (int)left : 0);
+      uint32_t w[8][4];
 #pragma unroll
-    for (int rp = 0; rp < 4; ++rp) {
-      float f0[8], f1[8];
-      unpack8<TT>(rows[2 * rp], f0);
-      unpack8<TT>(rows[2 * rp + 1], f1);
-      const uint32_t keep = (2 * rp < nvalid ? 0xffffu : 0u) | (2 * rp + 1 < nvalid ? 0xffff0000u : 0u);
+      for (int rp = 0; rp < 4; ++rp) {
+        float f0[8], f1[8];
+        unpack8<TT>(rows[2 * rp], f0);
+        unpack8<TT>(rows[2 * rp + 1], f1);
+        const uint32_t keep = (2 * rp < nvalid ? 0xffffu : 0u) | (2 * rp + 1 < nvalid ? 0xffff0000u : 0u);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) w[i][rp] = TT::pack2(f0[i] - cen[i], f1[i] - cen[i]) & keep;
+        for (int i = 0; i < 8; ++i) w[i][rp] = TT::pack2(f0[i] - cen[i], f1[i] - cen[i]) & keep;
+      }
+      uint4 op[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) op[i] = make_uint4(w[i][0], w[i][1], w[i][2], w[i][3]);
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) acc[t] = TT::mfma(op[tile_row(t)], op[tile_col(t)], acc[t]);
     }
-    uint4 op[8];
+  } else {
+    // fp32: Kc = K - mean in fp32 (the reference's fp32 subtraction), one
+    // token row per v_mfma_f32_16x16x4_f32 step: at step r lane (g, n)
+    // supplies Kc[token 8g + r][8n + i] as the k = g entry of operand i, so
+    // tile (i, j) accumulates the same C[8m + i][8m' + j] as above
+    const float* base = (const float*)head_base_t<TT>(k, bh);
+    for (int64_t blk = wave; blk < nblk; blk += kWaves) {
+      const int64_t tb = t0 + blk * 32 + 8 * g;
+      float rows[8][8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) op[i] = make_uint4(w[i][0], w[i][1], w[i][2], w[i][3]);
+      for (int r = 0; r < 8; ++r) ldrow32<VEC>(base, k, min((uint32_t)(tb + r), last), cl, nv, rows[r]);
+      const int64_t left = t1 - tb;
+      const int nvalid = !ch_ok ? 0 : left >= 8 ? 8 : (left > 0 ? (int)left : 0);
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) acc[t] = TT::mfma(op[tile_row(t)], op[tile_col(t)], acc[t]);
+      for (int r = 0; r < 8; ++r) {
+        float op[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t bits = __builtin_bit_cast(uint32_t, rows[r][i] - cen[i]);
+          op[i] = __builtin_bit_cast(float, r < nvalid ? bits : 0u);
+        }
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = F32::mfma(op[tile_row(t)], op[tile_col(t)], acc[t]);
+      }
+    }
   }
   // reduce the four waves: lane (g, n) of tile t holds C[8(4g+r)+i][8n+j]
   for (int w = 0; w < kWaves; ++w) {
@@ -254,15 +344,15 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
 // dtype (the einsum output dtype, kv_pruning_utils.py:114) and back to fp32,
 // and the tile writes cov[r][c] = 0.5 (C[r][c] + C[c][r])
 // (kv_pruning_utils.py:115) for r = 8m + i, c = 8n + j and the mirrored
-// entry.  C[c][r] of an off-diagonal tile is the same stored sum (the
-// accumulator holds the upper tiles only); a diagonal tile pairs (m, n)
-// with (n, m).  Tile 0 also writes mu [128].
+// entry, both < D.  C[c][r] of an off-diagonal tile is the same stored sum
+// (the accumulator holds the upper tiles only); a diagonal tile pairs
+// (m, n) with (n, m).  Tile 0 also writes mu [D].
 template <class TT>
 __global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int splits,
                                                           const float* mean_part, int mean_splits,
                                                           float mfac, float* cov, int64_t cs_b, int64_t cs_h,
                                                           int64_t cs_r, int64_t cs_c, float* mu, int64_t ms_b,
-                                                          int64_t ms_h, int64_t ms_c, int H) {
+                                                          int64_t ms_h, int64_t ms_c, int H, int D) {
   __shared__ float s_t[256];
   const int tid = threadIdx.x, t = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
@@ -276,9 +366,11 @@ __global__ void __launch_bounds__(kThreads) covfin_kernel(const float* part, int
   const int r = 8 * m + i, c = 8 * n + j;
   const float rc = s_t[tid];
   const float cr = i == j ? s_t[n * 16 + m] : rc;
-  cb[r * cs_r + c * cs_c] = 0.5f * (rc + cr);
-  if (i != j) cb[c * cs_r + r * cs_c] = 0.5f * (cr + rc);
-  if (t == 0 && tid < 128 && mu)
+  if (r < D && c < D) {
+    cb[r * cs_r + c * cs_c] = 0.5f * (rc + cr);
+    if (i != j) cb[c * cs_r + r * cs_c] = 0.5f * (cr + rc);
+  }
+  if (t == 0 && tid < D && mu)
     mu[b * ms_b + (int64_t)h * ms_h + tid * ms_c] = head_mean(mean_part, bh, mean_splits, tid, mfac);
 }
 
@@ -317,19 +409,31 @@ rot_kernel(const RotArgs a) {
   // this thread's batch is (c, kk) = (e % 128, e / 128): consecutive threads
   // take consecutive c; all loads are issued before any is converted.
   const int64_t rb = b * a.R_sb + (int64_t)h * a.R_sh;
+  const int D = a.k.D;
   constexpr int kPer = NT * 16 * 128 / kThreads;
   uint32_t raw[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int e = tid + i * kThreads, kk = e >> 7, c = e & 127;
-    raw[i] = load_raw(a.R, rb + c * a.R_sd + min(kk, a.Dk - 1) * a.R_sk, a.r_dtype);
+    raw[i] = load_raw(a.R, rb + min(c, D - 1) * a.R_sd + min(kk, a.Dk - 1) * a.R_sk, a.r_dtype);
   }
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int e = tid + i * kThreads, kk = e >> 7, c = e & 127;
-    s_rt[kk][c] = TT::from_f32(kk < a.Dk ? raw_to_f32(raw[i], a.r_dtype) : 0.f);
+    s_rt[kk][c] = TT::from_f32(kk < a.Dk && c < D ? raw_to_f32(raw[i], a.r_dtype) : 0.f);
   }
   __syncthreads();
+  // channel slots 32 ks + 8 g of this lane (past D: see the file comment)
+  uint32_t cl[4];
+  int nv[4];
+  bool cok[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    cl[ks] = slot_c0<VEC>(32 * ks + 8 * g, D);
+    nv[ks] = slot_nv(32 * ks + 8 * g, D);
+    cok[ks] = 32 * ks + 8 * g < D;
+  }
+  const bool dpart = VEC && D < 128;  // launch-uniform
 
   float sc[NT][4];
 #pragma unroll
@@ -353,7 +457,7 @@ rot_kernel(const RotArgs a) {
       const int64_t tok = ts + 16 * tb + n;
       const uint32_t tr = min((uint32_t)min(tok, (int64_t)last), last);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) bk[tb][ks] = ldrow<VEC>(base, a.k, tr, (uint32_t)(32 * ks + 8 * g));
+      for (int ks = 0; ks < 4; ++ks) bk[tb][ks] = ldrow<VEC>(base, a.k, tr, cl[ks], nv[ks]);
     }
   };
   auto compute = [&](uint4 (&bk)[TB][4], int64_t st) {
@@ -364,6 +468,13 @@ rot_kernel(const RotArgs a) {
         if (ts + 16 * tb + n >= t1)
 #pragma unroll
           for (int ks = 0; ks < 4; ++ks) bk[tb][ks] = make_uint4(0, 0, 0, 0);
+    }
+    if (dpart) {  // duplicated slots past D, which would meet R's zero rows
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          if (!cok[ks]) bk[tb][ks] = make_uint4(0, 0, 0, 0);
     }
 #pragma unroll(NT <= 2 ? NT : 1)
     for (int t = 0; t < NT; ++t) {
@@ -435,6 +546,128 @@ rot_kernel(const RotArgs a) {
   }
 }
 
+// fp32 Keys (the reference's update_rotatek on fp32 Keys, and BASELINE
+// config 0's selection at its precision): C^T = R^T K^T on
+// v_mfma_f32_16x16x4_f32 (fp32 products and sums).  Lane (g, n) holds
+// channels 32g .. 32g + 31 of token n of the wave's 16-token step and, in
+// MFMA step ks, supplies channel 32g + ks as the k = g entry of both
+// operands (A = R^T[16t + n][32g + ks] from LDS, B = K[token n][32g + ks]),
+// so the 32 steps sum all 128 channel slots (zero past D on both sides).
+// STORE writes C^T as fp32 (the Keys' dtype), SCORE sums |C^T| per lane.
+// grid (splits, B*H).
+template <int NT, bool VEC, bool SCORE>
+__global__ void __launch_bounds__(kThreads) rot32_kernel(const RotArgs a) {
+  __shared__ __attribute__((aligned(16))) float s_rt[NT * 16][128 + 4];  // R^T, padded rows
+  __shared__ float s_sc[kWaves][NT * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+  const int x = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / a.k.H, h = bh - b * a.k.H;
+  const float* base = (const float*)head_base_t<F32>(a.k, bh);
+  const int D = a.k.D;
+  const int64_t rb = b * a.R_sb + (int64_t)h * a.R_sh;
+  constexpr int kPer = NT * 16 * 128 / kThreads;
+  uint32_t raw[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid + i * kThreads, kk = e >> 7, c = e & 127;
+    raw[i] = load_raw(a.R, rb + min(c, D - 1) * a.R_sd + min(kk, a.Dk - 1) * a.R_sk, a.r_dtype);
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = tid + i * kThreads, kk = e >> 7, c = e & 127;
+    s_rt[kk][c] = kk < a.Dk && c < D ? raw_to_f32(raw[i], a.r_dtype) : 0.f;
+  }
+  __syncthreads();
+
+  float sc[NT][4];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[t][r] = 0.f;
+  const int64_t t0 = (int64_t)x * a.chunk, t1 = min(a.k.S, t0 + a.chunk);
+  const int64_t nstep = (t1 - t0 + 15) / 16;
+  const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
+  // the lane's 32 channels of token n: VEC, eight 16-byte loads (a quad past
+  // D re-reads the row's last quad, D a multiple of 8, and is zeroed);
+  // otherwise element loads of the channels < D
+  auto load = [&](float (&kr)[32], int64_t st) {
+    const int64_t tok = t0 + st * 16 + n;
+    const uint32_t tr = (uint32_t)min(tok, (int64_t)last);
+    const float* row = base + (int64_t)tr * a.k.ss;
+    if constexpr (VEC) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float4 v = *(const float4*)(row + min(32 * g + 4 * j, D - 4));
+        kr[4 * j] = v.x; kr[4 * j + 1] = v.y; kr[4 * j + 2] = v.z; kr[4 * j + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; ++j) kr[j] = 32 * g + j < D ? row[(int64_t)(32 * g + j) * a.k.sd] : 0.f;
+    }
+  };
+  auto compute = [&](float (&kr)[32], int64_t st) {
+    const int64_t tok = t0 + st * 16 + n;
+    const bool tok_ok = tok < t1;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) kr[j] = tok_ok && 32 * g + j < D ? kr[j] : 0.f;
+#pragma unroll(NT <= 2 ? NT : 1)
+    for (int t = 0; t < NT; ++t) {
+      f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q4 = 0; q4 < 8; ++q4) {
+        const float4 av = *(const float4*)&s_rt[16 * t + n][32 * g + 4 * q4];
+        c = F32::mfma(av.x, kr[4 * q4], c);
+        c = F32::mfma(av.y, kr[4 * q4 + 1], c);
+        c = F32::mfma(av.z, kr[4 * q4 + 2], c);
+        c = F32::mfma(av.w, kr[4 * q4 + 3], c);
+      }
+      if constexpr (SCORE) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[t][r] += fabsf(c[r]);
+      } else if (tok_ok) {
+        float* o = (float*)a.out + b * a.o_sb + (int64_t)h * a.o_sh + tok * a.o_ss;
+        const int k0 = 16 * t + 4 * g;
+        if (k0 + 3 < a.Dk && a.o_sd == 1 && (((uintptr_t)(o + k0)) & 15) == 0) {
+          *(float4*)(o + k0) = make_float4(c[0], c[1], c[2], c[3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (k0 + r < a.Dk) o[(k0 + r) * a.o_sd] = c[r];
+        }
+      }
+    }
+  };
+  float kA[32], kB[32];
+  if (wave < nstep) load(kA, wave);
+  for (int64_t st = wave; st < nstep; st += 2 * kWaves) {
+    if (st + kWaves < nstep) load(kB, st + kWaves);
+    compute(kA, st);
+    if (st + kWaves >= nstep) break;
+    if (st + 2 * kWaves < nstep) load(kA, st + 2 * kWaves);
+    compute(kB, st + kWaves);
+  }
+  if constexpr (SCORE) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = sc[t][r];
+        v += shfl_xor(v, 1);
+        v += shfl_xor(v, 2);
+        v += shfl_xor(v, 4);
+        v += shfl_xor(v, 8);
+        if (n == 0) s_sc[wave][16 * t + 4 * g + r] = v;
+      }
+    __syncthreads();
+    for (int kk = tid; kk < NT * 16; kk += kThreads) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) v += s_sc[w][kk];
+      a.spart[((int64_t)bh * a.splits + x) * (NT * 16) + kk] = v;
+    }
+  }
+}
+
 // grid (B*H): scores[c] = (sum of partials in fp64) / S for c < nk;
 // partial rows are `pstride` floats apart.
 __global__ void __launch_bounds__(128) scorefin_kernel(const float* spart, int splits, int pstride, int nk,
@@ -483,27 +716,29 @@ __global__ void __launch_bounds__(128) topk_kernel(const double* scores, int64_t
 }
 
 // grid (B*H), 128 threads: R_partial[:, kk] = dtype(R_full[:, idx[kk]]);
-// delta_mu = dtype(mu - (mu Rp) Rp^T) with Rp already in the key dtype.
+// delta_mu = dtype(mu - (mu Rp) Rp^T) with Rp already in the key dtype
+// (TT = F32: both stay fp32).  Rows d < D (head_dim).
 template <class TT>
 __global__ void __launch_bounds__(128) gather_kernel(const void* R, int r_dtype, int64_t R_sb, int64_t R_sh,
                                                      int64_t R_sd, int64_t R_sk, const int64_t* idx,
                                                      int64_t i_b, int64_t i_h, int64_t i_k, int k,
                                                      const float* mu, int64_t u_b, int64_t u_h, int64_t u_c,
-                                                     uint16_t* Rp, int64_t p_b, int64_t p_h, int64_t p_d,
-                                                     int64_t p_k, uint16_t* dm, int64_t d_b, int64_t d_h,
-                                                     int64_t d_c, int H) {
+                                                     void* Rp, int64_t p_b, int64_t p_h, int64_t p_d,
+                                                     int64_t p_k, void* dm, int64_t d_b, int64_t d_h,
+                                                     int64_t d_c, int H, int D) {
   __shared__ float s_mu[128];
   __shared__ float s_proj[128];
   __shared__ int64_t s_col[128];
-  __shared__ uint16_t s_rp[128][130];  // R_partial in the key dtype, row d
+  __shared__ float s_rp[128][129];  // R_partial (rounded to the key dtype), row d
   const int d = threadIdx.x, bh = blockIdx.x;
   const int b = bh / H, h = bh - b * H;
-  s_mu[d] = mu[b * u_b + (int64_t)h * u_h + d * u_c];
+  const int dd = min(d, D - 1);
+  s_mu[d] = d < D ? mu[b * u_b + (int64_t)h * u_h + dd * u_c] : 0.f;
   if (d < k) s_col[d] = idx[b * i_b + (int64_t)h * i_h + d * i_k];
   __syncthreads();
   // row d of R_partial, 32 columns per pass: all loads of a pass are issued
   // before any store (the stores could alias them otherwise)
-  const int64_t rb = b * R_sb + (int64_t)h * R_sh + d * R_sd;
+  const int64_t rb = b * R_sb + (int64_t)h * R_sh + dd * R_sd;
   for (int k0 = 0; k0 < k; k0 += 32) {
     uint32_t raw[32];
     if (r_dtype == 2) {
@@ -516,24 +751,34 @@ __global__ void __launch_bounds__(128) gather_kernel(const void* R, int r_dtype,
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
       if (k0 + j < k) {
-        const uint16_t v = TT::from_f32(raw_to_f32(raw[j], r_dtype));
-        s_rp[d][k0 + j] = v;
-        Rp[b * p_b + (int64_t)h * p_h + d * p_d + (k0 + j) * p_k] = v;
+        const auto v = TT::from_f32(raw_to_f32(raw[j], r_dtype));
+        s_rp[d][k0 + j] = d < D ? TT::to_f32(v) : 0.f;
+        if (d < D) {
+          if constexpr (TT::kBytes == 4)
+            ((uint32_t*)Rp)[b * p_b + (int64_t)h * p_h + d * p_d + (k0 + j) * p_k] = v;
+          else
+            ((uint16_t*)Rp)[b * p_b + (int64_t)h * p_h + d * p_d + (k0 + j) * p_k] = v;
+        }
       }
     }
   }
   __syncthreads();
   if (d < k) {
     float s = 0.f;
-    for (int e = 0; e < 128; ++e) s += s_mu[e] * TT::to_f32(s_rp[e][d]);
+    for (int e = 0; e < D; ++e) s += s_mu[e] * s_rp[e][d];
     s_proj[d] = s;
   }
   __syncthreads();
+  if (d >= D) return;
   float p = 0.f;
-  for (int kk = 0; kk < k; ++kk) p += s_proj[kk] * TT::to_f32(s_rp[d][kk]);
+  for (int kk = 0; kk < k; ++kk) p += s_proj[kk] * s_rp[d][kk];
   float dmu = s_mu[d] - p;           // fp32, then the key dtype (two roundings,
   asm volatile("" : "+v"(dmu));      // as the reference; see qweight_kernel)
-  dm[b * d_b + (int64_t)h * d_h + d * d_c] = TT::from_f32(dmu);
+  const auto o = TT::from_f32(dmu);
+  if constexpr (TT::kBytes == 4)
+    ((uint32_t*)dm)[b * d_b + (int64_t)h * d_h + d * d_c] = o;
+  else
+    ((uint16_t*)dm)[b * d_b + (int64_t)h * d_h + d * d_c] = o;
 }
 
 // grid (B*H_kv), 256 threads: query-aware weighting of one covariance
@@ -556,45 +801,75 @@ constexpr int kQHeads = 8;  // query heads whose window rows are loaded together
 // 8 c8..8 c8+7, G in order, kQHeads heads' loads issued at a time.
 template <class TT, bool QV>
 __device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, int64_t q_s, int64_t q_d,
-                                  int64_t S, int W, int G, int b, int kv, int tid, float (&acc)[2][8]) {
+                                  int64_t S, int W, int G, int D, int b, int kv, int tid, float (&acc)[2][8]) {
   const int rs = tid >> 4, c8 = tid & 15;
   const int w0 = rs, w1 = rs + 16;
-  const uint16_t* qb = q + b * q_b + (int64_t)(kv * G) * q_h + (S - W) * q_s + (int64_t)(8 * c8) * q_d;
+  // channel slot 8 c8.. (past D: the last slot re-read, or no element loads;
+  // zeroed in floored_query_norms)
+  const int c0 = QV ? min(8 * c8, D - 8) : 8 * c8, nv = slot_nv(8 * c8, D);
+  const int64_t off = b * q_b + (int64_t)(kv * G) * q_h + (S - W) * q_s + (int64_t)c0 * q_d;
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
   for (int g0 = 0; g0 < G; g0 += kQHeads) {
-    uint4 v[kQHeads][2];
+    float f[kQHeads][2][8];
+    if constexpr (TT::kBytes == 2) {
+      const uint16_t* qb = q + off;
+      uint4 v[kQHeads][2];
 #pragma unroll
-    for (int u = 0; u < kQHeads; ++u)
+      for (int u = 0; u < kQHeads; ++u)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int w = j ? w1 : w0;
-        v[u][j] = make_uint4(0u, 0u, 0u, 0u);
-        if (g0 + u < G && w < W) {
-          const uint16_t* p = qb + (int64_t)(g0 + u) * q_h + (int64_t)w * q_s;
-          if constexpr (QV) {
-            v[u][j] = *(const uint4*)p;
-          } else {
-            uint32_t wd[4] = {0, 0, 0, 0};
+        for (int j = 0; j < 2; ++j) {
+          const int w = j ? w1 : w0;
+          v[u][j] = make_uint4(0u, 0u, 0u, 0u);
+          if (g0 + u < G && w < W) {
+            const uint16_t* p = qb + (int64_t)(g0 + u) * q_h + (int64_t)w * q_s;
+            if constexpr (QV) {
+              v[u][j] = *(const uint4*)p;
+            } else {
+              uint32_t wd[4] = {0, 0, 0, 0};
 #pragma unroll
-            for (int e = 0; e < 8; ++e) wd[e >> 1] |= (uint32_t)p[e * q_d] << ((e & 1) * 16);
-            v[u][j] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+              for (int e = 0; e < 8; ++e)
+                if (e < nv) wd[e >> 1] |= (uint32_t)p[e * q_d] << ((e & 1) * 16);
+              v[u][j] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+            }
           }
         }
-      }
+#pragma unroll
+      for (int u = 0; u < kQHeads; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) unpack8<TT>(v[u][j], f[u][j]);
+    } else {
+      const float* qb = (const float*)q + off;
+#pragma unroll
+      for (int u = 0; u < kQHeads; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int w = j ? w1 : w0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[u][j][e] = 0.f;
+          if (g0 + u < G && w < W) {
+            const float* p = qb + (int64_t)(g0 + u) * q_h + (int64_t)w * q_s;
+            if constexpr (QV) {
+              const float4 a = *(const float4*)p, c = *(const float4*)(p + 4);
+              f[u][j][0] = a.x; f[u][j][1] = a.y; f[u][j][2] = a.z; f[u][j][3] = a.w;
+              f[u][j][4] = c.x; f[u][j][5] = c.y; f[u][j][6] = c.z; f[u][j][7] = c.w;
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                if (e < nv) f[u][j][e] = p[e * q_d];
+            }
+          }
+        }
+    }
 #pragma unroll
     for (int u = 0; u < kQHeads; ++u)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (g0 + u < G) {
-          float f[8];
-          unpack8<TT>(v[u][j], f);
+      for (int j = 0; j < 2; ++j)
+        if (g0 + u < G)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[j][e] += f[e];
-        }
-      }
+          for (int e = 0; e < 8; ++e) acc[j][e] += f[u][j][e];
   }
 }
 
@@ -603,11 +878,12 @@ __device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, i
 // first and then to the dtype, as torch's MeanOps does; the empty asm keeps
 // the product in an fp32 register, otherwise the multiply and the
 // conversion fuse into one v_fma_mix, a single rounding), the per-channel
-// L2 norms over the window, and the floor at 1e-3 x the lower median (the
-// norm of rank 63, ties by index).  Leaves s_qn[c] = the floored norms.
+// L2 norms over the window, and the floor at 1e-3 x the lower median of the
+// D norms (the norm of rank (D - 1) / 2, ties by index).  Leaves s_qn[c] =
+// the floored norms (0 past D).
 template <class TT>
-__device__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g, int tid, float (*s_part)[128],
-                                    float* s_qn, float* s_floor) {
+__device__ void floored_query_norms(const float (&acc)[2][8], int W, int D, float inv_g, int tid,
+                                    float (*s_part)[128], float* s_qn, float* s_floor) {
   const int rs = tid >> 4, c8 = tid & 15;
   float sq[8];
 #pragma unroll
@@ -631,11 +907,12 @@ __device__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g
     float t = 0.f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) t += s_part[r][tid];
-    s_qn[tid] = sqrtf(t);
+    // channels past D rank above every norm (they are not ranked themselves)
+    s_qn[tid] = tid < D ? sqrtf(t) : INFINITY;
   }
   __syncthreads();
   float v = 0.f;
-  if (tid < 128) {
+  if (tid < D) {
     v = s_qn[tid];
     int rank = 0;
 #pragma unroll
@@ -645,34 +922,36 @@ __device__ void floored_query_norms(const float (&acc)[2][8], int W, float inv_g
 #pragma unroll
       for (int e = 0; e < 4; ++e) rank += (uu[e] < v) || (uu[e] == v && 4 * j4 + e < tid);
     }
-    if (rank == 63) *s_floor = 1e-3f * v;  // exactly one thread when no norm is NaN
+    if (rank == (D - 1) / 2) *s_floor = 1e-3f * v;  // exactly one thread when no norm is NaN
   }
   __syncthreads();
   // torch.median of a row holding a NaN is NaN, and so is the clamp against
   // it: every weight of the head becomes NaN (written after the ranks, which
-  // a NaN leaves without a thread of rank 63)
-  if (tid < 128 && isnan(v)) *s_floor = __builtin_nanf("");
+  // a NaN leaves without a thread of the median's rank)
+  if (tid < D && isnan(v)) *s_floor = __builtin_nanf("");
   __syncthreads();
   if (tid < 128) {
     const float fl = *s_floor;
-    s_qn[tid] = isnan(fl) ? fl : fmaxf(v, fl);
+    s_qn[tid] = tid >= D ? 0.f : isnan(fl) ? fl : fmaxf(v, fl);
   }
   __syncthreads();
 }
 
 // 1e-4 max(mean|diag(C o qn qn^T)|, 1e-6) from the diagonal dg_in[c] =
-// C[c][c] (threads 0..127; the sum is a fixed xor tree in each of waves 0
-// and 1, then the two halves), as the weighted covariance's ridge.
-__device__ __forceinline__ float weighted_ridge(float diag, const float* s_qn, int tid, float* s_wsum) {
+// C[c][c] (threads 0..D-1; the sum is a fixed xor tree in each of waves 0
+// and 1, then the two halves, times torch's mean factor rfac = fp32(1/D)),
+// as the weighted covariance's ridge.
+__device__ __forceinline__ float weighted_ridge(float diag, const float* s_qn, int tid, int D, float rfac,
+                                                float* s_wsum) {
   if (tid < 128) {
     const float qd = s_qn[tid];
-    float dg = fabsf(diag * (qd * qd));
+    float dg = tid < D ? fabsf(diag * (qd * qd)) : 0.f;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) dg += shfl_xor(dg, off);
     if ((tid & 63) == 0) s_wsum[tid >> 6] = dg;
   }
   __syncthreads();
-  return 1e-4f * fmaxf((s_wsum[0] + s_wsum[1]) * (1.f / 128.f), 1e-6f);
+  return 1e-4f * fmaxf((s_wsum[0] + s_wsum[1]) * rfac, 1e-6f);
 }
 
 // grid (B*H_kv), 256 threads: query-aware weighting of one covariance
@@ -690,9 +969,9 @@ __device__ __forceinline__ float weighted_ridge(float diag, const float* s_qn, i
 template <class TT, bool CV, bool QV>
 __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t c_b, int64_t c_h, int64_t c_r,
                                                       int64_t c_c, const uint16_t* q, int64_t q_b, int64_t q_h,
-                                                      int64_t q_s, int64_t q_d, int64_t S, int W, int G,
-                                                      float inv_g, float* out, int64_t o_b, int64_t o_h,
-                                                      int64_t o_r, int64_t o_c, int H) {
+                                                      int64_t q_s, int64_t q_d, int64_t S, int W, int G, int D,
+                                                      float inv_g, float rfac, float* out, int64_t o_b,
+                                                      int64_t o_h, int64_t o_r, int64_t o_c, int H) {
   constexpr int CP = 129;
   __shared__ float s_C[128 * CP];
   __shared__ float s_part[16][128];
@@ -703,24 +982,28 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
   const int bh = blockIdx.x, b = bh / H, kv = bh - b * H;
   const float* C = cov + b * c_b + (int64_t)kv * c_h;
 
-  // ---- covariance loads (64 floats per thread)
+  // ---- covariance loads (64 floats per thread; entries past D are zero,
+  // their loads re-read an in-bounds entry)
   float cv[64];
-  if constexpr (CV) {
+  if constexpr (CV) {  // (D a multiple of 4)
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int e4 = tid + 256 * i, r = e4 >> 5, c = (e4 & 31) * 4;
-      const float4 v = *(const float4*)(C + r * c_r + c);
-      cv[4 * i] = v.x, cv[4 * i + 1] = v.y, cv[4 * i + 2] = v.z, cv[4 * i + 3] = v.w;
+      const bool ok = r < D && c < D;
+      const float4 v = *(const float4*)(C + min(r, D - 1) * c_r + min(c, D - 4));
+      cv[4 * i] = ok ? v.x : 0.f, cv[4 * i + 1] = ok ? v.y : 0.f, cv[4 * i + 2] = ok ? v.z : 0.f,
+      cv[4 * i + 3] = ok ? v.w : 0.f;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < 64; ++i) {
-      const int e = tid + 256 * i;
-      cv[i] = C[(e >> 7) * c_r + (e & 127) * c_c];
+      const int e = tid + 256 * i, r = e >> 7, c = e & 127;
+      const float v = C[min(r, D - 1) * c_r + min(c, D - 1) * c_c];
+      cv[i] = r < D && c < D ? v : 0.f;
     }
   }
   float acc[2][8];
-  window_group_sums<TT, QV>(q, q_b, q_h, q_s, q_d, S, W, G, b, kv, tid, acc);
+  window_group_sums<TT, QV>(q, q_b, q_h, q_s, q_d, S, W, G, D, b, kv, tid, acc);
 
   // ---- the covariance into LDS
   if constexpr (CV) {
@@ -737,8 +1020,8 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
       s_C[(e >> 7) * CP + (e & 127)] = cv[i];
     }
   }
-  floored_query_norms<TT>(acc, W, inv_g, tid, s_part, s_qn, &s_floor);
-  const float ridge = weighted_ridge(tid < 128 ? s_C[tid * CP + tid] : 0.f, s_qn, tid, s_wsum);
+  floored_query_norms<TT>(acc, W, D, inv_g, tid, s_part, s_qn, &s_floor);
+  const float ridge = weighted_ridge(tid < 128 ? s_C[tid * CP + tid] : 0.f, s_qn, tid, D, rfac, s_wsum);
   // ---- out[r][c] = 0.5 (C[r][c] w + C[c][r] w) + ridge [r == c], w = qn[r] qn[c]
   float* O = out + b * o_b + (int64_t)kv * o_h;
 #pragma unroll 8
@@ -746,7 +1029,7 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
     const int e = tid + 256 * i, r = e >> 7, c = e & 127;
     const float w = s_qn[r] * s_qn[c];
     const float a = s_C[r * CP + c] * w, bt = s_C[c * CP + r] * w;
-    O[r * o_r + c * o_c] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
+    if (r < D && c < D) O[r * o_r + c * o_c] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
   }
 }
 
@@ -764,7 +1047,8 @@ __global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, 
                                                              const float* mean_part, int mean_splits, float mfac,
                                                              const float* qn, float* cov, int64_t cs_b,
                                                              int64_t cs_h, int64_t cs_r, int64_t cs_c, float* mu,
-                                                             int64_t ms_b, int64_t ms_h, int64_t ms_c, int H) {
+                                                             int64_t ms_b, int64_t ms_h, int64_t ms_c, int H, int D,
+                                                             float rfac) {
   __shared__ float s_t[256];
   __shared__ __align__(16) float s_qn[128];
   __shared__ float s_wsum[2];
@@ -784,7 +1068,7 @@ __global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, 
   const float dx = TT::to_f32(TT::from_f32(dsum));
   const float diag = 0.5f * (dx + dx);  // the symmetrised diagonal, as covfin writes it
   __syncthreads();
-  const float ridge = weighted_ridge(diag, s_qn, tid, s_wsum);
+  const float ridge = weighted_ridge(diag, s_qn, tid, D, rfac, s_wsum);
   const int i = tile_row(t), j = tile_col(t), m = tid >> 4, n = tid & 15;
   float* cb = cov + b * cs_b + (int64_t)h * cs_h;
   const int r = 8 * m + i, c = 8 * n + j;
@@ -793,9 +1077,11 @@ __global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, 
   const float sym = 0.5f * (rc + cr), symt = 0.5f * (cr + rc);
   const float w = s_qn[r] * s_qn[c];
   const float a = sym * w, bt = symt * w;
-  cb[r * cs_r + c * cs_c] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
-  if (i != j) cb[c * cs_r + r * cs_c] = 0.5f * (bt + a);
-  if (t == 0 && tid < 128 && mu)
+  if (r < D && c < D) {
+    cb[r * cs_r + c * cs_c] = 0.5f * (a + bt) + (r == c ? ridge : 0.f);
+    if (i != j) cb[c * cs_r + r * cs_c] = 0.5f * (bt + a);
+  }
+  if (t == 0 && tid < D && mu)
     mu[b * ms_b + (int64_t)h * ms_h + tid * ms_c] = head_mean(mean_part, bh, mean_splits, tid, mfac);
 }
 
@@ -812,14 +1098,26 @@ using namespace rk::prefill;
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Keys descriptor [B, H, S, 128] (16-bit float).  Sets the view and the
-// fast-path flag.
+// Row loads of 16 bytes along the last dim: unit channel stride, 16-byte
+// aligned rows and base, whole 8-channel slots (D a multiple of 8).
+bool rows_vec(const rk_tensor* t, int64_t D) {
+  if (D % 8 != 0) return false;
+  const int64_t per16 = 16 / rk::dtype_size(t->dtype);
+  if (t->stride[t->ndim - 1] != 1 && t->shape[t->ndim - 1] > 1) return false;
+  for (int i = 0; i < t->ndim - 1; ++i)
+    if (t->shape[i] > 1 && (t->stride[i] % per16) != 0) return false;
+  return (((uintptr_t)t->data) & 15) == 0;
+}
+
+// Keys descriptor [B, H, S, D] (F16, BF16 or F32; 1 <= D <= 128).  Sets the
+// view and the fast-path flag.
 int key_view(const rk_tensor* t, KeyView* k, bool* vec) {
   int st = rk::check_desc(t, 4);
   if (st) return st;
-  if (!rk::is_half(t->dtype)) return RK_ERR_DTYPE;
-  if (t->shape[3] != 128) return RK_ERR_HEAD_DIM;
-  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1) * t->stride[2] : 0) + 127 * t->stride[3] + 8;
+  if (!rk::is_float_param(t->dtype)) return RK_ERR_DTYPE;
+  const int64_t D = t->shape[3];
+  if (D < 1 || D > 128) return RK_ERR_HEAD_DIM;
+  const int64_t span = (t->shape[2] > 0 ? (t->shape[2] - 1) * t->stride[2] : 0) + (D - 1) * t->stride[3] + 8;
   if (span >= (INT64_C(1) << 31) || t->stride[2] >= (INT64_C(1) << 31)) return RK_ERR_STRIDE;
   if (t->shape[0] * t->shape[1] > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
   k->data = (const uint16_t*)t->data;
@@ -829,7 +1127,8 @@ int key_view(const rk_tensor* t, KeyView* k, bool* vec) {
   k->sd = (uint32_t)t->stride[3];
   k->S = t->shape[2];
   k->H = (int32_t)t->shape[1];
-  *vec = rk::vec_ok(t);
+  k->D = (int32_t)D;
+  *vec = rows_vec(t, D);
   return RK_OK;
 }
 
@@ -900,8 +1199,10 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
   float* mpart = (float*)((char*)ws + p.off_mean);
   float* cpart = (float*)((char*)ws + p.off_cov);
   const dim3 gm((unsigned)p.mean_splits, (unsigned)bh), gc((unsigned)p.cov_splits, (unsigned)bh);
-  // mean over the token dim of [B, H, S, 128] (kv_pruning_utils.py:112)
-  const float mfac = rk::mean_factor(bh * 128, bh * k.S * 128);
+  // mean over the token dim of [B, H, S, D] (kv_pruning_utils.py:112)
+  const float mfac = rk::mean_factor(bh * k.D, bh * k.S * k.D);
+  // the ridge's mean over the D diagonal entries of each [D, D] matrix
+  const float rfac = rk::mean_factor(bh, bh * k.D);
   // with the weighting, the mean launch has one more column per head that
   // forms the head's floored query norms
   QNormArgs qa;
@@ -911,7 +1212,7 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
   if (qw) {
     const rk_tensor* q = qw->q;
     qa = QNormArgs{(const uint16_t*)q->data, q->stride[0], q->stride[1], q->stride[2], q->stride[3], q->shape[2],
-                   qw->W, (int)qw->G, qw->inv_g, qn};
+                   qw->W, (int)qw->G, k.D, qw->inv_g, qn};
     gmq.x += 1;
   }
   if (vec) {
@@ -937,15 +1238,24 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
     hipLaunchKernelGGL((covfin_qw_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart,
                        p.cov_splits, mpart, p.mean_splits, mfac, qn, cov, cov_t->stride[0], cov_t->stride[1],
                        cov_t->stride[2], cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0,
-                       mu_t ? mu_t->stride[1] : 0, mu_t ? mu_t->stride[2] : 0, k.H);
+                       mu_t ? mu_t->stride[1] : 0, mu_t ? mu_t->stride[2] : 0, k.H, k.D, rfac);
     return hipGetLastError();
   }
   hipLaunchKernelGGL((covfin_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, p.cov_splits,
-                     mpart,
-                     p.mean_splits, mfac, cov, cov_t->stride[0], cov_t->stride[1], cov_t->stride[2],
+                     mpart, p.mean_splits, mfac, cov, cov_t->stride[0], cov_t->stride[1], cov_t->stride[2],
                      cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0, mu_t ? mu_t->stride[1] : 0,
-                     mu_t ? mu_t->stride[2] : 0, k.H);
+                     mu_t ? mu_t->stride[2] : 0, k.H, k.D);
   return hipGetLastError();
+}
+
+hipError_t launch_cov_any(int dtype, const KeyView& k, bool vec, const CovPlan& p, int64_t B, float* ws,
+                          float* cov, const rk_tensor* cov_t, float* mu, const rk_tensor* mu_t, hipStream_t s,
+                          const QwArgs* qw = nullptr) {
+  switch (dtype) {
+    case RK_F16: return launch_cov<rk::F16>(k, vec, p, B, ws, cov, cov_t, mu, mu_t, s, qw);
+    case RK_BF16: return launch_cov<rk::BF16>(k, vec, p, B, ws, cov, cov_t, mu, mu_t, s, qw);
+    default: return launch_cov<rk::F32>(k, vec, p, B, ws, cov, cov_t, mu, mu_t, s, qw);
+  }
 }
 
 }  // namespace
@@ -959,8 +1269,8 @@ extern "C" int rk_key_covariance_check(const rk_tensor* keys, const rk_tensor* m
   if (st) return st;
   const int64_t B = keys->shape[0], H = keys->shape[1];
   if (!cov_out) return RK_ERR_NULL;
-  if ((st = check_f32_out(cov_out, 4, B, H, 128, RK_F32))) return st;
-  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, 128, RK_F32))) return st;
+  if ((st = check_f32_out(cov_out, 4, B, H, k.D, RK_F32))) return st;
+  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, k.D, RK_F32))) return st;
   const int cus = resolve_cus(num_cus, &st);
   if (st) return st;
   if (workspace_bytes) *workspace_bytes = cov_plan(B, H, k.S, cus).total;
@@ -975,46 +1285,40 @@ extern "C" int rk_key_covariance(const rk_tensor* keys, const rk_tensor* mean_ou
   if (st) return st;
   const int64_t B = keys->shape[0], H = keys->shape[1];
   if (!cov_out) return RK_ERR_NULL;
-  if ((st = check_f32_out(cov_out, 4, B, H, 128, RK_F32))) return st;
-  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, 128, RK_F32))) return st;
+  if ((st = check_f32_out(cov_out, 4, B, H, k.D, RK_F32))) return st;
+  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, k.D, RK_F32))) return st;
   const int cus = resolve_cus(0, &st);
   if (st) return st;
   const CovPlan p = cov_plan(B, H, k.S, cus);
   if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < p.total) return RK_ERR_WORKSPACE;
   if (B * H == 0) return RK_OK;
   if ((k.S > 0 && !k.data) || !cov_out->data) return RK_ERR_NULL;
-  hipStream_t s = (hipStream_t)stream;
-  const hipError_t e =
-      keys->dtype == RK_F16
-          ? launch_cov<rk::F16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
-                                mean_out ? (float*)mean_out->data : nullptr, mean_out, s)
-          : launch_cov<rk::BF16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
-                                 mean_out ? (float*)mean_out->data : nullptr, mean_out, s);
+  const hipError_t e = launch_cov_any(keys->dtype, k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
+                                      mean_out ? (float*)mean_out->data : nullptr, mean_out, (hipStream_t)stream);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 
 namespace {
 
-// Queries of the fused weighting: [B, H_kv * G, S_q, 128] in the key dtype,
+// Queries of the fused weighting: [B, H_kv * G, S_q, D] in the key dtype,
 // window = min(window, S_q) rows (window 1..32).
 int check_queries(const rk_tensor* keys, const rk_tensor* q, int64_t G, int32_t window, QwArgs* qw) {
   if (!q) return RK_ERR_NULL;
   int st = rk::check_desc(q, 4);
   if (st) return st;
   if (q->dtype != keys->dtype) return RK_ERR_DTYPE;
-  if (q->shape[3] != 128) return RK_ERR_HEAD_DIM;
+  if (q->shape[3] != keys->shape[3]) return RK_ERR_HEAD_DIM;
   if (G <= 0 || q->shape[0] != keys->shape[0] || q->shape[1] != keys->shape[1] * G) return RK_ERR_HEADS;
   if (window <= 0 || window > 32) return RK_ERR_ARG;
-  const int64_t S = q->shape[2];
+  const int64_t S = q->shape[2], D = q->shape[3];
   qw->q = q;
   qw->G = G;
   qw->W = (int)(S < window ? S : window);
   if (keys->shape[0] * keys->shape[1] > 0 && qw->W == 0) return RK_ERR_SHAPE;
   const int64_t B = keys->shape[0], H = keys->shape[1];
-  // the group mean over dim 2 of [B, H_kv, G, W, 128] (kv_pruning_utils.py:127-129)
-  qw->inv_g = rk::mean_factor(B * H * qw->W * 128, B * H * G * qw->W * 128);
-  qw->vec = q->stride[3] == 1 && q->stride[2] % 8 == 0 && q->stride[1] % 8 == 0 && q->stride[0] % 8 == 0 &&
-            ((uintptr_t)q->data & 15) == 0;
+  // the group mean over dim 2 of [B, H_kv, G, W, D] (kv_pruning_utils.py:127-129)
+  qw->inv_g = rk::mean_factor(B * H * qw->W * D, B * H * G * qw->W * D);
+  qw->vec = rows_vec(q, D);
   return RK_OK;
 }
 
@@ -1038,8 +1342,8 @@ extern "C" int rk_key_covariance_weighted(const rk_tensor* keys, const rk_tensor
   if (st) return st;
   const int64_t B = keys->shape[0], H = keys->shape[1];
   if (!cov_out) return RK_ERR_NULL;
-  if ((st = check_f32_out(cov_out, 4, B, H, 128, RK_F32))) return st;
-  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, 128, RK_F32))) return st;
+  if ((st = check_f32_out(cov_out, 4, B, H, k.D, RK_F32))) return st;
+  if (mean_out && (st = check_f32_out(mean_out, 3, B, H, k.D, RK_F32))) return st;
   QwArgs qw;
   if ((st = check_queries(keys, queries, num_kv_groups, window, &qw))) return st;
   const int cus = resolve_cus(0, &st);
@@ -1048,23 +1352,19 @@ extern "C" int rk_key_covariance_weighted(const rk_tensor* keys, const rk_tensor
   if (!workspace || (((uintptr_t)workspace) & 255) || workspace_bytes < p.total) return RK_ERR_WORKSPACE;
   if (B * H == 0) return RK_OK;
   if ((k.S > 0 && !k.data) || !cov_out->data || !queries->data) return RK_ERR_NULL;
-  hipStream_t s = (hipStream_t)stream;
-  const hipError_t e =
-      keys->dtype == RK_F16
-          ? launch_cov<rk::F16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
-                                mean_out ? (float*)mean_out->data : nullptr, mean_out, s, &qw)
-          : launch_cov<rk::BF16>(k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
-                                 mean_out ? (float*)mean_out->data : nullptr, mean_out, s, &qw);
+  const hipError_t e = launch_cov_any(keys->dtype, k, vec, p, B, (float*)workspace, (float*)cov_out->data, cov_out,
+                                      mean_out ? (float*)mean_out->data : nullptr, mean_out, (hipStream_t)stream,
+                                      &qw);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 
 namespace {
 
-int check_rotation(const rk_tensor* R, int64_t B, int64_t H, int64_t* Dk) {
+int check_rotation(const rk_tensor* R, int64_t B, int64_t H, int64_t D, int64_t* Dk) {
   int st = rk::check_desc(R, 4);
   if (st) return st;
   if (!rk::is_float_param(R->dtype)) return RK_ERR_DTYPE;
-  if (R->shape[0] != B || R->shape[1] != H || R->shape[2] != 128) return RK_ERR_SHAPE;
+  if (R->shape[0] != B || R->shape[1] != H || R->shape[2] != D) return RK_ERR_SHAPE;
   *Dk = R->shape[3];
   if (*Dk < 1 || *Dk > 128) return RK_ERR_KEEP_DIM;
   return RK_OK;
@@ -1072,10 +1372,17 @@ int check_rotation(const rk_tensor* R, int64_t B, int64_t H, int64_t* Dk) {
 
 template <class TT, int NT, bool SCORE>
 hipError_t launch_rot(const RotArgs& a, bool vec, dim3 grid, hipStream_t s) {
-  if (vec)
-    hipLaunchKernelGGL((rot_kernel<TT, NT, true, SCORE>), grid, dim3(kThreads), 0, s, a);
-  else
-    hipLaunchKernelGGL((rot_kernel<TT, NT, false, SCORE>), grid, dim3(kThreads), 0, s, a);
+  if constexpr (TT::kBytes == 4) {
+    if (vec)
+      hipLaunchKernelGGL((rot32_kernel<NT, true, SCORE>), grid, dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((rot32_kernel<NT, false, SCORE>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((rot_kernel<TT, NT, true, SCORE>), grid, dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((rot_kernel<TT, NT, false, SCORE>), grid, dim3(kThreads), 0, s, a);
+  }
   return hipGetLastError();
 }
 
@@ -1088,6 +1395,14 @@ hipError_t launch_rot_nt(int nt, bool score, const RotArgs& a, bool vec, dim3 gr
     case 3:
     case 4: return launch_rot<TT, 4, false>(a, vec, grid, s);
     default: return launch_rot<TT, 8, false>(a, vec, grid, s);
+  }
+}
+
+hipError_t launch_rot_any(int dtype, int nt, bool score, const RotArgs& a, bool vec, dim3 grid, hipStream_t s) {
+  switch (dtype) {
+    case RK_F16: return launch_rot_nt<rk::F16>(nt, score, a, vec, grid, s);
+    case RK_BF16: return launch_rot_nt<rk::BF16>(nt, score, a, vec, grid, s);
+    default: return launch_rot_nt<rk::F32>(nt, score, a, vec, grid, s);
   }
 }
 
@@ -1114,7 +1429,7 @@ extern "C" int rk_rotate_keys(const rk_tensor* keys, const rk_tensor* R_partial,
   if (st) return st;
   const int64_t B = keys->shape[0], H = keys->shape[1];
   int64_t Dk = 0;
-  if ((st = check_rotation(R_partial, B, H, &Dk))) return st;
+  if ((st = check_rotation(R_partial, B, H, k.D, &Dk))) return st;
   if ((st = rk::check_desc(out, 4))) return st;
   if (out->dtype != keys->dtype) return RK_ERR_DTYPE;
   if (out->shape[0] != B || out->shape[1] != H || out->shape[2] != k.S || out->shape[3] != Dk)
@@ -1135,9 +1450,7 @@ extern "C" int rk_rotate_keys(const rk_tensor* keys, const rk_tensor* R_partial,
   a.chunk = cdiv(k.S, a.splits);
   const dim3 grid((unsigned)a.splits, (unsigned)(B * H));
   const int nt = (int)cdiv(Dk, 16);
-  hipStream_t s = (hipStream_t)stream;
-  const hipError_t e = keys->dtype == RK_F16 ? launch_rot_nt<rk::F16>(nt, false, a, vec, grid, s)
-                                             : launch_rot_nt<rk::BF16>(nt, false, a, vec, grid, s);
+  const hipError_t e = launch_rot_any(keys->dtype, nt, false, a, vec, grid, (hipStream_t)stream);
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 
@@ -1150,7 +1463,7 @@ extern "C" int rk_channel_scores_check(const rk_tensor* keys, const rk_tensor* R
   if (st) return st;
   const int64_t B = keys->shape[0], H = keys->shape[1];
   int64_t Dk = 0;
-  if ((st = check_rotation(R_full, B, H, &Dk))) return st;
+  if ((st = check_rotation(R_full, B, H, k.D, &Dk))) return st;
   if (scores_out && (st = check_f32_out(scores_out, 3, B, H, Dk, RK_F64))) return st;
   const int cus = resolve_cus(num_cus, &st);
   if (st) return st;
@@ -1167,7 +1480,7 @@ extern "C" int rk_channel_scores(const rk_tensor* keys, const rk_tensor* R_full,
   if (st) return st;
   const int64_t B = keys->shape[0], H = keys->shape[1];
   int64_t Dk = 0;
-  if ((st = check_rotation(R_full, B, H, &Dk))) return st;
+  if ((st = check_rotation(R_full, B, H, k.D, &Dk))) return st;
   if (!scores_out) return RK_ERR_NULL;
   if ((st = check_f32_out(scores_out, 3, B, H, Dk, RK_F64))) return st;
   const int cus = resolve_cus(0, &st);
@@ -1184,9 +1497,7 @@ extern "C" int rk_channel_scores(const rk_tensor* keys, const rk_tensor* R_full,
   a.spart = (float*)workspace;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)a.splits, (unsigned)(B * H));
-  hipError_t e = keys->dtype == RK_F16 ? launch_rot_nt<rk::F16>(8, true, a, vec, grid, s)
-                                       : launch_rot_nt<rk::BF16>(8, true, a, vec, grid, s);
-  if (e != hipSuccess) return RK_ERR_HIP;
+  if (launch_rot_any(keys->dtype, 8, true, a, vec, grid, s) != hipSuccess) return RK_ERR_HIP;
   hipLaunchKernelGGL(scorefin_kernel, dim3((unsigned)(B * H)), dim3(128), 0, s, a.spart, a.splits, 128,
                      (int)Dk, k.S, (double*)scores_out->data, scores_out->stride[0], scores_out->stride[1],
                      scores_out->stride[2], k.H);
@@ -1227,20 +1538,20 @@ extern "C" int rk_gather_rotation(const rk_tensor* R_full, const rk_tensor* idx,
   int st = rk::check_desc(R_full, 4);
   if (st) return st;
   if (!rk::is_float_param(R_full->dtype)) return RK_ERR_DTYPE;
-  const int64_t B = R_full->shape[0], H = R_full->shape[1];
-  if (R_full->shape[2] != 128) return RK_ERR_HEAD_DIM;
+  const int64_t B = R_full->shape[0], H = R_full->shape[1], D = R_full->shape[2];
+  if (D < 1 || D > 128) return RK_ERR_HEAD_DIM;
   if (!idx || !mean || !R_out || !delta_mu_out) return RK_ERR_NULL;
   if ((st = rk::check_desc(idx, 3))) return st;
   if (idx->dtype != RK_I64) return RK_ERR_DTYPE;
   const int64_t k = idx->shape[2];
   if (idx->shape[0] != B || idx->shape[1] != H) return RK_ERR_SHAPE;
   if (k < 1 || k > 128) return RK_ERR_KEEP_DIM;
-  if ((st = check_f32_out(mean, 3, B, H, 128, RK_F32))) return st;
+  if ((st = check_f32_out(mean, 3, B, H, D, RK_F32))) return st;
   if ((st = rk::check_desc(R_out, 4))) return st;
-  if (!rk::is_half(R_out->dtype)) return RK_ERR_DTYPE;
-  if (R_out->shape[0] != B || R_out->shape[1] != H || R_out->shape[2] != 128 || R_out->shape[3] != k)
+  if (!rk::is_float_param(R_out->dtype)) return RK_ERR_DTYPE;
+  if (R_out->shape[0] != B || R_out->shape[1] != H || R_out->shape[2] != D || R_out->shape[3] != k)
     return RK_ERR_SHAPE;
-  if ((st = check_f32_out(delta_mu_out, 3, B, H, 128, R_out->dtype))) return st;
+  if ((st = check_f32_out(delta_mu_out, 3, B, H, D, R_out->dtype))) return st;
   if (B * H == 0) return RK_OK;
   if (!R_full->data || !idx->data || !mean->data || !R_out->data || !delta_mu_out->data) return RK_ERR_NULL;
   if (B * H > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
@@ -1251,14 +1562,16 @@ extern "C" int rk_gather_rotation(const rk_tensor* R_full, const rk_tensor* idx,
                        (int)R_full->dtype, R_full->stride[0], R_full->stride[1], R_full->stride[2],
                        R_full->stride[3], (const int64_t*)idx->data, idx->stride[0], idx->stride[1],
                        idx->stride[2], (int)k, (const float*)mean->data, mean->stride[0], mean->stride[1],
-                       mean->stride[2], (uint16_t*)R_out->data, R_out->stride[0], R_out->stride[1],
-                       R_out->stride[2], R_out->stride[3], (uint16_t*)delta_mu_out->data,
-                       delta_mu_out->stride[0], delta_mu_out->stride[1], delta_mu_out->stride[2], (int)H);
+                       mean->stride[2], R_out->data, R_out->stride[0], R_out->stride[1], R_out->stride[2],
+                       R_out->stride[3], delta_mu_out->data, delta_mu_out->stride[0], delta_mu_out->stride[1],
+                       delta_mu_out->stride[2], (int)H, (int)D);
   };
   if (R_out->dtype == RK_F16)
     go(rk::F16{});
-  else
+  else if (R_out->dtype == RK_BF16)
     go(rk::BF16{});
+  else
+    go(rk::F32{});
   return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 
@@ -1268,9 +1581,9 @@ extern "C" int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, i
   int st;
   if ((st = rk::check_desc(cov, 4)) || (st = rk::check_desc(queries, 4)) || (st = rk::check_desc(out, 4)))
     return st;
-  if (cov->dtype != RK_F32 || out->dtype != RK_F32 || !rk::is_half(queries->dtype)) return RK_ERR_DTYPE;
-  const int64_t B = cov->shape[0], H = cov->shape[1];
-  if (cov->shape[2] != 128 || cov->shape[3] != 128 || queries->shape[3] != 128) return RK_ERR_HEAD_DIM;
+  if (cov->dtype != RK_F32 || out->dtype != RK_F32 || !rk::is_float_param(queries->dtype)) return RK_ERR_DTYPE;
+  const int64_t B = cov->shape[0], H = cov->shape[1], D = cov->shape[2];
+  if (D < 1 || D > 128 || cov->shape[3] != D || queries->shape[3] != D) return RK_ERR_HEAD_DIM;
   for (int i = 0; i < 4; ++i)
     if (out->shape[i] != cov->shape[i]) return RK_ERR_SHAPE;
   if (num_kv_groups <= 0 || queries->shape[0] != B || queries->shape[1] != H * num_kv_groups) return RK_ERR_HEADS;
@@ -1282,29 +1595,32 @@ extern "C" int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, i
   if (!cov->data || !queries->data || !out->data) return RK_ERR_NULL;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)(B * H));
-  // the group mean over dim 2 of [B, H_kv, G, W, 128] (kv_pruning_utils.py:127-129)
-  const float inv_g = rk::mean_factor(B * H * W * 128, B * H * num_kv_groups * W * 128);
+  // the group mean over dim 2 of [B, H_kv, G, W, D] (kv_pruning_utils.py:127-129)
+  const float inv_g = rk::mean_factor(B * H * W * D, B * H * num_kv_groups * W * D);
+  const float rfac = rk::mean_factor(B * H, B * H * D);  // the ridge's mean over the diagonal
   // 16-byte loads: unit inner stride, rows (and the bases) 16-byte aligned
-  const bool cvec = cov->stride[3] == 1 && cov->stride[2] % 4 == 0 && cov->stride[1] % 4 == 0 &&
+  const bool cvec = D % 4 == 0 && cov->stride[3] == 1 && cov->stride[2] % 4 == 0 && cov->stride[1] % 4 == 0 &&
                     cov->stride[0] % 4 == 0 && ((uintptr_t)cov->data & 15) == 0;
-  const bool qvec = queries->stride[3] == 1 && queries->stride[2] % 8 == 0 && queries->stride[1] % 8 == 0 &&
-                    queries->stride[0] % 8 == 0 && ((uintptr_t)queries->data & 15) == 0;
+  const bool qvec = rows_vec(queries, D);
   auto go = [&](auto kern) {
     hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, (const float*)cov->data, cov->stride[0], cov->stride[1],
                        cov->stride[2], cov->stride[3], (const uint16_t*)queries->data, queries->stride[0],
-                       queries->stride[1], queries->stride[2], queries->stride[3], S, W, (int)num_kv_groups, inv_g,
-                       (float*)out->data, out->stride[0], out->stride[1], out->stride[2], out->stride[3], (int)H);
+                       queries->stride[1], queries->stride[2], queries->stride[3], S, W, (int)num_kv_groups, (int)D,
+                       inv_g, rfac, (float*)out->data, out->stride[0], out->stride[1], out->stride[2],
+                       out->stride[3], (int)H);
   };
-  if (queries->dtype == RK_F16) {
-    if (cvec && qvec) go(qweight_kernel<rk::F16, true, true>);
-    else if (cvec) go(qweight_kernel<rk::F16, true, false>);
-    else if (qvec) go(qweight_kernel<rk::F16, false, true>);
-    else go(qweight_kernel<rk::F16, false, false>);
-  } else {
-    if (cvec && qvec) go(qweight_kernel<rk::BF16, true, true>);
-    else if (cvec) go(qweight_kernel<rk::BF16, true, false>);
-    else if (qvec) go(qweight_kernel<rk::BF16, false, true>);
-    else go(qweight_kernel<rk::BF16, false, false>);
-  }
+  auto by_layout = [&](auto tt) {
+    using TT = decltype(tt);
+    if (cvec && qvec) go(qweight_kernel<TT, true, true>);
+    else if (cvec) go(qweight_kernel<TT, true, false>);
+    else if (qvec) go(qweight_kernel<TT, false, true>);
+    else go(qweight_kernel<TT, false, false>);
+  };
+  if (queries->dtype == RK_F16)
+    by_layout(rk::F16{});
+  else if (queries->dtype == RK_BF16)
+    by_layout(rk::BF16{});
+  else
+    by_layout(rk::F32{});
   return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
 }

@@ -58,7 +58,7 @@ template <int KP>
 __global__ void __launch_bounds__(kThreads) power_iter_kernel(
     const float* cov, int64_t c_sb, int64_t c_sh, int64_t c_sr, int64_t c_sc, const float* v0, int64_t v_sb,
     int64_t v_sh, int64_t v_sr, int64_t v_sc, float* out, int64_t o_sb, int64_t o_sh, int64_t o_sr,
-    int64_t o_sc, int H, int k, int iters, float eps, int32_t* info) {
+    int64_t o_sc, int H, int k, int iters, float eps, int32_t* info, int D) {
   // V / W and (L^-1)^T row stride, 4 mod 16: reads of rows 4g + r (r fixed)
   // at columns n = 0..15 hit banks 16g + n, and 16-byte reads of rows n at
   // column 4g cover all 64 banks
@@ -90,14 +90,18 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
 
   // Stage C and V0 in LDS.  The loads of a batch are all issued before any
   // of them is stored, so the copy costs a few memory round trips rather
-  // than one per element.
+  // than one per element.  With a head_dim D < 128 the rows and columns
+  // past D are zeros (their loads re-read an in-bounds entry): W = C V, G,
+  // L and V = W L^-T then equal the D x D iteration's, with exact zeros in
+  // the padded rows.
   constexpr int kCB = 16;  // elements per thread per batch
   for (int e0 = 0; e0 < kD * kD; e0 += kThreads * kCB) {
     float v[kCB];
 #pragma unroll
     for (int i = 0; i < kCB; ++i) {
       const int e = e0 + i * kThreads + tid, r = e >> 7, c = e & 127;
-      v[i] = C[r * c_sr + c * c_sc];
+      const float x = C[min(r, D - 1) * c_sr + min(c, D - 1) * c_sc];
+      v[i] = r < D && c < D ? x : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < kCB; ++i) {
@@ -112,7 +116,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
 #pragma unroll
     for (int i = 0; i < kVB; ++i) {
       const int e = e0 + i * kThreads + tid, r = e / KP, c = e - r * KP;
-      v[i] = c < k ? V0[r * v_sr + c * v_sc] : 0.f;
+      v[i] = c < k && r < D ? V0[r * v_sr + c * v_sc] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < kVB; ++i) {
@@ -460,7 +464,7 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
 
   if (info && tid == 0) info[bh] = bad ? 1 : 0;  // thread 0 is in wave 0, which ran the pivots
   float* O = out + b * o_sb + (int64_t)h * o_sh;
-  for (int e = tid; e < kD * k; e += kThreads) {
+  for (int e = tid; e < D * k; e += kThreads) {
     const int r = e / k, c = e - (e / k) * k;
     O[r * o_sr + c * o_sc] = sV[r * SP + c];
   }
@@ -489,7 +493,7 @@ __device__ __forceinline__ float xt_at(const lds_f32* P, int m, int j) {
 __global__ void __launch_bounds__(kThreads) power_iter128_kernel(
     const float* cov, int64_t c_sb, int64_t c_sh, int64_t c_sr, int64_t c_sc, const float* v0, int64_t v_sb,
     int64_t v_sh, int64_t v_sr, int64_t v_sc, float* out, int64_t o_sb, int64_t o_sh, int64_t o_sr,
-    int64_t o_sc, int H, int k, int iters, float eps, int32_t* info, int cvec) {
+    int64_t o_sc, int H, int k, int iters, float eps, int32_t* info, int cvec, int D) {
   __shared__ __align__(16) float sV[kD * kWS];
   __shared__ __align__(16) float sP[kW * kWG];
   __shared__ float sT[4 * 256];
@@ -503,7 +507,7 @@ __global__ void __launch_bounds__(kThreads) power_iter128_kernel(
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
       const int e = e0 + i * kThreads + tid, r = e >> 7, c = e & 127;
-      v[i] = c < k ? V0[r * v_sr + c * v_sc] : 0.f;
+      v[i] = c < k && r < D ? V0[r * v_sr + c * v_sc] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < kB; ++i) {
@@ -529,13 +533,19 @@ __global__ void __launch_bounds__(kThreads) power_iter128_kernel(
         float a[8][4];
 #pragma unroll
         for (int ti = 0; ti < 8; ++ti) {
-          const float* cr = C + (int64_t)(16 * ti + n) * c_sr;
-          if (cvec) {
+          if (cvec) {  // (D == 128)
+            const float* cr = C + (int64_t)(16 * ti + n) * c_sr;
             const float4 v = *(const float4*)(cr + 16 * q + 4 * g);
             a[ti][0] = v.x, a[ti][1] = v.y, a[ti][2] = v.z, a[ti][3] = v.w;
-          } else {
+          } else {  // rows and columns of C past D are zeros
+            const int row = 16 * ti + n;
+            const float* cr = C + (int64_t)min(row, D - 1) * c_sr;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) a[ti][r] = cr[(int64_t)(16 * q + 4 * g + r) * c_sc];
+            for (int r = 0; r < 4; ++r) {
+              const int col = 16 * q + 4 * g + r;
+              const float x = cr[(int64_t)min(col, D - 1) * c_sc];
+              a[ti][r] = row < D && col < D ? x : 0.f;
+            }
           }
         }
         float bv[2][4];
@@ -722,7 +732,7 @@ __global__ void __launch_bounds__(kThreads) power_iter128_kernel(
 
   if (info && tid == 0) info[bh] = bad ? 1 : 0;
   float* O = out + b * o_sb + (int64_t)h * o_sh;
-  for (int e = tid; e < kD * k; e += kThreads) {
+  for (int e = tid; e < D * k; e += kThreads) {
     const int r = e / k, c = e - (e / k) * k;
     O[r * o_sr + c * o_sc] = sV[r * kWS + c];
   }
@@ -730,11 +740,11 @@ __global__ void __launch_bounds__(kThreads) power_iter128_kernel(
 
 template <int KP>
 hipError_t launch(const rk_tensor* cov, const rk_tensor* v0, const rk_tensor* out, int64_t BH, int H, int k,
-                  int iters, float eps, int32_t* info, hipStream_t s) {
+                  int iters, float eps, int32_t* info, int D, hipStream_t s) {
   hipLaunchKernelGGL((power_iter_kernel<KP>), dim3((unsigned)BH), dim3(kThreads), 0, s, (const float*)cov->data,
                      cov->stride[0], cov->stride[1], cov->stride[2], cov->stride[3], (const float*)v0->data,
                      v0->stride[0], v0->stride[1], v0->stride[2], v0->stride[3], (float*)out->data, out->stride[0],
-                     out->stride[1], out->stride[2], out->stride[3], H, k, iters, eps, info);
+                     out->stride[1], out->stride[2], out->stride[3], H, k, iters, eps, info, D);
   return hipGetLastError();
 }
 
@@ -748,11 +758,13 @@ extern "C" int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, con
   int st;
   if ((st = rk::check_desc(cov, 4)) || (st = rk::check_desc(v0, 4)) || (st = rk::check_desc(out, 4))) return st;
   if (cov->dtype != RK_F32 || v0->dtype != RK_F32 || out->dtype != RK_F32) return RK_ERR_DTYPE;
-  if (cov->shape[2] != kD || cov->shape[3] != kD) return RK_ERR_HEAD_DIM;
+  // any head_dim D <= 128 (rotation.py:86-91 takes D = cov.shape[-1])
+  const int64_t D = cov->shape[2];
+  if (D < 1 || D > kD || cov->shape[3] != D) return RK_ERR_HEAD_DIM;
   const int64_t B = cov->shape[0], H = cov->shape[1], k = v0->shape[3];
   for (const rk_tensor* t : {v0, out})
-    if (t->shape[0] != B || t->shape[1] != H || t->shape[2] != kD || t->shape[3] != k) return RK_ERR_SHAPE;
-  if (k < 1 || k > 128) return RK_ERR_KEEP_DIM;
+    if (t->shape[0] != B || t->shape[1] != H || t->shape[2] != D || t->shape[3] != k) return RK_ERR_SHAPE;
+  if (k < 1 || k > D) return RK_ERR_KEEP_DIM;
   if (num_iters < 0 || !(eps >= 0.f)) return RK_ERR_ARG;
   if (B * H == 0) return RK_OK;
   if (B * H > (INT64_C(1) << 31) || H > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
@@ -760,19 +772,19 @@ extern "C" int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, con
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (k <= 16)
-    e = launch<16>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
+    e = launch<16>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, (int)D, s);
   else if (k <= 32)
-    e = launch<32>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
+    e = launch<32>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, (int)D, s);
   else if (k <= 64)
-    e = launch<64>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, s);
+    e = launch<64>(cov, v0, out, B * H, (int)H, (int)k, num_iters, eps, info, (int)D, s);
   else {
-    const int cvec = cov->stride[3] == 1 && cov->stride[2] % 4 == 0 && cov->stride[1] % 4 == 0 &&
+    const int cvec = D == kD && cov->stride[3] == 1 && cov->stride[2] % 4 == 0 && cov->stride[1] % 4 == 0 &&
                      cov->stride[0] % 4 == 0 && (((uintptr_t)cov->data) & 15) == 0;
     hipLaunchKernelGGL(power_iter128_kernel, dim3((unsigned)(B * H)), dim3(kThreads), 0, s, (const float*)cov->data,
                        cov->stride[0], cov->stride[1], cov->stride[2], cov->stride[3], (const float*)v0->data,
                        v0->stride[0], v0->stride[1], v0->stride[2], v0->stride[3], (float*)out->data,
                        out->stride[0], out->stride[1], out->stride[2], out->stride[3], (int)H, (int)k, num_iters, eps,
-                       info, cvec);
+                       info, cvec, (int)D);
     e = hipGetLastError();
   }
   return e == hipSuccess ? RK_OK : RK_ERR_HIP;

@@ -88,8 +88,15 @@ def topk_ascending(scores: torch.Tensor, k: int) -> torch.Tensor:
 
 
 def make_decode_inputs(c: DecodeConfig, device="cuda", seed: int = 0, with_raw: bool = False,
-                       with_dense: bool = False, chunk_b: int = 4) -> dict:
-    """Synthesise one decode step of configuration ``c`` on ``device``."""
+                       with_dense: bool = False, chunk_b: int = 4, hip_select: bool | None = None) -> dict:
+    """Synthesise one decode step of configuration ``c`` on ``device``.
+
+    ``hip_select`` (default: for fp32 configurations, i.e. BASELINE config
+    0, on a GPU) forms the kept channels, R_partial, delta_mu and k_sparse
+    with the HIP prefill kernels (channel scores at the Keys' precision,
+    head-wise top-k, gather, truncated write) instead of torch."""
+    if hip_select is None:
+        hip_select = c.dtype == torch.float32 and torch.device(device).type == "cuda"
     dev = torch.device(device)
     g = torch.Generator(device=dev).manual_seed(seed)
     B, Hq, Hkv, D, S_v, S_f = c.B, c.H_q, c.H_kv, c.D, c.S_v, c.S_f
@@ -120,13 +127,20 @@ def make_decode_inputs(c: DecodeConfig, device="cuda", seed: int = 0, with_raw: 
         Kv = (randn(b1 - b0, Hkv, S_v, D) * out_scale[b0:b1]).to(dt)
         Kf32 = Kv.float()
         Rb = Rk[b0:b1]
-        scores = torch.matmul(Kf32, Rb).abs().mean(dim=-2) if S_v else torch.zeros(b1 - b0, Hkv, D, device=dev)
-        idx = topk_ascending(scores, c.keep)
-        Rp = torch.gather(Rb, -1, idx.unsqueeze(-2).expand(-1, -1, D, -1)).to(dt)
-        mu = Kf32.mean(dim=-2) if S_v else torch.zeros(b1 - b0, Hkv, D, device=dev)
-        Rpf = Rp.float()
-        dmu = mu - torch.matmul(torch.matmul(mu.unsqueeze(-2), Rpf), Rpf.transpose(-1, -2)).squeeze(-2)
-        k_sparse[b0:b1] = torch.matmul(Kf32, Rpf).to(dt)
+        if hip_select and S_v and c.keep:
+            from rotatek_amd import prefill
+            idx = prefill.topk_channels(prefill.channel_scores(Kv, Rb), c.keep)[0]
+            mu = prefill.key_covariance(Kv)[0]
+            Rp, dmu = prefill.gather_rotation(Rb, idx, mu, dt)
+            k_sparse[b0:b1] = prefill.rotate_keys(Kv, Rp)
+        else:
+            scores = torch.matmul(Kf32, Rb).abs().mean(dim=-2) if S_v else torch.zeros(b1 - b0, Hkv, D, device=dev)
+            idx = topk_ascending(scores, c.keep)
+            Rp = torch.gather(Rb, -1, idx.unsqueeze(-2).expand(-1, -1, D, -1)).to(dt)
+            mu = Kf32.mean(dim=-2) if S_v else torch.zeros(b1 - b0, Hkv, D, device=dev)
+            Rpf = Rp.float()
+            dmu = mu - torch.matmul(torch.matmul(mu.unsqueeze(-2), Rpf), Rpf.transpose(-1, -2)).squeeze(-2)
+            k_sparse[b0:b1] = torch.matmul(Kf32, Rpf).to(dt)
         R_partial[b0:b1] = Rp
         delta_mu[b0:b1] = dmu.to(dt)
         keep_idx[b0:b1] = idx

@@ -414,9 +414,9 @@ def test_planner_knobs_read_once_per_plan():
 def _cov_check(shape=(2, 4, 300, 128), dtype=_lib.RK_BF16, cov_shape=None, mean_shape=None):
     lib = _lib.load()
     k = _t(shape, dtype)
-    B, H = shape[:2]
-    c = _t(cov_shape or (B, H, 128, 128), _lib.RK_F32)
-    m = _t(mean_shape or (B, H, 128), _lib.RK_F32)
+    B, H, _, D = shape
+    c = _t(cov_shape or (B, H, D, D), _lib.RK_F32)
+    m = _t(mean_shape or (B, H, D), _lib.RK_F32)
     need = ctypes.c_size_t(0)
     st = lib.rk_key_covariance_check(ctypes.byref(k), ctypes.byref(m), ctypes.byref(c), 256, ctypes.byref(need))
     return st, need.value
@@ -425,8 +425,12 @@ def _cov_check(shape=(2, 4, 300, 128), dtype=_lib.RK_BF16, cov_shape=None, mean_
 def test_covariance_check():
     st, need = _cov_check()
     assert st == 0 and need > 0
-    assert _cov_check(shape=(2, 4, 300, 64))[0] == -6
-    assert _cov_check(dtype=_lib.RK_F32)[0] == -3
+    assert _cov_check(shape=(2, 4, 300, 64))[0] == 0             # any head_dim 1..128
+    assert _cov_check(shape=(2, 4, 300, 1))[0] == 0
+    assert _cov_check(shape=(2, 4, 300, 129))[0] == -6
+    assert _cov_check(shape=(2, 4, 300, 64), cov_shape=(2, 4, 128, 128))[0] == -4
+    assert _cov_check(dtype=_lib.RK_F32)[0] == 0                  # fp32 Keys
+    assert _cov_check(dtype=_lib.RK_F64)[0] == -3
     assert _cov_check(cov_shape=(2, 4, 128, 64))[0] == -4
     assert _cov_check(mean_shape=(2, 3, 128))[0] == -4
 
@@ -446,10 +450,15 @@ def test_rotate_and_select_validation():
     assert lib.rk_topk_channels(ctypes.byref(sc), 129, ctypes.byref(idx), None, None) == -7
     Rf = _t((1, 2, 128, 128), _lib.RK_F32)
     mean = _t((1, 2, 128), _lib.RK_F32)
-    Ro = _t((1, 2, 128, 32), _lib.RK_F32)      # output must be 16-bit
-    dm = _t((1, 2, 128), _lib.RK_F32)
+    Ro = _t((1, 2, 128, 32), _lib.RK_F64)      # output must be F16 / BF16 / F32
+    dm = _t((1, 2, 128), _lib.RK_F64)
     assert lib.rk_gather_rotation(ctypes.byref(Rf), ctypes.byref(idx), ctypes.byref(mean), ctypes.byref(Ro),
                                   ctypes.byref(dm), None) == -3
+    Ro, dm = _t((1, 2, 128, 32), _lib.RK_F32), _t((1, 2, 128), _lib.RK_F32)
+    assert lib.rk_gather_rotation(ctypes.byref(Rf), ctypes.byref(idx), ctypes.byref(mean), ctypes.byref(Ro),
+                                  ctypes.byref(dm), None) == -1    # fp32 accepted; no device memory
+    R80 = _t((1, 2, 80, 32), _lib.RK_F16)
+    assert lib.rk_rotate_keys(ctypes.byref(k), ctypes.byref(R80), ctypes.byref(out_dt), None) == -4  # D mismatch
     need = ctypes.c_size_t(0)
     scores = _t((1, 2, 128), _lib.RK_F64)
     assert lib.rk_channel_scores_check(ctypes.byref(k), ctypes.byref(Rf), ctypes.byref(scores), 256,
@@ -515,7 +524,13 @@ def test_power_iteration_validation():
     w96 = _t((2, 4, 128, 96), _lib.RK_F32)
     assert lib.rk_power_iteration(r(cov), r(w96), r(w96), 5, 1e-4, None, None) == -1       # 96 is valid
     c64 = _t((2, 4, 64, 64), _lib.RK_F32)
-    assert lib.rk_power_iteration(r(c64), r(v0), r(out), 5, 1e-4, None, None) == -6
+    assert lib.rk_power_iteration(r(c64), r(v0), r(out), 5, 1e-4, None, None) == -4      # V0 rows != D
+    v64, o64 = _t((2, 4, 64, 16), _lib.RK_F32), _t((2, 4, 64, 16), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(c64), r(v64), r(o64), 5, 1e-4, None, None) == -1     # D = 64 is valid
+    w65 = _t((2, 4, 64, 65), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(c64), r(w65), r(w65), 5, 1e-4, None, None) == -7     # k > D
+    c129 = _t((2, 4, 129, 129), _lib.RK_F32)
+    assert lib.rk_power_iteration(r(c129), r(v0), r(out), 5, 1e-4, None, None) == -6
     o2 = _t((2, 4, 128, 8), _lib.RK_F32)
     assert lib.rk_power_iteration(r(cov), r(v0), r(o2), 5, 1e-4, None, None) == -4
     assert lib.rk_power_iteration(r(cov), r(v0), r(out), -1, 1e-4, None, None) == -10
@@ -530,7 +545,9 @@ def test_query_weight_validation():
     assert lib.rk_query_weight(r(cov), r(q), 5, 32, r(out), None) == -5      # H_q != H_kv * G
     assert lib.rk_query_weight(r(cov), r(q), 7, 33, r(out), None) == -10     # window above 32
     q32 = _t((2, 28, 50, 128), _lib.RK_F32)
-    assert lib.rk_query_weight(r(cov), r(q32), 7, 32, r(out), None) == -3
+    assert lib.rk_query_weight(r(cov), r(q32), 7, 32, r(out), None) == -1    # fp32 queries accepted
+    q64 = _t((2, 28, 50, 128), _lib.RK_F64)
+    assert lib.rk_query_weight(r(cov), r(q64), 7, 32, r(out), None) == -3
 
 
 def test_think_validation():

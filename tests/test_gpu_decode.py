@@ -410,8 +410,10 @@ def test_fp32_decode_matches_oracle(case, family):
 
 def test_fp32_config0_end_to_end():
     """BASELINE config 0 (B=1, 32 heads, 2304 visual + 128 text tokens, fp32,
-    seeded orthogonal R_k, top 32 channels by mean |K R_k|): the kept channels
-    and the decode against the oracle."""
+    seeded orthogonal R_k, top 32 channels by mean |K R_k|): the kept channels,
+    selected by the HIP prefill kernels at fp32 (synth's default for fp32:
+    channel scores, top-k, gather, truncated write), and the decode against
+    the oracle."""
     from rotatek_amd import synth
     from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
     from oracle import prefill as op

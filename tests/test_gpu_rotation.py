@@ -232,8 +232,12 @@ def test_power_iteration_gpu_other_float_types(dtype):
 def test_power_iteration_gpu_shapes():
     from rotatek_amd import rotation
     _say("power_iteration_gpu shapes")
-    with pytest.raises(ValueError):
-        rotation.power_iteration_gpu(torch.zeros(2, 64, 64, device="cuda"), k=8)
+    with pytest.raises(ValueError):       # head_dim past 128
+        rotation.power_iteration_gpu(torch.zeros(2, 129, 129, device="cuda"), k=8)
+    with pytest.raises(ValueError):       # not square
+        rotation.power_iteration_gpu(torch.zeros(2, 64, 32, device="cuda"), k=8)
+    with pytest.raises(ValueError):       # k past D
+        rotation.power_iteration_gpu(torch.zeros(2, 64, 64, device="cuda"), k=65)
     with pytest.raises(ValueError):
         rotation.power_iteration_gpu(torch.zeros(2, 128, 128, device="cuda"), k=129)
     cov = _cov(1, 6, seed=4)[0]                       # [6, 128, 128]: any leading dims
