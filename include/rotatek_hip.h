@@ -55,10 +55,13 @@
 extern "C" {
 #endif
 
-/* 2: rk_power_iteration takes eps and a per-matrix info flag; the decode
+/* 3: any head_dim 1..128 (decode, dense, span cache, prefill, power
+ * iteration); fp32 Keys / queries / R_partial in the prefill entries;
+ * rk_decode_workspace_release.
+ * 2: rk_power_iteration takes eps and a per-matrix info flag; the decode
  * plan carries the chunk-major layout fields; rk_rotatek_decode_noalloc,
  * rk_key_covariance_weighted and the merge / workspace entry points. */
-#define RK_ABI_VERSION 2
+#define RK_ABI_VERSION 3
 
 /* Element types. */
 typedef enum rk_dtype {
@@ -81,7 +84,7 @@ typedef enum rk_status {
   RK_ERR_HEADS = -5,         /* H_q / num_kv_groups != H_kv                 */
   RK_ERR_HEAD_DIM = -6,      /* head_dim outside 1..128                     */
   RK_ERR_KEEP_DIM = -7,      /* kept channels out of range (decode 0..128,
-                                prefill and power iteration 1..128)         */
+                                prefill 1..128, power iteration 1..D)       */
   RK_ERR_STRIDE = -8,        /* negative or overflowing stride              */
   RK_ERR_WORKSPACE = -9,     /* workspace NULL, misaligned or too small     */
   RK_ERR_ARG = -10,          /* other invalid scalar argument               */
@@ -180,14 +183,14 @@ int rk_rotatek_decode_noalloc(const rk_tensor* q_full, const rk_tensor* R_partia
 /* Variable-length variant for a preallocated span cache (no reference
  * counterpart: the reference re-concatenates the spans every decode step,
  * cache_utils.py:52-53, llama_visionzip.py:207-208).
- *   k_full    [B,H_kv,C,128]   prompt then text Keys, capacity C rows.
- *   v_buf     [B,H_kv,C+v_gap,128]  Values; logical prompt/text row t lives
+ *   k_full    [B,H_kv,C,D]     prompt then text Keys, capacity C rows.
+ *   v_buf     [B,H_kv,C+v_gap,D]  Values; logical prompt/text row t lives
  *             at row t + (t >= v_gap_at ? v_gap : 0), so the cache's
  *             [prompt | visual | text] Value buffer is passed whole with
  *             v_gap_at = S_prompt and v_gap = S_visual (v_gap 0: plain).
  *   mask_full [B,C] or NULL;  v_sparse usually a view of v_buf's visual rows.
  *   len_full  device int32 [B]: only rows t < len_full[b] are attended.
- *   k_new, v_new  [B,H_kv,1,128] or both NULL.  If given, the step appends
+ *   k_new, v_new  [B,H_kv,1,D] or both NULL.  If given, the step appends
  *             them first: the new token is attended, written to row
  *             len_full[b] of k_full / v_buf, and len_full[b] is incremented
  *             (all in the same two launches; a row whose buffer is full,
@@ -204,17 +207,17 @@ int rk_rotatek_decode_varlen(const rk_tensor* q_full, const rk_tensor* R_partial
                              size_t workspace_bytes, void* stream);
 
 /* Query-aware weighting of the Key covariance, replacing
- * kv_pruning_utils.py:116-140: cov [B,H_kv,128,128] F32, queries
- * [B,H_kv*G,S,128] F16/BF16 (the last min(window, S) rows are used,
+ * kv_pruning_utils.py:116-140: cov [B,H_kv,D,D] F32 (1 <= D <= 128), queries
+ * [B,H_kv*G,S,D] F16/BF16/F32 (the last min(window, S) rows are used,
  * window <= 32), out like cov (may alias it). */
 int rk_query_weight(const rk_tensor* cov, const rk_tensor* queries, int64_t num_kv_groups, int32_t window,
                     const rk_tensor* out, void* stream);
 
-/* Top-k eigenbasis of each 128 x 128 covariance by subspace iteration with
+/* Top-k eigenbasis of each D x D covariance by subspace iteration with
  * Cholesky-QR orthonormalisation, replacing rotation.py:21-91
  * (_power_iter_loop; power_iteration_gpu draws v0 with torch.randn from a
- * seeded device generator and calls this).  cov [B,H,128,128], v0 / out
- * [B,H,128,k] F32, 1 <= k <= 128; per iteration V = C V, G = V^T V +
+ * seeded device generator and calls this).  cov [B,H,D,D] (1 <= D <= 128),
+ * v0 / out [B,H,D,k] F32, 1 <= k <= D; per iteration V = C V, G = V^T V +
  * eps * mean(diag G) * I, V = V chol(G)^-T.  out may alias v0.  info
  * (device int32 [B*H], optional) receives 1 for a matrix whose Cholesky
  * met a pivot that is not positive and finite (its output is then not a
@@ -223,8 +226,8 @@ int rk_power_iteration(const rk_tensor* cov, const rk_tensor* v0, const rk_tenso
                        float eps, int32_t* info, void* stream);
 
 /* In-place decode append for the span cache (replaces the per-step
- * torch.cat of cache_utils.py:52-53): k_new/v_new [B,H,1,128] are written
- * to slot len_full[b] of k_buf/v_buf [B,H,capacity,128] and len_full[b] is
+ * torch.cat of cache_utils.py:52-53): k_new/v_new [B,H,1,D] are written
+ * to slot len_full[b] of k_buf/v_buf [B,H,capacity,D] and len_full[b] is
  * incremented on the device (a full buffer is left unchanged).  v_new and
  * v_buf may both be NULL. */
 int rk_append_kv(const rk_tensor* k_new, const rk_tensor* v_new, const rk_tensor* k_buf,
@@ -311,13 +314,16 @@ void rk_set_decode_chunk_align(int32_t tokens);
 void rk_set_decode_skew(int32_t permille);
 
 /* ------------------------------------------------------------------ prefill
- * Keys are the visual span of the layer's Keys, [B, H_kv, S_v, 128] in F16
- * or BF16, any strides (a head must span < 2^31 elements).
+ * Keys are the visual span of the layer's Keys, [B, H_kv, S_v, D] in F16,
+ * BF16 or F32 (the reference's update_rotatek is plain torch: any float
+ * dtype), 1 <= D <= 128, any strides (a head must span < 2^31 elements).
+ * For F32 Keys "the key dtype" below is fp32 (no 16-bit rounding), and the
+ * products run on the fp32 MFMA.
  *
  * Key covariance (kv_pruning_utils.py:112-115):
  *   mean_out[b,h,:] = fp32 mean of K over S_v                (F32, optional)
  *   cov_out[b,h]    = 0.5 (C + C^T), C = dtype(Kc^T Kc) in fp32,
- *                     Kc = dtype(K - dtype(mean))            (F32 [B,H,128,128])
+ *                     Kc = dtype(K - dtype(mean))            (F32 [B,H,D,D])
  * Three launches (mean partials, MFMA covariance partials, finalise); the
  * workspace size comes from rk_key_covariance_check. */
 int rk_key_covariance_check(const rk_tensor* keys, const rk_tensor* mean_out,
@@ -330,7 +336,7 @@ int rk_key_covariance(const rk_tensor* keys, const rk_tensor* mean_out,
 /* Key covariance followed by the query-aware weighting, in the same three
  * launches as rk_key_covariance (the weighting is folded into the last):
  * cov_out = the result of rk_key_covariance then rk_query_weight, bit for
- * bit (kv_pruning_utils.py:112-140).  queries [B,H_kv*G,S_q,128] in the key
+ * bit (kv_pruning_utils.py:112-140).  queries [B,H_kv*G,S_q,D] in the key
  * dtype, window 1..32 (the last min(window, S_q) rows).  Workspace size
  * from the _check variant (the same as rk_key_covariance's). */
 int rk_key_covariance_weighted_check(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_groups,
@@ -342,12 +348,12 @@ int rk_key_covariance_weighted(const rk_tensor* keys, const rk_tensor* queries, 
 
 /* Truncated visual-Key write (kv_pruning_utils.py:152):
  * out[b,h,s,:] = dtype(K[b,h,s,:] @ R_partial[b,h]), R_partial
- * [B,H,128,Dk] (F16/BF16/F32), out [B,H,S_v,Dk] in the key dtype. */
+ * [B,H,D,Dk] (F16/BF16/F32), out [B,H,S_v,Dk] in the key dtype. */
 int rk_rotate_keys(const rk_tensor* keys, const rk_tensor* R_partial,
                    const rk_tensor* out, void* stream);
 
 /* Channel scores of the head-wise selection: scores_out[b,h,c] =
- * mean_s |K R_full|[s,c] with fp64 final reduction; R_full [B,H,128,Dc]
+ * mean_s |K R_full|[s,c] with fp64 final reduction; R_full [B,H,D,Dc]
  * (Dc <= 128), scores_out [B,H,Dc] F64. */
 int rk_channel_scores_check(const rk_tensor* keys, const rk_tensor* R_full,
                             const rk_tensor* scores_out, int32_t num_cus,
@@ -366,9 +372,9 @@ int rk_topk_channels(const rk_tensor* scores, int64_t k, const rk_tensor* idx_ou
 /* R_partial / delta_mu (kv_pruning_utils.py:150-156):
  * R_out[b,h,:,j] = dtype(R_full[b,h,:,idx[b,h,j]]) and
  * delta_mu_out[b,h] = dtype(mean - (mean R_out) R_out^T) computed in fp32
- * from the rounded R_out.  R_full [B,H,128,*] F16/BF16/F32, idx [B,H,k] I64,
- * mean [B,H,128] F32, R_out [B,H,128,k] and delta_mu_out [B,H,128] in
- * F16/BF16. */
+ * from the rounded R_out.  R_full [B,H,D,*] F16/BF16/F32, idx [B,H,k] I64,
+ * mean [B,H,D] F32, R_out [B,H,D,k] and delta_mu_out [B,H,D] in F16, BF16
+ * or F32 (fp32 Keys: no rounding). */
 int rk_gather_rotation(const rk_tensor* R_full, const rk_tensor* idx,
                        const rk_tensor* mean, const rk_tensor* R_out,
                        const rk_tensor* delta_mu_out, void* stream);

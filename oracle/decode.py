@@ -14,7 +14,9 @@ the reference:
                           (243-273), sequential merge (277-290) and the
                           ``acc / (l + 1e-6)`` output (293);
 * ``full_channel_decode`` closed form of full_channel_flash_decoding.py:34-155
-                          (dense split-K baseline) and gqa_decode.py:67-118.
+                          (dense split-K baseline) and gqa_decode.py:67-118;
+* ``rotatek_decode_torch`` the closed form as batched torch ops on CPU
+                          tensors (the CPU baseline's timed restatement).
 
 Semantics fixed by the reference and kept here:
 
@@ -190,3 +192,47 @@ def rotatek_decode_paper_splitk(q_full, R_partial, delta_mu, k_full, v_full,
             out[b, h] = acc / (l + DENOM_EPS)                     # kernel 2 (c)
     return out[:, None]
 
+
+
+def rotatek_decode_torch(q_full, R_partial, delta_mu, k_full, v_full, mask_full,
+                         k_sparse, v_sparse, num_kv_groups):
+    """Batched torch restatement of ``rotatek_decode`` on CPU tensors, in
+    their dtype (fp32 for the CPU baseline): whole-span products over
+    [B, H_kv, G, S] (the G query heads of a KV head as one matrix) instead
+    of a loop over (b, kv).  Same maths as fused_decode.py:131-296: visual
+    logits (q R) k~ s + (q . delta_mu) s, prompt/text logits q k s with
+    ``mask_full == 0`` excluded, one softmax over both spans with the
+    running max floored at -1e30, ``acc / (l + 1e-6)``.  Returns
+    [B, 1, H_q, D].  Pinned by tests/test_oracle_decode.py against
+    ``rotatek_decode`` (fp64) on random shapes, GQA groups, masks and empty
+    spans."""
+    import torch
+
+    q = torch.as_tensor(q_full)
+    B, Hq, D = q.shape
+    R = torch.as_tensor(R_partial)
+    Hkv = R.shape[1]
+    G = int(num_kv_groups)
+    if Hq // G != Hkv:
+        raise ValueError(f"R_partial H_kv={Hkv} but H_q={Hq}, num_kv_groups={G}")
+    scale = 1.0 / math.sqrt(D)
+    qg = q.reshape(B, Hkv, G, D)
+    ks, vs = torch.as_tensor(k_sparse), torch.as_tensor(v_sparse)
+    kf, vf = torch.as_tensor(k_full), torch.as_tensor(v_full)
+    s_vis = torch.matmul(torch.matmul(qg, R), ks.transpose(-1, -2)) * scale          # [B,Hkv,G,S_v]
+    if delta_mu is not None:
+        bias = torch.matmul(qg, torch.as_tensor(delta_mu).unsqueeze(-1)) * scale     # [B,Hkv,G,1]
+        s_vis = s_vis + bias
+    s_full = torch.matmul(qg, kf.transpose(-1, -2)) * scale                          # [B,Hkv,G,S_f]
+    if mask_full is not None:
+        keep = torch.as_tensor(mask_full).to(torch.bool).reshape(B, 1, 1, -1)
+        s_full = s_full.masked_fill(~keep, float("-inf"))
+    m = torch.full((B, Hkv, G, 1), NEG_INIT, dtype=s_vis.dtype)
+    if s_vis.shape[-1]:
+        m = torch.maximum(m, s_vis.amax(dim=-1, keepdim=True))
+    if s_full.shape[-1]:
+        m = torch.maximum(m, s_full.amax(dim=-1, keepdim=True))
+    p_vis, p_full = torch.exp(s_vis - m), torch.exp(s_full - m)
+    l = p_vis.sum(-1, keepdim=True) + p_full.sum(-1, keepdim=True)
+    acc = torch.matmul(p_vis, vs) + torch.matmul(p_full, vf)
+    return (acc / (l + DENOM_EPS)).reshape(B, Hq, D)[:, None]

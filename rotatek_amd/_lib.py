@@ -128,7 +128,7 @@ _SIGNATURES = {
 
 _lib = None
 _lock = threading.Lock()
-ABI_VERSION = 2  # RK_ABI_VERSION of include/rotatek_hip.h
+ABI_VERSION = 3  # RK_ABI_VERSION of include/rotatek_hip.h
 
 
 class HipLibraryMissing(RuntimeError):

@@ -797,13 +797,13 @@ __global__ void __launch_bounds__(256) append_kernel(const uint16_t* kn, int64_t
                                                      int64_t kb_b, int64_t kb_h, int64_t kb_s,
                                                      int64_t kb_d, uint16_t* vb, int64_t vb_b,
                                                      int64_t vb_h, int64_t vb_s, int64_t vb_d,
-                                                     int32_t* len, int H, int64_t cap) {
+                                                     int32_t* len, int H, int D, int64_t cap) {
   const int b = blockIdx.x;
   const int32_t pos = len[b];
   __syncthreads();
   if (pos >= 0 && pos < cap) {
-    for (int i = threadIdx.x; i < H * 128; i += blockDim.x) {
-      const int h = i >> 7, d = i & 127;
+    for (int i = threadIdx.x; i < H * D; i += blockDim.x) {
+      const int h = i / D, d = i - h * D;
       kb[b * kb_b + h * kb_h + pos * kb_s + d * kb_d] = kn[b * kn_b + h * kn_h + d * kn_d];
       if (vn) vb[b * vb_b + h * vb_h + pos * vb_s + d * vb_d] = vn[b * vn_b + h * vn_h + d * vn_d];
     }
@@ -821,9 +821,10 @@ extern "C" int rk_append_kv(const rk_tensor* k_new, const rk_tensor* v_new, cons
   if (st) return st;
   if ((st = rk::check_desc(k_buf, 4))) return st;
   if (!rk::is_half(k_new->dtype) || k_buf->dtype != k_new->dtype) return RK_ERR_DTYPE;
-  const int64_t B = k_new->shape[0], H = k_new->shape[1];
-  if (k_new->shape[2] != 1 || k_new->shape[3] != 128) return RK_ERR_SHAPE;
-  if (k_buf->shape[0] != B || k_buf->shape[1] != H || k_buf->shape[3] != 128) return RK_ERR_SHAPE;
+  const int64_t B = k_new->shape[0], H = k_new->shape[1], D = k_new->shape[3];
+  if (D < 1 || D > 128) return RK_ERR_HEAD_DIM;
+  if (k_new->shape[2] != 1) return RK_ERR_SHAPE;
+  if (k_buf->shape[0] != B || k_buf->shape[1] != H || k_buf->shape[3] != D) return RK_ERR_SHAPE;
   if ((v_new == nullptr) != (v_buf == nullptr)) return RK_ERR_NULL;
   if (v_new) {
     if ((st = rk::check_desc(v_new, 4)) || (st = rk::check_desc(v_buf, 4))) return st;
@@ -833,7 +834,7 @@ extern "C" int rk_append_kv(const rk_tensor* k_new, const rk_tensor* v_new, cons
   }
   if (B == 0 || H == 0) return RK_OK;
   if (!k_new->data || !k_buf->data || (v_new && (!v_new->data || !v_buf->data))) return RK_ERR_NULL;
-  if (B > (INT64_C(1) << 30) || H * 128 > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
+  if (B > (INT64_C(1) << 30) || H * D > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
   hipLaunchKernelGGL(append_kernel, dim3((unsigned)B), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)k_new->data, k_new->stride[0], k_new->stride[1], k_new->stride[3],
                      v_new ? (const uint16_t*)v_new->data : nullptr, v_new ? v_new->stride[0] : 0,
@@ -841,7 +842,7 @@ extern "C" int rk_append_kv(const rk_tensor* k_new, const rk_tensor* v_new, cons
                      k_buf->stride[0], k_buf->stride[1], k_buf->stride[2], k_buf->stride[3],
                      v_buf ? (uint16_t*)v_buf->data : nullptr, v_buf ? v_buf->stride[0] : 0,
                      v_buf ? v_buf->stride[1] : 0, v_buf ? v_buf->stride[2] : 0, v_buf ? v_buf->stride[3] : 0,
-                     len_full, (int)H, k_buf->shape[2]);
+                     len_full, (int)H, (int)D, k_buf->shape[2]);
   return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
 

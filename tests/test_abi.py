@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_strerror():
     lib = _lib.load()
-    assert lib.rk_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.rk_abi_version() == _lib.ABI_VERSION == 3
     assert _lib.strerror(0) == "success"
     assert "H_kv" in _lib.strerror(-5)
     assert _lib.strerror(-999) == "unknown status"

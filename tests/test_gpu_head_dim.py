@@ -187,3 +187,45 @@ def test_head_dim_channels_past_d_are_not_read():
     out = _decode(inp, "gqa")
     assert torch.isfinite(out.float()).all()
     assert np.abs(_np(out) - _oracle(ref)).max() <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("D", [64, 80])
+def test_span_cache_decode_step_head_dim(D):
+    """The span cache at D < 128: decode_step (fused append through
+    rk_rotatek_decode_varlen) over five steps, each against the oracle over
+    the spans as they grow, then a plain append (rk_append_kv)."""
+    from rotatek_amd.cache import DynamicCache
+    _say(f"span cache decode_step head_dim {D}")
+    B, Hkv, G, S_p, S_v, S_t, Dk = 2, 4, 2, 5, 700, 9, 16
+    dt = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(D)
+
+    def rn(*s):
+        return torch.randn(*s, generator=g, device="cuda").to(dt)
+
+    cache = DynamicCache(reserve_tokens=8)
+    R = torch.linalg.qr(torch.randn(B, Hkv, D, D, generator=g, device="cuda"))[0][..., :Dk].contiguous().to(dt)
+    ks, kp, kt = rn(B, Hkv, S_v, Dk), rn(B, Hkv, S_p, D), rn(B, Hkv, S_t, D)
+    V = rn(B, Hkv, S_p + S_v + S_t, D)
+    dm = rn(B, Hkv, D)
+    cache.store_pruned(ks, kp, kt, torch.ones(B, Hkv, D, dtype=torch.bool, device="cuda"), V, 0)
+    cache.rotatek_rotations.append(R)
+    cache.rotatek_means.append(dm)
+    kfull, vfull = torch.cat([kp, kt], 2), torch.cat([V[:, :, :S_p], V[:, :, S_p + S_v:]], 2)
+    for step in range(5):
+        q, kn, vn = rn(B, Hkv * G, D), rn(B, Hkv, 1, D), rn(B, Hkv, 1, D)
+        out = cache.decode_step(q, kn, vn, 0, G)[0]
+        torch.cuda.synchronize()
+        kfull, vfull = torch.cat([kfull, kn], 2), torch.cat([vfull, vn], 2)
+        want = od.rotatek_decode(_np(q), _np(R), _np(dm), _np(kfull), _np(vfull), None, _np(ks),
+                                 _np(V[:, :, S_p:S_p + S_v]), G)
+        assert out.shape == (B, 1, Hkv * G, D)
+        assert np.abs(_np(out) - want).max() <= TOL[dt], step
+    cache.sync_lengths()
+    assert cache.get_seq_length(0) == S_p + S_v + S_t + 5
+    kn, vn = rn(B, Hkv, 1, D), rn(B, Hkv, 1, D)
+    cache.append_(0, kn, vn)
+    torch.cuda.synchronize()
+    cache.sync_lengths()
+    assert cache.get_seq_length(0) == S_p + S_v + S_t + 6
+    assert torch.equal(cache.key_cache_text[0][:, :, -1:], kn)

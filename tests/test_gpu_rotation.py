@@ -244,3 +244,55 @@ def test_power_iteration_gpu_shapes():
     out = rotation.power_iteration_gpu(cov, k=24)
     torch.cuda.synchronize()
     assert out.shape == (6, 128, 24) and torch.isfinite(out).all()
+
+
+def _lowrank_keys(B, H, S, seed, rank=32):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    U = torch.linalg.qr(torch.randn(B, H, 128, rank, generator=g, device="cuda"))[0]
+    Z = torch.randn(B, H, S, rank, generator=g, device="cuda")
+    E = torch.randn(B, H, S, 128, generator=g, device="cuda")
+    return (4.0 * Z @ U.transpose(-1, -2) + 0.5 * E).to(torch.bfloat16)
+
+
+def test_power_iteration_and_update_rotatek_in_a_hip_graph():
+    """power_iteration_gpu and a whole ChannelPruner.update_rotatek with the
+    reference's default solver (power_iter) captured in one HIP graph (the
+    capture-friendly path of rotation.py:58-65, ROTATEK_COMPILE
+    reduce-overhead).  After one eager call, which draws the seeded start
+    block as the reference does on every call, each replay equals the eager
+    results bit for bit: the subspace basis, the truncated Keys, R_partial,
+    delta_mu and the keep mask.  Outputs are poisoned before each replay,
+    and other eager iterations and prunings run between replays."""
+    from rotatek_amd.pruning import ChannelPruner
+    from rotatek_amd.rotation import power_iteration_gpu
+    _say("power iteration + update_rotatek captured in a HIP graph")
+    B, H, G, S = 2, 4, 7, 1100
+    cov = _cov(B, H, seed=77)
+    K = _lowrank_keys(B, H, S, seed=78)
+    Q = torch.randn(B, H * G, S, 128, device="cuda").to(torch.bfloat16)
+    V = torch.randn(B, H, S, 128, device="cuda").to(torch.bfloat16)
+    pr = ChannelPruner(0.75, 30, 40, solver="power_iter", query_aware=True)
+    want_R = power_iteration_gpu(cov, 32)
+    kept0, _, _, mask0, _ = pr.update_rotatek(K, Q, V, None, G)
+    want = [t.clone() for t in (want_R, kept0, pr.current_rotatek_R_partial, pr.current_rotatek_delta_mu, mask0)]
+    torch.cuda.synchronize()
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        R_g = power_iteration_gpu(cov, 32)
+        kept_g, _, _, mask_g, _ = pr.update_rotatek(K, Q, V, None, G)
+        got = [R_g, kept_g, pr.current_rotatek_R_partial, pr.current_rotatek_delta_mu, mask_g]
+    other_cov = _cov(1, 2, seed=79)
+    other = ChannelPruner(0.875, 10, 10, solver="power_iter", query_aware=True)
+    for i in range(3):
+        for t in got:
+            t.fill_(0 if t.dtype == torch.bool else float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("basis", "k_sparse", "R_partial", "delta_mu", "mask"), got, want):
+            assert torch.equal(a, b), (i, name)
+        power_iteration_gpu(other_cov, 24)
+        other.update_rotatek(K[:1, :2, :500], Q[:1, :14, :500], None, None, G)
+        torch.cuda.synchronize()
