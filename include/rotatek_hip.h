@@ -132,7 +132,8 @@ int rk_device_cu_count(int device, int* status);
  * delta_mu may be F16, BF16 or F32.
  * The workspace (size from rk_rotatek_decode_check, 256-byte aligned) holds
  * the split partials and, in its first RK_DECODE_TICKET_BYTES, the
- * counters of the single-launch merge.  Every call leaves the counters at
+ * counters of the single-launch merge (unit tickets, unit call epochs,
+ * batch-row tickets, at fixed offsets).  Every call leaves the tickets at
  * zero.  A workspace the library has not seen (by its address) gets them
  * zeroed by a fill kernel on `stream` ahead of its first single-launch
  * decode; rk_decode_workspace_init does the same explicitly, and

@@ -234,58 +234,100 @@ struct FullBuf {
 // Record (u, x, h) of a unit's workgroup x and head h sits at
 // part + ((u * np + x) * hpu + h) * kRecFloats.
 
-// Channels 8 c8 .. 8 c8 + 7 of a record's acc, and its (m, l).  COH: relaxed
-// agent-scope atomic loads, which the single-launch merge uses to read
-// records written by workgroups on other XCDs in the same launch (each XCD
-// has its own L2; these loads are coherent across them).
-template <bool COH>
-__device__ __forceinline__ void load_rec(const float* rec, int c8, float (&v)[8], float& m, float& l) {
-  if constexpr (COH) {
-    const uint64_t* p = (const uint64_t*)(rec + 8 * c8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      v[2 * i] = __builtin_bit_cast(float, (uint32_t)w);
-      v[2 * i + 1] = __builtin_bit_cast(float, (uint32_t)(w >> 32));
-    }
-    const uint64_t w = __hip_atomic_load((const uint64_t*)(rec + 128), __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-    m = __builtin_bit_cast(float, (uint32_t)w);
-    l = __builtin_bit_cast(float, (uint32_t)(w >> 32));
-  } else {
+// How a record is written and read back:
+//   kRecPlain     ordinary stores and loads (the merge kernel, a later launch);
+//   kRecCoherent  relaxed agent-scope atomic stores and loads: written through
+//                 to memory and read from it, for a single-launch merge whose
+//                 unit spans XCDs (each XCD has its own L2);
+//   kRecLocal     relaxed workgroup-scope atomic stores and loads, the ISA's
+//                 group scope (sc0): they complete at, and read from, the L2
+//                 of the XCD running them, never a CU's own vector cache (a
+//                 workgroup may span CUs), for the single-launch merge of a
+//                 chunk-major one-round grid whose units each run on one XCD
+//                 (see merge_fused).  Each record carries a tag (its writer's
+//                 XCD id and the unit's call epoch) that the merger checks.
+// A CU's vector cache is not invalidated between the launches of a stream,
+// so a plain load can return a line an earlier launch read at the same
+// address; only kRecPlain (whose records come from an earlier launch of the
+// same call, the merge kernel's producer) uses plain loads.
+constexpr int kRecPlain = 0, kRecCoherent = 1, kRecLocal = 2;
+
+struct RecTag {
+  uint32_t xcc, epoch;
+};
+
+// The XCD (accelerator complex die) running this wave.
+__device__ __forceinline__ uint32_t xcd_id() {
+  uint32_t x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  return x;
+}
+
+__device__ __forceinline__ uint64_t pack_f2(float a, float b) {
+  return (uint64_t)__builtin_bit_cast(uint32_t, a) | ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
+}
+__device__ __forceinline__ float lo_f(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)w); }
+__device__ __forceinline__ float hi_f(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)(w >> 32)); }
+
+// Channels 8 c8 .. 8 c8 + 7 of a record's acc, and its (m, l).  kRecLocal:
+// a record whose tag is not the merger's (another XCD, or an earlier call)
+// reads as NaN, so a placement other than the assumed one shows in the
+// output instead of merging stale data.
+template <int RM>
+__device__ __forceinline__ void load_rec(const float* rec, int c8, float (&v)[8], float& m, float& l,
+                                         RecTag tag) {
+  if constexpr (RM == kRecPlain) {
     const float4 s0 = ((const float4*)(rec + 8 * c8))[0], s1 = ((const float4*)(rec + 8 * c8))[1];
     const float2 ml = *(const float2*)(rec + 128);
     v[0] = s0.x; v[1] = s0.y; v[2] = s0.z; v[3] = s0.w;
     v[4] = s1.x; v[5] = s1.y; v[6] = s1.z; v[7] = s1.w;
     m = ml.x;
     l = ml.y;
+  } else {
+    constexpr int scope = RM == kRecCoherent ? __HIP_MEMORY_SCOPE_AGENT : __HIP_MEMORY_SCOPE_WORKGROUP;
+    const uint64_t* p = (const uint64_t*)(rec + 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, scope);
+      v[2 * i] = lo_f(w);
+      v[2 * i + 1] = hi_f(w);
+    }
+    const uint64_t w = __hip_atomic_load((const uint64_t*)(rec + 128), __ATOMIC_RELAXED, scope);
+    m = lo_f(w);
+    l = hi_f(w);
+    if constexpr (RM == kRecLocal) {
+      const uint64_t t = __hip_atomic_load((const uint64_t*)(rec + 130), __ATOMIC_RELAXED, scope);
+      if ((uint32_t)t != tag.xcc || (uint32_t)(t >> 32) != tag.epoch) {
+        l = __builtin_nanf("");
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
+      }
+    }
   }
 }
 
 // Store of a workgroup's record slice (the lane's eight acc channels; m, l
-// by the c8 == 0 lane).  COH: relaxed agent-scope atomic stores, which
-// write through to memory, so that after the storing thread's wait for
-// their completion any XCD reads them.
-template <bool COH>
-__device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8], float M, float L) {
-  if constexpr (COH) {
-    uint64_t* p = (uint64_t*)(rec + 8 * c8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      __hip_atomic_store(p + i,
-                         (uint64_t)__builtin_bit_cast(uint32_t, A[2 * i]) |
-                             ((uint64_t)__builtin_bit_cast(uint32_t, A[2 * i + 1]) << 32),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (c8 == 0)
-      __hip_atomic_store((uint64_t*)(rec + 128),
-                         (uint64_t)__builtin_bit_cast(uint32_t, M) |
-                             ((uint64_t)__builtin_bit_cast(uint32_t, L) << 32),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
+// and with kRecLocal the tag, by the c8 == 0 lane).  kRecCoherent: relaxed
+// agent-scope atomic stores, which write through to memory, so that after
+// the storing thread's wait for their completion any XCD reads them.
+template <int RM>
+__device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8], float M, float L, RecTag tag) {
+  if constexpr (RM == kRecPlain) {
     float4* dst = (float4*)(rec + 8 * c8);
     dst[0] = make_float4(A[0], A[1], A[2], A[3]);
     dst[1] = make_float4(A[4], A[5], A[6], A[7]);
     if (c8 == 0) *(float2*)(rec + 128) = make_float2(M, L);
+  } else {
+    constexpr int scope = RM == kRecCoherent ? __HIP_MEMORY_SCOPE_AGENT : __HIP_MEMORY_SCOPE_WORKGROUP;
+    uint64_t* p = (uint64_t*)(rec + 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) __hip_atomic_store(p + i, pack_f2(A[2 * i], A[2 * i + 1]), __ATOMIC_RELAXED, scope);
+    if (c8 == 0) {
+      __hip_atomic_store((uint64_t*)(rec + 128), pack_f2(M, L), __ATOMIC_RELAXED, scope);
+      if constexpr (RM == kRecLocal)
+        __hip_atomic_store((uint64_t*)(rec + 130), (uint64_t)tag.xcc | ((uint64_t)tag.epoch << 32),
+                           __ATOMIC_RELAXED, scope);
+    }
   }
 }
 
@@ -294,16 +336,16 @@ __device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8
 // and `rstride` the floats between consecutive x.  NB records' loads are
 // issued together; entries past np are clamped in-bounds loads with weight
 // zero (a batch's first entry is always valid, so its max is finite).
-template <bool COH, int NB = 8>
+template <int RM, int NB = 8>
 __device__ __forceinline__ void fold_records(const float* rec0, int64_t rstride, int np, int p0, int step,
-                                             int c8, float& M, float& L, float (&A)[8]) {
+                                             int c8, float& M, float& L, float (&A)[8], RecTag tag) {
   for (int p = p0; p < np; p += NB * step) {
     float mm[NB], ll[NB], vv[NB][8];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int q = p + step * i;
       const bool ok = q < np;
-      load_rec<COH>(rec0 + (int64_t)(ok ? q : p) * rstride, c8, vv[i], mm[i], ll[i]);
+      load_rec<RM>(rec0 + (int64_t)(ok ? q : p) * rstride, c8, vv[i], mm[i], ll[i], tag);
       if (!ok) {
         mm[i] = -INFINITY;
         ll[i] = 0.f;
@@ -381,10 +423,11 @@ __device__ __forceinline__ void write_out(const DecodeArgs& a, int b, int hq, in
 // in flight at a time, so one or two memory round trips cover a unit), and
 // the S slices of a head are combined pairwise, lower slice first: within a
 // wave by lane exchange, across waves through LDS (s_mrg, 16 x kRecFloats
-// floats).  COH: the records were written in this launch (coherent loads).
-template <class TT, bool COH>
+// floats).  RM: how the records were written (kRecPlain: by an earlier
+// launch).
+template <class TT, int RM>
 __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b, int h0, int nh, int tid,
-                                           float* s_mrg) {
+                                           float* s_mrg, RecTag tag) {
   int S = 16;
   while (S * nh > 16) S >>= 1;
   const int s = tid >> 4, c8 = tid & 15, h = s / S, j = s - (s / S) * S;
@@ -392,7 +435,7 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (act) {
     const float* rec0 = a.part + (u * a.np * a.hpu + h) * kRecFloats;
-    fold_records<COH>(rec0, (int64_t)a.hpu * kRecFloats, a.np, j, S, c8, M, L, A);
+    fold_records<RM>(rec0, (int64_t)a.hpu * kRecFloats, a.np, j, S, c8, M, L, A, tag);
   }
 #pragma unroll
   for (int d = 1; d <= 2; d <<= 1) {  // lane exchange: slices s ^ 1, s ^ 2 share a wave
@@ -431,23 +474,22 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b
 // slice: the records x = 0 .. np - 1 in order, eight loads in flight, no
 // cross-slice combine.  Both merges run this for such units (bit-identical
 // results); the merge kernel gives each slice of a workgroup its own unit.
-template <class TT, bool COH>
-__device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int b, int hq, int c8) {
+template <class TT, int RM>
+__device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int b, int hq, int c8, RecTag tag) {
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  fold_records<COH>(a.part + u * a.np * kRecFloats, kRecFloats, a.np, 0, 1, c8, M, L, A);
+  fold_records<RM>(a.part + u * a.np * kRecFloats, kRecFloats, a.np, 0, 1, c8, M, L, A, tag);
   write_out<TT>(a, b, hq, c8, L, A);
 }
 
 // Single-launch merge, run by every workgroup after it has stored its
-// record.  The workgroup waits until its record stores have completed
-// (they write through to memory), then takes a ticket on the unit's
-// counter; the last of the unit's np workgroups merges the unit's records,
-// read with coherent loads, in the order of the merge kernel (merge_unit;
-// the result is bit-identical to the two-launch merge).  No agent-scope
-// release or acquire fence is needed, so no XCD L2 is written back or
-// invalidated.  With a fused append, the last unit of a batch row to finish
-// advances len_full[b] behind a second ticket: by then every workgroup of
-// the row has read it.
+// record.  The workgroup waits until its record stores have completed,
+// then takes a ticket on the unit's counter; the last of the unit's np
+// workgroups merges the unit's records in the order of the merge kernel
+// (merge_unit / merge_slice; the result is bit-identical to the two-launch
+// merge).  No agent-scope release or acquire fence is needed, so no XCD L2
+// is written back or invalidated.  With a fused append, the last unit of a
+// batch row to finish advances len_full[b] behind a second ticket: by then
+// every workgroup of the row has read it.
 //
 // Tickets are atomic increments that wrap to zero at n - 1 (the hardware's
 // inc: old >= n - 1 ? 0 : old + 1), so the last arrival's increment is also
@@ -456,25 +498,44 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int 
 // initialised) would misplace the merge, which is why the host initialises
 // every workspace it has not seen before its first use.
 //
-// What this relies on, on gfx942 / gfx950 (the only targets that compile
-// it; the host never selects it elsewhere):
+// Two protocols (a.fused):
+//   1  records written through to memory (kRecCoherent) and read with
+//      coherent loads: any placement of the unit's workgroups;
+//   2  records through one XCD's L2 (kRecLocal): the host picks this for a
+//      chunk-major one-round grid with units a multiple of 8, where
+//      workgroup id x * units + u runs on XCD (x * units + u) mod 8 =
+//      u mod 8 (workgroups go to the XCDs round-robin by id), so every
+//      workgroup of unit u shares one L2.  Group-scope (sc0) stores
+//      complete at that L2 and group-scope loads read it, bypassing the CU
+//      vector caches, which keep lines across launches.  Each record
+//      carries its writer's XCD id and the unit's epoch (a per-unit call
+//      counter every workgroup reads at its start and the merger advances
+//      after merging); a record from another XCD or an earlier call reads
+//      as NaN, so a placement other than the assumed one shows in the
+//      output rather than silently merging stale data.
+//
+// What protocol 1 relies on, on gfx942 / gfx950 (the only targets that
+// compile either; the host never selects them elsewhere):
 //   * relaxed agent-scope atomic stores compile to global stores with the
 //     sc1 bit, which write through the XCD's L2 to the memory-side
 //     coherence point, and relaxed agent-scope atomic loads to sc1 loads,
 //     which read from that point, not from a possibly stale L2 line;
 //   * vmcnt counts stores on these targets (there is no separate store
 //     counter), so s_waitcnt vmcnt(0) returns only once the thread's
-//     write-through stores are acknowledged; the workgroup barrier then
-//     orders every thread's completed stores before the ticket;
+//     stores are acknowledged; the workgroup barrier then orders every
+//     thread's completed stores before the ticket;
 //   * agent-scope atomics on the ticket are performed at the coherence
 //     point, so the workgroup that sees n - 1 is the last of the unit, and
 //     its record loads, issued after the ticket returns (a dependency
 //     through LDS and a barrier), see every other record;
 //   * the signal fence keeps the compiler from moving the record stores
 //     past the wait.
+// Protocol 2 relies on the same wait, barrier and ticket, on group-scope
+// (sc0) loads and stores being served by the XCD's L2 rather than a CU's
+// vector cache, and on the round-robin placement (checked by the tags).
 template <class TT, bool APPEND>
 __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, int h0, int nh, int tid,
-                                            float* s_mrg) {
+                                            float* s_mrg, RecTag tag) {
 #if defined(__gfx942__) || defined(__gfx950__) || !defined(__HIP_DEVICE_COMPILE__)
   __shared__ uint32_t s_ticket;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -483,10 +544,20 @@ __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, i
   if (tid == 0) s_ticket = __builtin_amdgcn_atomic_inc32(a.ticket + u, (uint32_t)(a.np - 1), __ATOMIC_RELAXED, "agent");
   __syncthreads();
   if (s_ticket != (uint32_t)(a.np - 1)) return;
-  if (a.hpu == 1) {
-    if (tid < 16) merge_slice<TT, true>(a, u, b, h0, tid);
+  if (a.fused == 2) {
+    if (a.hpu == 1) {
+      if (tid < 16) merge_slice<TT, kRecLocal>(a, u, b, h0, tid, tag);
+    } else {
+      merge_unit<TT, kRecLocal>(a, u, b, h0, nh, tid, s_mrg, tag);
+    }
+    // the next call's records carry the next epoch
+    if (tid == 0) __hip_atomic_fetch_add(a.epoch + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
-    merge_unit<TT, true>(a, u, b, h0, nh, tid, s_mrg);
+    if (a.hpu == 1) {
+      if (tid < 16) merge_slice<TT, kRecCoherent>(a, u, b, h0, tid, tag);
+    } else {
+      merge_unit<TT, kRecCoherent>(a, u, b, h0, nh, tid, s_mrg, tag);
+    }
   }
   if constexpr (APPEND) {
     if (tid == 0) {
@@ -575,6 +646,12 @@ decode_kernel(const DecodeArgs a) {
   const int nh = min(a.hpu, a.G - jblk * a.hpu);
   const bool is_vis = HAS_VIS && x < a.wg_vis;
   const int xf = HAS_VIS ? x - a.wg_vis : x;
+  // XCD-local single-launch merge: the unit's epoch, copied into LDS by a DMA
+  // issued ahead of everything else (no register holds it across the ring)
+  __shared__ uint32_t s_epoch[64];
+  if (a.fused == 2 && wave == 0)
+    __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(a.epoch + u),
+                                     (__attribute__((address_space(3))) void*)s_epoch, 4, 0, 0);
 
   // Fused append: workgroup 0 of the unit stages the new token in LDS
   // behind the ring's prime and folds it into wave 0's state at the end.
@@ -1031,7 +1108,10 @@ decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) s_acc[wave][nq][32 * g + 8 * i + j] = acc[j][i];
   }
+  // (the epoch DMA has long completed: every load of the ring is in)
+  if (a.fused == 2) __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  const RecTag tag = a.fused == 2 ? RecTag{xcd_id(), s_epoch[0]} : RecTag{0u, 0u};
   {
     const int h = tid >> 4, c8 = tid & 15;
     if (h < nh) {
@@ -1047,13 +1127,15 @@ decode_kernel(const DecodeArgs a) {
         for (int e = 0; e < 8; ++e) A[e] += s_acc[w][h][8 * c8 + e] * wt;
       }
       float* rec = a.part + (((int64_t)u * a.np + x) * a.hpu + h) * kRecFloats;
-      if (a.fused)
-        store_rec<true>(rec, c8, A, M, L);
+      if (a.fused == 2)
+        store_rec<kRecLocal>(rec, c8, A, M, L, tag);
+      else if (a.fused)
+        store_rec<kRecCoherent>(rec, c8, A, M, L, tag);
       else
-        store_rec<false>(rec, c8, A, M, L);
+        store_rec<kRecPlain>(rec, c8, A, M, L, tag);
     }
   }
-  if (a.fused) merge_fused<TT, APPEND>(a, u, b, h0, nh, tid, HMAX >= 16 ? &s_acc[0][0][0] : (float*)s_rsep);
+  if (a.fused) merge_fused<TT, APPEND>(a, u, b, h0, nh, tid, HMAX >= 16 ? &s_acc[0][0][0] : (float*)s_rsep, tag);
 }
 
 // ---- fp32 decode (q, K, V and out in F32; R_partial and delta_mu F16,
@@ -1262,12 +1344,12 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
       for (int e = 0; e < 8; ++e) A[e] += s_acc[w][8 * c8 + e] * wt;
     }
     float* rec = a.part + ((int64_t)u * a.np + x) * kRecFloats;
-    if (a.fused)
-      store_rec<true>(rec, c8, A, M, L);
+    if (a.fused)  // (the host never selects the XCD-local protocol here)
+      store_rec<kRecCoherent>(rec, c8, A, M, L, RecTag{0u, 0u});
     else
-      store_rec<false>(rec, c8, A, M, L);
+      store_rec<kRecPlain>(rec, c8, A, M, L, RecTag{0u, 0u});
   }
-  if (a.fused) merge_fused<F32, false>(a, u, b, h0, 1, tid, s_mrg);
+  if (a.fused) merge_fused<F32, false>(a, u, b, h0, 1, tid, s_mrg, RecTag{0u, 0u});
 }
 
 // Second launch: one workgroup per unit runs merge_unit, or with one query
@@ -1287,9 +1369,9 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
   const int jblk = r_in_b - kv * a.spk;
   const int h0 = kv * a.G + jblk * a.hpu;
   if (sliced)
-    merge_slice<TT, false>(a, u, b, h0, tid & 15);
+    merge_slice<TT, kRecPlain>(a, u, b, h0, tid & 15, RecTag{0u, 0u});
   else
-    merge_unit<TT, false>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg);
+    merge_unit<TT, kRecPlain>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg, RecTag{0u, 0u});
   if (a.k_new && r_in_b == 0 && (tid & (sliced ? 15 : 255)) == 0) {
     const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
     if (pos < a.S_f) a.len_full[b] = pos + 1;

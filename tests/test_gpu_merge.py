@@ -71,9 +71,16 @@ def _poison_records(device):
         ws[_lib.DECODE_TICKET_BYTES:].view(torch.float32)[: n // 4].fill_(float("nan"))
 
 
+def _tickets_zero(ws):
+    """Unit and batch-row tickets of workspace ``ws`` are back at zero (the
+    unit epochs between them count calls)."""
+    words = ws[:_lib.DECODE_TICKET_BYTES].view(torch.int32)
+    n = _lib.DECODE_TICKET_UNITS
+    return int(torch.count_nonzero(words[:n]).item()) == 0 and int(torch.count_nonzero(words[2 * n:]).item()) == 0
+
+
 def _counters_zero(device):
-    ws = _lib._WORKSPACE[device.index if device.index is not None else torch.cuda.current_device()]
-    return int(torch.count_nonzero(ws[:_lib.DECODE_TICKET_BYTES]).item()) == 0
+    return _tickets_zero(_lib._WORKSPACE[device.index if device.index is not None else torch.cuda.current_device()])
 
 
 CASES = [
@@ -120,6 +127,22 @@ def test_alternating_inputs_on_one_workspace():
         got = _decode(sets[i % 2], "gqa", _lib.MERGE_SINGLE_LAUNCH)
         assert torch.equal(got, want[i % 2]), i
     assert _counters_zero(want[0].device)
+
+
+def test_shapes_of_different_unit_counts_share_a_workspace():
+    """Shapes of 8, 32 and 16 units (chunk-major one-round grids, merged
+    through their XCD's L2 with per-unit epochs) take turns on one
+    workspace: each call equals the two-launch merge of its own inputs, so
+    one shape's epochs never read as another shape's tickets."""
+    shapes = [(1, 8, 8, 32, 4000, 64), (1, 32, 32, 32, 8000, 640), (2, 8, 8, 32, 3001, 129)]
+    sets = [_inputs(*s, torch.float16, seed=sum(s)) for s in shapes]
+    want = [_decode(x, "paper", _lib.MERGE_TWO_LAUNCHES) for x in sets]
+    for i, j in enumerate([0, 1, 0, 2, 1, 2, 0, 1, 1, 2]):
+        _say(f"merge shape turns: call {i} shape {shapes[j]}")
+        _poison_records(want[0].device)
+        got = _decode(sets[j], "paper", _lib.MERGE_SINGLE_LAUNCH)
+        assert torch.equal(got, want[j]), (i, shapes[j])
+        assert _counters_zero(got.device)
 
 
 def test_dense_baseline_single_launch():
@@ -215,7 +238,7 @@ def test_uninitialised_workspace_with_garbage_counters(case):
     rk_decode_workspace_init, its counter region full of garbage: the first
     single-launch decode on it already equals the two-launch merge (the
     library zeroes the counters of an address it has not seen), so does the
-    next one, and the counters are zero after each.  After
+    next one, and the tickets are zero after each.  After
     rk_decode_workspace_release the address is treated as new again."""
     B, Hq, Hkv, Dk, S_v, S_f = case
     _say(f"garbage counters B={B} Hq={Hq} Hkv={Hkv}")
@@ -229,7 +252,7 @@ def test_uninitialised_workspace_with_garbage_counters(case):
         for call in range(2):
             got = _abi_decode(inp, ws)
             assert torch.equal(got, want), (round_, call)
-            assert int(torch.count_nonzero(ws[:_lib.DECODE_TICKET_BYTES]).item()) == 0
+            assert _tickets_zero(ws)
         _lib.load().rk_decode_workspace_release(ws.data_ptr())
         ws.fill_(0x5A)
         torch.cuda.synchronize()
