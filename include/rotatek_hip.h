@@ -132,9 +132,9 @@ int rk_device_cu_count(int device, int* status);
  * delta_mu may be F16, BF16 or F32.
  * The workspace (size from rk_rotatek_decode_check, 256-byte aligned) holds
  * the split partials and, in its first RK_DECODE_TICKET_BYTES, the
- * counters of the single-launch merge (unit tickets, unit call epochs,
- * batch-row tickets, at fixed offsets).  Every call leaves the tickets at
- * zero.  A workspace the library has not seen (by its address) gets them
+ * counters of the single-launch merge (unit tickets, then batch-row
+ * tickets, at fixed offsets).  Every call leaves the counters at zero.  A
+ * workspace the library has not seen (by its address) gets them
  * zeroed by a fill kernel on `stream` ahead of its first single-launch
  * decode; rk_decode_workspace_init does the same explicitly, and
  * rk_decode_workspace_release forgets an address (call it before the
@@ -261,11 +261,13 @@ void rk_decode_workspace_release(void* workspace);
 /* Merge of the decode entry points: 1 = two launches (split kernel, then a
  * merge kernel), 2 = one launch (the last split workgroup of each unit
  * merges, behind a counter in the workspace's ticket region) whenever the
- * counters fit, 0 (default) = one launch for a single round of workgroups
- * with one query head per unit, else two (what measured faster on
- * MI355X).  Both give bit-identical results.  The one-launch merge relies
- * on the cross-XCD store/load coherence of gfx942 / gfx950; on any other
- * device every mode runs two launches. */
+ * counters fit (up to 49152 units and 16384 batch rows), 0 (default) =
+ * one launch for a single round of workgroups with one query head per
+ * unit, else two (what measured faster on MI355X).  Both give
+ * bit-identical results.  The one-launch merge relies on the cross-XCD
+ * store/load coherence of gfx942 / gfx950 and is compiled into the F16 /
+ * BF16 kernels at head_dim 128 with 16-byte rows (and the F32 kernel); on
+ * any other device or layout every mode runs two launches. */
 void rk_set_decode_merge(int32_t mode);
 
 /* Split plan the decode entry points use for a shape (host only), exposed

@@ -265,8 +265,6 @@ def set_decode_skew(permille: int) -> None:
 
 MERGE_AUTO, MERGE_TWO_LAUNCHES, MERGE_SINGLE_LAUNCH = 0, 1, 2
 DECODE_TICKET_BYTES = 256 * 1024  # RK_DECODE_TICKET_BYTES
-# unit tickets, unit epochs (at this word) and batch-row tickets (at twice it)
-DECODE_TICKET_UNITS = 28672
 
 
 def set_decode_merge(mode: int) -> None:

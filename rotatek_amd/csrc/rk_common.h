@@ -159,22 +159,20 @@ __device__ __forceinline__ void load_any_n(const void* p, int64_t idx0, int64_t 
 
 // Rows row0 .. row0 + N - 1 of one column (element base + row * stride) of a
 // launch-uniform dtype, as load_any_n; rows at or past nrows are zero (their
-// loads read row nrows - 1, in bounds).
+// loads read the column's first row, in bounds).  Addresses step from the
+// column pointer one row at a time, so none is held across the loads.
 template <int N>
 __device__ __forceinline__ void load_any_rows(const void* p, int64_t base, int64_t stride, int dtype, int row0,
                                               int nrows, float (&out)[N]) {
-  int64_t idx[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) idx[i] = base + (int64_t)min(row0 + i, nrows - 1) * stride;
   if (dtype == 2) {
-    const float* f = (const float*)p;
+    const float* f = (const float*)p + base;
 #pragma unroll
-    for (int i = 0; i < N; ++i) out[i] = f[idx[i]];
+    for (int i = 0; i < N; ++i) out[i] = f[row0 + i < nrows ? (int64_t)(row0 + i) * stride : 0];
   } else {
-    const uint16_t* h = (const uint16_t*)p;
+    const uint16_t* h = (const uint16_t*)p + base;
     uint16_t r[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) r[i] = h[idx[i]];
+    for (int i = 0; i < N; ++i) r[i] = h[row0 + i < nrows ? (int64_t)(row0 + i) * stride : 0];
     if (dtype == 0) {
 #pragma unroll
       for (int i = 0; i < N; ++i) out[i] = F16::to_f32(r[i]);

@@ -37,13 +37,10 @@ struct DecodeArgs {
   // acc[0..127], then m, l (each record on cache lines of its own)
   float* part;
   // single-launch merge: per-unit arrival tickets and, with a fused append,
-  // per-batch-row unit tickets (both zero between calls); per-unit call
-  // epochs (the XCD-local protocol's record tags, any starting value)
+  // per-batch-row unit tickets; both zero between calls
   uint32_t* ticket;
   uint32_t* bticket;
-  uint32_t* epoch;
-  // 0: merge kernel; 1: single launch, records through memory; 2: single
-  // launch, records through the unit's XCD L2 (see merge_fused)
+  // 0: merge kernel; 1: single launch (merge_fused)
   int32_t fused;
   int64_t q_sb, q_sh, q_sd;
   int64_t R_sb, R_sh, R_sd, R_sk;

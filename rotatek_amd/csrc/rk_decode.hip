@@ -86,57 +86,51 @@ Knobs knobs() {
 }
 
 struct WsLayout {
-  size_t ticket, epoch, bticket, part, total;
+  size_t ticket, bticket, part, total;
 };
 
-// The ticket region (fixed size, at offset 0) holds three arrays at fixed
-// offsets, whatever the shape: unit tickets, unit epochs and batch-row
-// tickets.  Tickets return to zero at the end of every call, epochs count
-// calls; fixed offsets keep one shape's epochs out of another shape's
-// tickets.  Then one partial record per (unit, workgroup, head).
+// The ticket region (fixed size, at offset 0) holds two arrays at fixed
+// offsets, whatever the shape: unit tickets, then batch-row tickets (every
+// call leaves both at zero).  Then one partial record per (unit, workgroup,
+// head).
 constexpr int64_t kTicketWords = RK_DECODE_TICKET_BYTES / sizeof(uint32_t);
-constexpr int64_t kMaxTicketUnits = kTicketWords * 7 / 16;       // 28672
-constexpr int64_t kMaxTicketRows = kTicketWords - 2 * kMaxTicketUnits;  // 8192
+constexpr int64_t kMaxTicketUnits = kTicketWords * 3 / 4;            // 49152
+constexpr int64_t kMaxTicketRows = kTicketWords - kMaxTicketUnits;  // 16384
 
 WsLayout ws_layout(const rk_decode_plan& p) {
   const int64_t np = p.wg_vis + p.wg_full;
   const size_t parts = (size_t)p.units * np * p.heads_per_unit;
   WsLayout w;
   w.ticket = 0;
-  w.epoch = (size_t)kMaxTicketUnits * sizeof(uint32_t);
-  w.bticket = 2 * (size_t)kMaxTicketUnits * sizeof(uint32_t);
+  w.bticket = (size_t)kMaxTicketUnits * sizeof(uint32_t);
   w.part = RK_DECODE_TICKET_BYTES;
   w.total = w.part + align256(parts * rk::kRecFloats * sizeof(float));
   return w;
 }
 
 // Single-launch merge where the counters fit: on request (mode 2), or by
-// default (a) for one round of units of one query head each, where the
-// unit's last workgroup merges with one 16-lane slice (merge_slice), and
-// (b) for a chunk-major grid of one workgroup per CU whose unit count is a
-// multiple of 8, where every unit's records pass through one XCD's L2
-// (merge protocol 2, see merge_fused).  Measured on MI355X (eager / graph
-// us per step, two launches -> one): B=1, 32 heads, 16k context 35.9 /
-// 35.3 -> 33.8 / 33.4 (with write-through records); the same at 2.4k
-// tokens in fp32 32.4-33.2 / 26.9 -> 29.3-30.1 / 25.8; config 4 (28
-// layers of B=8, 4 KV heads of 7 query heads, one graph) at 4097 visual
-// tokens 638.6 / 563.0 / 538.7 -> 626.6 / 554.1 / 537.0 (keep 64 / 32 /
-// 16, XCD-local records).  Elsewhere one launch ends no earlier than two:
-// with write-through records its tail (stores written through and waited
+// default for one round of units of one query head each, where the unit's
+// last workgroup merges with one 16-lane slice (merge_slice).  Measured on
+// MI355X (eager / graph us per step, two launches -> one): B=1, 32 heads,
+// 16k context 35.9 / 35.3 -> 33.8 / 33.4; the same at 2.4k tokens in fp32
+// 32.4-33.2 / 26.9 -> 29.3-30.1 / 25.8.  Elsewhere one launch ends no
+// earlier than two: its tail (record stores written through and waited
 // for, ~2 us under load; the ticket, ~0.5 us; a multi-head unit's merge,
-// ~3.5 us) is as long as the kernel boundary plus the merge kernel (B=8
-// with 4 KV heads of 7 query heads, 12001 + 61 tokens, 28 layers in one
-// graph: 938 against 891 us per step); with XCD-local records at two
-// workgroups per CU it is still no faster (the same at 12001 tokens:
-// 862.4 -> 866.2 us, keep 64 1041.8 -> 1061.3).  On grids of many rounds
-// it is worse still: every workgroup holds its slot through its own wait
-// (B=32, 16k context: 935 against 815 us; B=4, 32 heads, 4.6k tokens, two
-// rounds: 44.2 -> 44.8 us).
+// ~3.5 us) is as long as the kernel boundary plus the merge kernel, and the
+// split phase's slowest workgroup finishes 1-2 us later (B=8 with 4 KV heads
+// of 7 query heads, 12001 + 61 tokens: both end at 34 us; over 28 layers in
+// one graph, one launch 938 us against 891 us per step).  On grids of many
+// rounds it is worse still: every workgroup holds its slot through its own
+// wait (B=32, 16k context: 935 against 815 us; B=4, 32 heads, 4.6k tokens,
+// two rounds: 44.2 -> 44.8 us).  Records passed through one XCD's L2
+// instead of memory (chunk-major grids put all of a unit's workgroups on
+// one XCD when units % 8 == 0; group-scope stores and loads) measured
+// slower still: config 1 33.6 against 32.1 us (graph), 28 config 4 layers at
+// 4097 visual tokens 562 against 548 us per step (keep 32, two launches).
 bool use_single_launch(const rk_decode_plan& p, int64_t B, int cus, const Knobs& k) {
   if (p.units > kMaxTicketUnits || B > kMaxTicketRows) return false;
   if (k.merge_mode != 0) return k.merge_mode == 2;
-  if (p.heads_per_unit == 1) return p.grid <= (int64_t)cus * k.resident();
-  return p.chunk_major && p.units % 8 == 0 && p.grid <= (int64_t)cus;
+  return p.heads_per_unit == 1 && p.grid <= (int64_t)cus * k.resident();
 }
 
 }  // namespace
@@ -579,7 +573,6 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   a.part = (float*)((char*)ws + w.part);
   a.ticket = (uint32_t*)((char*)ws + w.ticket);
   a.bticket = (uint32_t*)((char*)ws + w.bticket);
-  a.epoch = (uint32_t*)((char*)ws + w.epoch);
   // the single-launch merge's ordering holds on gfx942 / gfx950 only
   a.fused = p.single_launch && rk::device_has_coherent_tickets() ? 1 : 0;
   a.q_sb = q->stride[0];
@@ -685,14 +678,9 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   if (c.dtype == RK_F32) a.spk = (int32_t)c.G;  // one unit per query head
   a.scale_log2 = (float)(rk::kLog2e / sqrt((double)c.D));  // 1 / sqrt(D) (fused_decode.py:340)
   a.cmajor = has_vis && c.dtype != RK_F32 && !a.xgroup ? p.chunk_major : 0;
-  // A chunk-major grid whose unit count is a multiple of 8 runs every
-  // workgroup of a unit on one XCD (ids x * units + u go to the XCDs
-  // round-robin): its single-launch merge passes the records through that
-  // XCD's L2 instead of memory (merge_fused, protocol 2)
-  if (a.fused && a.cmajor && p.units % 8 == 0)
-    a.fused = 2;
-  else if (a.fused && p.heads_per_unit > 1 && knobs().merge_mode == 0)
-    a.fused = 0;  // the default picks one launch for multi-head units only with XCD-local records
+  // the 16-bit kernels carry the single-launch merge at head_dim 128 with
+  // 16-byte loads only; elsewhere the merge kernel runs
+  if (c.dtype != RK_F32 && !(vec && c.D == 128)) a.fused = 0;
   a.nfast = a.cmajor ? p.n_fast : 0;
   a.chunk_fast = p.chunk_fast;
   if (a.cmajor) a.rot_x = 0;

@@ -234,100 +234,58 @@ struct FullBuf {
 // Record (u, x, h) of a unit's workgroup x and head h sits at
 // part + ((u * np + x) * hpu + h) * kRecFloats.
 
-// How a record is written and read back:
-//   kRecPlain     ordinary stores and loads (the merge kernel, a later launch);
-//   kRecCoherent  relaxed agent-scope atomic stores and loads: written through
-//                 to memory and read from it, for a single-launch merge whose
-//                 unit spans XCDs (each XCD has its own L2);
-//   kRecLocal     relaxed workgroup-scope atomic stores and loads, the ISA's
-//                 group scope (sc0): they complete at, and read from, the L2
-//                 of the XCD running them, never a CU's own vector cache (a
-//                 workgroup may span CUs), for the single-launch merge of a
-//                 chunk-major one-round grid whose units each run on one XCD
-//                 (see merge_fused).  Each record carries a tag (its writer's
-//                 XCD id and the unit's call epoch) that the merger checks.
-// A CU's vector cache is not invalidated between the launches of a stream,
-// so a plain load can return a line an earlier launch read at the same
-// address; only kRecPlain (whose records come from an earlier launch of the
-// same call, the merge kernel's producer) uses plain loads.
-constexpr int kRecPlain = 0, kRecCoherent = 1, kRecLocal = 2;
-
-struct RecTag {
-  uint32_t xcc, epoch;
-};
-
-// The XCD (accelerator complex die) running this wave.
-__device__ __forceinline__ uint32_t xcd_id() {
-  uint32_t x;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
-  return x;
-}
-
+// Records are written and read back either with ordinary stores and loads
+// (COH false: the merge kernel reads what the split launch wrote) or, for
+// the single-launch merge, with relaxed agent-scope atomic stores and loads
+// (COH true): the stores write through the XCD's L2 to memory and the
+// loads read from there, so the unit's last workgroup, on any XCD, sees
+// every other workgroup's record (each XCD has its own L2).
 __device__ __forceinline__ uint64_t pack_f2(float a, float b) {
   return (uint64_t)__builtin_bit_cast(uint32_t, a) | ((uint64_t)__builtin_bit_cast(uint32_t, b) << 32);
 }
 __device__ __forceinline__ float lo_f(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)w); }
 __device__ __forceinline__ float hi_f(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)(w >> 32)); }
 
-// Channels 8 c8 .. 8 c8 + 7 of a record's acc, and its (m, l).  kRecLocal:
-// a record whose tag is not the merger's (another XCD, or an earlier call)
-// reads as NaN, so a placement other than the assumed one shows in the
-// output instead of merging stale data.
-template <int RM>
-__device__ __forceinline__ void load_rec(const float* rec, int c8, float (&v)[8], float& m, float& l,
-                                         RecTag tag) {
-  if constexpr (RM == kRecPlain) {
+// Channels 8 c8 .. 8 c8 + 7 of a record's acc, and its (m, l).
+template <bool COH>
+__device__ __forceinline__ void load_rec(const float* rec, int c8, float (&v)[8], float& m, float& l) {
+  if constexpr (COH) {
+    const uint64_t* p = (const uint64_t*)(rec + 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v[2 * i] = lo_f(w);
+      v[2 * i + 1] = hi_f(w);
+    }
+    const uint64_t w = __hip_atomic_load((const uint64_t*)(rec + 128), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    m = lo_f(w);
+    l = hi_f(w);
+  } else {
     const float4 s0 = ((const float4*)(rec + 8 * c8))[0], s1 = ((const float4*)(rec + 8 * c8))[1];
     const float2 ml = *(const float2*)(rec + 128);
     v[0] = s0.x; v[1] = s0.y; v[2] = s0.z; v[3] = s0.w;
     v[4] = s1.x; v[5] = s1.y; v[6] = s1.z; v[7] = s1.w;
     m = ml.x;
     l = ml.y;
-  } else {
-    constexpr int scope = RM == kRecCoherent ? __HIP_MEMORY_SCOPE_AGENT : __HIP_MEMORY_SCOPE_WORKGROUP;
-    const uint64_t* p = (const uint64_t*)(rec + 8 * c8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint64_t w = __hip_atomic_load(p + i, __ATOMIC_RELAXED, scope);
-      v[2 * i] = lo_f(w);
-      v[2 * i + 1] = hi_f(w);
-    }
-    const uint64_t w = __hip_atomic_load((const uint64_t*)(rec + 128), __ATOMIC_RELAXED, scope);
-    m = lo_f(w);
-    l = hi_f(w);
-    if constexpr (RM == kRecLocal) {
-      const uint64_t t = __hip_atomic_load((const uint64_t*)(rec + 130), __ATOMIC_RELAXED, scope);
-      if ((uint32_t)t != tag.xcc || (uint32_t)(t >> 32) != tag.epoch) {
-        l = __builtin_nanf("");
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = __builtin_nanf("");
-      }
-    }
   }
 }
 
-// Store of a workgroup's record slice (the lane's eight acc channels; m, l
-// and with kRecLocal the tag, by the c8 == 0 lane).  kRecCoherent: relaxed
-// agent-scope atomic stores, which write through to memory, so that after
-// the storing thread's wait for their completion any XCD reads them.
-template <int RM>
-__device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8], float M, float L, RecTag tag) {
-  if constexpr (RM == kRecPlain) {
+// Store of a workgroup's record slice (the lane's eight acc channels; m and
+// l by the c8 == 0 lane).
+template <bool COH>
+__device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8], float M, float L) {
+  if constexpr (COH) {
+    uint64_t* p = (uint64_t*)(rec + 8 * c8);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      __hip_atomic_store(p + i, pack_f2(A[2 * i], A[2 * i + 1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (c8 == 0)
+      __hip_atomic_store((uint64_t*)(rec + 128), pack_f2(M, L), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
     float4* dst = (float4*)(rec + 8 * c8);
     dst[0] = make_float4(A[0], A[1], A[2], A[3]);
     dst[1] = make_float4(A[4], A[5], A[6], A[7]);
     if (c8 == 0) *(float2*)(rec + 128) = make_float2(M, L);
-  } else {
-    constexpr int scope = RM == kRecCoherent ? __HIP_MEMORY_SCOPE_AGENT : __HIP_MEMORY_SCOPE_WORKGROUP;
-    uint64_t* p = (uint64_t*)(rec + 8 * c8);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) __hip_atomic_store(p + i, pack_f2(A[2 * i], A[2 * i + 1]), __ATOMIC_RELAXED, scope);
-    if (c8 == 0) {
-      __hip_atomic_store((uint64_t*)(rec + 128), pack_f2(M, L), __ATOMIC_RELAXED, scope);
-      if constexpr (RM == kRecLocal)
-        __hip_atomic_store((uint64_t*)(rec + 130), (uint64_t)tag.xcc | ((uint64_t)tag.epoch << 32),
-                           __ATOMIC_RELAXED, scope);
-    }
   }
 }
 
@@ -336,16 +294,16 @@ __device__ __forceinline__ void store_rec(float* rec, int c8, const float (&A)[8
 // and `rstride` the floats between consecutive x.  NB records' loads are
 // issued together; entries past np are clamped in-bounds loads with weight
 // zero (a batch's first entry is always valid, so its max is finite).
-template <int RM, int NB = 8>
+template <bool COH, int NB = 8>
 __device__ __forceinline__ void fold_records(const float* rec0, int64_t rstride, int np, int p0, int step,
-                                             int c8, float& M, float& L, float (&A)[8], RecTag tag) {
+                                             int c8, float& M, float& L, float (&A)[8]) {
   for (int p = p0; p < np; p += NB * step) {
     float mm[NB], ll[NB], vv[NB][8];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int q = p + step * i;
       const bool ok = q < np;
-      load_rec<RM>(rec0 + (int64_t)(ok ? q : p) * rstride, c8, vv[i], mm[i], ll[i], tag);
+      load_rec<COH>(rec0 + (int64_t)(ok ? q : p) * rstride, c8, vv[i], mm[i], ll[i]);
       if (!ok) {
         mm[i] = -INFINITY;
         ll[i] = 0.f;
@@ -423,11 +381,10 @@ __device__ __forceinline__ void write_out(const DecodeArgs& a, int b, int hq, in
 // in flight at a time, so one or two memory round trips cover a unit), and
 // the S slices of a head are combined pairwise, lower slice first: within a
 // wave by lane exchange, across waves through LDS (s_mrg, 16 x kRecFloats
-// floats).  RM: how the records were written (kRecPlain: by an earlier
-// launch).
-template <class TT, int RM>
+// floats).  COH: the records were written in this launch (coherent loads).
+template <class TT, bool COH>
 __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b, int h0, int nh, int tid,
-                                           float* s_mrg, RecTag tag) {
+                                           float* s_mrg) {
   int S = 16;
   while (S * nh > 16) S >>= 1;
   const int s = tid >> 4, c8 = tid & 15, h = s / S, j = s - (s / S) * S;
@@ -435,7 +392,7 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (act) {
     const float* rec0 = a.part + (u * a.np * a.hpu + h) * kRecFloats;
-    fold_records<RM>(rec0, (int64_t)a.hpu * kRecFloats, a.np, j, S, c8, M, L, A, tag);
+    fold_records<COH>(rec0, (int64_t)a.hpu * kRecFloats, a.np, j, S, c8, M, L, A);
   }
 #pragma unroll
   for (int d = 1; d <= 2; d <<= 1) {  // lane exchange: slices s ^ 1, s ^ 2 share a wave
@@ -474,10 +431,10 @@ __device__ __forceinline__ void merge_unit(const DecodeArgs& a, int64_t u, int b
 // slice: the records x = 0 .. np - 1 in order, eight loads in flight, no
 // cross-slice combine.  Both merges run this for such units (bit-identical
 // results); the merge kernel gives each slice of a workgroup its own unit.
-template <class TT, int RM>
-__device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int b, int hq, int c8, RecTag tag) {
+template <class TT, bool COH>
+__device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int b, int hq, int c8) {
   float M = -INFINITY, L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  fold_records<RM>(a.part + u * a.np * kRecFloats, kRecFloats, a.np, 0, 1, c8, M, L, A, tag);
+  fold_records<COH>(a.part + u * a.np * kRecFloats, kRecFloats, a.np, 0, 1, c8, M, L, A);
   write_out<TT>(a, b, hq, c8, L, A);
 }
 
@@ -498,24 +455,10 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int 
 // initialised) would misplace the merge, which is why the host initialises
 // every workspace it has not seen before its first use.
 //
-// Two protocols (a.fused):
-//   1  records written through to memory (kRecCoherent) and read with
-//      coherent loads: any placement of the unit's workgroups;
-//   2  records through one XCD's L2 (kRecLocal): the host picks this for a
-//      chunk-major one-round grid with units a multiple of 8, where
-//      workgroup id x * units + u runs on XCD (x * units + u) mod 8 =
-//      u mod 8 (workgroups go to the XCDs round-robin by id), so every
-//      workgroup of unit u shares one L2.  Group-scope (sc0) stores
-//      complete at that L2 and group-scope loads read it, bypassing the CU
-//      vector caches, which keep lines across launches.  Each record
-//      carries its writer's XCD id and the unit's epoch (a per-unit call
-//      counter every workgroup reads at its start and the merger advances
-//      after merging); a record from another XCD or an earlier call reads
-//      as NaN, so a placement other than the assumed one shows in the
-//      output rather than silently merging stale data.
-//
-// What protocol 1 relies on, on gfx942 / gfx950 (the only targets that
-// compile either; the host never selects them elsewhere):
+// Records are written through to memory and read with coherent loads
+// (COH), so the unit's workgroups may run on any XCDs.  What this relies
+// on, on gfx942 / gfx950 (the only targets that compile it; the host never
+// selects it elsewhere):
 //   * relaxed agent-scope atomic stores compile to global stores with the
 //     sc1 bit, which write through the XCD's L2 to the memory-side
 //     coherence point, and relaxed agent-scope atomic loads to sc1 loads,
@@ -530,12 +473,9 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int64_t u, int 
 //     through LDS and a barrier), see every other record;
 //   * the signal fence keeps the compiler from moving the record stores
 //     past the wait.
-// Protocol 2 relies on the same wait, barrier and ticket, on group-scope
-// (sc0) loads and stores being served by the XCD's L2 rather than a CU's
-// vector cache, and on the round-robin placement (checked by the tags).
-template <class TT, bool APPEND>
+template <class TT, bool APPEND, int HMAX>
 __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, int h0, int nh, int tid,
-                                            float* s_mrg, RecTag tag) {
+                                            float* s_mrg) {
 #if defined(__gfx942__) || defined(__gfx950__) || !defined(__HIP_DEVICE_COMPILE__)
   __shared__ uint32_t s_ticket;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -544,20 +484,12 @@ __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, i
   if (tid == 0) s_ticket = __builtin_amdgcn_atomic_inc32(a.ticket + u, (uint32_t)(a.np - 1), __ATOMIC_RELAXED, "agent");
   __syncthreads();
   if (s_ticket != (uint32_t)(a.np - 1)) return;
-  if (a.fused == 2) {
-    if (a.hpu == 1) {
-      if (tid < 16) merge_slice<TT, kRecLocal>(a, u, b, h0, tid, tag);
-    } else {
-      merge_unit<TT, kRecLocal>(a, u, b, h0, nh, tid, s_mrg, tag);
-    }
-    // the next call's records carry the next epoch
-    if (tid == 0) __hip_atomic_fetch_add(a.epoch + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // one query head per unit: one 16-lane slice (HMAX 1); else the unit's
+  // heads over the workgroup
+  if constexpr (HMAX == 1) {
+    if (tid < 16) merge_slice<TT, true>(a, u, b, h0, tid);
   } else {
-    if (a.hpu == 1) {
-      if (tid < 16) merge_slice<TT, kRecCoherent>(a, u, b, h0, tid, tag);
-    } else {
-      merge_unit<TT, kRecCoherent>(a, u, b, h0, nh, tid, s_mrg, tag);
-    }
+    merge_unit<TT, true>(a, u, b, h0, nh, tid, s_mrg);
   }
   if constexpr (APPEND) {
     if (tid == 0) {
@@ -583,10 +515,16 @@ __device__ __forceinline__ void merge_fused(const DecodeArgs& a, int u, int b, i
 // delta_mu past D are zeros.  The element-wise kernels (VEC false) take any
 // D: their loads past D are not issued and read as zeros.  With VEC and
 // not DPART, D is 128 and none of this is compiled.
-template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND, bool NTL = true, bool DPART = false>
+// FUSED (16-byte loads at head_dim 128 only): the single-launch merge
+// (a.fused set).  A separate instantiation: inlined into every
+// kernel, the merge's code raised the split pass's register pressure
+// enough to spill scalar registers in its loops.
+template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool APPEND, bool NTL = true, bool DPART = false,
+          bool FUSED = false>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 decode_kernel(const DecodeArgs a) {
   static_assert(!DPART || VEC, "the element-wise kernels mask head_dim at run time");
+  static_assert(!FUSED || (VEC && !DPART), "the single-launch merge runs at head_dim 128 with 16-byte loads");
   constexpr bool kMaskD = DPART || !VEC;  // channels past a.D possible
   constexpr int DKP = DKB * 32;
   // visual blocks in flight per wave: three for multi-head units of <= 32
@@ -646,13 +584,6 @@ decode_kernel(const DecodeArgs a) {
   const int nh = min(a.hpu, a.G - jblk * a.hpu);
   const bool is_vis = HAS_VIS && x < a.wg_vis;
   const int xf = HAS_VIS ? x - a.wg_vis : x;
-  // XCD-local single-launch merge: the unit's epoch, copied into LDS by a DMA
-  // issued ahead of everything else (no register holds it across the ring)
-  __shared__ uint32_t s_epoch[64];
-  if (a.fused == 2 && wave == 0)
-    __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(a.epoch + u),
-                                     (__attribute__((address_space(3))) void*)s_epoch, 4, 0, 0);
-
   // Fused append: workgroup 0 of the unit stages the new token in LDS
   // behind the ring's prime and folds it into wave 0's state at the end.
   __shared__ float s_new[2][128];  // k_new, v_new of this unit's KV head
@@ -913,7 +844,10 @@ decode_kernel(const DecodeArgs a) {
         for (int i = 0; i < kL; ++i) rv[i] = 0.f;
         if (a.Dk > 0) {
           const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)min(c, a.Dk - 1) * a.R_sk;
-          load_any_rows(a.R, rb, a.R_sd, a.r_dtype, part * kL, kMaskD ? a.D : 128, rv);
+          if constexpr (kMaskD)
+            load_any_rows(a.R, rb, a.R_sd, a.r_dtype, part * kL, a.D, rv);
+          else  // all 128 rows: addresses stepped on the fly
+            load_any_n(a.R, rb + (int64_t)(part * kL) * a.R_sd, a.R_sd, a.r_dtype, rv);
 #pragma unroll
           for (int i = 0; i < kL; ++i) rv[i] = c < a.Dk ? rv[i] : 0.f;
         }
@@ -1108,10 +1042,7 @@ decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) s_acc[wave][nq][32 * g + 8 * i + j] = acc[j][i];
   }
-  // (the epoch DMA has long completed: every load of the ring is in)
-  if (a.fused == 2) __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  const RecTag tag = a.fused == 2 ? RecTag{xcd_id(), s_epoch[0]} : RecTag{0u, 0u};
   {
     const int h = tid >> 4, c8 = tid & 15;
     if (h < nh) {
@@ -1127,15 +1058,10 @@ decode_kernel(const DecodeArgs a) {
         for (int e = 0; e < 8; ++e) A[e] += s_acc[w][h][8 * c8 + e] * wt;
       }
       float* rec = a.part + (((int64_t)u * a.np + x) * a.hpu + h) * kRecFloats;
-      if (a.fused == 2)
-        store_rec<kRecLocal>(rec, c8, A, M, L, tag);
-      else if (a.fused)
-        store_rec<kRecCoherent>(rec, c8, A, M, L, tag);
-      else
-        store_rec<kRecPlain>(rec, c8, A, M, L, tag);
+      store_rec<FUSED>(rec, c8, A, M, L);
     }
   }
-  if (a.fused) merge_fused<TT, APPEND>(a, u, b, h0, nh, tid, HMAX >= 16 ? &s_acc[0][0][0] : (float*)s_rsep, tag);
+  if constexpr (FUSED) merge_fused<TT, APPEND, HMAX>(a, u, b, h0, nh, tid, HMAX >= 16 ? &s_acc[0][0][0] : (float*)s_rsep);
 }
 
 // ---- fp32 decode (q, K, V and out in F32; R_partial and delta_mu F16,
@@ -1344,12 +1270,12 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
       for (int e = 0; e < 8; ++e) A[e] += s_acc[w][8 * c8 + e] * wt;
     }
     float* rec = a.part + ((int64_t)u * a.np + x) * kRecFloats;
-    if (a.fused)  // (the host never selects the XCD-local protocol here)
-      store_rec<kRecCoherent>(rec, c8, A, M, L, RecTag{0u, 0u});
+    if (a.fused)
+      store_rec<true>(rec, c8, A, M, L);
     else
-      store_rec<kRecPlain>(rec, c8, A, M, L, RecTag{0u, 0u});
+      store_rec<false>(rec, c8, A, M, L);
   }
-  if (a.fused) merge_fused<F32, false>(a, u, b, h0, 1, tid, s_mrg, RecTag{0u, 0u});
+  if (a.fused) merge_fused<F32, false, 1>(a, u, b, h0, 1, tid, s_mrg);
 }
 
 // Second launch: one workgroup per unit runs merge_unit, or with one query
@@ -1369,9 +1295,9 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
   const int jblk = r_in_b - kv * a.spk;
   const int h0 = kv * a.G + jblk * a.hpu;
   if (sliced)
-    merge_slice<TT, kRecPlain>(a, u, b, h0, tid & 15, RecTag{0u, 0u});
+    merge_slice<TT, false>(a, u, b, h0, tid & 15);
   else
-    merge_unit<TT, kRecPlain>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg, RecTag{0u, 0u});
+    merge_unit<TT, false>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg);
   if (a.k_new && r_in_b == 0 && (tid & (sliced ? 15 : 255)) == 0) {
     const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
     if (pos < a.S_f) a.len_full[b] = pos + 1;
@@ -1382,27 +1308,44 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
 
 template <class TT, int DKB, bool VEC, int HMAX, bool HAS_VIS, bool DPART>
 hipError_t launch_one(const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  // the single-launch merge is compiled into the 16-byte kernels at head_dim
+  // 128 only (the host selects it nowhere else)
+  constexpr bool kCanFuse = VEC && !DPART;
+  if (a.fused && !kCanFuse) return hipErrorInvalidValue;
   bool launched = false;
   // grouped one-unit-per-query-head mode (temporal loads): the dense
   // baseline's paper family at G > 1 only (the RotateK entries run that
   // family grouped, see rotatek_policy)
   if constexpr (VEC && HMAX == 1 && !HAS_VIS) {
     if (a.xgroup > 1) {
-      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false, DPART>), grid,
-                         dim3(kThreads), 0, s, a);
+      if (a.fused)
+        hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false, DPART, kCanFuse>), grid,
+                           dim3(kThreads), 0, s, a);
+      else
+        hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, false, DPART>), grid,
+                           dim3(kThreads), 0, s, a);
       launched = true;
     }
   }
   if constexpr (HAS_VIS) {  // the span cache's step always carries the visual span
     if (!launched && a.k_new) {
-      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, true, true, true, DPART>), grid, dim3(kThreads), 0,
-                         s, a);
+      if (a.fused)
+        hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, true, true, true, DPART, kCanFuse>), grid,
+                           dim3(kThreads), 0, s, a);
+      else
+        hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, true, true, true, DPART>), grid, dim3(kThreads),
+                           0, s, a);
       launched = true;
     }
   }
-  if (!launched)
-    hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, true, DPART>), grid, dim3(kThreads), 0,
-                       s, a);
+  if (!launched) {
+    if (a.fused)
+      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, true, DPART, kCanFuse>), grid,
+                         dim3(kThreads), 0, s, a);
+    else
+      hipLaunchKernelGGL((decode_kernel<TT, DKB, VEC, HMAX, HAS_VIS, false, true, DPART>), grid, dim3(kThreads),
+                         0, s, a);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.fused) return e;
   hipLaunchKernelGGL((merge_kernel<TT>), dim3(merge_grid(a)), dim3(kThreads), 0, s, a);

@@ -698,12 +698,8 @@ def test_plan_one_workgroup_per_cu_for_small_short_rounds():
     for keep in (16, 32, 64):
         p = _lib.plan_decode(8, 28, 4, keep, 4097, 61, policy=1)
         assert p["chunk_major"] == 1 and p["n_fast"] == 0 and p["grid"] == 256, (keep, p)
-        # 32 units on one XCD each: the merge runs in the split launch
-        assert p["units"] == 32 and p["single_launch"] == 1, (keep, p)
-        # two slots per CU at 12001 tokens: two launches
-        assert _lib.plan_decode(8, 28, 4, keep, 12001, 61, policy=1)["single_launch"] == 0
-    # multi-head units of a count that is not a multiple of 8: two launches
-    assert _lib.plan_decode(3, 12, 4, 32, 2049, 17, policy=1)["single_launch"] == 0
+        # multi-head units: the merge kernel
+        assert p["single_launch"] == 0, (keep, p)
     p = _lib.plan_decode(1, 32, 32, 32, 4000, 640, policy=0)
     assert p["chunk_major"] == 1 and p["grid"] == 256 and p["single_launch"] == 1
     # units of one query head take one workgroup per CU up to 256 KB two-slot
