@@ -385,15 +385,16 @@ int rk_gather_rotation(const rk_tensor* R_full, const rk_tensor* idx,
 /* ---- ThinK / SparK baselines (the methods RotateK is compared against).
  * Rounding follows the reference's torch GPU ops: each square rounded to
  * the key dtype, a 16-bit mean = dtype(fp32 sum * float(n_out)/float(n_in)),
- * products of two stored values rounded once. */
+ * products of two stored values rounded once.  Head dim D: any 1..128
+ * (RK_ERR_HEAD_DIM otherwise), the same in every tensor of a call. */
 
 /* ThinK prefill, replaces rotatek/baselines/think.py:15-58
- * (think_score_and_compact).  keys_vision [B,H,S_v,128] and queries_recent
- * [B,H_q,Q,128] (F16/BF16, same dtype, H_q a multiple of
+ * (think_score_and_compact).  keys_vision [B,H,S_v,D] and queries_recent
+ * [B,H_q,Q,D] (F16/BF16, same dtype, H_q a multiple of
  * num_kv_heads == H); score[c] = dtype(queries_norm[c] * keys_norm[c]); the
- * prune_count (0..128) smallest scores are pruned, equal scores lowest
- * channel first.  k_compact_out [B,H,S_v,128-prune_count] (kept channels,
- * ascending), keep_mask_out [B,H,128] U8 (1 = kept).  Workspace size from
+ * prune_count (0..D) smallest scores are pruned, equal scores lowest
+ * channel first.  k_compact_out [B,H,S_v,D-prune_count] (kept channels,
+ * ascending), keep_mask_out [B,H,D] U8 (1 = kept).  Workspace size from
  * the _check variant. */
 int rk_think_score_and_compact_check(const rk_tensor* keys_vision,
                                      const rk_tensor* queries_recent,
@@ -410,11 +411,12 @@ int rk_think_score_and_compact(const rk_tensor* keys_vision,
 
 /* SparK prefill, replaces rotatek/baselines/spark.py:15-60
  * (per_token_channel_prune) together with the query group mean of
- * kv_pruning_utils.py:76-79.  queries [B,H*num_kv_groups,W,128] are averaged
- * over each KV head's group (num_kv_groups = 1: already grouped), q_norm =
- * dtype(||q||_2 over W); per token score = dtype(dtype(k^2) * q_norm), the
- * 128-prune_count largest kept (equal scores lowest channel first).
- * k_compact_out [B,H,S_v,128-prune_count], keep_mask_out [B,H,S_v,128] U8,
+ * kv_pruning_utils.py:76-79.  keys_vision [B,H,S_v,D]; queries
+ * [B,H*num_kv_groups,W,D] are averaged over each KV head's group
+ * (num_kv_groups = 1: already grouped), q_norm = dtype(||q||_2 over W); per
+ * token score = dtype(dtype(k^2) * q_norm), the D-prune_count largest kept
+ * (equal scores lowest channel first).
+ * k_compact_out [B,H,S_v,D-prune_count], keep_mask_out [B,H,S_v,D] U8,
  * pruned_mean_out [B,H,S_v,1] = dtype-mean of the pruned values (NaN when
  * prune_count is 0, as torch's mean of nothing). */
 int rk_spark_prune_check(const rk_tensor* keys_vision, const rk_tensor* queries,
@@ -432,11 +434,11 @@ int rk_spark_prune(const rk_tensor* keys_vision, const rk_tensor* queries,
 /* Decode-time Key recovery, replaces the zero-filled (ThinK) / mean-filled
  * (SparK) tensor, its boolean-index scatter and the torch.cat of
  * llama_visionzip.py:216-234 (qwen2_5vl_visionzip.py:996-1010).  out
- * [B,H,S_p+S_v+S_t,128] gets k_prompt [B,H,S_p,128] (optional, NULL = none),
- * then the S_v recovered rows, then k_text [B,H,S_t,128] (optional).  Each
+ * [B,H,S_p+S_v+S_t,D] gets k_prompt [B,H,S_p,D] (optional, NULL = none),
+ * then the S_v recovered rows, then k_text [B,H,S_t,D] (optional).  Each
  * visual row takes its kept channels (mask 1) from k_pruned [B,H,S_v,Dk] in
- * ascending channel order; the others are 0 (ThinK, think_mask [B,H,128] U8)
- * or the row's pruned_mean [B,H,S_v,1] (SparK, spark_mask [B,H,S_v,128] U8).
+ * ascending channel order; the others are 0 (ThinK, think_mask [B,H,D] U8)
+ * or the row's pruned_mean [B,H,S_v,1] (SparK, spark_mask [B,H,S_v,D] U8).
  * Masks must hold exactly Dk kept channels per head / row, as the prefill
  * entries write them (extra kept channels are filled like pruned ones). */
 int rk_think_recover_check(const rk_tensor* k_prompt, const rk_tensor* k_pruned,
@@ -453,9 +455,9 @@ int rk_spark_recover(const rk_tensor* k_prompt, const rk_tensor* k_pruned,
                      const rk_tensor* pruned_mean, const rk_tensor* out,
                      void* stream);
 
-/* One-hot selection rotation from a per-head keep mask [B,H,128] U8:
+/* One-hot selection rotation from a per-head keep mask [B,H,D] U8:
  * R_out[b,h,c,j] = 1 if c is the j-th kept channel (ascending), else 0;
- * R_out [B,H,128,Dk] F16/BF16/F32.  No counterpart in the reference: with
+ * R_out [B,H,D,Dk] F16/BF16/F32, 1 <= Dk <= D <= 128.  No counterpart in the reference: with
  * it rk_rotatek_decode (delta_mu NULL) runs ThinK's zero-filled attention
  * straight from the compact Keys, for callers that want ThinK without the
  * recovery pass. */

@@ -4,7 +4,7 @@ rotatek/baselines/spark.py:15-60).
 ``spark_prune`` is the whole prefill step of ``update_spark``
 (kv_pruning_utils.py:63-90): the mean of the G query heads of each KV head,
 the per-channel L2 norm over the window, and one wave per visual token that
-scores its 128 channels, keeps the ``D - prune_count`` largest (equal scores
+scores its D <= 128 channels, keeps the ``D - prune_count`` largest (equal scores
 lowest channel first, as torch's GPU argsort(descending) orders them) by a
 radix select, and writes the compact Keys, the per-token mask and the mean
 of the pruned values.  ``per_token_channel_prune`` is the reference's

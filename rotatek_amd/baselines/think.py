@@ -29,7 +29,7 @@ def think_score_and_compact(
     ``keys_vision`` [B, H_kv, S_v, D] and ``queries_recent`` [B, H_q, Q, D]
     (already sliced to the query window, same dtype); returns
     ``K_compact`` [B, H_kv, S_v, D - prune_count] (kept channels in ascending
-    order) and ``keep_mask`` [B, H_kv, D] bool.  ``D`` must be 128.
+    order) and ``keep_mask`` [B, H_kv, D] bool, for any head dim ``D`` <= 128.
     """
     if not keys_vision.is_cuda:
         raise RuntimeError("keys_vision must be a GPU tensor: the ThinK kernels run only on the HIP device")

@@ -33,6 +33,12 @@
 //                        a per-head mask, so the RotateK decode kernel can
 //                        run ThinK's zero-filled attention from K_compact.
 //
+// Head dim D <= 128: the kernels keep 128 channel slots (lanes, LDS
+// columns, workspace rows) and treat slots at or past D as absent: their
+// loads are not issued and read as zeros, their selection keys sit below
+// every real channel's, and nothing is written for them.  16-byte row
+// paths need D % 8 == 0 (whole 8-channel groups in or out).
+//
 // Mean factors: torch reduces a 16-bit mean as dtype(fp32 sum * f) with
 // f = float(n_out) / float(n_in) (ATen MeanOps); the host computes each f
 // that way and passes it in.  Ties: torch's GPU topk (largest=False) takes
@@ -97,14 +103,17 @@ __device__ __forceinline__ uint32_t order_key(float v) {
   return (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
 }
 
+// Channels c0 .. c0 + 7 of row t; channels at or past D read as zeros (no
+// load).  VEC: one 16-byte load (D % 8 == 0, so the group is all in or out).
 template <bool VEC>
-__device__ __forceinline__ uint4 ld8(const uint16_t* base, int64_t ss, int64_t sc, int64_t t, int c0) {
+__device__ __forceinline__ uint4 ld8(const uint16_t* base, int64_t ss, int64_t sc, int64_t t, int c0, int D) {
   if constexpr (VEC) {
-    return *(const uint4*)(base + t * ss + c0);
+    return c0 < D ? *(const uint4*)(base + t * ss + c0) : make_uint4(0u, 0u, 0u, 0u);
   } else {
     uint32_t w[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w[e >> 1] |= (uint32_t)base[t * ss + (c0 + e) * sc] << ((e & 1) * 16);
+    for (int e = 0; e < 8; ++e)
+      if (c0 + e < D) w[e >> 1] |= (uint32_t)base[t * ss + (c0 + e) * sc] << ((e & 1) * 16);
     return make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
@@ -112,29 +121,35 @@ __device__ __forceinline__ uint4 ld8(const uint16_t* base, int64_t ss, int64_t s
 // Eight elements to row t at channel c0.  VEC: one non-temporal 16-byte
 // store (the recovered Keys are written once and read by the next kernel
 // far beyond L2 / MALL capacity; measured ~2 % faster recover + decode).
+// (channels at or past D are not written)
 template <bool VEC>
-__device__ __forceinline__ void st8(uint16_t* base, int64_t ss, int64_t sc, int64_t t, int c0, const uint4& v) {
+__device__ __forceinline__ void st8(uint16_t* base, int64_t ss, int64_t sc, int64_t t, int c0, const uint4& v,
+                                    int D) {
   if constexpr (VEC) {
     const u32x4 w = {v.x, v.y, v.z, v.w};
-    __builtin_nontemporal_store(w, (u32x4*)(base + t * ss + c0));
+    if (c0 < D) __builtin_nontemporal_store(w, (u32x4*)(base + t * ss + c0));
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) base[t * ss + (c0 + e) * sc] = (uint16_t)(word(v, e >> 1) >> ((e & 1) * 16));
+    for (int e = 0; e < 8; ++e)
+      if (c0 + e < D) base[t * ss + (c0 + e) * sc] = (uint16_t)(word(v, e >> 1) >> ((e & 1) * 16));
   }
 }
 
 // Kept flags of the eight mask bytes p[0], p[sc], ..., p[7 sc] (bit e set
-// when byte e is non-zero); VEC: one 8-byte load (sc == 1, 8-byte aligned).
+// when byte e is non-zero), n of them present (the rest read as pruned, not
+// loaded); VEC: one 8-byte load (sc == 1, 8-byte aligned, n 0 or 8).
 template <bool VEC>
-__device__ __forceinline__ uint32_t mask8(const uint8_t* p, int64_t sc) {
+__device__ __forceinline__ uint32_t mask8(const uint8_t* p, int64_t sc, int n) {
   uint32_t f = 0u;
   if constexpr (VEC) {
+    if (n <= 0) return 0u;
     const uint64_t m = *(const uint64_t*)p;
 #pragma unroll
     for (int e = 0; e < 8; ++e) f |= (((m >> (8 * e)) & 0xFFu) != 0u ? 1u : 0u) << e;
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f |= (p[e * sc] != 0 ? 1u : 0u) << e;
+    for (int e = 0; e < 8; ++e)
+      if (e < n) f |= (p[e * sc] != 0 ? 1u : 0u) << e;
   }
   return f;
 }
@@ -205,7 +220,7 @@ __global__ void __launch_bounds__(kThreads) sqsum_kernel(View k, int64_t chunk, 
   for (int64_t t = t0 + rg; t < t1; t += 64) {
     uint4 v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = ld8<VEC>(base, k.ss, k.sc, min(t + 16 * i, last), 8 * c8);
+    for (int i = 0; i < 4; ++i) v[i] = ld8<VEC>(base, k.ss, k.sc, min(t + 16 * i, last), 8 * c8, k.C);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (t + 16 * i < t1) {
@@ -231,7 +246,7 @@ __global__ void __launch_bounds__(kThreads) sqsum_kernel(View k, int64_t chunk, 
 struct ThinkArgs {
   const float* part;
   int splits;
-  View q;        // queries_recent [B, H_q, Q, 128]
+  View q;        // queries_recent [B, H_q, Q, D]
   int G;         // query heads per KV head
   int keep;      // kept channels
   int H;         // KV heads
@@ -240,9 +255,10 @@ struct ThinkArgs {
   float f_grp;   // mean factor over the G heads
   MaskView mask;
   int32_t* idx;  // [B*H][128] ascending kept channels
+  int D;         // head dim (channels past it take no part)
 };
 
-// grid (B*H), 128 threads (one per channel).
+// grid (B*H), 128 threads (one per channel slot).
 template <class TT>
 __global__ void __launch_bounds__(kD) think_select_kernel(const ThinkArgs a) {
   __shared__ uint32_t s_key[kD];
@@ -251,8 +267,9 @@ __global__ void __launch_bounds__(kD) think_select_kernel(const ThinkArgs a) {
   float s = 0.f;
   for (int x = 0; x < a.splits; ++x) s += a.part[((int64_t)bh * a.splits + x) * kD + c];
   const float kn = rnd<TT>(pin(s * a.f_keys));
+  const bool real = c < a.D;
   float qacc = 0.f;
-  for (int gi = 0; gi < a.G; ++gi) {
+  for (int gi = 0; gi < (real ? a.G : 0); ++gi) {
     const uint16_t* qb = a.q.data + head_off(a.q.sb, a.q.sh, b, h * a.G + gi) + c * a.q.sc;
     float w = 0.f;
     for (int64_t t = 0; t < a.q.S; ++t) {
@@ -263,14 +280,15 @@ __global__ void __launch_bounds__(kD) think_select_kernel(const ThinkArgs a) {
   }
   const float qn = rnd<TT>(pin(qacc * a.f_grp));
   const float score = rnd<TT>(qn * kn);  // product of two 16-bit values: exact in fp32
-  const uint32_t key = (order_key<TT>(score) << 7) | (uint32_t)c;
+  // (order keys are >= 0x7F, so a slot past D, key 0, is below every channel)
+  const uint32_t key = real ? (order_key<TT>(score) << 7) | (uint32_t)c : 0u;
   s_key[c] = key;
   __syncthreads();
   int above = 0;
   for (int j = 0; j < kD; ++j) above += s_key[j] > key;
-  const int kept = above < a.keep;
+  const int kept = real && above < a.keep;
   s_kept[c] = kept;
-  a.mask.data[head_off(a.mask.sb, a.mask.sh, b, h) + c * a.mask.sc] = (uint8_t)kept;
+  if (real) a.mask.data[head_off(a.mask.sb, a.mask.sh, b, h) + c * a.mask.sc] = (uint8_t)kept;
   __syncthreads();
   if (kept) {
     int pos = 0;
@@ -300,7 +318,8 @@ __global__ void __launch_bounds__(kThreads) compact_kernel(View k, const int32_t
 #pragma unroll
     for (int i = 0; i < kTile / 16; ++i) {
       const int64_t t = tile + rq + 16 * i;
-      if (t < t1) *(uint4*)(s_k + (rq + 16 * i) * (kD + kTilePad) + 8 * c8) = ld8<VEC>(base, k.ss, k.sc, t, 8 * c8);
+      if (t < t1)
+        *(uint4*)(s_k + (rq + 16 * i) * (kD + kTilePad) + 8 * c8) = ld8<VEC>(base, k.ss, k.sc, t, 8 * c8, k.C);
     }
     __syncthreads();
     if (8 * c8 < Dk) {
@@ -332,7 +351,7 @@ template <class TT>
 __global__ void __launch_bounds__(kD) spark_qnorm_kernel(View q, int G, int H, float f_grp, float* qn) {
   const int c = threadIdx.x, bh = blockIdx.x, b = bh / H, h = bh - b * H;
   float acc = 0.f;
-  for (int64_t t = 0; t < q.S; ++t) {
+  for (int64_t t = 0; t < (c < q.C ? q.S : 0); ++t) {
     float s = 0.f;
     for (int gi = 0; gi < G; ++gi) s += TT::to_f32(q.data[head_off(q.sb, q.sh, b, h * G + gi) + t * q.ss + c * q.sc]);
     const float g = rnd<TT>(pin(s * f_grp));
@@ -348,7 +367,7 @@ struct SparkArgs {
   int64_t chunk;
   float f_pruned;  // mean factor over the pruned channels
   OutView kc;      // [B, H, S, Dk]
-  MaskView mask;   // [B, H, S, 128]
+  MaskView mask;   // [B, H, S, D]
   OutView pm;      // [B, H, S, 1]
 };
 
@@ -475,7 +494,7 @@ __global__ void __launch_bounds__(kThreads) spark_kernel(const SparkArgs a) {
   auto load = [&](uint4 (&v)[4], int64_t tb) {
     const int64_t t = min(tb + qd, t1 - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = ld8<KVEC>(kb, a.k.ss, a.k.sc, t, 32 * q + 8 * i);
+    for (int i = 0; i < 4; ++i) v[i] = ld8<KVEC>(kb, a.k.ss, a.k.sc, t, 32 * q + 8 * i, a.k.C);
   };
 
   uint4 cur[4], nxt[4];
@@ -559,17 +578,19 @@ __global__ void __launch_bounds__(kThreads) spark_kernel(const SparkArgs a) {
         for (int e = q; e < keep; e += 4) cb[t * a.kc.ss + e * a.kc.sc] = row[e];
       }
       // kept flags as bytes: bytes 0 and 2 of two mask dwords -> channels 4d..4d+3
+      // (none written past D; MVEC: D % 8 == 0)
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
         const uint32_t m4 = ~__builtin_amdgcn_perm(pm[2 * d + 1], pm[2 * d], 0x06040200u) & 0x01010101u;
         if constexpr (MVEC) {
-          if ((d & 1) == 0) continue;
+          if ((d & 1) == 0 || 32 * q + 4 * (d - 1) >= a.k.C) continue;
           const uint32_t m0 = ~__builtin_amdgcn_perm(pm[2 * d - 1], pm[2 * d - 2], 0x06040200u) & 0x01010101u;
           *(uint64_t*)(mb + t * a.mask.ss + 32 * q + 4 * (d - 1)) = (uint64_t)m0 | ((uint64_t)m4 << 32);
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            mb[t * a.mask.ss + (32 * q + 4 * d + e) * a.mask.sc] = (uint8_t)((m4 >> (8 * e)) & 1u);
+            if (32 * q + 4 * d + e < a.k.C)
+              mb[t * a.mask.ss + (32 * q + 4 * d + e) * a.mask.sc] = (uint8_t)((m4 >> (8 * e)) & 1u);
         }
       }
       if (q == 0) pb[t * a.pm.ss] = TT::from_f32(pin(psum * a.f_pruned));
@@ -587,12 +608,13 @@ struct RecoverArgs {
   View pr;  // prompt rows (S = 0 when absent)
   View kc;  // K_compact [B, H, S_v, Dk]
   View tx;  // text rows (S = 0 when absent)
-  MaskView mask;         // ThinK [B, H, 128] (ss = 0) or SparK [B, H, S_v, 128]
+  MaskView mask;         // ThinK [B, H, D] (ss = 0) or SparK [B, H, S_v, D]
   const uint16_t* pm;    // SparK pruned mean [B, H, S_v, 1]
   int64_t p_sb, p_sh, p_ss;
-  OutView out;           // [B, H, rows, 128]
+  OutView out;           // [B, H, rows, D]
   int64_t rows, chunk;
   int H;
+  int D;                 // head dim
 };
 
 // grid (splits, B*H); tiles of 64 output rows.  The tile's compact rows are
@@ -617,9 +639,10 @@ __global__ void __launch_bounds__(kThreads) recover_kernel(const RecoverArgs a) 
   const uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
   const uint16_t* fb = SPARK ? a.pm + head_off(a.p_sb, a.p_sh, b, h) : nullptr;
   uint16_t* ob = a.out.data + head_off(a.out.sb, a.out.sh, b, h);
+  const int D = a.D, nch = min(max(D - 8 * c8, 0), 8);  // this lane's channels present
   int map[8];  // ThinK: K_compact column of channel 8 c8 + e, -1 = pruned
   if constexpr (!SPARK) {
-    const uint32_t f = mask8<false>(mb + 8 * c8 * a.mask.sc, a.mask.sc);
+    const uint32_t f = mask8<false>(mb + 8 * c8 * a.mask.sc, a.mask.sc, nch);
     int rank = prefix16(__popc(f));
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -650,13 +673,13 @@ __global__ void __launch_bounds__(kThreads) recover_kernel(const RecoverArgs a) 
       const bool live = r < r1, vis = live && r >= Sp && r < Sp + Sv;
       uint32_t f = 0u;
       if constexpr (SPARK) {
-        if (vis) f = mask8<FAST>(mb + (r - Sp) * a.mask.ss + 8 * c8 * a.mask.sc, a.mask.sc);
+        if (vis) f = mask8<FAST>(mb + (r - Sp) * a.mask.ss + 8 * c8 * a.mask.sc, a.mask.sc, nch);
       }
       int rank = SPARK ? prefix16(__popc(f)) : 0;  // every lane of the row takes part
       if (!live) continue;
       uint4 v;
       if (r < Sp) {
-        v = ld8<FAST>(pb, a.pr.ss, a.pr.sc, r, 8 * c8);
+        v = ld8<FAST>(pb, a.pr.ss, a.pr.sc, r, 8 * c8, D);
       } else if (vis) {
         const uint16_t* row = s_c + (r - tile) * kD;
         uint32_t w[4] = {0u, 0u, 0u, 0u};
@@ -675,24 +698,26 @@ __global__ void __launch_bounds__(kThreads) recover_kernel(const RecoverArgs a) 
         }
         v = make_uint4(w[0], w[1], w[2], w[3]);
       } else {
-        v = ld8<FAST>(tb, a.tx.ss, a.tx.sc, r - Sp - Sv, 8 * c8);
+        v = ld8<FAST>(tb, a.tx.ss, a.tx.sc, r - Sp - Sv, 8 * c8, D);
       }
-      st8<FAST>(ob, a.out.ss, a.out.sc, r, 8 * c8, v);
+      st8<FAST>(ob, a.out.ss, a.out.sc, r, 8 * c8, v, D);
     }
     __syncthreads();
   }
 }
 
 // grid (B*H), 128 threads: R[b,h,c,j] = 1 if c is the j-th kept channel of
-// the head's mask (ascending), else 0; `one` is 1.0 in R's dtype.
+// the head's mask (ascending), else 0, for the D rows c < D; `one` is 1.0
+// in R's dtype.
 template <class E>
-__global__ void __launch_bounds__(kD) selection_kernel(MaskView m, int H, int Dk, E* R, int64_t r_sb, int64_t r_sh,
-                                                       int64_t r_sr, int64_t r_sc, E one) {
+__global__ void __launch_bounds__(kD) selection_kernel(MaskView m, int H, int D, int Dk, E* R, int64_t r_sb,
+                                                       int64_t r_sh, int64_t r_sr, int64_t r_sc, E one) {
   __shared__ int s_kept[kD];
   const int c = threadIdx.x, bh = blockIdx.x, b = bh / H, h = bh - b * H;
-  const int kept = m.data[head_off(m.sb, m.sh, b, h) + c * m.sc] != 0;
+  const int kept = c < D && m.data[head_off(m.sb, m.sh, b, h) + c * m.sc] != 0;
   s_kept[c] = kept;
   __syncthreads();
+  if (c >= D) return;
   int pos = 0;
   for (int j = 0; j < c; ++j) pos += s_kept[j];
   E* row = R + head_off(r_sb, r_sh, b, h) + c * r_sr;
@@ -714,13 +739,17 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 using rk::mean_factor;
 
-// [B, H, S, C] descriptor of a 16-bit float tensor with C == want_c (or any
-// C <= 128 when want_c < 0).
+// [B, H, S, C] descriptor of a 16-bit float tensor: a head dim 1 <= C <=
+// 128 (want_c == 0), C == want_c (> 0), or any C <= 128 (want_c < 0).
 int view_of(const rk_tensor* t, int want_c, View* v) {
   int st = rk::check_desc(t, 4);
   if (st) return st;
   if (!rk::is_half(t->dtype)) return RK_ERR_DTYPE;
-  if (want_c >= 0 ? t->shape[3] != want_c : t->shape[3] > 128) return want_c == 128 ? RK_ERR_HEAD_DIM : RK_ERR_SHAPE;
+  if (want_c == 0) {
+    if (t->shape[3] < 1 || t->shape[3] > 128) return RK_ERR_HEAD_DIM;
+  } else if (want_c > 0 ? t->shape[3] != want_c : t->shape[3] > 128) {
+    return RK_ERR_SHAPE;
+  }
   if (t->shape[1] > (INT64_C(1) << 30) || t->shape[0] * t->shape[1] > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
   v->data = (const uint16_t*)t->data;
   v->sb = t->stride[0];
@@ -743,13 +772,13 @@ OutView out_of(const rk_tensor* t) {
   return o;
 }
 
-// Per-head [B, H, 128] or per-token [B, H, S, 128] bool/uint8 mask.
-int mask_of(const rk_tensor* t, int64_t B, int64_t H, int64_t S, bool per_token, MaskView* m) {
+// Per-head [B, H, D] or per-token [B, H, S, D] bool/uint8 mask.
+int mask_of(const rk_tensor* t, int64_t B, int64_t H, int64_t S, int64_t D, bool per_token, MaskView* m) {
   int st = rk::check_desc(t, per_token ? 4 : 3);
   if (st) return st;
   if (t->dtype != RK_U8) return RK_ERR_DTYPE;
   if (t->shape[0] != B || t->shape[1] != H) return RK_ERR_SHAPE;
-  if (per_token ? (t->shape[2] != S || t->shape[3] != 128) : t->shape[2] != 128) return RK_ERR_SHAPE;
+  if (per_token ? (t->shape[2] != S || t->shape[3] != D) : t->shape[2] != D) return RK_ERR_SHAPE;
   m->data = (uint8_t*)t->data;
   m->sb = t->stride[0];
   m->sh = t->stride[1];
@@ -818,17 +847,17 @@ int think_check(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_
                 int64_t* keep) {
   if (!keys || !queries || !kc_out || !mask_out) return RK_ERR_NULL;
   int st;
-  if ((st = view_of(keys, 128, kv)) || (st = view_of(queries, 128, qv))) return st;
+  if ((st = view_of(keys, 0, kv)) || (st = view_of(queries, 0, qv))) return st;
   if (queries->dtype != keys->dtype) return RK_ERR_DTYPE;
-  const int64_t B = keys->shape[0], H = keys->shape[1];
-  if (queries->shape[0] != B) return RK_ERR_SHAPE;
+  const int64_t B = keys->shape[0], H = keys->shape[1], D = keys->shape[3];
+  if (queries->shape[0] != B || queries->shape[3] != D) return RK_ERR_SHAPE;
   if (num_kv_heads != H || H < 1 || queries->shape[1] % H != 0) return RK_ERR_HEADS;
-  if (prune_count < 0 || prune_count > 128) return RK_ERR_KEEP_DIM;
-  *keep = 128 - prune_count;
+  if (prune_count < 0 || prune_count > D) return RK_ERR_KEEP_DIM;
+  *keep = D - prune_count;
   if ((st = rk::check_desc(kc_out, 4))) return st;
   if (kc_out->dtype != keys->dtype) return RK_ERR_DTYPE;
   if (!same_bhs(kc_out, B, H, keys->shape[2]) || kc_out->shape[3] != *keep) return RK_ERR_SHAPE;
-  if ((st = mask_of(mask_out, B, H, 0, false, mv))) return st;
+  if ((st = mask_of(mask_out, B, H, 0, D, false, mv))) return st;
   return RK_OK;
 }
 
@@ -856,6 +885,7 @@ hipError_t launch_think(const View& kv, bool kvec, const View& qv, int G, int ke
   a.f_grp = f_grp;
   a.mask = mv;
   a.idx = idx;
+  a.D = kv.C;
   hipLaunchKernelGGL((think_select_kernel<TT>), dim3((unsigned)bh), dim3(kD), 0, s, a);
   if (keep > 0 && kv.S > 0) {
     const OutView o = out_of(kc_out);
@@ -892,18 +922,18 @@ int spark_check(const rk_tensor* keys, const rk_tensor* queries, int64_t num_kv_
                 MaskView* mv, int64_t* keep) {
   if (!keys || !queries || !kc_out || !mask_out || !pm_out) return RK_ERR_NULL;
   int st;
-  if ((st = view_of(keys, 128, kv)) || (st = view_of(queries, 128, qv))) return st;
+  if ((st = view_of(keys, 0, kv)) || (st = view_of(queries, 0, qv))) return st;
   if (queries->dtype != keys->dtype) return RK_ERR_DTYPE;
-  const int64_t B = keys->shape[0], H = keys->shape[1], S = keys->shape[2];
-  if (queries->shape[0] != B) return RK_ERR_SHAPE;
+  const int64_t B = keys->shape[0], H = keys->shape[1], S = keys->shape[2], D = keys->shape[3];
+  if (queries->shape[0] != B || queries->shape[3] != D) return RK_ERR_SHAPE;
   if (num_kv_groups < 1 || queries->shape[1] != H * num_kv_groups) return RK_ERR_HEADS;
-  if (prune_count < 0 || prune_count > 128) return RK_ERR_KEEP_DIM;
-  *keep = 128 - prune_count;
+  if (prune_count < 0 || prune_count > D) return RK_ERR_KEEP_DIM;
+  *keep = D - prune_count;
   if ((st = rk::check_desc(kc_out, 4)) || (st = rk::check_desc(pm_out, 4))) return st;
   if (kc_out->dtype != keys->dtype || pm_out->dtype != keys->dtype) return RK_ERR_DTYPE;
   if (!same_bhs(kc_out, B, H, S) || kc_out->shape[3] != *keep) return RK_ERR_SHAPE;
   if (!same_bhs(pm_out, B, H, S) || pm_out->shape[3] != 1) return RK_ERR_SHAPE;
-  if ((st = mask_of(mask_out, B, H, S, true, mv))) return st;
+  if ((st = mask_of(mask_out, B, H, S, D, true, mv))) return st;
   return RK_OK;
 }
 
@@ -936,13 +966,14 @@ hipError_t launch_spark(const View& kv, bool kvec, bool mvec, const View& qv, in
   return hipGetLastError();
 }
 
-// Optional prompt / text spans of the recovery: NULL -> an empty view.
-int span_of(const rk_tensor* t, const rk_tensor* kc, View* v) {
+// Optional prompt / text spans of the recovery (head dim D): NULL -> an
+// empty view.
+int span_of(const rk_tensor* t, const rk_tensor* kc, int D, View* v) {
   if (!t) {
-    *v = View{nullptr, 0, 0, 0, 0, 0, (int32_t)kc->shape[1], 128};
+    *v = View{nullptr, 0, 0, 0, 0, 0, (int32_t)kc->shape[1], D};
     return RK_OK;
   }
-  int st = view_of(t, 128, v);
+  int st = view_of(t, D, v);
   if (st) return st;
   if (t->dtype != kc->dtype) return RK_ERR_DTYPE;
   if (t->shape[0] != kc->shape[0] || t->shape[1] != kc->shape[1]) return RK_ERR_SHAPE;
@@ -957,8 +988,13 @@ int recover(bool spark, const rk_tensor* k_prompt, const rk_tensor* k_pruned, co
   int st;
   if ((st = view_of(k_pruned, -1, &a.kc))) return st;
   const int64_t B = k_pruned->shape[0], H = k_pruned->shape[1], Sv = k_pruned->shape[2];
-  if ((st = span_of(k_prompt, k_pruned, &a.pr)) || (st = span_of(k_text, k_pruned, &a.tx))) return st;
-  if ((st = mask_of(mask, B, H, Sv, spark, &a.mask))) return st;
+  // the head dim: the output rows' width
+  if ((st = rk::check_desc(out, 4))) return st;
+  const int64_t D = out->shape[3];
+  if (D < 1 || D > 128) return RK_ERR_HEAD_DIM;
+  if (a.kc.C > D) return RK_ERR_SHAPE;
+  if ((st = span_of(k_prompt, k_pruned, (int)D, &a.pr)) || (st = span_of(k_text, k_pruned, (int)D, &a.tx))) return st;
+  if ((st = mask_of(mask, B, H, Sv, D, spark, &a.mask))) return st;
   a.pm = nullptr;
   a.p_sb = a.p_sh = a.p_ss = 0;
   if (spark) {
@@ -970,11 +1006,9 @@ int recover(bool spark, const rk_tensor* k_prompt, const rk_tensor* k_pruned, co
     a.p_sh = pruned_mean->stride[1];
     a.p_ss = pruned_mean->stride[2];
   }
-  if ((st = rk::check_desc(out, 4))) return st;
   if (out->dtype != k_pruned->dtype) return RK_ERR_DTYPE;
   a.rows = a.pr.S + Sv + a.tx.S;
   if (!same_bhs(out, B, H, a.rows)) return RK_ERR_SHAPE;
-  if (out->shape[3] != 128) return RK_ERR_HEAD_DIM;
   if (!launch) return RK_OK;
   if (B * H == 0 || a.rows == 0) return RK_OK;
   if (!out->data || (Sv > 0 && !mask->data) || (Sv > 0 && a.kc.C > 0 && !k_pruned->data) ||
@@ -985,13 +1019,14 @@ int recover(bool spark, const rk_tensor* k_prompt, const rk_tensor* k_pruned, co
   if (st) return st;
   a.out = out_of(out);
   a.H = (int)H;
+  a.D = (int)D;
   int splits = token_splits(B * H, a.rows, cus, 8, kTile);
   a.chunk = cdiv(cdiv(a.rows, splits), kTile) * kTile;
   splits = (int)cdiv(a.rows, a.chunk);
   const dim3 grid((unsigned)splits, (unsigned)(B * H));
   hipStream_t s = (hipStream_t)stream;
-  // 16-byte rows everywhere, 8-byte mask rows (SparK)
-  bool fast = rows16(out) && (!k_prompt || rows16(k_prompt)) && (!k_text || rows16(k_text)) &&
+  // 16-byte rows everywhere (whole 8-channel groups), 8-byte mask rows (SparK)
+  bool fast = D % 8 == 0 && rows16(out) && (!k_prompt || rows16(k_prompt)) && (!k_text || rows16(k_text)) &&
               a.kc.C % 8 == 0 && (a.kc.C == 0 || rows16(k_pruned));
   if (spark)
     fast = fast && mask->stride[3] == 1 && mask->stride[0] % 8 == 0 && mask->stride[1] % 8 == 0 &&
@@ -1047,10 +1082,11 @@ extern "C" int rk_think_score_and_compact(const rk_tensor* keys_vision, const rk
   if ((kv.S > 0 && !kv.data) || (qv.S > 0 && !qv.data) || !mv.data || (keep > 0 && kv.S > 0 && !k_compact_out->data))
     return RK_ERR_NULL;
   const int G = (int)(Hq / H);
-  const float f_keys = mean_factor(B * H * 128, B * H * kv.S * 128);
-  const float f_win = mean_factor(B * Hq * 128, B * Hq * qv.S * 128);
-  const float f_grp = mean_factor(B * H * 128, B * Hq * 128);
-  const bool kvec = rows16(keys_vision);
+  const int64_t D = kv.C;
+  const float f_keys = mean_factor(B * H * D, B * H * kv.S * D);
+  const float f_win = mean_factor(B * Hq * D, B * Hq * qv.S * D);
+  const float f_grp = mean_factor(B * H * D, B * Hq * D);
+  const bool kvec = rows16(keys_vision) && D % 8 == 0;
   hipStream_t s = (hipStream_t)stream;
   const hipError_t e = keys_vision->dtype == RK_F16
                            ? launch_think<rk::F16>(kv, kvec, qv, G, (int)keep, p, B, f_keys, f_win, f_grp, mv,
@@ -1095,11 +1131,11 @@ extern "C" int rk_spark_prune(const rk_tensor* keys_vision, const rk_tensor* que
   if ((kv.S > 0 && (!kv.data || !mv.data || !pruned_mean_out->data || (keep > 0 && !k_compact_out->data))) ||
       (qv.S > 0 && !qv.data))
     return RK_ERR_NULL;
-  const int64_t W = qv.S;
-  const float f_grp = mean_factor(B * H * W * 128, B * H * num_kv_groups * W * 128);
+  const int64_t W = qv.S, D = kv.C;
+  const float f_grp = mean_factor(B * H * W * D, B * H * num_kv_groups * W * D);
   const float f_pruned = mean_factor(B * H * kv.S, B * H * kv.S * prune_count);
-  const bool kvec = rows16(keys_vision);
-  const bool mvec = keep_mask_out->stride[3] == 1 && keep_mask_out->stride[0] % 8 == 0 &&
+  const bool kvec = rows16(keys_vision) && D % 8 == 0;
+  const bool mvec = D % 8 == 0 && keep_mask_out->stride[3] == 1 && keep_mask_out->stride[0] % 8 == 0 &&
                     keep_mask_out->stride[1] % 8 == 0 && keep_mask_out->stride[2] % 8 == 0 &&
                     (((uintptr_t)keep_mask_out->data) & 7) == 0;
   hipStream_t s = (hipStream_t)stream;
@@ -1140,23 +1176,23 @@ extern "C" int rk_channel_selection(const rk_tensor* keep_mask, const rk_tensor*
   int st = rk::check_desc(R_out, 4);
   if (st) return st;
   if (!rk::is_float_param(R_out->dtype)) return RK_ERR_DTYPE;
-  const int64_t B = R_out->shape[0], H = R_out->shape[1], Dk = R_out->shape[3];
-  if (R_out->shape[2] != 128) return RK_ERR_HEAD_DIM;
-  if (Dk < 1 || Dk > 128) return RK_ERR_KEEP_DIM;
+  const int64_t B = R_out->shape[0], H = R_out->shape[1], D = R_out->shape[2], Dk = R_out->shape[3];
+  if (D < 1 || D > 128) return RK_ERR_HEAD_DIM;
+  if (Dk < 1 || Dk > D) return RK_ERR_KEEP_DIM;
   if (H > (INT64_C(1) << 30) || B * H > (INT64_C(1) << 30)) return RK_ERR_SHAPE;
   MaskView m;
-  if ((st = mask_of(keep_mask, B, H, 0, false, &m))) return st;
+  if ((st = mask_of(keep_mask, B, H, 0, D, false, &m))) return st;
   if (B * H == 0) return RK_OK;
   if (!m.data || !R_out->data) return RK_ERR_NULL;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)(B * H));
   const int64_t* rs = R_out->stride;
   if (R_out->dtype == RK_F32) {
-    hipLaunchKernelGGL((selection_kernel<float>), grid, dim3(kD), 0, s, m, (int)H, (int)Dk, (float*)R_out->data,
-                       rs[0], rs[1], rs[2], rs[3], 1.0f);
+    hipLaunchKernelGGL((selection_kernel<float>), grid, dim3(kD), 0, s, m, (int)H, (int)D, (int)Dk,
+                       (float*)R_out->data, rs[0], rs[1], rs[2], rs[3], 1.0f);
   } else {
     const uint16_t one = R_out->dtype == RK_F16 ? (uint16_t)0x3C00 : (uint16_t)0x3F80;
-    hipLaunchKernelGGL((selection_kernel<uint16_t>), grid, dim3(kD), 0, s, m, (int)H, (int)Dk,
+    hipLaunchKernelGGL((selection_kernel<uint16_t>), grid, dim3(kD), 0, s, m, (int)H, (int)D, (int)Dk,
                        (uint16_t*)R_out->data, rs[0], rs[1], rs[2], rs[3], one);
   }
   return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;

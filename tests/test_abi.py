@@ -567,7 +567,14 @@ def test_think_validation():
     assert chk(prune=129, kc=(2, 4, 50, 1)) == _lib.RK_ERR_KEEP_DIM
     assert chk(heads=3) == _lib.RK_ERR_HEADS
     assert chk(q=(2, 6, 32, 128), heads=4) == _lib.RK_ERR_HEADS
-    assert chk(keys=(2, 4, 50, 64)) == _lib.RK_ERR_HEAD_DIM
+    # any head dim 1..128, the same in keys, queries and the mask
+    assert chk(keys=(2, 4, 50, 64), q=(2, 8, 32, 64), kc=(2, 4, 50, 40), prune=24, mask=(2, 4, 64)) == 0
+    assert chk(keys=(2, 4, 50, 5), q=(2, 8, 32, 5), kc=(2, 4, 50, 5), prune=0, mask=(2, 4, 5)) == 0
+    assert chk(keys=(2, 4, 50, 64), q=(2, 8, 32, 64), kc=(2, 4, 50, 40), prune=24) == _lib.RK_ERR_SHAPE
+    assert chk(keys=(2, 4, 50, 64), kc=(2, 4, 50, 40), prune=24, mask=(2, 4, 64)) == _lib.RK_ERR_SHAPE
+    assert chk(keys=(2, 4, 50, 64), q=(2, 8, 32, 64), kc=(2, 4, 50, 1), prune=65,
+               mask=(2, 4, 64)) == _lib.RK_ERR_KEEP_DIM
+    assert chk(keys=(2, 4, 50, 129), q=(2, 8, 32, 129), mask=(2, 4, 129)) == _lib.RK_ERR_HEAD_DIM
     assert chk(qdt=_lib.RK_F16) == _lib.RK_ERR_DTYPE
     assert chk(kc=(2, 4, 50, 33)) == _lib.RK_ERR_SHAPE
     assert chk(mask=(2, 4, 127)) == _lib.RK_ERR_SHAPE
@@ -599,6 +606,12 @@ def test_spark_validation():
     assert chk(pm=(2, 4, 50, 2)) == _lib.RK_ERR_SHAPE
     assert chk(kc=(2, 4, 49, 32)) == _lib.RK_ERR_SHAPE
     assert chk(dt=_lib.RK_F32) == _lib.RK_ERR_DTYPE
+    # head dim 80: keys, queries, mask and compact width follow it
+    assert chk(keys=(2, 4, 50, 80), q=(2, 28, 32, 80), prune=60, kc=(2, 4, 50, 20), mask=(2, 4, 50, 80)) == 0
+    assert chk(keys=(2, 4, 50, 80), q=(2, 28, 32, 80), prune=60, kc=(2, 4, 50, 20)) == _lib.RK_ERR_SHAPE
+    assert chk(keys=(2, 4, 50, 80), prune=60, kc=(2, 4, 50, 20), mask=(2, 4, 50, 80)) == _lib.RK_ERR_SHAPE
+    assert chk(keys=(2, 4, 50, 0), q=(2, 28, 32, 0), prune=0, kc=(2, 4, 50, 0),
+               mask=(2, 4, 50, 0)) == _lib.RK_ERR_HEAD_DIM
 
 
 def test_recover_validation():
@@ -621,8 +634,22 @@ def test_recover_validation():
     assert lib.rk_think_recover_check(None, wide, None, r(tm), r(vis)) == _lib.RK_ERR_SHAPE
     sel = _t((B, H, 128, Dk), _lib.RK_F32)
     assert lib.rk_channel_selection(r(tm), r(_t((B, H, 128, 0), _lib.RK_F32)), None) == _lib.RK_ERR_KEEP_DIM
-    assert lib.rk_channel_selection(r(tm), r(_t((B, H, 64, Dk), _lib.RK_F32)), None) == _lib.RK_ERR_HEAD_DIM
+    assert lib.rk_channel_selection(r(tm), r(_t((B, H, 64, Dk), _lib.RK_F32)), None) == _lib.RK_ERR_SHAPE
+    assert lib.rk_channel_selection(r(tm), r(_t((B, H, 129, Dk), _lib.RK_F32)), None) == _lib.RK_ERR_HEAD_DIM
     assert lib.rk_channel_selection(r(sm), r(sel), None) == _lib.RK_ERR_RANK
+    # head dim 64: mask [B,H,64], R [B,H,64,Dk <= 64], recovered rows of 64
+    tm64, sm64 = _t((B, H, 64), _lib.RK_U8), _t((B, H, Sv, 64), _lib.RK_U8)
+    # (valid shapes pass validation and stop at the descriptors' missing data)
+    assert lib.rk_channel_selection(r(tm64), r(_t((B, H, 64, Dk), _lib.RK_F32)), None) == _lib.RK_ERR_NULL
+    assert lib.rk_channel_selection(r(tm64), r(_t((B, H, 64, 65), _lib.RK_F32)), None) == _lib.RK_ERR_KEEP_DIM
+    kp64, kt64 = _t((B, H, Sp, 64)), _t((B, H, St, 64))
+    out64 = _t((B, H, Sp + Sv + St, 64))
+    assert lib.rk_think_recover_check(r(kp64), r(kc), r(kt64), r(tm64), r(out64)) == 0
+    assert lib.rk_spark_recover_check(r(kp64), r(kc), r(kt64), r(sm64), r(pm), r(out64)) == 0
+    assert lib.rk_think_recover_check(r(kp), r(kc), r(kt64), r(tm64), r(out64)) == _lib.RK_ERR_SHAPE
+    assert lib.rk_think_recover_check(r(kp64), r(kc), r(kt64), r(tm), r(out64)) == _lib.RK_ERR_SHAPE
+    assert lib.rk_think_recover_check(None, r(_t((B, H, Sv, 65))), None, r(tm64),
+                                      r(_t((B, H, Sv, 64)))) == _lib.RK_ERR_SHAPE
 
 
 def test_plan_small_span_does_not_starve_the_other():
