@@ -337,8 +337,10 @@ extern "C" int rk_plan_decode(int64_t B, int64_t H_q, int64_t H_kv, int64_t Dk, 
   rk_decode_plan p;
   memset(&p, 0, sizeof(p));
   if (policy == RK_POLICY_GQA) {
-    p.heads_per_unit = (int32_t)(G < 16 ? G : 16);
-    p.head_blocks = (int32_t)cdiv(G, 16);
+    // blocks of up to 16 query heads (fp32, the VALU kernel: 8) per unit
+    const int64_t hmax = elem_bytes == 4 ? 8 : 16;
+    p.heads_per_unit = (int32_t)(G < hmax ? G : hmax);
+    p.head_blocks = (int32_t)cdiv(G, hmax);
     p.units = B * H_kv * p.head_blocks;
   } else {
     p.heads_per_unit = 1;
@@ -500,12 +502,11 @@ int32_t rotatek_policy(int32_t policy, int64_t G) {
   return policy == RK_POLICY_PAPER && G > 1 ? RK_POLICY_GQA : policy;
 }
 
-// The plan of a checked call.  fp32 runs one unit per query head (the
-// VALU kernel has no grouped form) over 4-byte elements.
+// The plan of a checked call (fp32 over 4-byte elements).
 int plan_for(const Checked& c, bool has_vis, int32_t policy, int cus, rk_decode_plan* p) {
   const bool f32 = c.dtype == RK_F32;
-  return rk_plan_decode(c.B, c.H_q, c.H_kv, has_vis ? c.Dk : 0, has_vis ? c.S_v : 0, c.S_f, f32 ? 4 : 2,
-                        f32 ? RK_POLICY_PAPER : policy, cus, p);
+  return rk_plan_decode(c.B, c.H_q, c.H_kv, has_vis ? c.Dk : 0, has_vis ? c.S_v : 0, c.S_f, f32 ? 4 : 2, policy,
+                        cus, p);
 }
 
 int resolve_cus(int32_t num_cus, int* st) {
@@ -675,7 +676,6 @@ int run_decode(const Checked& c, const rk_tensor* q, const rk_tensor* R, const r
   a.units = (int32_t)p.units;
   a.xgroup = policy == RK_POLICY_PAPER && c.G > 1 && c.dtype != RK_F32 ? (int32_t)c.G : 0;
   if (a.xgroup || c.dtype == RK_F32) a.rot_x = 0;
-  if (c.dtype == RK_F32) a.spk = (int32_t)c.G;  // one unit per query head
   a.scale_log2 = (float)(rk::kLog2e / sqrt((double)c.D));  // 1 / sqrt(D) (fused_decode.py:340)
   a.cmajor = has_vis && c.dtype != RK_F32 && !a.xgroup ? p.chunk_major : 0;
   // the 16-bit kernels carry the single-launch merge at head_dim 128 with

@@ -1069,13 +1069,16 @@ decode_kernel(const DecodeArgs a) {
 // reference kernels load any float input as fp32 and compute in fp32
 // (fused_decode.py:133,166,174; full_channel_flash_decoding.py:65,84,92);
 // so does this kernel, on the VALU: fp32 has no MFMA path that keeps its
-// precision at this arithmetic intensity.  One unit per query head (hpu 1),
-// the plan's grid and records as the 16-bit kernel, so both merges apply.
-// Each wave walks 64-token blocks of its workgroup's chunk (blocks wave,
-// wave + 4, ...): lane t scores token t0 + t as a dot product over its
-// row, the wave runs the online softmax (log2 domain), and lane j
-// accumulates channels 2j, 2j + 1 of P V over the block's rows, with the
-// block's probabilities broadcast from LDS.
+// precision at this arithmetic intensity.  A unit is up to HG query heads
+// of one KV head (HG 1: one query head; HG 8: the grouped decomposition,
+// gqa_decode.py:121-210, each K and V row read once for the unit's heads),
+// with the plan's grid and records as the 16-bit kernel, so both merges
+// apply.  Each wave walks 64-token blocks of its workgroup's chunk (blocks
+// wave, wave + 4, ...): lane t loads the row of token t0 + t once and
+// scores it against every head's query, the wave runs one online softmax
+// per head (log2 domain), and lane j accumulates channels 2j, 2j + 1 of
+// each head's P V over the block's V rows (loaded once), with the block's
+// probabilities broadcast from LDS.
 constexpr int kBlk32 = 64;
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -1089,76 +1092,108 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// sum_c w[c] * row[c * sd], c < n <= KMAX; w in LDS.  VEC: unit stride,
-// 16-byte aligned row, n a multiple of 4: all KMAX / 4 16-byte loads are
-// issued before any is used (those past n re-read the row's last four
-// floats, in bounds, and are not used), so the row costs one memory round
-// trip; float4 i accumulates into s0 (i even) or s1 (i odd).
-template <bool VEC, int KMAX>
-__device__ __forceinline__ float dot_row32(const float* row, uint32_t sd, const float* w, int n) {
-  float s0 = 0.f, s1 = 0.f;
+// d[h] = sum_c w[h * 128 + c] * row[c * sd] for the heads h < nh, c < n <=
+// KMAX; w in LDS.  VEC: unit stride, 16-byte aligned row, n a multiple of
+// 4: all KMAX / 4 16-byte loads are issued before any is used (those past
+// n re-read the row's last four floats, in bounds, and are not used), so
+// the row costs one memory round trip; float4 i accumulates into the even
+// (i even) or odd partial sum of each head.
+template <bool VEC, int KMAX, int HG>
+__device__ __forceinline__ void dot_rows32(const float* row, uint32_t sd, const float* w, int n, int nh,
+                                           float (&d)[HG]) {
+  float s0[HG], s1[HG];
+#pragma unroll
+  for (int h = 0; h < HG; ++h) s0[h] = s1[h] = 0.f;
   if constexpr (VEC) {
-    if (n <= 0) return 0.f;
-    float4 r[KMAX / 4];
+    if (n > 0) {
+      float4 r[KMAX / 4];
 #pragma unroll
-    for (int i = 0; i < KMAX / 4; ++i) r[i] = *(const float4*)(row + min(4 * i, n - 4));
+      for (int i = 0; i < KMAX / 4; ++i) r[i] = *(const float4*)(row + min(4 * i, n - 4));
 #pragma unroll
-    for (int i = 0; i < KMAX / 4; ++i) {
-      if (4 * i < n) {
-        const float4 w4 = *(const float4*)(w + 4 * i);
-        float& acc = (i & 1) ? s1 : s0;
-        acc = fmaf(w4.x, r[i].x, acc);
-        acc = fmaf(w4.y, r[i].y, acc);
-        acc = fmaf(w4.z, r[i].z, acc);
-        acc = fmaf(w4.w, r[i].w, acc);
+      for (int i = 0; i < KMAX / 4; ++i) {
+        if (4 * i < n) {
+#pragma unroll
+          for (int h = 0; h < HG; ++h) {
+            if (h < nh) {
+              const float4 w4 = *(const float4*)(w + h * 128 + 4 * i);
+              float& acc = (i & 1) ? s1[h] : s0[h];
+              acc = fmaf(w4.x, r[i].x, acc);
+              acc = fmaf(w4.y, r[i].y, acc);
+              acc = fmaf(w4.z, r[i].z, acc);
+              acc = fmaf(w4.w, r[i].w, acc);
+            }
+          }
+        }
       }
     }
   } else {
-    for (int c = 0; c < n; ++c) s0 = fmaf(w[c], row[(int64_t)c * sd], s0);
+    for (int c = 0; c < n; ++c) {
+      const float x = row[(int64_t)c * sd];
+#pragma unroll
+      for (int h = 0; h < HG; ++h)
+        if (h < nh) s0[h] = fmaf(w[h * 128 + c], x, s0[h]);
+    }
   }
-  return s0 + s1;
+#pragma unroll
+  for (int h = 0; h < HG; ++h) d[h] = s0[h] + s1[h];
 }
 
-template <bool HAS_VIS, bool VEC>
+template <bool HAS_VIS, bool VEC, int HG>
 __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) float s_q[128];
-  __shared__ __attribute__((aligned(16))) float s_qt[128];
-  __shared__ float s_bias[2];
-  __shared__ float s_p[kWaves][kBlk32];
-  __shared__ float s_m[kWaves], s_l[kWaves];
-  __shared__ float s_acc[kWaves][128];
+  __shared__ __attribute__((aligned(16))) float s_q[HG][128];
+  __shared__ __attribute__((aligned(16))) float s_qt[HG][128];
+  __shared__ float s_bias[HG][2];
+  __shared__ float s_p[kWaves][HG][kBlk32];
+  __shared__ float s_m[kWaves][HG], s_l[kWaves][HG];
+  __shared__ float s_acc[kWaves][HG][128];
   __shared__ float s_mrg[16 * kRecFloats];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int u = blockIdx.y, x = blockIdx.x;
   const int b = u / a.units_per_b;
   const int r_in_b = u - b * a.units_per_b;
   const int kv = r_in_b / a.spk;
-  const int h0 = kv * a.G + (r_in_b - kv * a.spk) * a.hpu;
+  const int jblk = r_in_b - kv * a.spk;
+  const int h0 = kv * a.G + jblk * a.hpu;
+  const int nh = HG == 1 ? 1 : min(a.hpu, a.G - jblk * a.hpu);  // this unit's query heads
   const bool is_vis = HAS_VIS && x < a.wg_vis;
   const int xf = HAS_VIS ? x - a.wg_vis : x;
   const float* q = (const float*)a.q;
 
   // channels past head_dim D are zeros (q, R_partial's rows, delta_mu);
   // V lanes past D read an in-bounds duplicate (16-byte rows: the row's last
-  // two channels; else no load) that feeds only output channels not written
-  if (tid < 128) s_q[tid] = tid < a.D ? q[b * a.q_sb + (int64_t)h0 * a.q_sh + (int64_t)tid * a.q_sd] : 0.f;
+  // two channels; else no load) that feeds only output channels not written;
+  // rows of absent heads (h >= nh) are zeros
+  for (int i = tid; i < HG * 128; i += kThreads) {
+    const int h = i >> 7, c = i & 127;
+    (&s_q[0][0])[i] = h < nh && c < a.D ? q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + (int64_t)c * a.q_sd] : 0.f;
+  }
   __syncthreads();
   const int vc = min(2 * lane, a.D - 2);  // (VEC: D is a multiple of 4)
   const bool v0ok = 2 * lane < a.D, v1ok = 2 * lane + 1 < a.D;
 
-  float m = kNegInit, l = 0.f, acc0 = 0.f, acc1 = 0.f;
-  // online-softmax step over one block: s = log2-domain score of token
-  // t0 + lane (-inf when invalid), V rows clamped to t_last
-  auto step = [&](float s, const float* vb, uint32_t vss, uint32_t vsd, int64_t t0, int64_t t_last,
+  float m[HG], l[HG], acc0[HG], acc1[HG];
+#pragma unroll
+  for (int h = 0; h < HG; ++h) {
+    m[h] = kNegInit;
+    l[h] = acc0[h] = acc1[h] = 0.f;
+  }
+  // online-softmax step over one block: s[h] = log2-domain score of token
+  // t0 + lane for head h (-inf when invalid), V rows clamped to t_last
+  auto step = [&](const float (&s)[HG], const float* vb, uint32_t vss, uint32_t vsd, int64_t t0, int64_t t_last,
                   uint32_t gap_at, uint32_t gap) {
-    const float m_new = fmaxf(m, wave_max(s));
-    const float alpha = fast_exp2(m - m_new);
-    const float p = fast_exp2(s - m_new);
-    l = l * alpha + wave_sum(p);
-    acc0 *= alpha;
-    acc1 *= alpha;
-    m = m_new;
-    s_p[wave][lane] = p;
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      if (h < nh) {
+        const float m_new = fmaxf(m[h], wave_max(s[h]));
+        const float alpha = fast_exp2(m[h] - m_new);
+        const float p = fast_exp2(s[h] - m_new);
+        l[h] = l[h] * alpha + wave_sum(p);
+        acc0[h] *= alpha;
+        acc1[h] *= alpha;
+        m[h] = m_new;
+        s_p[wave][h][lane] = p;
+      }
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1183,10 +1218,15 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
         }
       }
 #pragma unroll
-      for (int jj = 0; jj < kVB; ++jj) {
-        const float pj = s_p[wave][j0 + jj];
-        acc0 = fmaf(pj, v0[jj], acc0);
-        acc1 = fmaf(pj, v1[jj], acc1);
+      for (int h = 0; h < HG; ++h) {
+        if (h < nh) {
+#pragma unroll
+          for (int jj = 0; jj < kVB; ++jj) {
+            const float pj = s_p[wave][h][j0 + jj];
+            acc0[h] = fmaf(pj, v0[jj], acc0[h]);
+            acc1[h] = fmaf(pj, v1[jj], acc1[h]);
+          }
+        }
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1196,31 +1236,49 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
 
   if (is_vis) {
     {  // q R_partial: thread (half, c) sums rows 64 half .. 64 half + 63 of
-       // column c, all 64 loads in flight; the halves meet in LDS
+       // column c for every head, all 64 loads in flight; the halves meet
+       // in LDS
       const int c = tid & 127, half = tid >> 7;
       const int cc = min(c, max(a.Dk - 1, 0));
       const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)cc * a.R_sk;
-      float sum = 0.f;
+      float sum[HG];
+#pragma unroll
+      for (int h = 0; h < HG; ++h) sum[h] = 0.f;
       if (a.Dk > 0) {
         float rv[64];
         load_any_rows(a.R, rb, a.R_sd, a.r_dtype, 64 * half, a.D, rv);
 #pragma unroll
-        for (int i = 0; i < 64; ++i) sum = fmaf(s_q[64 * half + i], rv[i], sum);
+        for (int h = 0; h < HG; ++h)
+          if (h < nh) {
+#pragma unroll
+            for (int i = 0; i < 64; ++i) sum[h] = fmaf(s_q[h][64 * half + i], rv[i], sum[h]);
+          }
       }
-      s_acc[half][c] = sum;  // s_acc is free until the epilogue
+#pragma unroll
+      for (int h = 0; h < HG; ++h) s_acc[half][h][c] = sum[h];  // s_acc is free until the epilogue
       __syncthreads();
-      if (tid < 128) s_qt[tid] = tid < a.Dk ? s_acc[0][tid] + s_acc[1][tid] : 0.f;
+      for (int i = tid; i < HG * 128; i += kThreads) {
+        const int h = i >> 7, c2 = i & 127;
+        (&s_qt[0][0])[i] = c2 < a.Dk ? s_acc[0][h][c2] + s_acc[1][h][c2] : 0.f;
+      }
     }
-    if (wave < 2) {  // q . delta_mu
+    if (wave < 2) {  // q . delta_mu, every head of the unit
       const int d = tid;
-      const float t = a.has_bias && d < a.D
-                          ? s_q[d] * load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)d * a.dm_sd, a.dm_dtype)
-                          : 0.f;
-      const float w = wave_sum(t);
-      if (lane == 0) s_bias[wave] = w;
+      const float dm = a.has_bias && d < a.D
+                           ? load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)d * a.dm_sd, a.dm_dtype)
+                           : 0.f;
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
+        if (h < nh) {
+          const float w = wave_sum(s_q[h][d] * dm);
+          if (lane == 0) s_bias[h][wave] = w;
+        }
+      }
     }
     __syncthreads();
-    const float bias2 = (s_bias[0] + s_bias[1]) * a.scale_log2;
+    float bias2[HG];
+#pragma unroll
+    for (int h = 0; h < HG; ++h) bias2[h] = h < nh ? (s_bias[h][0] + s_bias[h][1]) * a.scale_log2 : 0.f;
     const int64_t t_begin = (int64_t)x * a.chunk_vis;
     const int64_t t_end = min(a.S_v, t_begin + a.chunk_vis);
     const float* ksb = (const float*)a.ks + b * a.ks_sb + kv * a.ks_sh;
@@ -1228,11 +1286,16 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
       const int64_t t = t0 + lane;
       const float* kr = ksb + (int64_t)min(t, t_end - 1) * a.ks_ss;
-      const float d = a.Dk <= 32   ? dot_row32<VEC, 32>(kr, a.ks_sd, s_qt, a.Dk)
-                      : a.Dk <= 64 ? dot_row32<VEC, 64>(kr, a.ks_sd, s_qt, a.Dk)
-                                   : dot_row32<VEC, 128>(kr, a.ks_sd, s_qt, a.Dk);
-      const float s = t < t_end ? fmaf(d, a.scale_log2, bias2) : -INFINITY;
-      step(s, vsb, a.vs_ss, a.vs_sd, t0, t_end - 1, UINT32_MAX, 0u);
+      float d[HG], sc[HG];
+      if (a.Dk <= 32)
+        dot_rows32<VEC, 32, HG>(kr, a.ks_sd, &s_qt[0][0], a.Dk, nh, d);
+      else if (a.Dk <= 64)
+        dot_rows32<VEC, 64, HG>(kr, a.ks_sd, &s_qt[0][0], a.Dk, nh, d);
+      else
+        dot_rows32<VEC, 128, HG>(kr, a.ks_sd, &s_qt[0][0], a.Dk, nh, d);
+#pragma unroll
+      for (int h = 0; h < HG; ++h) sc[h] = t < t_end ? fmaf(d[h], a.scale_log2, bias2[h]) : -INFINITY;
+      step(sc, vsb, a.vs_ss, a.vs_sd, t0, t_end - 1, UINT32_MAX, 0u);
     }
   } else {
     const int64_t t_begin = (int64_t)xf * a.chunk_full;
@@ -1242,40 +1305,48 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
       const int64_t t = t0 + lane;
       const int64_t tc = min(t, t_end - 1);
-      const float d = dot_row32<VEC, 128>(kfb + tc * a.kf_ss, a.kf_sd, s_q, a.D);
+      float d[HG], sc[HG];
+      dot_rows32<VEC, 128, HG>(kfb + tc * a.kf_ss, a.kf_sd, &s_q[0][0], a.D, nh, d);
       const bool ok = t < t_end && (!a.mask || a.mask[b * a.mf_sb + tc * a.mf_ss] != 0);
-      step(ok ? d * a.scale_log2 : -INFINITY, vfb, a.vf_ss, a.vf_sd, t0, t_end - 1, a.vf_gap_at, a.vf_gap);
+#pragma unroll
+      for (int h = 0; h < HG; ++h) sc[h] = ok ? d[h] * a.scale_log2 : -INFINITY;
+      step(sc, vfb, a.vf_ss, a.vf_sd, t0, t_end - 1, a.vf_gap_at, a.vf_gap);
     }
   }
 
-  // the four wave states -> this workgroup's record
-  if (lane == 0) {
-    s_m[wave] = m;
-    s_l[wave] = l;
+  // the four wave states of each head -> this workgroup's records
+#pragma unroll
+  for (int h = 0; h < HG; ++h) {
+    if (h < nh) {
+      if (lane == 0) {
+        s_m[wave][h] = m[h];
+        s_l[wave][h] = l[h];
+      }
+      s_acc[wave][h][2 * lane] = acc0[h];
+      s_acc[wave][h][2 * lane + 1] = acc1[h];
+    }
   }
-  s_acc[wave][2 * lane] = acc0;
-  s_acc[wave][2 * lane + 1] = acc1;
   __syncthreads();
-  if (tid < 16) {
-    const int c8 = tid;
+  if (tid < 16 * nh) {
+    const int h = tid >> 4, c8 = tid & 15;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][h]);
     float L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float wt = fast_exp2(s_m[w] - M);
-      L += s_l[w] * wt;
+      const float wt = fast_exp2(s_m[w][h] - M);
+      L += s_l[w][h] * wt;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) A[e] += s_acc[w][8 * c8 + e] * wt;
+      for (int e = 0; e < 8; ++e) A[e] += s_acc[w][h][8 * c8 + e] * wt;
     }
-    float* rec = a.part + ((int64_t)u * a.np + x) * kRecFloats;
+    float* rec = a.part + (((int64_t)u * a.np + x) * a.hpu + h) * kRecFloats;
     if (a.fused)
       store_rec<true>(rec, c8, A, M, L);
     else
       store_rec<false>(rec, c8, A, M, L);
   }
-  if (a.fused) merge_fused<F32, false, 1>(a, u, b, h0, 1, tid, s_mrg);
+  if (a.fused) merge_fused<F32, false, HG>(a, u, b, h0, nh, tid, s_mrg);
 }
 
 // Second launch: one workgroup per unit runs merge_unit, or with one query

@@ -305,8 +305,9 @@ def _check_plan(p, B, Hq, Hkv, Dk, S_v, S_f, policy, elem_bytes, cus):
     chunks, the grid, one round for chunk-major grids, and one workgroup per
     CU for the one-slot plans."""
     G = Hq // Hkv
-    if policy == 1:  # (the fp32 entry points plan policy 0 themselves)
-        assert p["heads_per_unit"] == min(G, 16) and p["units"] == B * Hkv * -(-G // 16)
+    if policy == 1:  # blocks of up to 16 query heads (fp32: 8)
+        hmax = 8 if elem_bytes == 4 else 16
+        assert p["heads_per_unit"] == min(G, hmax) and p["units"] == B * Hkv * -(-G // hmax)
     else:
         assert p["heads_per_unit"] == 1 and p["units"] == B * Hq
     if S_v > 0:
@@ -743,6 +744,13 @@ def test_plan_one_workgroup_per_cu_for_small_short_rounds():
         p = _lib.plan_decode(1, 32, 32, 32, S_v, 128, elem_bytes=4, policy=0)
         assert p["grid"] == want and p["chunk_major"] == 0, (S_v, p)
     assert _lib.plan_decode(2, 32, 32, 32, 1152, 128, elem_bytes=4, policy=0)["grid"] == 384
+    # fp32 GQA: units of up to 8 query heads of one KV head (K / V read once
+    # per unit), 16-bit: up to 16
+    for G in (4, 7, 8, 12, 16):
+        p4 = _lib.plan_decode(2, 4 * G, 4, 32, 3000, 64, elem_bytes=4, policy=1)
+        assert p4["heads_per_unit"] == min(G, 8) and p4["head_blocks"] == -(-G // 8)
+        assert p4["units"] == 2 * 4 * p4["head_blocks"]
+        assert _lib.plan_decode(2, 4 * G, 4, 32, 3000, 64, elem_bytes=2, policy=1)["heads_per_unit"] == min(G, 16)
     for shape, pol in (((8, 28, 4, 32, 12001, 61), 1), ((1, 32, 32, 32, 15360, 640), 0)):
         assert _lib.plan_decode(*shape, policy=pol)["grid"] == 512
     p = _lib.plan_decode(16, 28, 4, 32, 2049, 61, policy=1)

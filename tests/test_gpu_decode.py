@@ -393,6 +393,8 @@ FP32_CASES = [
     (2, 4, 4, 32, 0, 257),          # no visual span
     (1, 28, 4, 128, 513, 65),
     (1, 2, 2, 6, 5, 3),             # Dk not a multiple of 4 (element loads)
+    (1, 24, 2, 32, 700, 40),        # G = 12: head blocks of 8 and 4 query heads
+    (2, 16, 1, 64, 400, 30),        # G = 16: two blocks of 8
 ]
 
 
@@ -406,6 +408,28 @@ def test_fp32_decode_matches_oracle(case, family):
     assert out.dtype == torch.float32 and out.shape == (B, 1, Hq, 128)
     err = np.abs(_np(out) - _oracle(inp)).max()
     assert err <= TOL32, err
+
+
+@pytest.mark.parametrize("case", [(2, 28, 4, 32, 1500, 61), (1, 24, 2, 64, 900, 33)])
+def test_fp32_grouped_merges_are_bit_identical(case):
+    """fp32 units of up to 8 query heads of one KV head (each K / V row
+    read once for the unit's heads): the single-launch merge equals the
+    merge kernel bit for bit, and both match the oracle."""
+    from rotatek_amd import _lib
+    B, Hq, Hkv, Dk, S_v, S_f = case
+    _say(f"fp32 grouped merges B={B} Hq={Hq} Hkv={Hkv} Dk={Dk}")
+    p = _lib.plan_decode(B, Hq, Hkv, Dk, S_v, S_f, 4, _lib.RK_POLICY_GQA)
+    assert p["heads_per_unit"] == min(Hq // Hkv, 8) and p["units"] == B * Hkv * -(-(Hq // Hkv) // 8)
+    inp = _rand_inputs(B, Hq, Hkv, Dk, S_v, S_f, torch.float32, seed=sum(case), mask_p=0.2)
+    try:
+        _lib.set_decode_merge(_lib.MERGE_TWO_LAUNCHES)
+        two = _decode(inp, "gqa")
+        _lib.set_decode_merge(_lib.MERGE_SINGLE_LAUNCH)
+        one = _decode(inp, "gqa")
+    finally:
+        _lib.set_decode_merge(_lib.MERGE_AUTO)
+    assert torch.equal(one, two)
+    assert np.abs(_np(two) - _oracle(inp)).max() <= TOL32
 
 
 def test_fp32_config0_end_to_end():
