@@ -248,7 +248,12 @@ def _cfg0_leg(budget_s=3.0):
                         "by the HIP prefill kernels at fp32"}
 
 
-DECODE_SOURCE = os.path.join(ROOT, "rotatek_amd", "csrc", "rk_decode.hip")
+# the decode path's sources: host code, kernels, their per-dtype units and
+# the shared device helpers
+DECODE_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f)
+                  for f in ("rk_decode.hip", "rk_decode.h", "rk_decode_dev.h", "rk_decode_f16.hip",
+                            "rk_decode_bf16.hip", "rk_decode_f32.hip", "rk_common.h")]
+PREFILL_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f) for f in ("rk_prefill.hip", "rk_common.h")]
 
 
 def _code_text(src: str) -> str:
@@ -262,19 +267,24 @@ def _code_text(src: str) -> str:
     return " ".join(src.split())
 
 
-def _source_sha(text: str | None = None):
-    """sha256 prefix of the decode source's code (comments stripped)."""
+def _source_sha(text: str | None = None, files=None):
+    """sha256 prefix of the code (comments stripped) of ``text``, or of the
+    files (default: the decode sources), each preceded by its name."""
     import hashlib
     if text is None:
-        with open(DECODE_SOURCE) as f:
-            text = f.read()
+        parts = []
+        for path in files or DECODE_SOURCES:
+            with open(path) as f:
+                parts.append(os.path.basename(path) + " " + _code_text(f.read()))
+        text = "\n".join(parts)
+        return hashlib.sha256(text.encode()).hexdigest()[:16]
     return hashlib.sha256(_code_text(text).encode()).hexdigest()[:16]
 
 
 def _traffic(cfg_name):
     """HBM bytes per decode launch from the committed counter summary, or
     None when that summary was taken on other decode code than this tree's
-    (it records the sha256 of rk_decode.hip's code, comments stripped)."""
+    (it records the sha256 of the decode sources' code, comments stripped)."""
     path = os.path.join(ROOT, "profiles", f"traffic_{cfg_name}.json")
     if not os.path.exists(path):
         return None
@@ -609,7 +619,13 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES")
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc passes (no GPU needed)")
+    ap.add_argument("--source-sha", action="store_true",
+                    help="print the code hashes (comments stripped) that profiles are stamped with")
     args = ap.parse_args()
+    if args.source_sha:
+        print(json.dumps({"decode_source_sha256": _source_sha(), "prefill_source_sha256": _source_sha(
+            files=PREFILL_SOURCES)}))
+        return
     args.steps_given = any(a == "--steps" or a.startswith("--steps=") for a in sys.argv[1:])
     args.family_given = any(a == "--family" or a.startswith("--family=") for a in sys.argv[1:])
     if args.chunk_align and not args.pmc_summary:
