@@ -253,7 +253,8 @@ def _cfg0_leg(budget_s=3.0):
 DECODE_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f)
                   for f in ("rk_decode.hip", "rk_decode.h", "rk_decode_dev.h", "rk_decode_f16.hip",
                             "rk_decode_bf16.hip", "rk_decode_f32.hip", "rk_common.h")]
-PREFILL_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f) for f in ("rk_prefill.hip", "rk_common.h")]
+PREFILL_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f) for f in ("rk_prefill.hip", "rk_rotation.hip",
+                                                                          "rk_common.h")]
 
 
 def _code_text(src: str) -> str:

@@ -95,18 +95,34 @@ __global__ void __launch_bounds__(kThreads) power_iter_kernel(
   // L and V = W L^-T then equal the D x D iteration's, with exact zeros in
   // the padded rows.
   constexpr int kCB = 16;  // elements per thread per batch
-  for (int e0 = 0; e0 < kD * kD; e0 += kThreads * kCB) {
-    float v[kCB];
+  if (D == kD) {  // (the addresses step by two rows per element, no clamps)
+    for (int e0 = 0; e0 < kD * kD; e0 += kThreads * kCB) {
+      float v[kCB];
 #pragma unroll
-    for (int i = 0; i < kCB; ++i) {
-      const int e = e0 + i * kThreads + tid, r = e >> 7, c = e & 127;
-      const float x = C[min(r, D - 1) * c_sr + min(c, D - 1) * c_sc];
-      v[i] = r < D && c < D ? x : 0.f;
+      for (int i = 0; i < kCB; ++i) {
+        const int e = e0 + i * kThreads + tid, r = e >> 7, c = e & 127;
+        v[i] = C[r * c_sr + c * c_sc];
+      }
+#pragma unroll
+      for (int i = 0; i < kCB; ++i) {
+        const int e = e0 + i * kThreads + tid;
+        sC[(e >> 7) * kCPad + (e & 127)] = v[i];
+      }
     }
+  } else {
+    for (int e0 = 0; e0 < kD * kD; e0 += kThreads * kCB) {
+      float v[kCB];
 #pragma unroll
-    for (int i = 0; i < kCB; ++i) {
-      const int e = e0 + i * kThreads + tid;
-      sC[(e >> 7) * kCPad + (e & 127)] = v[i];
+      for (int i = 0; i < kCB; ++i) {
+        const int e = e0 + i * kThreads + tid, r = e >> 7, c = e & 127;
+        const float x = C[min(r, D - 1) * c_sr + min(c, D - 1) * c_sc];
+        v[i] = r < D && c < D ? x : 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < kCB; ++i) {
+        const int e = e0 + i * kThreads + tid;
+        sC[(e >> 7) * kCPad + (e & 127)] = v[i];
+      }
     }
   }
   constexpr int kVB = kD * KP / kThreads < kCB ? kD * KP / kThreads : kCB;  // divides kD * KP / kThreads
