@@ -626,7 +626,9 @@ struct RecoverArgs {
 // mask row with more than Dk kept channels) are filled like pruned channels,
 // so no read leaves the row.  FAST: 16-byte loads and stores of every span
 // (unit channel stride, aligned rows), 8-byte mask loads, Dk % 8 == 0.
-template <bool SPARK, bool FAST>
+// DFULL: head dim 128, so the channel guards fold away (they cost the
+// SparK recovery 7 % at config 2's shapes when left to run time).
+template <bool SPARK, bool FAST, bool DFULL>
 __global__ void __launch_bounds__(kThreads) recover_kernel(const RecoverArgs a) {
   __shared__ __align__(16) uint16_t s_c[kTile * kD];
   const int tid = threadIdx.x, c8 = tid & 15, rq = tid >> 4;
@@ -639,7 +641,7 @@ __global__ void __launch_bounds__(kThreads) recover_kernel(const RecoverArgs a) 
   const uint8_t* mb = a.mask.data + head_off(a.mask.sb, a.mask.sh, b, h);
   const uint16_t* fb = SPARK ? a.pm + head_off(a.p_sb, a.p_sh, b, h) : nullptr;
   uint16_t* ob = a.out.data + head_off(a.out.sb, a.out.sh, b, h);
-  const int D = a.D, nch = min(max(D - 8 * c8, 0), 8);  // this lane's channels present
+  const int D = DFULL ? kD : a.D, nch = min(max(D - 8 * c8, 0), 8);  // this lane's channels present
   int map[8];  // ThinK: K_compact column of channel 8 c8 + e, -1 = pruned
   if constexpr (!SPARK) {
     const uint32_t f = mask8<false>(mb + 8 * c8 * a.mask.sc, a.mask.sc, nch);
@@ -1031,16 +1033,18 @@ int recover(bool spark, const rk_tensor* k_prompt, const rk_tensor* k_pruned, co
   if (spark)
     fast = fast && mask->stride[3] == 1 && mask->stride[0] % 8 == 0 && mask->stride[1] % 8 == 0 &&
            mask->stride[2] % 8 == 0 && (((uintptr_t)mask->data) & 7) == 0;
+  const bool full = D == kD;
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, s, a); };
   if (spark) {
     if (fast)
-      hipLaunchKernelGGL((recover_kernel<true, true>), grid, dim3(kThreads), 0, s, a);
+      full ? go(recover_kernel<true, true, true>) : go(recover_kernel<true, true, false>);
     else
-      hipLaunchKernelGGL((recover_kernel<true, false>), grid, dim3(kThreads), 0, s, a);
+      full ? go(recover_kernel<true, false, true>) : go(recover_kernel<true, false, false>);
   } else {
     if (fast)
-      hipLaunchKernelGGL((recover_kernel<false, true>), grid, dim3(kThreads), 0, s, a);
+      full ? go(recover_kernel<false, true, true>) : go(recover_kernel<false, true, false>);
     else
-      hipLaunchKernelGGL((recover_kernel<false, false>), grid, dim3(kThreads), 0, s, a);
+      full ? go(recover_kernel<false, false, true>) : go(recover_kernel<false, false, false>);
   }
   return hipGetLastError() == hipSuccess ? RK_OK : RK_ERR_HIP;
 }
