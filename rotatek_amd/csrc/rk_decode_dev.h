@@ -1068,17 +1068,24 @@ decode_kernel(const DecodeArgs a) {
 // BF16 or F32), the dtype of the reference's CPU-scale configuration.  The
 // reference kernels load any float input as fp32 and compute in fp32
 // (fused_decode.py:133,166,174; full_channel_flash_decoding.py:65,84,92);
-// so does this kernel, on the VALU: fp32 has no MFMA path that keeps its
-// precision at this arithmetic intensity.  A unit is up to HG query heads
-// of one KV head (HG 1: one query head; HG 8: the grouped decomposition,
-// gqa_decode.py:121-210, each K and V row read once for the unit's heads),
-// with the plan's grid and records as the 16-bit kernel, so both merges
-// apply.  Each wave walks 64-token blocks of its workgroup's chunk (blocks
-// wave, wave + 4, ...): lane t loads the row of token t0 + t once and
-// scores it against every head's query, the wave runs one online softmax
-// per head (log2 domain), and lane j accumulates channels 2j, 2j + 1 of
-// each head's P V over the block's V rows (loaded once), with the block's
-// probabilities broadcast from LDS.
+// so do these kernels, on the VALU: fp32 has no MFMA path that keeps its
+// precision at this arithmetic intensity.  Plan, grid and records are the
+// 16-bit kernel's, so both merges apply.  Each wave walks 64-token blocks
+// of its workgroup's chunk (blocks wave, wave + 4, ...): lane t scores
+// token t0 + t as a dot product over its row, the wave runs the online
+// softmax (log2 domain), and lane j accumulates channels 2j, 2j + 1 of
+// P V over the block's rows, with the block's probabilities broadcast
+// from LDS.
+//   decode32_kernel   one query head per unit (G = 1, or the paper
+//                     family's dense baseline);
+//   decode32g_kernel  up to HG = 8 query heads of one KV head per unit (the
+//                     grouped decomposition, gqa_decode.py:121-210): each
+//                     K and V row is loaded once and serves every head (one
+//                     online softmax per head).  A separate kernel: folded
+//                     into one template with the one-head case, the
+//                     one-head instantiations compiled to fewer registers
+//                     and fewer loads in flight, and config 0 ran 9 % (the
+//                     dense baseline 29 %) slower.
 constexpr int kBlk32 = 64;
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -1090,6 +1097,202 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += shfl_xor(v, off);
   return v;
+}
+
+// sum_c w[c] * row[c * sd], c < n <= KMAX; w in LDS.  VEC: unit stride,
+// 16-byte aligned row, n a multiple of 4: all KMAX / 4 16-byte loads are
+// issued before any is used (those past n re-read the row's last four
+// floats, in bounds, and are not used), so the row costs one memory round
+// trip; float4 i accumulates into s0 (i even) or s1 (i odd).
+template <bool VEC, int KMAX>
+__device__ __forceinline__ float dot_row32(const float* row, uint32_t sd, const float* w, int n) {
+  float s0 = 0.f, s1 = 0.f;
+  if constexpr (VEC) {
+    if (n <= 0) return 0.f;
+    float4 r[KMAX / 4];
+#pragma unroll
+    for (int i = 0; i < KMAX / 4; ++i) r[i] = *(const float4*)(row + min(4 * i, n - 4));
+#pragma unroll
+    for (int i = 0; i < KMAX / 4; ++i) {
+      if (4 * i < n) {
+        const float4 w4 = *(const float4*)(w + 4 * i);
+        float& acc = (i & 1) ? s1 : s0;
+        acc = fmaf(w4.x, r[i].x, acc);
+        acc = fmaf(w4.y, r[i].y, acc);
+        acc = fmaf(w4.z, r[i].z, acc);
+        acc = fmaf(w4.w, r[i].w, acc);
+      }
+    }
+  } else {
+    for (int c = 0; c < n; ++c) s0 = fmaf(w[c], row[(int64_t)c * sd], s0);
+  }
+  return s0 + s1;
+}
+
+// DFULL: head_dim 128, a compile-time constant (the run-time bound cost the
+// full-row dot product its loads in flight and spilled scalar registers in
+// the loop: config 0 18.8 -> 20.5 us, its dense baseline 20.9 -> 26.8 us).
+template <bool HAS_VIS, bool VEC, bool DFULL>
+__global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) {
+  const int D = DFULL ? 128 : a.D;
+  __shared__ __attribute__((aligned(16))) float s_q[128];
+  __shared__ __attribute__((aligned(16))) float s_qt[128];
+  __shared__ float s_bias[2];
+  __shared__ float s_p[kWaves][kBlk32];
+  __shared__ float s_m[kWaves], s_l[kWaves];
+  __shared__ float s_acc[kWaves][128];
+  __shared__ float s_mrg[16 * kRecFloats];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int u = blockIdx.y, x = blockIdx.x;
+  const int b = u / a.units_per_b;
+  const int r_in_b = u - b * a.units_per_b;
+  const int kv = r_in_b / a.spk;
+  const int h0 = kv * a.G + (r_in_b - kv * a.spk) * a.hpu;
+  const bool is_vis = HAS_VIS && x < a.wg_vis;
+  const int xf = HAS_VIS ? x - a.wg_vis : x;
+  const float* q = (const float*)a.q;
+
+  // channels past head_dim D are zeros (q, R_partial's rows, delta_mu);
+  // V lanes past D read an in-bounds duplicate (16-byte rows: the row's last
+  // two channels; else no load) that feeds only output channels not written
+  if (tid < 128) s_q[tid] = tid < D ? q[b * a.q_sb + (int64_t)h0 * a.q_sh + (int64_t)tid * a.q_sd] : 0.f;
+  __syncthreads();
+  const int vc = min(2 * lane, D - 2);  // (VEC: D is a multiple of 4)
+  const bool v0ok = 2 * lane < D, v1ok = 2 * lane + 1 < D;
+
+  float m = kNegInit, l = 0.f, acc0 = 0.f, acc1 = 0.f;
+  // online-softmax step over one block: s = log2-domain score of token
+  // t0 + lane (-inf when invalid), V rows clamped to t_last
+  auto step = [&](float s, const float* vb, uint32_t vss, uint32_t vsd, int64_t t0, int64_t t_last,
+                  uint32_t gap_at, uint32_t gap) {
+    const float m_new = fmaxf(m, wave_max(s));
+    const float alpha = fast_exp2(m - m_new);
+    const float p = fast_exp2(s - m_new);
+    l = l * alpha + wave_sum(p);
+    acc0 *= alpha;
+    acc1 *= alpha;
+    m = m_new;
+    s_p[wave][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // the block's V rows in two batches of 32 loads in flight (one memory
+    // round trip each), then their fused multiply-adds in token order
+    constexpr int kVB = 32;
+#pragma unroll
+    for (int j0 = 0; j0 < kBlk32; j0 += kVB) {
+      float v0[kVB], v1[kVB];
+#pragma unroll
+      for (int jj = 0; jj < kVB; ++jj) {
+        uint32_t row = (uint32_t)min(t0 + j0 + jj, t_last);
+        row += row >= gap_at ? gap : 0u;
+        const float* vr = vb + (int64_t)row * vss;
+        if constexpr (VEC) {
+          const float2 v = *(const float2*)(vr + vc);
+          v0[jj] = v.x;
+          v1[jj] = v.y;
+        } else {
+          v0[jj] = v0ok ? vr[(int64_t)(2 * lane) * vsd] : 0.f;
+          v1[jj] = v1ok ? vr[(int64_t)(2 * lane + 1) * vsd] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < kVB; ++jj) {
+        const float pj = s_p[wave][j0 + jj];
+        acc0 = fmaf(pj, v0[jj], acc0);
+        acc1 = fmaf(pj, v1[jj], acc1);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  if (is_vis) {
+    {  // q R_partial: thread (half, c) sums rows 64 half .. 64 half + 63 of
+       // column c, all 64 loads in flight; the halves meet in LDS
+      const int c = tid & 127, half = tid >> 7;
+      const int cc = min(c, max(a.Dk - 1, 0));
+      const int64_t rb = b * a.R_sb + kv * a.R_sh + (int64_t)cc * a.R_sk;
+      float sum = 0.f;
+      if (a.Dk > 0) {
+        float rv[64];
+        if constexpr (DFULL)  // all 128 rows: addresses stepped on the fly
+          load_any_n(a.R, rb + (int64_t)(64 * half) * a.R_sd, a.R_sd, a.r_dtype, rv);
+        else
+          load_any_rows(a.R, rb, a.R_sd, a.r_dtype, 64 * half, D, rv);
+#pragma unroll
+        for (int i = 0; i < 64; ++i) sum = fmaf(s_q[64 * half + i], rv[i], sum);
+      }
+      s_acc[half][c] = sum;  // s_acc is free until the epilogue
+      __syncthreads();
+      if (tid < 128) s_qt[tid] = tid < a.Dk ? s_acc[0][tid] + s_acc[1][tid] : 0.f;
+    }
+    if (wave < 2) {  // q . delta_mu
+      const int d = tid;
+      const float t = a.has_bias && d < D
+                          ? s_q[d] * load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)d * a.dm_sd, a.dm_dtype)
+                          : 0.f;
+      const float w = wave_sum(t);
+      if (lane == 0) s_bias[wave] = w;
+    }
+    __syncthreads();
+    const float bias2 = (s_bias[0] + s_bias[1]) * a.scale_log2;
+    const int64_t t_begin = (int64_t)x * a.chunk_vis;
+    const int64_t t_end = min(a.S_v, t_begin + a.chunk_vis);
+    const float* ksb = (const float*)a.ks + b * a.ks_sb + kv * a.ks_sh;
+    const float* vsb = (const float*)a.vs + b * a.vs_sb + kv * a.vs_sh;
+    for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
+      const int64_t t = t0 + lane;
+      const float* kr = ksb + (int64_t)min(t, t_end - 1) * a.ks_ss;
+      const float d = a.Dk <= 32   ? dot_row32<VEC, 32>(kr, a.ks_sd, s_qt, a.Dk)
+                      : a.Dk <= 64 ? dot_row32<VEC, 64>(kr, a.ks_sd, s_qt, a.Dk)
+                                   : dot_row32<VEC, 128>(kr, a.ks_sd, s_qt, a.Dk);
+      const float s = t < t_end ? fmaf(d, a.scale_log2, bias2) : -INFINITY;
+      step(s, vsb, a.vs_ss, a.vs_sd, t0, t_end - 1, UINT32_MAX, 0u);
+    }
+  } else {
+    const int64_t t_begin = (int64_t)xf * a.chunk_full;
+    const int64_t t_end = min(a.S_f, t_begin + a.chunk_full);
+    const float* kfb = (const float*)a.kf + b * a.kf_sb + kv * a.kf_sh;
+    const float* vfb = (const float*)a.vf + b * a.vf_sb + kv * a.vf_sh;
+    for (int64_t t0 = t_begin + (int64_t)wave * kBlk32; t0 < t_end; t0 += kWaves * kBlk32) {
+      const int64_t t = t0 + lane;
+      const int64_t tc = min(t, t_end - 1);
+      const float d = dot_row32<VEC, 128>(kfb + tc * a.kf_ss, a.kf_sd, s_q, D);
+      const bool ok = t < t_end && (!a.mask || a.mask[b * a.mf_sb + tc * a.mf_ss] != 0);
+      step(ok ? d * a.scale_log2 : -INFINITY, vfb, a.vf_ss, a.vf_sd, t0, t_end - 1, a.vf_gap_at, a.vf_gap);
+    }
+  }
+
+  // the four wave states -> this workgroup's record
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+  }
+  s_acc[wave][2 * lane] = acc0;
+  s_acc[wave][2 * lane + 1] = acc1;
+  __syncthreads();
+  if (tid < 16) {
+    const int c8 = tid;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w]);
+    float L = 0.f, A[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = fast_exp2(s_m[w] - M);
+      L += s_l[w] * wt;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) A[e] += s_acc[w][8 * c8 + e] * wt;
+    }
+    float* rec = a.part + ((int64_t)u * a.np + x) * kRecFloats;
+    if (a.fused)
+      store_rec<true>(rec, c8, A, M, L);
+    else
+      store_rec<false>(rec, c8, A, M, L);
+  }
+  if (a.fused) merge_fused<F32, false, 1>(a, u, b, h0, 1, tid, s_mrg);
 }
 
 // d[h] = sum_c w[h * 128 + c] * row[c * sd] for the heads h < nh, c < n <=
@@ -1138,8 +1341,9 @@ __device__ __forceinline__ void dot_rows32(const float* row, uint32_t sd, const 
   for (int h = 0; h < HG; ++h) d[h] = s0[h] + s1[h];
 }
 
-template <bool HAS_VIS, bool VEC, int HG>
-__global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) {
+template <bool HAS_VIS, bool VEC, int HG, bool DFULL>
+__global__ void __launch_bounds__(kThreads) decode32g_kernel(const DecodeArgs a) {
+  const int D = DFULL ? 128 : a.D;  // head_dim (DFULL: 128, as in decode32_kernel)
   __shared__ __attribute__((aligned(16))) float s_q[HG][128];
   __shared__ __attribute__((aligned(16))) float s_qt[HG][128];
   __shared__ float s_bias[HG][2];
@@ -1165,11 +1369,11 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
   // rows of absent heads (h >= nh) are zeros
   for (int i = tid; i < HG * 128; i += kThreads) {
     const int h = i >> 7, c = i & 127;
-    (&s_q[0][0])[i] = h < nh && c < a.D ? q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + (int64_t)c * a.q_sd] : 0.f;
+    (&s_q[0][0])[i] = h < nh && c < D ? q[b * a.q_sb + (int64_t)(h0 + h) * a.q_sh + (int64_t)c * a.q_sd] : 0.f;
   }
   __syncthreads();
-  const int vc = min(2 * lane, a.D - 2);  // (VEC: D is a multiple of 4)
-  const bool v0ok = 2 * lane < a.D, v1ok = 2 * lane + 1 < a.D;
+  const int vc = min(2 * lane, D - 2);  // (VEC: D is a multiple of 4)
+  const bool v0ok = 2 * lane < D, v1ok = 2 * lane + 1 < D;
 
   float m[HG], l[HG], acc0[HG], acc1[HG];
 #pragma unroll
@@ -1246,7 +1450,10 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
       for (int h = 0; h < HG; ++h) sum[h] = 0.f;
       if (a.Dk > 0) {
         float rv[64];
-        load_any_rows(a.R, rb, a.R_sd, a.r_dtype, 64 * half, a.D, rv);
+        if constexpr (DFULL)  // all 128 rows: addresses stepped on the fly
+          load_any_n(a.R, rb + (int64_t)(64 * half) * a.R_sd, a.R_sd, a.r_dtype, rv);
+        else
+          load_any_rows(a.R, rb, a.R_sd, a.r_dtype, 64 * half, D, rv);
 #pragma unroll
         for (int h = 0; h < HG; ++h)
           if (h < nh) {
@@ -1264,7 +1471,7 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
     }
     if (wave < 2) {  // q . delta_mu, every head of the unit
       const int d = tid;
-      const float dm = a.has_bias && d < a.D
+      const float dm = a.has_bias && d < D
                            ? load_any(a.dm, b * a.dm_sb + kv * a.dm_sh + (int64_t)d * a.dm_sd, a.dm_dtype)
                            : 0.f;
 #pragma unroll
@@ -1306,7 +1513,7 @@ __global__ void __launch_bounds__(kThreads) decode32_kernel(const DecodeArgs a) 
       const int64_t t = t0 + lane;
       const int64_t tc = min(t, t_end - 1);
       float d[HG], sc[HG];
-      dot_rows32<VEC, 128, HG>(kfb + tc * a.kf_ss, a.kf_sd, &s_q[0][0], a.D, nh, d);
+      dot_rows32<VEC, 128, HG>(kfb + tc * a.kf_ss, a.kf_sd, &s_q[0][0], D, nh, d);
       const bool ok = t < t_end && (!a.mask || a.mask[b * a.mf_sb + tc * a.mf_ss] != 0);
 #pragma unroll
       for (int h = 0; h < HG; ++h) sc[h] = ok ? d[h] * a.scale_log2 : -INFINITY;
