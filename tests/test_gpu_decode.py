@@ -2,7 +2,9 @@
 
 Tolerances (north star): max-abs 2e-3 for fp16 and 1e-2 for bf16 outputs
 against the float64 oracle evaluated on the very same (already rounded)
-inputs.  Every case prints its name before touching the GPU.
+inputs.  The bf16 bar is 1e-2 or the output's own rounding (2^-7 |out|),
+whichever is larger; the outputs here are O(1), where the flat 1e-2 holds.
+Every case prints its name before touching the GPU.
 """
 import math
 import sys
