@@ -131,21 +131,35 @@ template <class TT>
 __device__ void floored_query_norms(const float (&acc)[2][8], int W, int D, float inv_g, int tid,
                                     float (*s_part)[128], float* s_qn, float* s_floor);
 
-template <class TT, bool VEC, bool QV = false>
-__global__ void __launch_bounds__(kThreads) mean_kernel(KeyView k, int64_t chunk, int splits,
-                                                        float* part, QNormArgs qa) {
+// The floored query norms of head bh into qa.qn[bh] (the mean launch's
+// extra column; s_part: 16 x 128 floats of LDS).
+template <class TT, bool QV>
+__device__ __forceinline__ void head_query_norms(const KeyView& k, const QNormArgs& qa, int bh, int tid,
+                                                 float (*s_part)[128]) {
+  __shared__ __align__(16) float s_qn[128];
+  __shared__ float s_floor;
+  const int b = bh / k.H, kv = bh - b * k.H;
+  float acc[2][8];
+  window_group_sums<TT, QV>(qa.q, qa.q_b, qa.q_h, qa.q_s, qa.q_d, qa.S, qa.W, qa.G, qa.D, b, kv, tid, acc);
+  floored_query_norms<TT>(acc, qa.W, qa.D, qa.inv_g, tid, s_part, s_qn, &s_floor);
+  if (tid < 128) qa.qn[(int64_t)bh * 128 + tid] = s_qn[tid];
+}
+
+// QN (weighted covariance only): the grid has one more column per head
+// (x == splits) that forms the head's floored query norms.  Only these
+// instantiations carry that code: its registers would otherwise set the
+// occupancy of the summing loop.
+template <class TT, bool VEC, bool QN, bool QV>
+__global__ void __launch_bounds__(kThreads) mean_kernel(KeyView k, int64_t chunk, int splits, float* part,
+                                                        QNormArgs qa) {
   __shared__ float s_sum[16][128];
   const int tid = threadIdx.x, rg = tid >> 4, c8 = tid & 15;
   const int x = blockIdx.x, bh = blockIdx.y;
-  if (x == splits) {  // the extra column (weighted covariance only): this head's query norms
-    __shared__ __align__(16) float s_qn[128];
-    __shared__ float s_floor;
-    const int b = bh / k.H, kv = bh - b * k.H;
-    float acc[2][8];
-    window_group_sums<TT, QV>(qa.q, qa.q_b, qa.q_h, qa.q_s, qa.q_d, qa.S, qa.W, qa.G, qa.D, b, kv, tid, acc);
-    floored_query_norms<TT>(acc, qa.W, qa.D, qa.inv_g, tid, s_sum, s_qn, &s_floor);
-    if (tid < 128) qa.qn[(int64_t)bh * 128 + tid] = s_qn[tid];
-    return;
+  if constexpr (QN) {
+    if (x == splits) {
+      head_query_norms<TT, QV>(k, qa, bh, tid, s_sum);
+      return;
+    }
   }
   const int64_t t0 = (int64_t)x * chunk, t1 = min(k.S, t0 + chunk);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -234,11 +248,13 @@ __host__ __device__ constexpr int tile_col(int t) { return tile_row(t) + t - til
 
 // grid (splits, B*H): each wave accumulates Kc^T Kc over its interleaved
 // 32-token blocks for all 36 upper tiles; the four waves are summed in LDS
-// and the workgroup writes one [36][256] partial.
+// and the workgroup writes one [36][256] partial, and, with dpart, its 128
+// diagonal entries once more as one contiguous row dpart[bh][x][128] (what
+// the weighted finalisation sums for the ridge).
 template <class TT, bool VEC>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mean_splits, float mfac,
-           float* part) {
+           float* part, float* dpart) {
   __shared__ float s_c[128];
   __shared__ float s_red[kTiles * 256];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
@@ -336,6 +352,9 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
   }
   float* out = part + ((int64_t)bh * splits + x) * (kTiles * 256);
   for (int i = tid; i < kTiles * 256; i += kThreads) out[i] = s_red[i];
+  // C[c][c], c = 8 m + i: tile (i, i), entry (m, m)
+  if (dpart && tid < 128)
+    dpart[((int64_t)bh * splits + x) * 128 + tid] = s_red[tile_index(tid & 7, tid & 7) * 256 + 17 * (tid >> 3)];
 }
 
 // grid (kTiles, B*H): one workgroup per upper tile (i, j) of one head.
@@ -798,7 +817,8 @@ constexpr int kQHeads = 8;  // query heads whose window rows are loaded together
 
 // Thread (rs = t/16, c8 = t%16) of 256: the fp32 sums over the G query
 // heads of window rows rs and rs + 16 (of the last W rows), channels
-// 8 c8..8 c8+7, G in order, kQHeads heads' loads issued at a time.
+// 8 c8..8 c8+7, G in order, the loads of kQHeads heads (16-byte rows) or
+// two heads (element-wise) issued at a time.
 template <class TT, bool QV>
 __device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, int64_t q_s, int64_t q_d,
                                   int64_t S, int W, int G, int D, int b, int kv, int tid, float (&acc)[2][8]) {
@@ -812,13 +832,16 @@ __device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, i
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-  for (int g0 = 0; g0 < G; g0 += kQHeads) {
-    float f[kQHeads][2][8];
+  // element-wise loads take 64-bit addresses each: two heads at a time
+  // keep them in registers (the sums run in the same head order)
+  constexpr int kQH = QV ? kQHeads : 2;
+  for (int g0 = 0; g0 < G; g0 += kQH) {
+    float f[kQH][2][8];
     if constexpr (TT::kBytes == 2) {
       const uint16_t* qb = q + off;
-      uint4 v[kQHeads][2];
+      uint4 v[kQH][2];
 #pragma unroll
-      for (int u = 0; u < kQHeads; ++u)
+      for (int u = 0; u < kQH; ++u)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int w = j ? w1 : w0;
@@ -837,13 +860,13 @@ __device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, i
           }
         }
 #pragma unroll
-      for (int u = 0; u < kQHeads; ++u)
+      for (int u = 0; u < kQH; ++u)
 #pragma unroll
         for (int j = 0; j < 2; ++j) unpack8<TT>(v[u][j], f[u][j]);
     } else {
       const float* qb = (const float*)q + off;
 #pragma unroll
-      for (int u = 0; u < kQHeads; ++u)
+      for (int u = 0; u < kQH; ++u)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const int w = j ? w1 : w0;
@@ -864,7 +887,7 @@ __device__ void window_group_sums(const uint16_t* q, int64_t q_b, int64_t q_h, i
         }
     }
 #pragma unroll
-    for (int u = 0; u < kQHeads; ++u)
+    for (int u = 0; u < kQH; ++u)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         if (g0 + u < G)
@@ -1038,12 +1061,13 @@ __global__ void __launch_bounds__(256) qweight_kernel(const float* cov, int64_t 
 // qweight_kernel.  The floored query norms come from the mean launch's
 // extra column (qn [B*H][128]).  Each tile workgroup sums its tile's
 // partials (as covfin) and the 128 diagonal entries' partials (for the
-// ridge), loads in flight together, then writes its weighted tile and the
-// mirror:  out[r][c] = 0.5 (a + a) + ridge [r == c],  a = sym[r][c] (qn[r] qn[c]),
+// ridge; the contiguous copies dpart[bh][x][128], the same values in the
+// same order), loads in flight together, then writes its weighted tile and
+// the mirror:  out[r][c] = 0.5 (a + a) + ridge [r == c],  a = sym[r][c] (qn[r] qn[c]),
 // sym = 0.5 (C[r][c] + C[c][r]) the symmetrised covariance, which is what
 // qweight_kernel reads back from covfin's output.
 template <class TT>
-__global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, int splits,
+__global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, const float* dpart, int splits,
                                                              const float* mean_part, int mean_splits, float mfac,
                                                              const float* qn, float* cov, int64_t cs_b,
                                                              int64_t cs_h, int64_t cs_r, int64_t cs_c, float* mu,
@@ -1055,11 +1079,9 @@ __global__ void __launch_bounds__(kThreads) covfin_qw_kernel(const float* part, 
   const int tid = threadIdx.x, t = blockIdx.x, bh = blockIdx.y;
   const int b = bh / H, h = bh - b * H;
   const float* pb = part + (int64_t)bh * splits * (kTiles * 256);
-  // tile entry tid and (threads < 128) diagonal entry C[tid][tid]: tile
-  // (tid % 8, tid % 8), entry 17 (tid / 8)
+  // tile entry tid and (threads < 128) diagonal entry C[tid][tid]
   float sum = strided_sum(pb + t * 256 + tid, splits, kTiles * 256);
-  const int dt = tile_index(tid & 7, tid & 7);
-  float dsum = strided_sum(pb + dt * 256 + 17 * ((tid & 127) >> 3), splits, kTiles * 256);
+  float dsum = strided_sum(dpart + (int64_t)bh * splits * 128 + (tid & 127), splits, 128);
   const float qv = qn[(int64_t)bh * 128 + (tid & 127)];
   asm volatile("" : "+v"(sum));  // fp32, then the key dtype (two roundings)
   asm volatile("" : "+v"(dsum));
@@ -1147,7 +1169,7 @@ int splits_for(int64_t bh, int64_t S, int cus, int64_t min_tokens) {
 struct CovPlan {
   int mean_splits, cov_splits;
   int64_t mean_chunk, cov_chunk;
-  size_t off_mean, off_cov, off_qn, total;
+  size_t off_mean, off_cov, off_diag, off_qn, total;
 };
 
 CovPlan cov_plan(int64_t B, int64_t H, int64_t S, int cus) {
@@ -1159,8 +1181,10 @@ CovPlan cov_plan(int64_t B, int64_t H, int64_t S, int cus) {
   p.cov_chunk = cdiv(S > 0 ? S : 1, p.cov_splits);
   p.off_mean = 0;
   p.off_cov = align256((size_t)bh * p.mean_splits * 128 * sizeof(float));
-  p.off_qn = p.off_cov + align256((size_t)bh * p.cov_splits * kTiles * 256 * sizeof(float));
-  p.total = p.off_qn + align256((size_t)bh * 128 * sizeof(float));  // floored query norms (weighted only)
+  p.off_diag = p.off_cov + align256((size_t)bh * p.cov_splits * kTiles * 256 * sizeof(float));
+  // the partials' diagonals and the floored query norms (weighted only)
+  p.off_qn = p.off_diag + align256((size_t)bh * p.cov_splits * 128 * sizeof(float));
+  p.total = p.off_qn + align256((size_t)bh * 128 * sizeof(float));
   return p;
 }
 
@@ -1204,38 +1228,41 @@ hipError_t launch_cov(const KeyView& k, bool vec, const CovPlan& p, int64_t B, f
   // the ridge's mean over the D diagonal entries of each [D, D] matrix
   const float rfac = rk::mean_factor(bh, bh * k.D);
   // with the weighting, the mean launch has one more column per head that
-  // forms the head's floored query norms
+  // forms the head's floored query norms, and the covariance launch writes
+  // its partials' diagonals once more, contiguously
   QNormArgs qa;
   memset(&qa, 0, sizeof(qa));
   float* qn = (float*)((char*)ws + p.off_qn);
+  float* dpart = nullptr;
   dim3 gmq = gm;
   if (qw) {
     const rk_tensor* q = qw->q;
     qa = QNormArgs{(const uint16_t*)q->data, q->stride[0], q->stride[1], q->stride[2], q->stride[3], q->shape[2],
                    qw->W, (int)qw->G, k.D, qw->inv_g, qn};
+    dpart = (float*)((char*)ws + p.off_diag);
     gmq.x += 1;
   }
+  const int64_t mc = p.mean_chunk, cc = p.cov_chunk;
+  const int ms = p.mean_splits, cs = p.cov_splits;
   if (vec) {
-    if (qw && qw->vec)
-      hipLaunchKernelGGL((mean_kernel<TT, true, true>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits,
-                         mpart, qa);
+    if (!qw)
+      hipLaunchKernelGGL((mean_kernel<TT, true, false, false>), gm, dim3(kThreads), 0, s, k, mc, ms, mpart, qa);
+    else if (qw->vec)
+      hipLaunchKernelGGL((mean_kernel<TT, true, true, true>), gmq, dim3(kThreads), 0, s, k, mc, ms, mpart, qa);
     else
-      hipLaunchKernelGGL((mean_kernel<TT, true, false>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits,
-                         mpart, qa);
-    hipLaunchKernelGGL((cov_kernel<TT, true>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
-                       p.mean_splits, mfac, cpart);
+      hipLaunchKernelGGL((mean_kernel<TT, true, true, false>), gmq, dim3(kThreads), 0, s, k, mc, ms, mpart, qa);
+    hipLaunchKernelGGL((cov_kernel<TT, true>), gc, dim3(kThreads), 0, s, k, cc, cs, mpart, ms, mfac, cpart, dpart);
   } else {
-    if (qw && qw->vec)
-      hipLaunchKernelGGL((mean_kernel<TT, false, true>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk, p.mean_splits,
-                         mpart, qa);
+    if (!qw)
+      hipLaunchKernelGGL((mean_kernel<TT, false, false, false>), gm, dim3(kThreads), 0, s, k, mc, ms, mpart, qa);
+    else if (qw->vec)
+      hipLaunchKernelGGL((mean_kernel<TT, false, true, true>), gmq, dim3(kThreads), 0, s, k, mc, ms, mpart, qa);
     else
-      hipLaunchKernelGGL((mean_kernel<TT, false, false>), gmq, dim3(kThreads), 0, s, k, p.mean_chunk,
-                         p.mean_splits, mpart, qa);
-    hipLaunchKernelGGL((cov_kernel<TT, false>), gc, dim3(kThreads), 0, s, k, p.cov_chunk, p.cov_splits, mpart,
-                       p.mean_splits, mfac, cpart);
+      hipLaunchKernelGGL((mean_kernel<TT, false, true, false>), gmq, dim3(kThreads), 0, s, k, mc, ms, mpart, qa);
+    hipLaunchKernelGGL((cov_kernel<TT, false>), gc, dim3(kThreads), 0, s, k, cc, cs, mpart, ms, mfac, cpart, dpart);
   }
   if (qw) {
-    hipLaunchKernelGGL((covfin_qw_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart,
+    hipLaunchKernelGGL((covfin_qw_kernel<TT>), dim3(kTiles, (unsigned)bh), dim3(kThreads), 0, s, cpart, dpart,
                        p.cov_splits, mpart, p.mean_splits, mfac, qn, cov, cov_t->stride[0], cov_t->stride[1],
                        cov_t->stride[2], cov_t->stride[3], mu, mu_t ? mu_t->stride[0] : 0,
                        mu_t ? mu_t->stride[1] : 0, mu_t ? mu_t->stride[2] : 0, k.H, k.D, rfac);

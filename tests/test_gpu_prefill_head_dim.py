@@ -311,7 +311,16 @@ def test_update_rotatek_fp32_and_head_dim(dtype, D, solver):
     assert kept.shape == (B, H, S - 70, keep) and kept.dtype == dtype
     assert int(mask[0, 0].sum()) == keep and mask.shape == (B, H, D)
     full = op.update_rotatek(_np(K), _np(Q), 30, 40, ratio, G, DT[dtype], query_aware=True)
-    assert np.abs(_np(covw) - full["cov"]).max() <= 1e-5 * np.abs(full["cov"]).max()
+    got, want = _np(covw), full["cov"]
+    if dtype == torch.float32:
+        assert np.abs(got - want).max() <= 1e-5 * np.abs(want).max()
+    else:
+        # the weighted entries are fp32 products of the covariance stored in
+        # the key dtype: one storage ulp of that covariance (where fp32 and
+        # fp64 sums round to neighbouring 16-bit values) times the weight is
+        # at most two storage ulps of the weighted entry
+        err = np.abs(got - want)
+        assert np.all(err <= 2 * _storage_ulp(got, want, dtype) + 1e-6 * np.abs(want).max()), err.max()
     ref = op.update_rotatek(_np(K), _np(Q), 30, 40, ratio, G, DT[dtype], query_aware=True,
                             cov=_np(covw), mean=_np(mean))
     R = _np(pr.current_rotatek_R_partial)
