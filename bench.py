@@ -255,6 +255,8 @@ DECODE_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f)
                             "rk_decode_bf16.hip", "rk_decode_f32.hip", "rk_common.h")]
 PREFILL_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f) for f in ("rk_prefill.hip", "rk_rotation.hip",
                                                                           "rk_common.h")]
+# the ThinK / SparK baseline kernels (their dense decode is the decode path's)
+BASELINE_SOURCES = [os.path.join(ROOT, "rotatek_amd", "csrc", f) for f in ("rk_baselines.hip", "rk_common.h")]
 
 
 def _code_text(src: str) -> str:
@@ -624,8 +626,9 @@ def main():
                     help="print the code hashes (comments stripped) that profiles are stamped with")
     args = ap.parse_args()
     if args.source_sha:
-        print(json.dumps({"decode_source_sha256": _source_sha(), "prefill_source_sha256": _source_sha(
-            files=PREFILL_SOURCES)}))
+        print(json.dumps({"decode_source_sha256": _source_sha(),
+                          "prefill_source_sha256": _source_sha(files=PREFILL_SOURCES),
+                          "baseline_source_sha256": _source_sha(files=BASELINE_SOURCES)}))
         return
     args.steps_given = any(a == "--steps" or a.startswith("--steps=") for a in sys.argv[1:])
     args.family_given = any(a == "--family" or a.startswith("--family=") for a in sys.argv[1:])
