@@ -1559,7 +1559,9 @@ __global__ void __launch_bounds__(kThreads) decode32g_kernel(const DecodeArgs a)
 // Second launch: one workgroup per unit runs merge_unit, or with one query
 // head per unit (hpu == 1) one workgroup per 16 units, a slice each
 // (merge_slice).  With a fused append the unit holding query head 0 of row
-// b advances len_full[b]; the split launch that read it has completed.
+// b advances len_full[b]; the split launch that read it has completed.  Its
+// read is issued before the merge's loads, so its latency overlaps them
+// (nothing else writes len_full[b] during this launch).
 template <class TT>
 __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
   __shared__ float s_mrg[16 * kRecFloats];
@@ -1572,12 +1574,19 @@ __global__ void __launch_bounds__(kThreads) merge_kernel(const DecodeArgs a) {
   const int kv = r_in_b / a.spk;
   const int jblk = r_in_b - kv * a.spk;
   const int h0 = kv * a.G + jblk * a.hpu;
+  // (every thread reads it under the launch-uniform k_new: a read under the
+  // per-thread condition below would wait for its data on the spot; the
+  // empty asm after the merge keeps any use of the value, and so its wait,
+  // behind the merge)
+  int32_t len0 = a.k_new ? a.len_full[b] : 0;
+  const bool advance = a.k_new && r_in_b == 0 && (tid & (sliced ? 15 : 255)) == 0;
   if (sliced)
     merge_slice<TT, false>(a, u, b, h0, tid & 15);
   else
     merge_unit<TT, false>(a, u, b, h0, min(a.hpu, a.G - jblk * a.hpu), tid, s_mrg);
-  if (a.k_new && r_in_b == 0 && (tid & (sliced ? 15 : 255)) == 0) {
-    const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(a.len_full[b], 0));
+  asm volatile("" : "+v"(len0));
+  if (advance) {
+    const int32_t pos = (int32_t)min(a.S_f, (int64_t)max(len0, 0));
     if (pos < a.S_f) a.len_full[b] = pos + 1;
   }
 }
