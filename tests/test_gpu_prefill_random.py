@@ -1,0 +1,106 @@
+"""Seeded random shapes for the prefill covariance path against the oracle.
+
+The covariance launches depend on the shape: (B*H, S) set the split counts
+of the mean and covariance passes (and so which workgroups hold a partial or
+an empty chunk), D < 128 masks channel slots, strided views take the
+element-wise loads, and the weighted form adds the query-norm column to the
+mean launch and reads the partials' diagonals back for the ridge.  This test
+draws 40 shapes with a fixed seed (B 1-4, H 1-6, S from one token to past
+several split boundaries, D in {128, 96, 64, 40, 100, 8}, fp16 / bf16 / fp32
+Keys, G in {1, 2, 4, 7}, contiguous or sliced out of a longer buffer;
+x8 outlier channels except in fp16, whose covariance would overflow to
+infinity as the reference's does) and checks, per shape:
+
+  * the mean against the oracle's fp32 mean (1e-5 relative);
+  * the covariance against the oracle centred on the kernel's own mean: one
+    storage ulp of the key dtype (fp32 Keys: 1e-5 of the largest entry);
+  * the weighted covariance bit for bit against the two-stage result
+    (covariance, then the standalone weighting kernel);
+  * the weighted covariance against the oracle's weighting applied to the
+    kernel's own covariance (1e-5 of the largest entry: fp32 against fp64
+    arithmetic on identical inputs).
+
+Every case prints its parameters before it touches the GPU.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import prefill as op
+
+pytestmark = pytest.mark.gpu
+
+DT = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+S_CHOICES = [1, 2, 7, 31, 32, 33, 255, 256, 257, 511, 513, 1000, 2049, 4097]
+
+
+def _np(t):
+    return t.detach().cpu().to(torch.float64).numpy()
+
+
+def _say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def _storage_ulp(a, b, dtype):
+    m = np.maximum(np.abs(a), np.abs(b))
+    e = np.floor(np.log2(np.maximum(m, 1e-30)))
+    return 2.0 ** e * ULP[dtype]
+
+
+def _cases(n=40, seed=7):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([128, 128, 128, 96, 64, 40, 100, 8]))
+        out.append(dict(i=i, B=int(rng.integers(1, 5)), H=int(rng.integers(1, 7)), S=int(rng.choice(S_CHOICES)),
+                        D=D, dtype=[torch.float16, torch.bfloat16, torch.float32][int(rng.integers(0, 3))],
+                        G=int(rng.choice([1, 2, 4, 7])), sliced=bool(rng.integers(0, 2)),
+                        offset=float(rng.choice([0.0, 0.5, 3.0]))))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"{c['i']}")
+def test_covariance_random_shapes(case):
+    from rotatek_amd import prefill
+    c = case
+    B, H, S, D, dtype, G = c["B"], c["H"], c["S"], c["D"], c["dtype"], c["G"]
+    _say(f"prefill random {c}")
+    g = torch.Generator(device="cuda").manual_seed(1000 + c["i"])
+    pad = 23 if c["sliced"] else 0
+    full = torch.randn(B, H, S + 2 * pad, D, generator=g, device="cuda")
+    if dtype != torch.float16:
+        # x8 outlier channels; fp16 keeps unit variance, so that a diagonal
+        # sum over 4097 tokens stays inside its range (65504)
+        full[..., ::37] *= 8.0
+    full = (full + c["offset"]).to(dtype)
+    K = full[:, :, pad:pad + S]
+    Q = torch.randn(B, H * G, 48, D, generator=g, device="cuda").to(dtype)
+
+    mean, cov = prefill.key_covariance(K)
+    mean_w, cov_w = prefill.key_covariance(K, Q, G)
+    two = prefill.query_weight(cov, Q, G)
+    torch.cuda.synchronize()
+
+    Kn = _np(K)
+    om, _ = op.key_covariance(Kn, DT[dtype])
+    np.testing.assert_allclose(_np(mean), om, rtol=1e-5, atol=1e-6)
+    _, oc = op.key_covariance(Kn, DT[dtype], mean=_np(mean))
+    got = _np(cov)
+    if dtype == torch.float32:
+        assert np.abs(got - oc).max() <= 1e-5 * max(np.abs(oc).max(), 1e-30)
+    else:
+        scale = np.abs(oc).max(axis=(-1, -2), keepdims=True)
+        err = np.abs(got - oc)
+        assert np.all(err <= _storage_ulp(oc, got, dtype) + 1e-6 * scale), err.max()
+    np.testing.assert_array_equal(got, np.swapaxes(got, -1, -2))
+
+    # the weighted launches: the same mean, and the two-stage result bit for bit
+    assert torch.equal(mean_w, mean)
+    assert torch.equal(cov_w, two)
+    ow = op.query_weight(got, _np(Q), G, dtype=DT[dtype])
+    assert np.abs(_np(cov_w) - ow).max() <= 1e-5 * np.abs(ow).max()
