@@ -35,6 +35,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "rk_common.h"
 #include "rk_host.h"
 #include "rotatek_hip.h"
@@ -282,17 +284,20 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
   const uint32_t last = (uint32_t)max(t1 - 1, (int64_t)0);
   if constexpr (TT::kBytes == 2) {
     const uint16_t* base = head_base(k, bh);
-    for (int64_t blk = wave; blk < nblk; blk += kWaves) {
+    // Centre in fp32 and round to the key dtype, two tokens of one channel
+    // per conversion, which is already the transposed operand word:
+    // op[i] element r = Kc[token 8g + r][channel 8n + i].  MASK: rows past
+    // the end (clamped loads) and channel slots past D are masked to zero
+    // after the conversion (a select around the conversion itself compiled
+    // to one branch per element); whole blocks at head_dim 128 need neither
+    // the mask nor the row clamps.
+    auto block = [&](int64_t blk, auto mask) {
+      constexpr bool MASK = decltype(mask)::value;
       const int64_t tb = t0 + blk * 32 + 8 * g;
       uint4 rows[8];
 #pragma unroll
-      for (int r = 0; r < 8; ++r) rows[r] = ldrow<VEC>(base, k, min((uint32_t)(tb + r), last), cl, nv);
-      // Centre in fp32 and round to the key dtype, two tokens of one channel
-      // per conversion, which is already the transposed operand word:
-      // op[i] element r = Kc[token 8g + r][channel 8n + i].  Rows past the end
-      // (clamped loads) and channel slots past D are masked to zero after the
-      // conversion: a select around the conversion itself compiled to one
-      // branch per element.
+      for (int r = 0; r < 8; ++r)
+        rows[r] = ldrow<VEC>(base, k, MASK ? min((uint32_t)(tb + r), last) : (uint32_t)(tb + r), cl, nv);
       const int64_t left = t1 - tb;
       const int nvalid = !ch_ok ? 0 : left >= 8 ? 8 : (left > 0 ? (int)left : 0);
       uint32_t w[8][4];
@@ -303,14 +308,22 @@ cov_kernel(KeyView k, int64_t chunk, int splits, const float* mean_part, int mea
         unpack8<TT>(rows[2 * rp + 1], f1);
         const uint32_t keep = (2 * rp < nvalid ? 0xffffu : 0u) | (2 * rp + 1 < nvalid ? 0xffff0000u : 0u);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) w[i][rp] = TT::pack2(f0[i] - cen[i], f1[i] - cen[i]) & keep;
+        for (int i = 0; i < 8; ++i) {
+          w[i][rp] = TT::pack2(f0[i] - cen[i], f1[i] - cen[i]);
+          if constexpr (MASK) w[i][rp] &= keep;
+        }
       }
       uint4 op[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) op[i] = make_uint4(w[i][0], w[i][1], w[i][2], w[i][3]);
 #pragma unroll
       for (int t = 0; t < kTiles; ++t) acc[t] = TT::mfma(op[tile_row(t)], op[tile_col(t)], acc[t]);
-    }
+    };
+    // whole 32-token blocks of a head_dim-128 head first, then the rest
+    const int64_t nfull = VEC && k.D == 128 ? (t1 - t0) / 32 : 0;
+    int64_t blk = wave;
+    for (; blk < nfull; blk += kWaves) block(blk, std::false_type{});
+    for (; blk < nblk; blk += kWaves) block(blk, std::true_type{});
   } else {
     // fp32: Kc = K - mean in fp32 (the reference's fp32 subtraction), one
     // token row per v_mfma_f32_16x16x4_f32 step: at step r lane (g, n)
