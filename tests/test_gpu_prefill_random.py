@@ -7,7 +7,8 @@ element-wise loads, and the weighted form adds the query-norm column to the
 mean launch and reads the partials' diagonals back for the ridge.  This test
 draws 40 shapes with a fixed seed (B 1-4, H 1-6, S from one token to past
 several split boundaries, D in {128, 96, 64, 40, 100, 8}, fp16 / bf16 / fp32
-Keys, G in {1, 2, 4, 7}, contiguous or sliced out of a longer buffer;
+Keys, G in {1, 2, 4, 7}, contiguous or sliced out of a longer and wider
+buffer;
 x8 outlier channels except in fp16, whose covariance would overflow to
 infinity as the reference's does) and checks, per shape:
 
@@ -72,13 +73,16 @@ def test_covariance_random_shapes(case):
     _say(f"prefill random {c}")
     g = torch.Generator(device="cuda").manual_seed(1000 + c["i"])
     pad = 23 if c["sliced"] else 0
-    full = torch.randn(B, H, S + 2 * pad, D, generator=g, device="cuda")
+    # sliced views also take a row stride wider than D (16-byte rows stay
+    # aligned: D + 32 channels)
+    wide = D + 32 if c["sliced"] and D % 8 == 0 else D
+    full = torch.randn(B, H, S + 2 * pad, wide, generator=g, device="cuda")
     if dtype != torch.float16:
         # x8 outlier channels; fp16 keeps unit variance, so that a diagonal
         # sum over 4097 tokens stays inside its range (65504)
         full[..., ::37] *= 8.0
     full = (full + c["offset"]).to(dtype)
-    K = full[:, :, pad:pad + S]
+    K = full[:, :, pad:pad + S, :D]
     Q = torch.randn(B, H * G, 48, D, generator=g, device="cuda").to(dtype)
 
     mean, cov = prefill.key_covariance(K)
