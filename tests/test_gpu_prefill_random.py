@@ -21,6 +21,10 @@ infinity as the reference's does) and checks, per shape:
     kernel's own covariance (1e-5 of the largest entry: fp32 against fp64
     arithmetic on identical inputs).
 
+A second draw of 24 shapes (head dims as above, any keep from 1 to D)
+runs the selection and write stages: channel scores, head-wise top-k, the
+R_partial / delta_mu gather and the truncated Key write.
+
 Every case prints its parameters before it touches the GPU.
 """
 import sys
@@ -108,3 +112,62 @@ def test_covariance_random_shapes(case):
     assert torch.equal(cov_w, two)
     ow = op.query_weight(got, _np(Q), G, dtype=DT[dtype])
     assert np.abs(_np(cov_w) - ow).max() <= 1e-5 * np.abs(ow).max()
+
+
+def _rot_cases(n=24, seed=11):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([128, 128, 96, 64, 40, 100, 8]))
+        out.append(dict(i=i, B=int(rng.integers(1, 4)), H=int(rng.integers(1, 5)), S=int(rng.choice(S_CHOICES)),
+                        D=D, keep=int(rng.integers(1, D + 1)),
+                        dtype=[torch.float16, torch.bfloat16, torch.float32][int(rng.integers(0, 3))],
+                        sliced=bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _rot_cases(), ids=lambda c: f"{c['i']}")
+def test_rotate_score_select_random_shapes(case):
+    """The selection and write stages on the same kind of draws: channel
+    scores against the oracle on R rounded to the key dtype (1e-5 relative),
+    head-wise top-k bit for bit against the oracle's on the kernel's own
+    scores, the R_partial gather exact and delta_mu within one storage ulp
+    (fp32: 1e-6 relative), the truncated Key write within one storage ulp
+    (fp32: 1e-5 of the largest entry)."""
+    from rotatek_amd import prefill
+    from oracle.numerics import round_to
+    c = case
+    B, H, S, D, keep, dtype = c["B"], c["H"], c["S"], c["D"], c["keep"], c["dtype"]
+    _say(f"rotate/score/select random {c}")
+    g = torch.Generator(device="cuda").manual_seed(2000 + c["i"])
+    pad = 17 if c["sliced"] else 0
+    wide = D + 32 if c["sliced"] and D % 8 == 0 else D
+    full = torch.randn(B, H, S + 2 * pad, wide, generator=g, device="cuda")
+    K = (full + 0.5).to(dtype)[:, :, pad:pad + S, :D]
+    R = torch.linalg.qr(torch.randn(B, H, D, D, generator=g, device="cuda", dtype=torch.float64))[0].float()
+    mean = torch.randn(B, H, D, generator=g, device="cuda") * 2
+
+    sc = prefill.channel_scores(K, R)
+    idx, mask = prefill.topk_channels(sc, keep)
+    Rp, dm = prefill.gather_rotation(R, idx, mean, dtype)
+    kept = prefill.rotate_keys(K, Rp)
+    torch.cuda.synchronize()
+
+    Kn = _np(K)
+    want = op.channel_scores(Kn, round_to(_np(R), DT[dtype]))
+    np.testing.assert_allclose(_np(sc), want, rtol=1e-5, atol=1e-7)
+    wi, wm = op.topk_channels(_np(sc), keep)
+    np.testing.assert_array_equal(idx.cpu().numpy(), wi)
+    np.testing.assert_array_equal(mask.cpu().numpy(), wm)
+    wR = round_to(np.take_along_axis(_np(R), wi[:, :, None, :], axis=-1), DT[dtype])
+    np.testing.assert_array_equal(_np(Rp), wR)
+    wd = op.delta_mu(_np(mean), wR, DT[dtype])
+    wk = op.rotate_keys(Kn, wR, DT[dtype])
+    if dtype == torch.float32:
+        assert np.abs(_np(dm) - wd).max() <= 1e-6 * max(np.abs(wd).max(), 1.0)
+        assert np.abs(_np(kept) - wk).max() <= 1e-5 * max(np.abs(wk).max(), 1e-30)
+    else:
+        err = np.abs(_np(dm) - wd)
+        assert np.all(err <= _storage_ulp(wd, _np(dm), dtype) + 1e-5), err.max()
+        err = np.abs(_np(kept) - wk)
+        assert np.all(err <= _storage_ulp(wk, _np(kept), dtype) + 1e-3 * ULP[dtype]), err.max()
