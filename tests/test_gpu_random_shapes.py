@@ -10,8 +10,10 @@ checks every output against the float64 oracle at the north-star bars
 (max-abs 2e-3 fp16, 1e-2 bf16), under each planner layout of one-round
 grids (unit-major, chunk-major, chunk-major with enlarged first-dispatched
 chunks at two workgroups per CU, the default, which takes one workgroup per
-CU for a round of small workgroups).  Every case prints its parameters
-first.
+CU for a round of small workgroups).  A second draw of 32 shapes runs
+fp32 inputs (the VALU kernels, one query head per unit or grouped units of
+up to 8 heads of one KV head; D_keep from 0 to 128, G up to 16) at max-abs
+1e-4.  Every case prints its parameters first.
 """
 import sys
 
@@ -94,3 +96,58 @@ def test_random_shape_matches_oracle(case, planner):
     assert got.shape == want.shape
     err = float(np.nanmax(np.abs(got - want))) if got.size else 0.0
     assert np.isfinite(got).all() and err <= TOL[dtype], (case, err)
+
+
+def _cases32(n=32, seed=4242):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4]))
+        G = int(rng.choice([1, 1, 2, 3, 7, 8, 9, 16]))
+        B = int(rng.choice([1, 2, 3]))
+        dk = int(rng.choice([0, 8, 16, 32, 32, 40, 64, 128]))
+        S_v = int(rng.choice([0, 1, 63, 129, 777, 2049, 4097]))
+        S_f = int(rng.choice([0, 1, 17, 80, 300, 1025]))
+        if S_v + S_f == 0:
+            S_f = 5
+        family = "paper" if rng.random() < 0.5 else "gqa"
+        mask_p = float(rng.choice([0.0, 0.0, 0.3]))
+        out.append((i, B, hkv * G, hkv, dk, S_v, S_f, torch.float32, family, mask_p))
+    return out
+
+
+CASES32 = _cases32()
+
+
+@pytest.mark.parametrize("case", CASES32, ids=[f"f{c[0]}" for c in CASES32])
+def test_random_shape_fp32_matches_oracle(case):
+    """fp32 inputs (the VALU kernels: one query head per unit, or up to 8
+    heads of one KV head sharing its K/V rows), random shapes including
+    zero kept channels, empty and odd spans and groups of 9 and 16 heads
+    (two units per KV head), max-abs 1e-4 against the float64 oracle."""
+    from rotatek_amd.kernels.fused_decode import rotatek_decode_fused
+    from rotatek_amd.kernels.gqa_decode import rotatek_decode_gqa
+    i, B, Hq, Hkv, dk, S_v, S_f, dtype, family, mask_p = case
+    print(f"[case] fp32 {case}", flush=True)
+    sys.stdout.flush()
+    g = torch.Generator(device="cuda").manual_seed(3000 + i)
+
+    def rn(*s, scale=1.0):
+        return torch.randn(*s, generator=g, device="cuda") * scale
+
+    R = torch.linalg.qr(torch.randn(B, Hkv, D, D, generator=g, device="cuda"))[0][..., :dk].contiguous()
+    V = rn(B, Hkv, S_v + S_f, D)
+    mask = (torch.rand(B, S_f, generator=g, device="cuda") >= mask_p).to(torch.uint8)
+    inp = dict(q_full=rn(B, Hq, D), R_partial=R, delta_mu=rn(B, Hkv, D, scale=0.5), k_full=rn(B, Hkv, S_f, D),
+               v_full=V[:, :, S_v:], mask_full=mask, k_sparse=rn(B, Hkv, S_v, dk, scale=2.0),
+               v_sparse=V[:, :, :S_v], num_kv_groups=Hq // Hkv)
+    fn = rotatek_decode_gqa if family == "gqa" else rotatek_decode_fused
+    out = fn(**inp)[0]
+    torch.cuda.synchronize()
+    a = {k: (v.detach().cpu().numpy().astype(np.float64) if torch.is_tensor(v) else v) for k, v in inp.items()}
+    want = od.rotatek_decode(a["q_full"], a["R_partial"], a["delta_mu"], a["k_full"], a["v_full"],
+                             a["mask_full"], a["k_sparse"], a["v_sparse"], a["num_kv_groups"])
+    got = out.cpu().numpy().astype(np.float64)
+    assert got.shape == want.shape
+    err = float(np.nanmax(np.abs(got - want))) if got.size else 0.0
+    assert np.isfinite(got).all() and err <= 1e-4, (case, err)
