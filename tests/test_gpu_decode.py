@@ -528,3 +528,38 @@ def test_pruner_ratio_one_decodes():
     out, _, _ = rotatek_decode_gqa(**args)
     torch.cuda.synchronize()
     assert np.abs(_np(out) - _oracle(args)).max() <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("family", ["paper", "gqa"])
+def test_more_units_than_the_reported_grid_y(dtype, family):
+    """66560 work units (B=2080, 32 MHA heads): the unit-major grid puts the
+    unit in blockIdx.y, past the 65536 that hipDeviceProp_t.maxGridSize[1]
+    reports (the dispatch packet's 32-bit grid size takes it; the reference
+    launches B * H programs along its first grid axis).  Sampled batch rows,
+    the last one included, against the oracle on their own slices."""
+    B, H, Dk, S_v, S_f = 2080, 32, 8, 40, 8
+    _say(f"66560 units {family} {dtype}")
+    g = torch.Generator(device="cuda").manual_seed(66560)
+
+    def rn(*s, scale=1.0):
+        return (torch.randn(*s, generator=g, device="cuda") * scale).to(dtype)
+
+    # one orthogonal basis for every head (a batched QR of 66560 matrices
+    # would dominate the test)
+    R1 = torch.linalg.qr(torch.randn(128, 128, generator=g, device="cuda"))[0][:, :Dk]
+    R = R1.to(dtype).expand(B, H, 128, Dk).contiguous()
+    V = rn(B, H, S_v + S_f, 128)
+    inp = dict(q_full=rn(B, H, 128), R_partial=R, delta_mu=rn(B, H, 128, scale=0.5), k_full=rn(B, H, S_f, 128),
+               v_full=V[:, :, S_v:], mask_full=torch.ones(B, S_f, dtype=torch.uint8, device="cuda"),
+               k_sparse=rn(B, H, S_v, Dk, scale=2.0), v_sparse=V[:, :, :S_v], num_kv_groups=1)
+    from rotatek_amd import _lib
+    p = _lib.plan_decode(B, H, H, Dk, S_v, S_f, torch.tensor([], dtype=dtype).element_size(),
+                         _lib.RK_POLICY_GQA if family == "gqa" else _lib.RK_POLICY_PAPER)
+    assert p["units"] == B * H > 65536
+    out = _decode(inp, family)
+    assert torch.isfinite(out.float()).all()
+    for b in (0, 1037, B - 1):
+        sl = {k: (v[b:b + 1] if torch.is_tensor(v) else v) for k, v in inp.items()}
+        err = np.abs(_np(out[b:b + 1]) - _oracle(sl)).max()
+        assert err <= (TOL32 if dtype == torch.float32 else TOL[dtype]), (b, err)

@@ -171,3 +171,46 @@ def test_rotate_score_select_random_shapes(case):
         assert np.all(err <= _storage_ulp(wd, _np(dm), dtype) + 1e-5), err.max()
         err = np.abs(_np(kept) - wk)
         assert np.all(err <= _storage_ulp(wk, _np(kept), dtype) + 1e-3 * ULP[dtype]), err.max()
+
+
+def test_prefill_stages_past_the_reported_grid_y():
+    """B * H = 66560 heads (B=2080, 32 KV heads, 40 tokens): every prefill
+    stage puts the head in blockIdx.y (or x), past the 65536 that
+    hipDeviceProp_t.maxGridSize[1] reports.  Sampled heads, the last one
+    included, against the oracle as in the random cases above."""
+    from rotatek_amd import prefill
+    from oracle.numerics import round_to
+    B, H, S, D, keep, dtype = 2080, 32, 40, 128, 32, torch.bfloat16
+    _say(f"prefill stages B={B} H={H} S={S}")
+    g = torch.Generator(device="cuda").manual_seed(4)
+    K = (torch.randn(B, H, S, D, generator=g, device="cuda") + 0.5).to(dtype)
+    Q = torch.randn(B, H, 8, D, generator=g, device="cuda").to(dtype)
+    R1 = torch.linalg.qr(torch.randn(D, D, generator=g, device="cuda", dtype=torch.float64))[0].float()
+    R = R1.expand(B, H, D, D).contiguous()
+    mean, cov = prefill.key_covariance(K)
+    _, cov_w = prefill.key_covariance(K, Q, 1)
+    sc = prefill.channel_scores(K, R)
+    idx, mask = prefill.topk_channels(sc, keep)
+    Rp, dm = prefill.gather_rotation(R, idx, mean, dtype)
+    kept = prefill.rotate_keys(K, Rp)
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (1037, 17), (B - 1, H - 1)):
+        Kn = _np(K[b:b + 1, h:h + 1])
+        om, _ = op.key_covariance(Kn, "bfloat16")
+        np.testing.assert_allclose(_np(mean[b:b + 1, h:h + 1]), om, rtol=1e-5, atol=1e-6)
+        _, oc = op.key_covariance(Kn, "bfloat16", mean=_np(mean[b:b + 1, h:h + 1]))
+        got = _np(cov[b:b + 1, h:h + 1])
+        scale = np.abs(oc).max()
+        assert np.all(np.abs(got - oc) <= _storage_ulp(oc, got, dtype) + 1e-6 * scale)
+        ow = op.query_weight(got, _np(Q[b:b + 1, h:h + 1]), 1, dtype="bfloat16")
+        assert np.abs(_np(cov_w[b:b + 1, h:h + 1]) - ow).max() <= 1e-5 * np.abs(ow).max()
+        want = op.channel_scores(Kn, round_to(_np(R[b:b + 1, h:h + 1]), "bfloat16"))
+        np.testing.assert_allclose(_np(sc[b:b + 1, h:h + 1]), want, rtol=1e-5, atol=1e-7)
+        wi, wm = op.topk_channels(_np(sc[b:b + 1, h:h + 1]), keep)
+        np.testing.assert_array_equal(idx[b:b + 1, h:h + 1].cpu().numpy(), wi)
+        np.testing.assert_array_equal(mask[b:b + 1, h:h + 1].cpu().numpy(), wm)
+        wR = round_to(np.take_along_axis(_np(R[b:b + 1, h:h + 1]), wi[:, :, None, :], axis=-1), "bfloat16")
+        np.testing.assert_array_equal(_np(Rp[b:b + 1, h:h + 1]), wR)
+        wk = op.rotate_keys(Kn, wR, "bfloat16")
+        err = np.abs(_np(kept[b:b + 1, h:h + 1]) - wk)
+        assert np.all(err <= _storage_ulp(wk, _np(kept[b:b + 1, h:h + 1]), dtype) + 1e-3 * ULP[dtype])
