@@ -884,17 +884,41 @@ decode_kernel(const DecodeArgs a) {
       __syncthreads();
     }
 
+    // q R as a 16-bit hi + lo pair (the score operand).  An entry of 2^15 or
+    // more (fp16 ends at 65504; queries of order 10^4) would overflow the
+    // hi part: then the pair is formed again from q R scaled by 2^-qsh, and
+    // the score multiplier takes 2^qsh.  The scaling is exact, so the scores
+    // equal the unsplit fp32 ones the reference's paper kernel computes
+    // (fused_decode.py:133-139, 166-167).  The unit's largest entry sets qsh
+    // (every wave sees every head and kept channel): one scalar per wave,
+    // and one vote on the common path.
     uint4 qh[DKB], ql[DKB];
+    float qmax = 0.f;
+    auto split_q = [&](float qscale) {
 #pragma unroll
-    for (int kb = 0; kb < DKB; ++kb) {
-      uint16_t hv[8], lv[8];
+      for (int kb = 0; kb < DKB; ++kb) {
+        uint16_t hv[8], lv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = (n < HMAX) ? s_qt[nq][kb * 32 + 8 * g + e] : 0.f;
-        TT::split(v, hv[e], lv[e]);
+        for (int e = 0; e < 8; ++e) {
+          const float v = (n < HMAX) ? s_qt[nq][kb * 32 + 8 * g + e] : 0.f;
+          qmax = fmaxf(qmax, fabsf(v));
+          TT::split(v * qscale, hv[e], lv[e]);
+        }
+        qh[kb] = pack8(hv);
+        ql[kb] = pack8(lv);
       }
-      qh[kb] = pack8(hv);
-      ql[kb] = pack8(lv);
+    };
+    split_q(1.f);
+    float sl2 = a.scale_log2;
+    if (__builtin_amdgcn_ballot_w64(qmax >= 32768.f) != 0) {  // wave-uniform
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) qmax = fmaxf(qmax, shfl_xor(qmax, off));
+      int qexp = 0;
+      (void)frexpf(qmax, &qexp);  // qmax < 2^qexp
+      const int qsh = __builtin_amdgcn_readfirstlane(qmax < INFINITY && qexp > 15 ? qexp - 15 : 0);
+      split_q(ldexpf(1.f, -qsh));
+      sl2 = __builtin_bit_cast(float,
+                               __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, ldexpf(a.scale_log2, qsh))));
     }
     const float bias2 = (n < HMAX ? s_bias[nq] : 0.f) * a.scale_log2;
     auto compute = [&](VisBuf<DKB>& B, int64_t blk) {
@@ -910,7 +934,7 @@ decode_kernel(const DecodeArgs a) {
         for (int kb = 0; kb < DKB; ++kb) cc = TT::mfma(zero_if(kval[kb], B.k[sb][kb]), ql[kb], cc);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          s[4 * sb + i] = (8 * g + 4 * sb + i < lim) ? fmaf(cc[i], a.scale_log2, bias2) : -INFINITY;
+          s[4 * sb + i] = (8 * g + 4 * sb + i < lim) ? fmaf(cc[i], sl2, bias2) : -INFINITY;
       }
       softmax_pv<TT>(s, B.v, m, l, acc);
     };

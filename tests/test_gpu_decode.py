@@ -563,3 +563,26 @@ def test_more_units_than_the_reported_grid_y(dtype, family):
         sl = {k: (v[b:b + 1] if torch.is_tensor(v) else v) for k, v in inp.items()}
         err = np.abs(_np(out[b:b + 1]) - _oracle(sl)).max()
         assert err <= (TOL32 if dtype == torch.float32 else TOL[dtype]), (b, err)
+
+
+@pytest.mark.parametrize("family", ["paper", "gqa"])
+def test_fp16_queries_past_the_split_range(family):
+    """fp16 queries of order 3e4: entries of q R reach ~1e5, past fp16's
+    65504, where a plain fp16 hi + lo split would overflow to inf.  The
+    reference's paper kernel forms q R and the scores in fp32
+    (fused_decode.py:133-139, 166-167); the kernel scales q R by a power of
+    two before the split and the score multiplier back, so the output
+    matches the float64 oracle (softmax over scores of order 1e5: nearly one
+    row).  The scaling is exact and off (factor 1) below 2^15."""
+    B, Hq, Hkv, Dk, S_v, S_f = 2, 8, 4, 32, 300, 40
+    _say(f"fp16 q past the split range {family}")
+    inp = _rand_inputs(B, Hq, Hkv, Dk, S_v, S_f, torch.float16, seed=30000)
+    g = torch.Generator(device="cuda").manual_seed(30001)
+    q = (torch.randn(B, Hq, 128, generator=g, device="cuda") * 3e4).clamp(-6e4, 6e4)
+    inp["q_full"] = q.to(torch.float16)
+    qr = torch.einsum("bhd,bhdk->bhk", inp["q_full"].float(),
+                      inp["R_partial"].float().repeat_interleave(Hq // Hkv, dim=1))
+    assert qr.abs().max().item() > 65504  # the case the split must survive
+    out = _decode(inp, family)
+    assert torch.isfinite(out.float()).all()
+    assert np.abs(_np(out) - _oracle(inp)).max() <= TOL[torch.float16]
