@@ -13,7 +13,9 @@ chunks at two workgroups per CU, the default, which takes one workgroup per
 CU for a round of small workgroups).  A second draw of 32 shapes runs
 fp32 inputs (the VALU kernels, one query head per unit or grouped units of
 up to 8 heads of one KV head; D_keep from 0 to 128, G up to 16) at max-abs
-1e-4.  Every case prints its parameters first.
+1e-4.  A third draw of 24 runs the full-channel baseline through both of its
+entries (head dims 8-128, 1 to 9001 tokens, G up to 20, fp16 / bf16 / fp32,
+contiguous or sliced K / V).  Every case prints its parameters first.
 """
 import sys
 
@@ -151,3 +153,56 @@ def test_random_shape_fp32_matches_oracle(case):
     assert got.shape == want.shape
     err = float(np.nanmax(np.abs(got - want))) if got.size else 0.0
     assert np.isfinite(got).all() and err <= 1e-4, (case, err)
+
+
+def _dense_cases(n=24, seed=99):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        out.append(dict(i=i, B=int(rng.choice([1, 2, 3, 5])), Hkv=hkv, G=int(rng.choice([1, 1, 2, 4, 7, 16, 20])),
+                        S=int(rng.choice([1, 2, 31, 33, 257, 1000, 4097, 9001])),
+                        D=int(rng.choice([128, 128, 96, 64, 40, 8])),
+                        dtype=[torch.float16, torch.bfloat16, torch.float32][int(rng.integers(0, 3))],
+                        strided=bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _dense_cases(), ids=lambda c: f"d{c['i']}")
+def test_dense_baseline_random_shapes(case):
+    """The full-channel baseline (rk_full_channel_decode) on seeded random
+    shapes: both entries (one unit per query head, and the grouped one that
+    reads each K / V row once per KV head), head dims 8-128, one to 9001
+    tokens, G up to 20, fp16 / bf16 / fp32, contiguous or sliced K / V,
+    against the float64 oracle at the decode bars (fp32: 1e-4)."""
+    from rotatek_amd.kernels.full_channel_flash_decoding import full_channel_decode
+    from rotatek_amd.kernels.gqa_decode import full_channel_decode_gqa
+    c = case
+    B, Hkv, G, S, D, dtype = c["B"], c["Hkv"], c["G"], c["S"], c["D"], c["dtype"]
+    print(f"[case] dense random {c}", flush=True)
+    sys.stdout.flush()
+    g = torch.Generator(device="cuda").manual_seed(7000 + c["i"])
+
+    def rn(*s):
+        return torch.randn(*s, generator=g, device="cuda").to(dtype)
+
+    q = rn(B, Hkv * G, D)
+    if c["strided"]:
+        big_k, big_v = rn(B, Hkv, S + 9, D + 8 if D % 8 == 0 else D), rn(B, Hkv, S + 9, D)
+        k, v = big_k[:, :, 4:4 + S, :D], big_v[:, :, 5:5 + S]
+    else:
+        k, v = rn(B, Hkv, S, D), rn(B, Hkv, S, D)
+    want = od.full_channel_decode(_np_t(q), _np_t(k), _np_t(v), G)
+    tol = 1e-4 if dtype == torch.float32 else TOL[dtype]
+    for fn in (full_channel_decode, full_channel_decode_gqa):
+        out = fn(q, k, v, G)
+        torch.cuda.synchronize()
+        got = _np_t(out)
+        assert got.shape == want.shape
+        assert np.isfinite(got).all()
+        err = float(np.abs(got - want).max())
+        assert err <= tol, (fn.__name__, err)
+
+
+def _np_t(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
