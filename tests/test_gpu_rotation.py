@@ -296,3 +296,40 @@ def test_power_iteration_and_update_rotatek_in_a_hip_graph():
         power_iteration_gpu(other_cov, 24)
         other.update_rotatek(K[:1, :2, :500], Q[:1, :14, :500], None, None, G)
         torch.cuda.synchronize()
+
+
+def _pi_cases(n=20, seed=31):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        D = int(rng.choice([8, 24, 40, 64, 80, 100, 128]))
+        out.append(dict(i=i, D=D, k=int(rng.integers(1, D + 1)), iters=int(rng.choice([1, 3, 5, 8])),
+                        B=int(rng.integers(1, 3)), H=int(rng.integers(1, 4))))
+    return out
+
+
+@pytest.mark.parametrize("case", _pi_cases(), ids=lambda c: f"{c['i']}")
+def test_power_iteration_random_shapes(case):
+    """Seeded random head dims (8-128), widths k (1..D) and iteration counts
+    (1-8), from the same start block as the float64 oracle, ridge 1e-4:
+    2e-3 of the largest entry while k <= D / 2, 1e-2 for wider bases (they
+    reach eigenvalues down to 0.01 of the top block's 20)."""
+    from rotatek_amd.rotation import power_iteration_hip
+    c = case
+    D, k, iters, B, H = c["D"], c["k"], c["iters"], c["B"], c["H"]
+    _say(f"power iteration random {c}")
+    g = torch.Generator(device="cuda").manual_seed(900 + c["i"])
+    Q = torch.linalg.qr(torch.randn(B, H, D, D, generator=g, device="cuda", dtype=torch.float64))[0]
+    lam = torch.linspace(1.0, 0.01, D, device="cuda", dtype=torch.float64)
+    lam[:min(16, D)] *= 20.0
+    lam = lam * (1 + 0.1 * torch.rand(B, H, D, generator=g, device="cuda", dtype=torch.float64))
+    C = (Q * lam[..., None, :]) @ Q.transpose(-1, -2)
+    cov = (0.5 * (C + C.transpose(-1, -2))).float().contiguous()
+    V0 = torch.randn(B, H, D, k, generator=g, device="cuda")
+    got = power_iteration_hip(cov, V0, iters, 1e-4)
+    torch.cuda.synchronize()
+    want = op.power_iteration(cov.double().cpu().numpy(), V0.double().cpu().numpy(), iters, 1e-4)
+    g_np = got.double().cpu().numpy()
+    assert g_np.shape == want.shape == (B, H, D, k)
+    tol = 2e-3 if 2 * k <= D else 1e-2
+    assert np.abs(g_np - want).max() < tol * max(1.0, np.abs(want).max())
